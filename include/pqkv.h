@@ -1,0 +1,215 @@
+/*
+ * pqkv.h - C ABI of the MI355X (gfx950) PolarQuant-KV hot path.
+ *
+ * One shared library, libpqkv_hip.so, exports every function below. All
+ * tensor arguments are device pointers owned by the caller; `stream` is a
+ * hipStream_t passed as void* (NULL = the null stream). Work is enqueued on
+ * that stream and the call returns without synchronising. Every function
+ * validates its arguments in host code before any HIP call and returns a
+ * status (PQKV_OK = 0, negative on error); pqkv_last_error() gives the
+ * message of the last failure on the calling thread. No function keeps state
+ * between calls or allocates device memory, except the reference-compatible
+ * polarquant_* entry points at the end, which mirror the reference's own
+ * ownership rules.
+ *
+ * Storage format (README.md:73-78 of the reference, "block_pq4"):
+ *   one head vector of d coordinates = d/32 blocks; block = {fp16 radius;
+ *   uint8 qs[16]} (18 B) for 4-bit codes, {fp16 radius; uint8 qs[8]} (10 B)
+ *   for 2-bit codes. The radius is the fp16 (RNE) norm of the whole rotated
+ *   vector, repeated in each block. Code of coordinate 32b+2i sits in the
+ *   low nibble of qs[i], 32b+2i+1 in the high nibble; 2-bit codes pack
+ *   v0 | v1<<2 | v2<<4 | v3<<6.
+ * A KV cache is [B][H][S_max][d/32 blocks], i.e. each (batch, head) owns a
+ * contiguous run of S_max vectors.
+ */
+#ifndef PQKV_H
+#define PQKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status and dtypes ------------------------------------------------ */
+#define PQKV_OK               0
+#define PQKV_ERR_INVALID     -1  /* null pointer, negative or inconsistent size   */
+#define PQKV_ERR_UNSUPPORTED -2  /* head dim, bit width, dtype or group size       */
+#define PQKV_ERR_WORKSPACE   -3  /* workspace smaller than the *_workspace_bytes  */
+#define PQKV_ERR_HIP         -4  /* a HIP launch or runtime call failed            */
+
+#define PQKV_F32  0
+#define PQKV_F16  1
+#define PQKV_BF16 2
+
+#define PQKV_MAX_HEADS 256       /* kv heads per call (mixed-width tables)  */
+
+int         pqkv_version(void);
+const char *pqkv_status_string(int status);
+const char *pqkv_last_error(void);
+
+/* Bytes of one block (18 for 4-bit, 10 for 2-bit) and of one d-vector.
+ * Pure host functions; return <= 0 for unsupported arguments. */
+int     pqkv_block_bytes(int n_bits);
+int64_t pqkv_vector_bytes(int d, int n_bits);
+
+/* Lloyd-Max codebook for one rotated unit-vector coordinate, computed on the
+ * host (Beta((d-1)/2,(d-1)/2) on a grid over +-6/sqrt(d), midpoint/centroid
+ * iterations). Replaces build_lloyd_max_codebook,
+ * src/polarquant_kv_cuda/lloyd_max.py:12-79. centroids has 2^n_bits floats,
+ * boundaries (nullable) 2^n_bits+1. Pure host function. */
+int pqkv_lloyd_max_codebook(int d, int n_bits, int n_iterations, int grid_size,
+                            float *centroids, float *boundaries);
+
+/* ---- rotation ----------------------------------------------------------
+ * y = x R^T (inverse = 0) or y = x R (inverse = 1) for n vectors of d.
+ * x_dtype / y_dtype in {PQKV_F32, PQKV_F16}. Each output is one fp32 FMA
+ * chain over j in increasing order, the arithmetic of the reference's
+ * rotate kernels (integration/polarquant-kv.patch:395-437,
+ * csrc/polarquant_full.cu:25-40,125-140) and of its encode kernel
+ * (csrc/flash_turboquant.cu:132-137). d <= 256. */
+int pqkv_rotate(const void *x, int x_dtype, const float *R, void *y, int y_dtype,
+                int64_t n, int d, int inverse, void *stream);
+
+/* ---- encode ------------------------------------------------------------
+ * Bit-exact quantiser on fp32 rotated input (the parity surface):
+ * radius by the reference's 128-slot tree of squares and sqrtf, direction by
+ * IEEE divide, nearest centroid by a strict '<' scan, codes packed to blocks.
+ * Replaces the quantise half of turboquant_compress_kernel
+ * (csrc/flash_turboquant.cu:141-173). radius_out (nullable) receives the fp32
+ * radius. d in {64, 128}, n_bits in {2, 4}. */
+int pqkv_quantize_rotated(const float *x_rot, const float *codebook, int n_bits,
+                          uint8_t *blocks_out, float *radius_out,
+                          int64_t n, int d, void *stream);
+
+/* Fused encoder: rotate, quantise and pack n_outer x n_inner vectors.
+ * x: fp16 or fp32, vector (o, i) at x + (o * x_outer_stride + i * d) elements.
+ * blocks: vector (o, i) at blocks + o * blocks_outer_stride + i * vector_bytes.
+ * Optional QJL sign sketch of the key residual (p_rot = P R^T, [m][d] fp32,
+ * m = d): signs at qjl + o * qjl_outer_stride + i * (m/8), bit i of the
+ * sketch = (p_rot[i] . (x_rot - r c[idx]) >= 0), LSB first
+ * (src/polarquant_kv_cuda/compress_kernel.py:166-175, qjl_kernel.py:6-37).
+ * Replaces turboquant_compress (csrc/flash_turboquant.cu:213-225) and
+ * polarquant_compress_cuda (patch:443-467). */
+int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride,
+                const float *R, const float *codebook, int n_bits,
+                uint8_t *blocks, int64_t blocks_outer_stride,
+                int64_t n_outer, int64_t n_inner, int d,
+                const float *p_rot, int m, uint8_t *qjl, int64_t qjl_outer_stride,
+                void *stream);
+
+/* ---- decode attention ----------------------------------------------------
+ * One query token per sequence against a block-encoded cache:
+ *   q_rot = q R^T; s_t = scale * r_k,t * q_rot . c_k[idx_t]
+ *           (+ scale * (1/m) sum_i (2 sign_i - 1) (p_rot q_rot)_i if qjl)
+ *   w = softmax(s);  out = (sum_t w_t r_v,t c_v[vidx_t]) R
+ * q [B][Hq][d] (fp16/fp32), out [B][Hq][d] (fp16/fp32), caches
+ * [B][Hkv][S_max] vectors, first S valid. q-head h reads kv-head
+ * h / (Hq/Hkv). k_head_bits / v_head_bits: host arrays of Hkv widths (2 or 4)
+ * for mixed-width heads, or NULL for uniform k_bits / v_bits; with mixed
+ * widths each (b, h) run still holds S_max vectors of its own width, runs laid
+ * out in (b, h) order. k_codebooks / v_codebooks: device [Hkv][16] fp32
+ * per-head tables, or one table when the *_head_bits pointer is NULL.
+ * Replaces turboquant_full_attention (csrc/flash_turboquant.cu:180-211),
+ * polarquant_fused_attention_cuda (patch:469-506) plus the query and output
+ * rotations around them (patch:395-437). S = 0 writes zeros. */
+size_t pqkv_decode_workspace_bytes(int B, int Hq, int Hkv, int S, int d);
+
+int pqkv_decode_attn(const void *q, int q_dtype, const float *R,
+                     const uint8_t *k_cache, const uint8_t *v_cache,
+                     const float *k_codebooks, const float *v_codebooks,
+                     int k_bits, int v_bits,
+                     const int *k_head_bits, const int *v_head_bits,
+                     const uint8_t *qjl_signs, const float *p_rot, int m,
+                     int B, int Hq, int Hkv, int S, int S_max, int d, float scale,
+                     void *out, int out_dtype,
+                     void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- chunked prefill attention -------------------------------------------
+ * Sq query tokens per sequence (absolute positions q_start .. q_start+Sq-1)
+ * against a cache that already holds them (append-then-attend,
+ * src/polarquant_kv_cuda/inference/attention.py:59-61). With causal = 1
+ * query i attends to cache positions <= q_start + i; with causal = 0 to all
+ * S positions. q / out [B][Hq][Sq][d]. Uniform widths only. */
+size_t pqkv_prefill_workspace_bytes(int B, int Hq, int Hkv, int Sq, int S, int d);
+
+int pqkv_prefill_attn(const void *q, int q_dtype, const float *R,
+                      const uint8_t *k_cache, const uint8_t *v_cache,
+                      const float *k_codebook, const float *v_codebook,
+                      int k_bits, int v_bits,
+                      int B, int Hq, int Hkv, int Sq, int q_start, int S, int S_max,
+                      int d, float scale, int causal,
+                      void *out, int out_dtype,
+                      void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- layout converters ---------------------------------------------------
+ * SoA (the reference kernels' format: packed u8 [n][d/2] + fp32 radius [n],
+ * csrc/flash_turboquant.cu:29-32) <-> block_pq4. 4-bit codes only. */
+int pqkv_soa_to_blocks(const uint8_t *packed, const float *radius,
+                       uint8_t *blocks, int64_t n, int d, void *stream);
+int pqkv_blocks_to_soa(const uint8_t *blocks, uint8_t *packed, float *radius,
+                       int64_t n, int d, void *stream);
+
+/* ---- measurement hook (no counterpart in the reference) -----------------
+ * With profiling on, the library brackets each launch of its main kernels
+ * with hipEvents recorded on the launch stream. pqkv_profile_collect waits
+ * for those events and returns, for kernels whose name contains `name`
+ * ("decode_split", "decode_merge", "encode", "rotate", ...), the summed
+ * duration in ms and the number of launches, then forgets them. Used by
+ * bench.py; off by default, and costs nothing when off. */
+int pqkv_profile_enable(int on);
+int pqkv_profile_collect(const char *name, double *total_ms, int64_t *launches);
+
+/* ---- reference-compatible entry points -------------------------------------
+ * Same names, arguments and return types as the extern "C" exports of the
+ * reference's ggml CUDA backend (integration/polarquant-kv.patch:695-763),
+ * which llama.cpp resolves with dlsym (patch:1508-1557). SoA layout (packed
+ * u8 [N][D/2] + fp32 radius [N]); errors print to stderr and return, like
+ * the reference's silent early returns (patch:452,481,515,534). */
+typedef struct polarquant_kv_layer {
+    uint8_t *k_packed;  /* [n_kv_heads][n_kv_max][head_dim/2] */
+    float   *k_radius;  /* [n_kv_heads][n_kv_max]             */
+    uint8_t *v_packed;
+    float   *v_radius;
+} polarquant_kv_layer;
+
+typedef struct polarquant_state {
+    int    enabled;     /* bool in the reference (patch:958); int here for a C ABI */
+    int    n_bits;
+    int    n_levels;
+    int    head_dim;
+    int    n_kv_heads;
+    int    n_q_heads;
+    int    n_layers;
+    int    n_kv_max;
+    float *codebook;    /* device [n_levels]            */
+    float *rotation;    /* device [head_dim][head_dim]  */
+    polarquant_kv_layer *layers;  /* host array of n_layers */
+} polarquant_state;
+
+polarquant_state *polarquant_init_c(int head_dim, int n_kv_heads, int n_q_heads,
+                                    int n_layers, int n_kv_max, int n_bits);
+void polarquant_free_c(polarquant_state *state);
+void polarquant_compress_cuda_c(const float *input, const float *rotation,
+                                const float *codebook, float *radius_out,
+                                uint8_t *packed_out, int N, int D, int n_levels,
+                                void *stream);
+void polarquant_rotate_query_cuda_c(const float *q_input, const float *rotation,
+                                    float *q_rotated, int total_q_heads, int D,
+                                    void *stream);
+void polarquant_fused_attention_cuda_c(const float *q_rotated, const uint8_t *packed_k,
+                                       const float *k_radius, const uint8_t *packed_v,
+                                       const float *v_radius, const float *codebook,
+                                       float *output, int total_q_heads,
+                                       int total_kv_heads, int S, int D, int n_levels,
+                                       float scale, void *stream);
+void polarquant_inverse_rotate_cuda_c(const float *input, const float *rotation,
+                                      float *output, int total_q_heads, int D,
+                                      void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PQKV_H */

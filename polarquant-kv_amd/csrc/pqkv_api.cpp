@@ -1,0 +1,423 @@
+// C ABI of libpqkv_hip.so (declared in include/pqkv.h).
+//
+// Every entry point validates its arguments in host code first and only then
+// touches HIP, so argument errors are testable on a machine without a GPU.
+#include "../../include/pqkv.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "pqkv_launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char *what) {
+  if (e == hipSuccess) return PQKV_OK;
+  return fail(PQKV_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool supported_d(int d) { return d == 64 || d == 128; }
+bool supported_bits(int b) { return b == 2 || b == 4; }
+bool float_dtype(int t) { return t == PQKV_F32 || t == PQKV_F16; }
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Split-K plan: about 1024 workgroups, whole 64-token tiles per wave.
+void decode_plan(int B, int Hkv, int S, int *splits, int *tps) {
+  const int64_t streams = (int64_t)B * Hkv;
+  int64_t want = (1024 + streams - 1) / streams;
+  int64_t t = (S + want - 1) / want;
+  if (t < 256) t = 256;
+  t = (t + 63) / 64 * 64;
+  *tps = (int)t;
+  *splits = (int)((S + t - 1) / t);
+  if (*splits < 1) *splits = 1;
+}
+
+struct ProfRecord {
+  std::string name;
+  hipEvent_t start, stop;
+  bool closed;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+std::vector<ProfRecord> g_prof;
+
+}  // namespace
+
+namespace pqkv {
+
+int prof_begin(const char *name, hipStream_t s) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  if (!g_prof_on) return -1;
+  ProfRecord r{name, nullptr, nullptr, false};
+  if (hipEventCreate(&r.start) != hipSuccess || hipEventCreate(&r.stop) != hipSuccess) return -1;
+  if (hipEventRecord(r.start, s) != hipSuccess) return -1;
+  g_prof.push_back(r);
+  return (int)g_prof.size() - 1;
+}
+
+void prof_end(int token, hipStream_t s) {
+  if (token < 0) return;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  if (token < (int)g_prof.size() && hipEventRecord(g_prof[token].stop, s) == hipSuccess) g_prof[token].closed = true;
+}
+
+}  // namespace pqkv
+
+extern "C" {
+
+int pqkv_profile_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_prof_on = on != 0;
+  return PQKV_OK;
+}
+
+int pqkv_profile_collect(const char *name, double *total_ms, int64_t *launches) {
+  if (!name || !total_ms || !launches) return fail(PQKV_ERR_INVALID, "profile_collect: null pointer");
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  double tot = 0.0;
+  int64_t n = 0;
+  std::vector<ProfRecord> keep;
+  for (auto &r : g_prof) {
+    if (r.name.find(name) == std::string::npos) {
+      keep.push_back(r);
+      continue;
+    }
+    if (r.closed && hipEventSynchronize(r.stop) == hipSuccess) {
+      float ms = 0.0f;
+      if (hipEventElapsedTime(&ms, r.start, r.stop) == hipSuccess) {
+        tot += ms;
+        ++n;
+      }
+    }
+    (void)hipEventDestroy(r.start);
+    (void)hipEventDestroy(r.stop);
+  }
+  g_prof.swap(keep);
+  *total_ms = tot;
+  *launches = n;
+  return PQKV_OK;
+}
+
+int pqkv_version(void) { return 1; }
+
+const char *pqkv_status_string(int status) {
+  switch (status) {
+    case PQKV_OK: return "ok";
+    case PQKV_ERR_INVALID: return "invalid argument";
+    case PQKV_ERR_UNSUPPORTED: return "unsupported configuration";
+    case PQKV_ERR_WORKSPACE: return "workspace too small";
+    case PQKV_ERR_HIP: return "HIP error";
+    default: return "unknown status";
+  }
+}
+
+const char *pqkv_last_error(void) { return g_err; }
+
+int pqkv_block_bytes(int n_bits) { return supported_bits(n_bits) ? pqkv::block_bytes(n_bits) : -1; }
+
+int64_t pqkv_vector_bytes(int d, int n_bits) {
+  if (d <= 0 || d % 32 || !supported_bits(n_bits)) return -1;
+  return (int64_t)(d / 32) * pqkv::block_bytes(n_bits);
+}
+
+// ---------------------------------------------------------------------------
+// Lloyd-Max codebook (host). Same iteration as lloyd_max.py:12-79; sums use
+// numpy's pairwise order so the float32 results match the reference's.
+// ---------------------------------------------------------------------------
+static double pairwise_sum(const double *a, size_t n) {
+  if (n < 8) {
+    double r = 0.0;
+    for (size_t i = 0; i < n; ++i) r += a[i];
+    return r;
+  }
+  if (n <= 128) {
+    double r[8];
+    for (int k = 0; k < 8; ++k) r[k] = a[k];
+    size_t i;
+    for (i = 8; i < n - (n % 8); i += 8)
+      for (int k = 0; k < 8; ++k) r[k] += a[i + k];
+    double res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+    for (; i < n; ++i) res += a[i];
+    return res;
+  }
+  size_t n2 = n / 2;
+  n2 -= n2 % 8;
+  return pairwise_sum(a, n2) + pairwise_sum(a + n2, n - n2);
+}
+
+int pqkv_lloyd_max_codebook(int d, int n_bits, int n_iterations, int grid_size, float *centroids,
+                            float *boundaries) {
+  if (d < 2 || n_bits < 1 || n_bits > 8 || n_iterations < 0 || grid_size < 2 || centroids == nullptr)
+    return fail(PQKV_ERR_INVALID, "lloyd_max: bad arguments d=%d bits=%d iters=%d grid=%d", d, n_bits,
+                n_iterations, grid_size);
+  const int L = 1 << n_bits;
+  const double alpha = (d - 1) / 2.0;
+  const double sigma = 1.0 / std::sqrt((double)d);
+  const double xr = 6 * sigma;
+  std::vector<double> grid(grid_size), pdf(grid_size);
+  const double step = (xr - (-xr)) / (double)(grid_size - 1);
+  for (int i = 0; i < grid_size; ++i) grid[i] = (double)i * step + (-xr);
+  grid[grid_size - 1] = xr;
+  // Beta(alpha, alpha) density of t = (x + 1) / 2, times the Jacobian 1/2.
+  const double lbeta = 2 * std::lgamma(alpha) - std::lgamma(2 * alpha);
+  for (int i = 0; i < grid_size; ++i) {
+    double t = (grid[i] + 1) / 2;
+    if (t < 1e-10) t = 1e-10;
+    if (t > 1 - 1e-10) t = 1 - 1e-10;
+    pdf[i] = std::exp((alpha - 1) * std::log(t) + (alpha - 1) * std::log1p(-t) - lbeta) / 2;
+  }
+  const double norm = pairwise_sum(pdf.data(), pdf.size()) * (grid[1] - grid[0]);
+  for (auto &p : pdf) p = p / norm;
+  std::vector<double> c(L), bnd(L + 1, 0.0), nc(L), gw, ww;
+  for (int i = 0; i < L; ++i) c[i] = L == 1 ? -xr : (double)i * ((xr - (-xr)) / (double)(L - 1)) + (-xr);
+  if (L > 1) c[L - 1] = xr;
+  for (int it = 0; it < n_iterations; ++it) {
+    bnd[0] = -xr * 2;
+    bnd[L] = xr * 2;
+    for (int i = 1; i < L; ++i) bnd[i] = (c[i - 1] + c[i]) / 2;
+    for (int i = 0; i < L; ++i) {
+      gw.clear();
+      ww.clear();
+      for (int g = 0; g < grid_size; ++g)
+        if (grid[g] >= bnd[i] && grid[g] < bnd[i + 1]) {
+          ww.push_back(pdf[g]);
+          gw.push_back(grid[g] * pdf[g]);
+        }
+      if (!ww.empty()) {
+        const double wsum = pairwise_sum(ww.data(), ww.size());
+        nc[i] = wsum > 0 ? pairwise_sum(gw.data(), gw.size()) / wsum : c[i];
+      } else {
+        nc[i] = c[i];
+      }
+    }
+    c = nc;
+  }
+  for (int i = 0; i < L; ++i) centroids[i] = (float)c[i];
+  if (boundaries)
+    for (int i = 0; i <= L; ++i) boundaries[i] = (float)bnd[i];
+  return PQKV_OK;
+}
+
+// ---------------------------------------------------------------------------
+int pqkv_rotate(const void *x, int x_dtype, const float *R, void *y, int y_dtype, int64_t n, int d, int inverse,
+                void *stream) {
+  if (n < 0) return fail(PQKV_ERR_INVALID, "rotate: n=%lld < 0", (long long)n);
+  if (!supported_d(d)) return fail(PQKV_ERR_UNSUPPORTED, "rotate: d=%d (supported: 64, 128)", d);
+  if (!float_dtype(x_dtype) || !float_dtype(y_dtype))
+    return fail(PQKV_ERR_UNSUPPORTED, "rotate: dtypes %d -> %d", x_dtype, y_dtype);
+  if (n == 0) return PQKV_OK;
+  if (!x || !R || !y) return fail(PQKV_ERR_INVALID, "rotate: null pointer");
+  return hip_status(pqkv::launch_rotate(x, x_dtype, R, y, y_dtype, n, d, inverse ? 1 : 0, 1.0f,
+                                        (hipStream_t)stream),
+                    "rotate launch");
+}
+
+int pqkv_quantize_rotated(const float *x_rot, const float *codebook, int n_bits, uint8_t *blocks_out,
+                          float *radius_out, int64_t n, int d, void *stream) {
+  if (n < 0) return fail(PQKV_ERR_INVALID, "quantize_rotated: n < 0");
+  if (!supported_d(d) || !supported_bits(n_bits))
+    return fail(PQKV_ERR_UNSUPPORTED, "quantize_rotated: d=%d bits=%d", d, n_bits);
+  if (n == 0) return PQKV_OK;
+  if (!x_rot || !codebook || !blocks_out) return fail(PQKV_ERR_INVALID, "quantize_rotated: null pointer");
+  return hip_status(pqkv::launch_quantize_rotated(x_rot, codebook, n_bits, blocks_out, radius_out, n, d,
+                                                  (hipStream_t)stream),
+                    "quantize_rotated launch");
+}
+
+int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride, const float *R, const float *codebook,
+                int n_bits, uint8_t *blocks, int64_t blocks_outer_stride, int64_t n_outer, int64_t n_inner, int d,
+                const float *p_rot, int m, uint8_t *qjl, int64_t qjl_outer_stride, void *stream) {
+  if (n_outer < 0 || n_inner < 0) return fail(PQKV_ERR_INVALID, "encode: negative count");
+  if (!supported_d(d) || !supported_bits(n_bits))
+    return fail(PQKV_ERR_UNSUPPORTED, "encode: d=%d bits=%d", d, n_bits);
+  if (!float_dtype(x_dtype)) return fail(PQKV_ERR_UNSUPPORTED, "encode: x dtype %d", x_dtype);
+  if ((qjl == nullptr) != (p_rot == nullptr)) return fail(PQKV_ERR_INVALID, "encode: qjl and p_rot go together");
+  if (qjl && m != d) return fail(PQKV_ERR_UNSUPPORTED, "encode: QJL needs m == d (m=%d, d=%d)", m, d);
+  if (n_outer * n_inner == 0) return PQKV_OK;
+  if (!x || !R || !codebook || !blocks) return fail(PQKV_ERR_INVALID, "encode: null pointer");
+  const int64_t vb = pqkv_vector_bytes(d, n_bits);
+  if (n_outer > 1 && (x_outer_stride < n_inner * d || blocks_outer_stride < n_inner * vb))
+    return fail(PQKV_ERR_INVALID, "encode: outer strides overlap rows");
+  if (qjl && n_outer > 1 && qjl_outer_stride < n_inner * (m / 8))
+    return fail(PQKV_ERR_INVALID, "encode: qjl outer stride overlaps rows");
+  pqkv::EncodeArgs a{x, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride, n_outer, n_inner,
+                     d, p_rot, m, qjl, qjl_outer_stride};
+  const int tok = pqkv::prof_begin("encode_exact", (hipStream_t)stream);
+  const hipError_t e = pqkv::launch_encode_exact(a, x_dtype, (hipStream_t)stream);
+  pqkv::prof_end(tok, (hipStream_t)stream);
+  return hip_status(e, "encode launch");
+}
+
+size_t pqkv_decode_workspace_bytes(int B, int Hq, int Hkv, int S, int d) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || S < 0 || d <= 0) return 0;
+  int splits = 1, tps = 0;
+  decode_plan(B, Hkv, S > 0 ? S : 1, &splits, &tps);
+  return align256((size_t)B * Hq * d * 2) + align256((size_t)B * Hq * splits * (d + 2) * 4);
+}
+
+int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *k_cache, const uint8_t *v_cache,
+                     const float *k_codebooks, const float *v_codebooks, int k_bits, int v_bits,
+                     const int *k_head_bits, const int *v_head_bits, const uint8_t *qjl_signs, const float *p_rot,
+                     int m, int B, int Hq, int Hkv, int S, int S_max, int d, float scale, void *out, int out_dtype,
+                     void *workspace, size_t workspace_bytes, void *stream) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || S < 0 || S_max < S)
+    return fail(PQKV_ERR_INVALID, "decode: B=%d Hq=%d Hkv=%d S=%d S_max=%d", B, Hq, Hkv, S, S_max);
+  if (Hq % Hkv) return fail(PQKV_ERR_INVALID, "decode: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
+  if (Hq / Hkv > 8) return fail(PQKV_ERR_UNSUPPORTED, "decode: group size %d > 8", Hq / Hkv);
+  if (!supported_d(d)) return fail(PQKV_ERR_UNSUPPORTED, "decode: d=%d", d);
+  if (!float_dtype(q_dtype) || !float_dtype(out_dtype)) return fail(PQKV_ERR_UNSUPPORTED, "decode: dtype");
+  const bool mixed = k_head_bits != nullptr || v_head_bits != nullptr;
+  if (mixed && Hkv > pqkv::kMaxListHeads)
+    return fail(PQKV_ERR_UNSUPPORTED, "decode: mixed widths support at most %d kv heads", pqkv::kMaxListHeads);
+  std::vector<int> kb(Hkv, k_bits), vb(Hkv, v_bits);
+  for (int h = 0; h < Hkv; ++h) {
+    if (k_head_bits) kb[h] = k_head_bits[h];
+    if (v_head_bits) vb[h] = v_head_bits[h];
+    if (!supported_bits(kb[h]) || !supported_bits(vb[h]))
+      return fail(PQKV_ERR_UNSUPPORTED, "decode: head %d widths k=%d v=%d", h, kb[h], vb[h]);
+  }
+  if ((qjl_signs == nullptr) != (p_rot == nullptr)) return fail(PQKV_ERR_INVALID, "decode: qjl and p_rot go together");
+  if (qjl_signs && m != d) return fail(PQKV_ERR_UNSUPPORTED, "decode: QJL needs m == d");
+  if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(PQKV_ERR_INVALID, "decode: scale must be > 0");
+  if (!q || !R || !out) return fail(PQKV_ERR_INVALID, "decode: null pointer");
+  const size_t need = pqkv_decode_workspace_bytes(B, Hq, Hkv, S, d);
+  if (S > 0) {
+    if (!k_cache || !v_cache || !k_codebooks || !v_codebooks)
+      return fail(PQKV_ERR_INVALID, "decode: null cache or codebook");
+    if (!workspace || workspace_bytes < need)
+      return fail(PQKV_ERR_WORKSPACE, "decode: workspace %zu < %zu bytes", workspace_bytes, need);
+  }
+  hipStream_t st = (hipStream_t)stream;
+  if (S == 0) {
+    const size_t ob = (size_t)B * Hq * d * (out_dtype == PQKV_F32 ? 4 : 2);
+    return hip_status(pqkv::launch_fill_zero(out, ob, st), "decode zero fill");
+  }
+  int splits = 1, tps = 0;
+  decode_plan(B, Hkv, S, &splits, &tps);
+  uint16_t *q16 = (uint16_t *)workspace;
+  float *part = (float *)((char *)workspace + align256((size_t)B * Hq * d * 2));
+  const float kLog2e = 1.4426950408889634f;
+  int tok = pqkv::prof_begin("decode_rotate", st);
+  hipError_t e = pqkv::launch_rotate(q, q_dtype, R, q16, PQKV_F16, (int64_t)B * Hq, d, 0, scale * kLog2e, st);
+  pqkv::prof_end(tok, st);
+  if (e != hipSuccess) return hip_status(e, "decode query rotation");
+
+  pqkv::DecodeArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = q16;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.k_cb = k_codebooks;
+  a.v_cb = v_codebooks;
+  a.cb_head_stride = mixed ? 16 : 0;
+  a.qjl = qjl_signs;
+  a.p_rot = p_rot;
+  a.part = part;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.S = S;
+  a.S_max = S_max;
+  a.d = d;
+  a.splits = splits;
+  a.tokens_per_split = tps;
+  if (!mixed) {
+    const int64_t kvb = pqkv_vector_bytes(d, k_bits), vvb = pqkv_vector_bytes(d, v_bits);
+    a.k_head_stride = (int64_t)S_max * kvb;
+    a.v_head_stride = (int64_t)S_max * vvb;
+    a.k_batch_stride = a.k_head_stride * Hkv;
+    a.v_batch_stride = a.v_head_stride * Hkv;
+    a.n_heads = Hkv;
+    a.listed = 0;
+    tok = pqkv::prof_begin("decode_split", st);
+    e = pqkv::launch_decode_split(a, k_bits, v_bits, st);
+    pqkv::prof_end(tok, st);
+    if (e != hipSuccess) return hip_status(e, "decode split launch");
+  } else {
+    // Per-(b, h) runs of S_max vectors of the head's own width, (b, h) order.
+    std::vector<int64_t> koff(Hkv + 1, 0), voff(Hkv + 1, 0);
+    for (int h = 0; h < Hkv; ++h) {
+      koff[h + 1] = koff[h] + (int64_t)S_max * pqkv_vector_bytes(d, kb[h]);
+      voff[h + 1] = voff[h] + (int64_t)S_max * pqkv_vector_bytes(d, vb[h]);
+    }
+    a.k_batch_stride = koff[Hkv];
+    a.v_batch_stride = voff[Hkv];
+    a.listed = 1;
+    for (int kbits : {4, 2})
+      for (int vbits : {4, 2}) {
+        int n = 0;
+        for (int h = 0; h < Hkv; ++h)
+          if (kb[h] == kbits && vb[h] == vbits) {
+            a.heads[n] = (int16_t)h;
+            a.k_head_off[n] = koff[h];
+            a.v_head_off[n] = voff[h];
+            ++n;
+          }
+        if (n == 0) continue;
+        a.n_heads = n;
+        tok = pqkv::prof_begin("decode_split", st);
+        e = pqkv::launch_decode_split(a, kbits, vbits, st);
+        pqkv::prof_end(tok, st);
+        if (e != hipSuccess) return hip_status(e, "decode split launch");
+      }
+  }
+  tok = pqkv::prof_begin("decode_merge", st);
+  e = pqkv::launch_decode_merge(part, R, out, out_dtype, B * Hq, splits, d, st);
+  pqkv::prof_end(tok, st);
+  return hip_status(e, "decode merge launch");
+}
+
+size_t pqkv_prefill_workspace_bytes(int B, int Hq, int Hkv, int Sq, int S, int d) {
+  (void)B; (void)Hq; (void)Hkv; (void)Sq; (void)S; (void)d;
+  return 0;
+}
+
+int pqkv_prefill_attn(const void *q, int q_dtype, const float *R, const uint8_t *k_cache, const uint8_t *v_cache,
+                      const float *k_codebook, const float *v_codebook, int k_bits, int v_bits, int B, int Hq,
+                      int Hkv, int Sq, int q_start, int S, int S_max, int d, float scale, int causal, void *out,
+                      int out_dtype, void *workspace, size_t workspace_bytes, void *stream) {
+  (void)q; (void)q_dtype; (void)R; (void)k_cache; (void)v_cache; (void)k_codebook; (void)v_codebook;
+  (void)k_bits; (void)v_bits; (void)B; (void)Hq; (void)Hkv; (void)Sq; (void)q_start; (void)S; (void)S_max;
+  (void)d; (void)scale; (void)causal; (void)out; (void)out_dtype; (void)workspace; (void)workspace_bytes;
+  (void)stream;
+  return fail(PQKV_ERR_UNSUPPORTED, "prefill: not built yet");
+}
+
+int pqkv_soa_to_blocks(const uint8_t *packed, const float *radius, uint8_t *blocks, int64_t n, int d,
+                       void *stream) {
+  if (n < 0) return fail(PQKV_ERR_INVALID, "soa_to_blocks: n < 0");
+  if (!supported_d(d)) return fail(PQKV_ERR_UNSUPPORTED, "soa_to_blocks: d=%d", d);
+  if (n == 0) return PQKV_OK;
+  if (!packed || !radius || !blocks) return fail(PQKV_ERR_INVALID, "soa_to_blocks: null pointer");
+  return hip_status(pqkv::launch_soa_to_blocks(packed, radius, blocks, n, d, (hipStream_t)stream),
+                    "soa_to_blocks launch");
+}
+
+int pqkv_blocks_to_soa(const uint8_t *blocks, uint8_t *packed, float *radius, int64_t n, int d, void *stream) {
+  if (n < 0) return fail(PQKV_ERR_INVALID, "blocks_to_soa: n < 0");
+  if (!supported_d(d)) return fail(PQKV_ERR_UNSUPPORTED, "blocks_to_soa: d=%d", d);
+  if (n == 0) return PQKV_OK;
+  if (!packed || !radius || !blocks) return fail(PQKV_ERR_INVALID, "blocks_to_soa: null pointer");
+  return hip_status(pqkv::launch_blocks_to_soa(blocks, packed, radius, n, d, (hipStream_t)stream),
+                    "blocks_to_soa launch");
+}
+
+}  // extern "C"

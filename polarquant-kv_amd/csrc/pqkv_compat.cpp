@@ -1,0 +1,224 @@
+// Reference-compatible exports: the extern "C" surface of the reference's
+// ggml CUDA backend (integration/polarquant-kv.patch:695-763), which
+// llama.cpp binds with dlsym (patch:1508-1557). Same names, arguments, return
+// types and ownership; SoA cache layout (packed u8 [N][D/2] + fp32 radius).
+// Kernels are the library's own: the SoA encoder reproduces the reference's
+// arithmetic exactly; attention converts the SoA operands to block_pq4 and
+// runs the split-K decode kernel with an identity rotation, because these
+// entry points take an already-rotated query and return a rotated output.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "../../include/pqkv.h"
+#include "pqkv_launch.h"
+
+namespace {
+
+bool report(hipError_t e, const char *what) {
+  if (e == hipSuccess) return true;
+  fprintf(stderr, "PolarQuant (HIP): %s: %s\n", what, hipGetErrorString(e));
+  return false;
+}
+
+// Orthogonal matrix from srand(seed)/rand() entries in [-1, 1] followed by
+// row-wise Gram-Schmidt in float, the generator of polarquant_init
+// (patch:549-579). Depends on the C library's rand().
+void gram_schmidt_rotation(float *R, int D, unsigned seed) {
+  srand(seed);
+  for (int i = 0; i < D * D; ++i) {
+    const float u = (float)rand() / (float)RAND_MAX;
+    const float two_u = u * 2.0f;
+    R[i] = two_u - 1.0f;
+  }
+  for (int i = 0; i < D; ++i) {
+    for (int j = 0; j < i; ++j) {
+      float dot = 0.0f;
+      for (int k = 0; k < D; ++k) {
+        const float p = R[i * D + k] * R[j * D + k];
+        dot = dot + p;
+      }
+      for (int k = 0; k < D; ++k) {
+        const float p = dot * R[j * D + k];
+        R[i * D + k] = R[i * D + k] - p;
+      }
+    }
+    float nrm = 0.0f;
+    for (int k = 0; k < D; ++k) {
+      const float p = R[i * D + k] * R[i * D + k];
+      nrm = nrm + p;
+    }
+    nrm = sqrtf(nrm);
+    if (nrm > 1e-10f)
+      for (int k = 0; k < D; ++k) R[i * D + k] = R[i * D + k] / nrm;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+polarquant_state *polarquant_init_c(int head_dim, int n_kv_heads, int n_q_heads, int n_layers, int n_kv_max,
+                                    int n_bits) {
+  if ((head_dim != 64 && head_dim != 128) || n_kv_heads <= 0 || n_q_heads <= 0 || n_layers <= 0 ||
+      n_kv_max <= 0) {
+    fprintf(stderr, "PolarQuant (HIP): init: unsupported head_dim=%d n_kv_heads=%d n_q_heads=%d n_layers=%d "
+                    "n_kv_max=%d\n", head_dim, n_kv_heads, n_q_heads, n_layers, n_kv_max);
+    return nullptr;
+  }
+  polarquant_state *st = new polarquant_state();
+  memset(st, 0, sizeof(*st));
+  if (n_bits != 2 && n_bits != 3 && n_bits != 4) {
+    fprintf(stderr, "PolarQuant: unsupported n_bits=%d, using 4\n", n_bits);
+    n_bits = 4;
+  }
+  st->enabled = 1;
+  st->n_bits = n_bits;
+  st->n_levels = 1 << n_bits;
+  st->head_dim = head_dim;
+  st->n_kv_heads = n_kv_heads;
+  st->n_q_heads = n_q_heads;
+  st->n_layers = n_layers;
+  st->n_kv_max = n_kv_max;
+
+  float cb[16];
+  if (pqkv_lloyd_max_codebook(head_dim, n_bits, 300, 50000, cb, nullptr) != PQKV_OK) {
+    delete st;
+    return nullptr;
+  }
+  std::vector<float> R((size_t)head_dim * head_dim);
+  gram_schmidt_rotation(R.data(), head_dim, 42);
+  bool ok = report(hipMalloc(&st->codebook, st->n_levels * sizeof(float)), "hipMalloc codebook") &&
+            report(hipMemcpy(st->codebook, cb, st->n_levels * sizeof(float), hipMemcpyHostToDevice), "copy cb") &&
+            report(hipMalloc(&st->rotation, R.size() * sizeof(float)), "hipMalloc rotation") &&
+            report(hipMemcpy(st->rotation, R.data(), R.size() * sizeof(float), hipMemcpyHostToDevice), "copy R");
+  st->layers = new polarquant_kv_layer[n_layers];
+  memset(st->layers, 0, sizeof(polarquant_kv_layer) * n_layers);
+  const size_t packed = (size_t)n_kv_heads * n_kv_max * (head_dim / 2);
+  const size_t rad = (size_t)n_kv_heads * n_kv_max * sizeof(float);
+  for (int l = 0; ok && l < n_layers; ++l) {
+    polarquant_kv_layer &L = st->layers[l];
+    ok = report(hipMalloc(&L.k_packed, packed), "hipMalloc k_packed") &&
+         report(hipMalloc(&L.k_radius, rad), "hipMalloc k_radius") &&
+         report(hipMalloc(&L.v_packed, packed), "hipMalloc v_packed") &&
+         report(hipMalloc(&L.v_radius, rad), "hipMalloc v_radius") &&
+         report(hipMemset(L.k_packed, 0, packed), "memset") && report(hipMemset(L.k_radius, 0, rad), "memset") &&
+         report(hipMemset(L.v_packed, 0, packed), "memset") && report(hipMemset(L.v_radius, 0, rad), "memset");
+  }
+  if (!ok) {
+    polarquant_free_c(st);
+    return nullptr;
+  }
+  const double comp = (double)n_layers * 2 * n_kv_heads * n_kv_max * (head_dim / 2 + sizeof(float));
+  const double orig = (double)n_layers * 2 * n_kv_heads * n_kv_max * head_dim * sizeof(float);
+  fprintf(stderr, "PolarQuant-KV initialized (HIP):\n  head_dim=%d, n_kv_heads=%d, n_q_heads=%d, n_layers=%d\n"
+                  "  n_bits=%d, n_levels=%d, n_kv_max=%d\n"
+                  "  Compressed KV Cache: %.2f MB (original FP32: %.2f MB, ratio: %.1fx)\n",
+          head_dim, n_kv_heads, n_q_heads, n_layers, st->n_bits, st->n_levels, n_kv_max, comp / (1024.0 * 1024.0),
+          orig / (1024.0 * 1024.0), orig / comp);
+  return st;
+}
+
+void polarquant_free_c(polarquant_state *st) {
+  if (!st) return;
+  if (st->codebook) (void)hipFree(st->codebook);
+  if (st->rotation) (void)hipFree(st->rotation);
+  if (st->layers) {
+    for (int l = 0; l < st->n_layers; ++l) {
+      polarquant_kv_layer &L = st->layers[l];
+      if (L.k_packed) (void)hipFree(L.k_packed);
+      if (L.k_radius) (void)hipFree(L.k_radius);
+      if (L.v_packed) (void)hipFree(L.v_packed);
+      if (L.v_radius) (void)hipFree(L.v_radius);
+    }
+    delete[] st->layers;
+  }
+  delete st;
+}
+
+void polarquant_compress_cuda_c(const float *input, const float *rotation, const float *codebook,
+                                float *radius_out, uint8_t *packed_out, int N, int D, int n_levels, void *stream) {
+  if (N <= 0 || D <= 0) return;
+  if ((D != 64 && D != 128) || n_levels < 2 || n_levels > 16) {
+    fprintf(stderr, "PolarQuant (HIP): compress: unsupported D=%d n_levels=%d\n", D, n_levels);
+    return;
+  }
+  report(pqkv::launch_encode_soa(input, rotation, codebook, n_levels, radius_out, packed_out, N, D,
+                                 (hipStream_t)stream),
+         "compress launch");
+}
+
+void polarquant_rotate_query_cuda_c(const float *q_input, const float *rotation, float *q_rotated,
+                                    int total_q_heads, int D, void *stream) {
+  if (total_q_heads <= 0 || D <= 0) return;
+  if (D != 64 && D != 128) {
+    fprintf(stderr, "PolarQuant (HIP): rotate: unsupported D=%d\n", D);
+    return;
+  }
+  report(pqkv::launch_rotate(q_input, PQKV_F32, rotation, q_rotated, PQKV_F32, total_q_heads, D, 0, 1.0f,
+                             (hipStream_t)stream),
+         "rotate launch");
+}
+
+void polarquant_inverse_rotate_cuda_c(const float *input, const float *rotation, float *output, int total_q_heads,
+                                      int D, void *stream) {
+  if (total_q_heads <= 0 || D <= 0) return;
+  if (D != 64 && D != 128) {
+    fprintf(stderr, "PolarQuant (HIP): inverse rotate: unsupported D=%d\n", D);
+    return;
+  }
+  report(pqkv::launch_rotate(input, PQKV_F32, rotation, output, PQKV_F32, total_q_heads, D, 1, 1.0f,
+                             (hipStream_t)stream),
+         "inverse rotate launch");
+}
+
+void polarquant_fused_attention_cuda_c(const float *q_rotated, const uint8_t *packed_k, const float *k_radius,
+                                       const uint8_t *packed_v, const float *v_radius, const float *codebook,
+                                       float *output, int total_q_heads, int total_kv_heads, int S, int D,
+                                       int n_levels, float scale, void *stream) {
+  if (total_q_heads <= 0 || S <= 0 || D <= 0) return;
+  if ((D != 64 && D != 128) || total_kv_heads <= 0 || total_q_heads % total_kv_heads ||
+      total_q_heads / total_kv_heads > 8 || n_levels < 2 || n_levels > 16) {
+    fprintf(stderr, "PolarQuant (HIP): attention: unsupported Hq=%d Hkv=%d D=%d n_levels=%d\n", total_q_heads,
+            total_kv_heads, D, n_levels);
+    return;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t n = (int64_t)total_kv_heads * S;
+  const int64_t vb = pqkv_vector_bytes(D, 4);
+  const size_t ws = pqkv_decode_workspace_bytes(1, total_q_heads, total_kv_heads, S, D);
+  const size_t cache_bytes = (size_t)n * vb;
+  const size_t r_bytes = (size_t)D * D * sizeof(float);
+  const size_t total = 2 * ((cache_bytes + 255) & ~size_t(255)) + ((r_bytes + 255) & ~size_t(255)) + 256 + ws;
+  char *tmp = nullptr;
+  if (!report(hipMallocAsync((void **)&tmp, total, st), "hipMallocAsync")) return;
+  uint8_t *kb = (uint8_t *)tmp;
+  uint8_t *vbk = kb + ((cache_bytes + 255) & ~size_t(255));
+  float *eye = (float *)(vbk + ((cache_bytes + 255) & ~size_t(255)));
+  float *cb16 = (float *)((char *)eye + ((r_bytes + 255) & ~size_t(255)));
+  void *work = (char *)cb16 + 256;
+  std::vector<float> I((size_t)D * D, 0.0f);
+  for (int i = 0; i < D; ++i) I[(size_t)i * D + i] = 1.0f;
+  bool ok = report(hipMemcpyAsync(eye, I.data(), r_bytes, hipMemcpyHostToDevice, st), "copy identity") &&
+            report(pqkv::launch_fill_zero(cb16, 64, st), "zero codebook") &&
+            report(hipMemcpyAsync(cb16, codebook, n_levels * sizeof(float), hipMemcpyDeviceToDevice, st),
+                   "copy codebook") &&
+            report(pqkv::launch_soa_to_blocks(packed_k, k_radius, kb, n, D, st), "convert K") &&
+            report(pqkv::launch_soa_to_blocks(packed_v, v_radius, vbk, n, D, st), "convert V");
+  if (ok) {
+    const int rc = pqkv_decode_attn(q_rotated, PQKV_F32, eye, kb, vbk, cb16, cb16, 4, 4, nullptr, nullptr, nullptr,
+                                    nullptr, 0, 1, total_q_heads, total_kv_heads, S, S, D, scale, output, PQKV_F32,
+                                    work, ws, stream);
+    if (rc != PQKV_OK) fprintf(stderr, "PolarQuant (HIP): attention: %s\n", pqkv_last_error());
+  }
+  // The identity matrix is copied from pageable host memory; wait for the
+  // stream before the host vector goes away and the scratch is released.
+  report(hipStreamSynchronize(st), "stream sync");
+  report(hipFreeAsync(tmp, st), "hipFreeAsync");
+}
+
+}  // extern "C"

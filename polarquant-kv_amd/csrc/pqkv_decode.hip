@@ -1,0 +1,417 @@
+// Split-K ("flash-decoding") attention over a block_pq4 / block_pq2 cache.
+//
+// Semantics follow the reference decode kernels (csrc/flash_turboquant.cu:
+// 27-105, integration/polarquant-kv.patch:277-389): scores are dot products
+// of the rotated query with codebook[idx] scaled by the key radius, softmax
+// over the sequence, output = sum of weights * codebook[vidx] * value radius,
+// all in the rotated space, followed by one inverse rotation.
+//
+// Mapping (one workgroup = 4 waves = one (batch, kv-head, split)):
+//   * every packed token is decoded once and used by all G = Hq/Hkv query
+//     heads of its group;
+//   * a wave streams 64-token tiles of K and V into its own LDS slots;
+//   * scores: lane = token, 256-entry byte -> (code, code) half2 table,
+//     v_dot2_f32_f16 against the LDS-resident fp16 query pairs;
+//   * online softmax per head with wave reductions, exp2 domain (the query is
+//     pre-multiplied by scale * log2(e));
+//   * values: lane = (token group, qs dword); two tokens' nibbles are
+//     interleaved into one byte so a single table read yields
+//     (c[token a], c[token b]) for one coordinate and v_dot2_f32_f16 applies
+//     both tokens' weights at once, accumulating in fp32;
+//   * per-split (max, sum, unnormalised output) go to the workspace and a
+//     merge kernel combines splits, normalises and applies x R.
+#include "pqkv_device.h"
+#include "pqkv_launch.h"
+
+namespace pqkv {
+
+constexpr int kTile = 64;
+constexpr int kWaves = 4;
+
+template <int BITS>
+__device__ __forceinline__ void build_lut(uint32_t *lut, const float *cb, int tid) {
+  // 4-bit: lut[b] = half2(c[b & 15], c[b >> 4])
+  // 2-bit: lut[2b], lut[2b+1] = half2(c[b&3], c[(b>>2)&3]), half2(c[(b>>4)&3], c[b>>6])
+  if (tid < 256) {
+    if (BITS == 4) {
+      half2_t v = {(half_t)cb[tid & 15], (half_t)cb[tid >> 4]};
+      lut[tid] = __builtin_bit_cast(uint32_t, v);
+    } else {
+      half2_t v0 = {(half_t)cb[tid & 3], (half_t)cb[(tid >> 2) & 3]};
+      half2_t v1 = {(half_t)cb[(tid >> 4) & 3], (half_t)cb[tid >> 6]};
+      lut[2 * tid] = __builtin_bit_cast(uint32_t, v0);
+      lut[2 * tid + 1] = __builtin_bit_cast(uint32_t, v1);
+    }
+  }
+}
+
+__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+
+// Copy nbytes (multiple of 4) from global to a wave-private LDS slot.
+__device__ __forceinline__ void load_tile(uint32_t *dst, const uint8_t *src, int nbytes, bool al16, int lane) {
+  if (al16) {
+    const int nchunk = nbytes >> 4;
+    const u32x4 *s4 = (const u32x4 *)src;
+    u32x4 *d4 = (u32x4 *)dst;
+    for (int c = lane; c < nchunk; c += kWave) d4[c] = __builtin_nontemporal_load(s4 + c);
+    const int tail = (nbytes & 15) >> 2;
+    if (lane < tail) dst[(nchunk << 2) + lane] = ((const uint32_t *)src)[(nchunk << 2) + lane];
+  } else {
+    const int nw = nbytes >> 2;
+    const uint32_t *s1 = (const uint32_t *)src;
+    for (int c = lane; c < nw; c += kWave) dst[c] = s1[c];
+  }
+}
+
+template <int D, int G, int KB, int VBITS, bool QJL>
+__global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
+  constexpr int VBK = vector_bytes(D, KB), VBV = vector_bytes(D, VBITS);
+  constexpr int KW = VBK / 4, VW = VBV / 4;                 // dwords per token
+  constexpr int NQK = KB == 4 ? D / 8 : D / 16;             // K qs dwords per token
+  constexpr int NQV = VBITS == 4 ? D / 8 : D / 16;          // V qs dwords per token
+  constexpr int NG = kWave / NQV;                           // V token groups
+  constexpr int CPL = VBITS == 4 ? 8 : 16;                  // V coords per lane
+  constexpr int LUTK = KB == 4 ? 256 : 512, LUTV = VBITS == 4 ? 256 : 512;
+  constexpr int TILE_DW = kTile * (KW + VW);
+  constexpr int M = D;                                      // QJL projections
+
+  __shared__ uint32_t lut_k[LUTK];
+  __shared__ uint32_t lut_v[LUTV];
+  __shared__ uint32_t q_lds[G][D / 2];
+  __shared__ uint32_t tiles[kWaves * TILE_DW + 4];
+  __shared__ uint32_t pr_lds[kWaves][G][kTile / 2];
+  __shared__ float pq_lds[QJL ? G : 1][QJL ? M : 1];
+  __shared__ float red_m[kWaves][G], red_l[kWaves][G];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int split = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / a.n_heads, hi = bh - b * a.n_heads;
+  const int h = a.listed ? a.heads[hi] : hi;
+  const int t_begin = split * a.tokens_per_split;
+  const int t_end = min(a.S, t_begin + a.tokens_per_split);
+
+  const uint8_t *kstream, *vstream;
+  if (a.listed) {
+    kstream = a.k_cache + b * a.k_batch_stride + a.k_head_off[hi];
+    vstream = a.v_cache + b * a.v_batch_stride + a.v_head_off[hi];
+  } else {
+    kstream = a.k_cache + b * a.k_batch_stride + h * a.k_head_stride;
+    vstream = a.v_cache + b * a.v_batch_stride + h * a.v_head_stride;
+  }
+  const bool kal = (((uintptr_t)kstream) & 15) == 0, val = (((uintptr_t)vstream) & 15) == 0;
+
+  build_lut<KB>(lut_k, a.k_cb + h * a.cb_head_stride, tid);
+  build_lut<VBITS>(lut_v, a.v_cb + h * a.cb_head_stride, tid);
+  for (int i = tid; i < G * D / 2; i += 256) {
+    const int hh = i / (D / 2), p = i - hh * (D / 2);
+    q_lds[hh][p] = ((const uint32_t *)a.q)[((int64_t)(b * a.Hq + h * G + hh) * D) / 2 + p];
+  }
+  __syncthreads();
+  if (QJL) {
+    // pq[h][i] = (p_rot[i] . q_h) / m, q already carries scale * log2(e).
+    for (int i = tid; i < G * M; i += 256) {
+      const int hh = i / M, r = i - hh * M;
+      float acc = 0.0f;
+      const float *pr = a.p_rot + (int64_t)r * D;
+      for (int k = 0; k < D / 2; ++k) {
+        const half2_t qq = as_h2(q_lds[hh][k]);
+        acc = __builtin_fmaf(pr[2 * k], (float)qq.x, acc);
+        acc = __builtin_fmaf(pr[2 * k + 1], (float)qq.y, acc);
+      }
+      pq_lds[hh][r] = acc * (1.0f / M);
+    }
+    __syncthreads();
+  }
+
+  uint32_t *ktile = tiles + wave * TILE_DW;
+  uint32_t *vtile = ktile + kTile * KW;
+
+  float m_run[G], l_run[G], o[G][CPL];
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) {
+    m_run[hh] = -INFINITY;
+    l_run[hh] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) o[hh][c] = 0.0f;
+  }
+
+  // V-phase lane roles.
+  const int vw = lane % NQV, vg = lane / NQV;
+  const int vob = VBITS == 4 ? (vw >> 2) * kPq4BlockBytes + 2 + 4 * (vw & 3)
+                             : (vw >> 1) * kPq2BlockBytes + 2 + 4 * (vw & 1);
+  const int vodw = vob >> 2, vosh = vob & 3;
+
+  for (int tile = wave;; tile += kWaves) {
+    const int t0 = t_begin + tile * kTile;
+    if (t0 >= t_end) break;
+    const int ntok = min(kTile, t_end - t0);
+    load_tile(ktile, kstream + (int64_t)t0 * VBK, ntok * VBK, kal, lane);
+    load_tile(vtile, vstream + (int64_t)t0 * VBV, ntok * VBV, val, lane);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- scores: lane = token ----
+    const bool valid = lane < ntok;
+    const uint32_t *kt = ktile + lane * KW;
+    uint32_t W[KW];
+#pragma unroll
+    for (int i = 0; i < KW; ++i) W[i] = kt[i];
+    const float rk = half_bits_to_float(W[0] & 0xFFFFu);
+    float s[G];
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) s[hh] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NQK; ++k) {
+      const int ob = KB == 4 ? (k >> 2) * kPq4BlockBytes + 2 + 4 * (k & 3)
+                             : (k >> 1) * kPq2BlockBytes + 2 + 4 * (k & 1);
+      const uint32_t w = (ob & 3) ? align_bytes(W[(ob >> 2) + 1], W[ob >> 2], 2) : W[ob >> 2];
+      if (KB == 4) {
+        const half2_t c0 = as_h2(lut_k[w & 0xFF]), c1 = as_h2(lut_k[(w >> 8) & 0xFF]);
+        const half2_t c2 = as_h2(lut_k[(w >> 16) & 0xFF]), c3 = as_h2(lut_k[w >> 24]);
+#pragma unroll
+        for (int hh = 0; hh < G; ++hh) {
+          const uint4 qv = *(const uint4 *)&q_lds[hh][4 * k];
+          s[hh] = fdot2(c0, as_h2(qv.x), s[hh]);
+          s[hh] = fdot2(c1, as_h2(qv.y), s[hh]);
+          s[hh] = fdot2(c2, as_h2(qv.z), s[hh]);
+          s[hh] = fdot2(c3, as_h2(qv.w), s[hh]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t byte = (w >> (8 * j)) & 0xFF;
+          const uint2 e = *(const uint2 *)&lut_k[2 * byte];
+          const int p = 4 * k + j;  // coordinates 4p .. 4p+3
+#pragma unroll
+          for (int hh = 0; hh < G; ++hh) {
+            const uint2 qv = *(const uint2 *)&q_lds[hh][2 * p];
+            s[hh] = fdot2(as_h2(e.x), as_h2(qv.x), s[hh]);
+            s[hh] = fdot2(as_h2(e.y), as_h2(qv.y), s[hh]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) s[hh] *= rk;
+    if (QJL) {
+      // + (1/m) sum_i (2 sign_i - 1) (P q)_i, skipped for zero keys.
+      const uint32_t *sg = (const uint32_t *)(a.qjl + (((int64_t)(b * a.Hkv + h) * a.S_max) + t0 + lane) * (M / 8));
+      if (valid && rk > 0.0f) {
+#pragma unroll
+        for (int wd = 0; wd < M / 32; ++wd) {
+          const uint32_t bits = sg[wd];
+#pragma unroll
+          for (int i = 0; i < 32; ++i) {
+            const float sgn = ((bits >> i) & 1u) ? 1.0f : -1.0f;
+#pragma unroll
+            for (int hh = 0; hh < G; ++hh) s[hh] = __builtin_fmaf(sgn, pq_lds[hh][32 * wd + i], s[hh]);
+          }
+        }
+      }
+    }
+    const float rv = half_bits_to_float(vtile[lane * VW] & 0xFFFFu);
+    float alpha[G];
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) {
+      const float sv = valid ? s[hh] : -INFINITY;
+      const float mnew = fmaxf(m_run[hh], wave_max(sv));
+      alpha[hh] = __builtin_amdgcn_exp2f(m_run[hh] - mnew);
+      const float p = valid ? __builtin_amdgcn_exp2f(sv - mnew) : 0.0f;
+      l_run[hh] = l_run[hh] * alpha[hh] + p;
+      m_run[hh] = mnew;
+      const float pr = valid ? p * rv : 0.0f;
+      ((uint16_t *)&pr_lds[wave][hh][0])[lane] = float_to_half_bits(pr);
+    }
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) o[hh][c] *= alpha[hh];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- values: lane = (token group vg, qs dword vw), token pairs ----
+#pragma unroll 2
+    for (int j = 0; j < 32 / NG; ++j) {
+      const int pi = vg + NG * j;  // pair index: tokens 2pi, 2pi+1
+      const uint32_t *pa = vtile + (2 * pi) * VW, *pb = pa + VW;
+      const uint32_t wa = align_bytes(pa[vodw + 1], pa[vodw], vosh);
+      const uint32_t wb = align_bytes(pb[vodw + 1], pb[vodw], vosh);
+      half2_t pp[G];
+#pragma unroll
+      for (int hh = 0; hh < G; ++hh) pp[hh] = as_h2(pr_lds[wave][hh][pi]);
+      if (VBITS == 4) {
+        const uint32_t x = (wa & 0x0F0F0F0Fu) | ((wb << 4) & 0xF0F0F0F0u);
+        const uint32_t y = ((wa >> 4) & 0x0F0F0F0Fu) | (wb & 0xF0F0F0F0u);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const half2_t cx = as_h2(lut_v[(x >> (8 * k)) & 0xFF]);
+          const half2_t cy = as_h2(lut_v[(y >> (8 * k)) & 0xFF]);
+#pragma unroll
+          for (int hh = 0; hh < G; ++hh) {
+            o[hh][2 * k] = fdot2(cx, pp[hh], o[hh][2 * k]);
+            o[hh][2 * k + 1] = fdot2(cy, pp[hh], o[hh][2 * k + 1]);
+          }
+        }
+      } else {
+        const uint32_t x = (wa & 0x33333333u) | ((wb & 0x33333333u) << 2);
+        const uint32_t y = ((wa >> 2) & 0x33333333u) | (wb & 0xCCCCCCCCu);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint2 ex = *(const uint2 *)&lut_v[2 * ((x >> (8 * k)) & 0xFF)];
+          const uint2 ey = *(const uint2 *)&lut_v[2 * ((y >> (8 * k)) & 0xFF)];
+#pragma unroll
+          for (int hh = 0; hh < G; ++hh) {
+            o[hh][4 * k] = fdot2(as_h2(ex.x), pp[hh], o[hh][4 * k]);
+            o[hh][4 * k + 2] = fdot2(as_h2(ex.y), pp[hh], o[hh][4 * k + 2]);
+            o[hh][4 * k + 1] = fdot2(as_h2(ey.x), pp[hh], o[hh][4 * k + 1]);
+            o[hh][4 * k + 3] = fdot2(as_h2(ey.y), pp[hh], o[hh][4 * k + 3]);
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  // ---- combine token groups, then the four waves ----
+#pragma unroll
+  for (int sft = NQV; sft < kWave; sft <<= 1)
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) o[hh][c] += shfl_xor_f(o[hh][c], sft);
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) l_run[hh] = wave_sum(l_run[hh]);
+
+  __syncthreads();
+  float *red_o = (float *)tiles;  // [kWaves][G][D]
+  if (vg == 0) {
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) red_o[(wave * G + hh) * D + vw * CPL + c] = o[hh][c];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) {
+      red_m[wave][hh] = m_run[hh];
+      red_l[wave][hh] = l_run[hh];
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < G * D; i += 256) {
+    const int hh = i / D, c = i - hh * D;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, red_m[w][hh]);
+    float L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float sc = red_m[w][hh] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w][hh] - mx);
+      L += red_l[w][hh] * sc;
+      O += red_o[(w * G + hh) * D + c] * sc;
+    }
+    float *dst = a.part + (((int64_t)(b * a.Hq + h * G + hh) * a.splits) + split) * (D + 2);
+    if (c == 0) {
+      dst[0] = mx;
+      dst[1] = L;
+    }
+    dst[2 + c] = O;
+  }
+}
+
+// Combine splits, normalise and rotate back: out = (sum_s w_s o_s / L) R.
+template <int D, typename TOUT>
+__global__ void __launch_bounds__(D) decode_merge_kernel(const float *__restrict__ part,
+                                                         const float *__restrict__ R,
+                                                         TOUT *__restrict__ out, int splits) {
+  __shared__ float os[D];
+  const int j = threadIdx.x;
+  const float *p = part + (int64_t)blockIdx.x * splits * (D + 2);
+  float mx = -INFINITY;
+  for (int s = 0; s < splits; ++s) mx = fmaxf(mx, p[s * (D + 2)]);
+  float L = 0.0f, O = 0.0f;
+  for (int s = 0; s < splits; ++s) {
+    const float ms = p[s * (D + 2)];
+    const float sc = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - mx);
+    L += p[s * (D + 2) + 1] * sc;
+    O += p[s * (D + 2) + 2 + j] * sc;
+  }
+  os[j] = L > 0.0f ? O / L : 0.0f;
+  __syncthreads();
+  float acc = 0.0f;
+#pragma unroll 8
+  for (int k = 0; k < D; ++k) acc = __builtin_fmaf(os[k], R[k * D + j], acc);
+  out[(int64_t)blockIdx.x * D + j] = (TOUT)acc;
+}
+
+__global__ void fill_zero_kernel(uint32_t *p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+// ---------------------------------------------------------------------------
+template <int D, int G, int KB, int VB>
+static void launch_dqg(const DecodeArgs &a, bool qjl, hipStream_t s) {
+  dim3 grid(a.splits, a.B * a.n_heads);
+  if (qjl) decode_split_kernel<D, G, KB, VB, true><<<grid, 256, 0, s>>>(a);
+  else decode_split_kernel<D, G, KB, VB, false><<<grid, 256, 0, s>>>(a);
+}
+
+template <int D, int KB, int VB>
+static void launch_dq(const DecodeArgs &a, int G, bool qjl, hipStream_t s) {
+  switch (G) {
+    case 1: launch_dqg<D, 1, KB, VB>(a, qjl, s); break;
+    case 2: launch_dqg<D, 2, KB, VB>(a, qjl, s); break;
+    case 3: launch_dqg<D, 3, KB, VB>(a, qjl, s); break;
+    case 4: launch_dqg<D, 4, KB, VB>(a, qjl, s); break;
+    case 5: launch_dqg<D, 5, KB, VB>(a, qjl, s); break;
+    case 6: launch_dqg<D, 6, KB, VB>(a, qjl, s); break;
+    case 7: launch_dqg<D, 7, KB, VB>(a, qjl, s); break;
+    default: launch_dqg<D, 8, KB, VB>(a, qjl, s); break;
+  }
+}
+
+template <int D>
+static void launch_dd(const DecodeArgs &a, int kb, int vb, int G, bool qjl, hipStream_t s) {
+  if (kb == 4 && vb == 4) launch_dq<D, 4, 4>(a, G, qjl, s);
+  else if (kb == 4) launch_dq<D, 4, 2>(a, G, qjl, s);
+  else if (vb == 4) launch_dq<D, 2, 4>(a, G, qjl, s);
+  else launch_dq<D, 2, 2>(a, G, qjl, s);
+}
+
+hipError_t launch_decode_split(const DecodeArgs &a, int k_bits, int v_bits, hipStream_t s) {
+  const int G = a.Hq / a.Hkv;
+  const bool qjl = a.qjl != nullptr;
+  if (a.d == 128) launch_dd<128>(a, k_bits, v_bits, G, qjl, s);
+  else launch_dd<64>(a, k_bits, v_bits, G, qjl, s);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_merge(const float *part, const float *R, void *out, int out_dtype, int BHq, int splits,
+                               int d, hipStream_t s) {
+  if (d == 128) {
+    if (out_dtype == 0) decode_merge_kernel<128, float><<<BHq, 128, 0, s>>>(part, R, (float *)out, splits);
+    else decode_merge_kernel<128, half_t><<<BHq, 128, 0, s>>>(part, R, (half_t *)out, splits);
+  } else {
+    if (out_dtype == 0) decode_merge_kernel<64, float><<<BHq, 64, 0, s>>>(part, R, (float *)out, splits);
+    else decode_merge_kernel<64, half_t><<<BHq, 64, 0, s>>>(part, R, (half_t *)out, splits);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t s) {
+  const int64_t n = (int64_t)(bytes / 4);
+  if (n > 0) {
+    int64_t g = (n + 255) / 256;
+    if (g > 4096) g = 4096;
+    fill_zero_kernel<<<(int)g, 256, 0, s>>>((uint32_t *)p, n);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace pqkv

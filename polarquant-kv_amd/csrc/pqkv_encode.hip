@@ -1,0 +1,411 @@
+// Rotation, bit-exact quantiser, exact fused encoder and layout converters.
+//
+// Arithmetic contract (the reference's encode kernel, csrc/flash_turboquant.cu
+// :111-175, and its ggml copy, integration/polarquant-kv.patch:193-269):
+//   rot[j]  = fp32 FMA chain over k = 0..d-1 of x[k] * R[j][k]
+//   radius  = sqrtf of the 128-slot shared-memory tree of rot[j]^2
+//   dir[j]  = rot[j] / radius (IEEE), 0 when radius <= 1e-30
+//   code[j] = first i minimising |dir[j] - c[i]|
+// The tree maps onto a wave64 as lane t = slot t: the s = 64 step is done in
+// lane (x[t]^2 + x[t+64]^2), the remaining steps are shuffle-downs. The file
+// is compiled without FP contraction inside the quantiser so squares and adds
+// round separately, as in the reference.
+#include "pqkv_device.h"
+#include "pqkv_launch.h"
+
+namespace pqkv {
+
+// ---------------------------------------------------------------------------
+// Per-wave quantiser of one vector held as lane t -> (x0 = y[t], x1 = y[t+64])
+// for D = 128, or x0 = y[t] for D = 64. Returns the fp32 radius (all lanes)
+// and this lane's two codes; nl <= 16 levels, strict '<' scan.
+// ---------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ float quantize_wave(float x0, float x1, const float *cb, int nl, int *c0, int *c1) {
+#pragma clang fp contract(off)
+  float v = x0 * x0;
+  if (D == 128) {
+    float w = x1 * x1;
+    v = v + w;            // tree step s = 64
+  }
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) v = v + shfl_down_f(v, s);
+  const float r = __fsqrt_rn(__shfl(v, 0, kWave));
+  const bool nz = r > 1e-30f;
+  const float d0 = nz ? __fdiv_rn(x0, r) : 0.0f;
+  const float d1 = nz ? __fdiv_rn(x1, r) : 0.0f;
+  int b0 = 0, b1 = 0;
+  float m0 = 1e30f, m1 = 1e30f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if (i < nl) {
+      const float c = cb[i];
+      float e0 = fabsf(d0 - c);
+      if (e0 < m0) { m0 = e0; b0 = i; }
+      float e1 = fabsf(d1 - c);
+      if (e1 < m1) { m1 = e1; b1 = i; }
+    }
+  }
+  *c0 = b0;
+  *c1 = b1;
+  return r;
+}
+
+// Pack the wave's codes into one block_pq4 / block_pq2 vector.
+template <int D, int BITS>
+__device__ __forceinline__ void store_blocks_wave(int b0, int b1, float r, uint8_t *out_vec) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int cv = b0 | (b1 << 4);
+  const uint16_t r16 = float_to_half_bits(r);
+  if (BITS == 4) {
+    // qs byte p holds coordinates 2p (low nibble) and 2p+1 (high nibble).
+    const int a = (2 * lane) & 63;
+    const int va = __shfl(cv, a, kWave), vb = __shfl(cv, a + 1, kWave);
+    const int sh = (D == 128 && lane >= 32) ? 4 : 0;
+    const uint8_t byte = (uint8_t)(((va >> sh) & 15) | (((vb >> sh) & 15) << 4));
+    if (lane < D / 2) {
+      out_vec[qs_offset(lane, 4)] = byte;
+      if ((lane & 15) == 0) *(uint16_t *)(out_vec + (lane >> 4) * kPq4BlockBytes) = r16;
+    }
+  } else {
+    // qs byte p holds coordinates 4p .. 4p+3, two bits each, lowest first.
+    const int a = (4 * lane) & 63;
+    const int sh = (D == 128 && lane >= 16) ? 4 : 0;
+    int byte = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) byte |= ((__shfl(cv, a + k, kWave) >> sh) & 3) << (2 * k);
+    if (lane < D / 4) {
+      out_vec[qs_offset(lane, 2)] = (uint8_t)byte;
+      if ((lane & 7) == 0) *(uint16_t *)(out_vec + (lane >> 3) * kPq2BlockBytes) = r16;
+    }
+  }
+}
+
+// Reference SoA output: packed[p] = code(2p) | code(2p+1) << 4 for any level
+// count (csrc/flash_turboquant.cu:173), fp32 radius.
+template <int D>
+__device__ __forceinline__ void store_soa_wave(int b0, int b1, float r, uint8_t *packed, float *radius) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int cv = b0 | (b1 << 4);
+  const int a = (2 * lane) & 63;
+  const int va = __shfl(cv, a, kWave), vb = __shfl(cv, a + 1, kWave);
+  const int sh = (D == 128 && lane >= 32) ? 4 : 0;
+  if (lane < D / 2) packed[lane] = (uint8_t)(((va >> sh) & 15) | (((vb >> sh) & 15) << 4));
+  if (lane == 0) *radius = r;
+}
+
+template <int D, int BITS>
+__device__ __forceinline__ void quantize_store_wave(float x0, float x1, const float *cb, uint8_t *out_vec,
+                                                    float *radius_out, float *r_f32, uint32_t *codes) {
+  int b0, b1;
+  const float r = quantize_wave<D>(x0, x1, cb, 1 << BITS, &b0, &b1);
+  store_blocks_wave<D, BITS>(b0, b1, r, out_vec);
+  *r_f32 = r;
+  *codes = (uint32_t)(b0 | (b1 << 4));
+  if (radius_out != nullptr && (threadIdx.x & 63) == 0) *radius_out = r;
+}
+
+// One wave per vector; fp32 rotated input.
+template <int D, int BITS>
+__global__ void __launch_bounds__(256) quantize_rotated_kernel(const float *__restrict__ x_rot,
+                                                               const float *__restrict__ codebook,
+                                                               uint8_t *__restrict__ blocks,
+                                                               float *__restrict__ radius_out,
+                                                               int64_t n) {
+  __shared__ float cb[16];
+  if (threadIdx.x < (1 << BITS)) cb[threadIdx.x] = codebook[threadIdx.x];
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int64_t waves = (int64_t)gridDim.x * (blockDim.x / kWave);
+  for (int64_t v = (int64_t)blockIdx.x * (blockDim.x / kWave) + (threadIdx.x >> 6); v < n; v += waves) {
+    const float *xv = x_rot + v * D;
+    const float x0 = xv[lane];
+    const float x1 = D == 128 ? xv[lane + 64] : 0.0f;
+    float r;
+    uint32_t codes;
+    quantize_store_wave<D, BITS>(x0, x1, cb, blocks + v * vector_bytes(D, BITS),
+                                 radius_out ? radius_out + v : nullptr, &r, &codes);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Rotation: thread j of a vector group keeps row j (forward) or column j
+// (inverse) of R in registers; x comes from LDS (broadcast reads).
+// y[j] = fma chain over k ascending, then optional scale and dtype cast.
+// ---------------------------------------------------------------------------
+template <int D, bool INVERSE>
+__device__ __forceinline__ void load_r_row(const float *__restrict__ R, int j, float (&rr)[D]) {
+#pragma unroll
+  for (int k = 0; k < D; ++k) rr[k] = INVERSE ? R[k * D + j] : R[j * D + k];
+}
+
+template <typename T>
+__device__ __forceinline__ float load_as_float(const T *p) { return (float)*p; }
+
+template <int D, bool INVERSE, typename TIN, typename TOUT>
+__global__ void __launch_bounds__(256) rotate_kernel(const TIN *__restrict__ x, const float *__restrict__ R,
+                                                     TOUT *__restrict__ y, int64_t n, float out_scale) {
+  constexpr int NV = 256 / D;  // vectors per iteration
+  __shared__ float xs[NV][D];
+  const int j = threadIdx.x % D, g = threadIdx.x / D;
+  float rr[D];
+  load_r_row<D, INVERSE>(R, j, rr);
+  for (int64_t base = (int64_t)blockIdx.x * NV; base < n; base += (int64_t)gridDim.x * NV) {
+    const int64_t v = base + g;
+    if (v < n) xs[g][j] = load_as_float(x + v * D + j);
+    __syncthreads();
+    if (v < n) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < D; ++k) acc = __builtin_fmaf(xs[g][k], rr[k], acc);
+      y[v * D + j] = (TOUT)(acc * out_scale);
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Exact fused encoder: the rotation above (bit-identical FMA chain) followed by
+// the per-wave quantiser, plus the optional QJL sign sketch. 256 threads, NV
+// vectors per iteration.
+// ---------------------------------------------------------------------------
+template <int D, int BITS, typename TIN>
+__global__ void __launch_bounds__(256) encode_exact_kernel(EncodeArgs a) {
+  constexpr int NV = 256 / D;
+  constexpr int VB = vector_bytes(D, BITS);
+  __shared__ float xs[NV][D];
+  __shared__ float ys[NV][D + 1];
+  __shared__ float rs[NV];
+  __shared__ uint32_t cs[NV][64];
+  __shared__ float cb[16];
+  const int tid = threadIdx.x;
+  const int j = tid % D, g = tid / D;
+  const int lane = tid & 63, wave = tid >> 6;
+  if (tid < (1 << BITS)) cb[tid] = a.codebook[tid];
+  float rr[D];
+  load_r_row<D, false>(a.R, j, rr);
+  const TIN *x = (const TIN *)a.x;
+  const int64_t n = a.n_outer * a.n_inner;
+  for (int64_t base = (int64_t)blockIdx.x * NV; base < n; base += (int64_t)gridDim.x * NV) {
+    const int64_t v = base + g;
+    int64_t vo = 0, vi = 0;
+    if (v < n) {
+      vo = v / a.n_inner;
+      vi = v - vo * a.n_inner;
+      xs[g][j] = load_as_float(x + vo * a.x_outer_stride + vi * D + j);
+    }
+    __syncthreads();
+    if (v < n) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < D; ++k) acc = __builtin_fmaf(xs[g][k], rr[k], acc);
+      ys[g][j] = acc;
+    }
+    __syncthreads();
+    // Quantise: wave w < NV handles vector base + w.
+    if (wave < NV) {
+      const int64_t qv = base + wave;
+      if (qv < n) {
+        const int64_t qo = qv / a.n_inner, qi = qv - qo * a.n_inner;
+        const float x0 = ys[wave][lane];
+        const float x1 = D == 128 ? ys[wave][lane + 64] : 0.0f;
+        float r;
+        uint32_t codes;
+        quantize_store_wave<D, BITS>(x0, x1, cb, a.blocks + qo * a.blocks_outer_stride + qi * VB,
+                                     nullptr, &r, &codes);
+        cs[wave][lane] = codes;
+        if (lane == 0) rs[wave] = r;
+      }
+    }
+    if (a.qjl != nullptr) {
+      __syncthreads();
+      // Residual e = y - r * c[code] in LDS (overwrites xs), then sign of
+      // p_rot[i] . e for i = j (m = D projections, one per thread).
+      if (v < n) {
+        const uint32_t cw = cs[g][j & 63];
+        const int code = D == 128 ? ((j < 64) ? (cw & 15) : (cw >> 4)) : (cw & 15);
+        xs[g][j] = ys[g][j] - rs[g] * cb[code];
+      }
+      __syncthreads();
+      float proj = 0.0f;
+      if (v < n) {
+#pragma unroll 8
+        for (int k = 0; k < D; ++k) proj = __builtin_fmaf(a.p_rot[j * D + k], xs[g][k], proj);
+      }
+      const uint64_t bits = __ballot(proj >= 0.0f);
+      if (v < n && lane == 0) {
+        const int64_t qo = v / a.n_inner, qi = v - qo * a.n_inner;
+        uint8_t *dst = a.qjl + qo * a.qjl_outer_stride + qi * (D / 8) + (j / 64) * 8;
+        if (D == 64) {
+          *(uint64_t *)dst = bits;
+        } else {
+          *(uint64_t *)dst = bits;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Reference-format encoder (fp32 input, SoA output, any level count <= 16):
+// the exact rotation and quantiser above, written as packed nibbles plus fp32
+// radius, i.e. the output of turboquant_compress_kernel.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ void __launch_bounds__(256) encode_soa_kernel(const float *__restrict__ x, const float *__restrict__ R,
+                                                         const float *__restrict__ codebook, int nl,
+                                                         float *__restrict__ radius_out,
+                                                         uint8_t *__restrict__ packed_out, int64_t n) {
+  constexpr int NV = 256 / D;
+  __shared__ float xs[NV][D];
+  __shared__ float ys[NV][D + 1];
+  __shared__ float cb[16];
+  const int tid = threadIdx.x;
+  const int j = tid % D, g = tid / D;
+  const int lane = tid & 63, wave = tid >> 6;
+  if (tid < 16) cb[tid] = tid < nl ? codebook[tid] : 0.0f;
+  float rr[D];
+  load_r_row<D, false>(R, j, rr);
+  for (int64_t base = (int64_t)blockIdx.x * NV; base < n; base += (int64_t)gridDim.x * NV) {
+    const int64_t v = base + g;
+    if (v < n) xs[g][j] = x[v * D + j];
+    __syncthreads();
+    if (v < n) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < D; ++k) acc = __builtin_fmaf(xs[g][k], rr[k], acc);
+      ys[g][j] = acc;
+    }
+    __syncthreads();
+    if (wave < NV && base + wave < n) {
+      const int64_t qv = base + wave;
+      int b0, b1;
+      const float r = quantize_wave<D>(ys[wave][lane], D == 128 ? ys[wave][lane + 64] : 0.0f, cb, nl, &b0, &b1);
+      store_soa_wave<D>(b0, b1, r, packed_out + qv * (D / 2), radius_out + qv);
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// SoA (packed u8 [n][d/2] + f32 radius [n]) <-> block_pq4.
+// ---------------------------------------------------------------------------
+__global__ void soa_to_blocks_kernel(const uint8_t *__restrict__ packed, const float *__restrict__ radius,
+                                     uint8_t *__restrict__ blocks, int64_t n, int d) {
+  const int64_t per = d / 2 + d / 32;  // qs bytes + radius halves per vector
+  const int64_t total = n * per;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t v = t / per;
+    const int e = (int)(t - v * per);
+    uint8_t *dst = blocks + v * (int64_t)vector_bytes(d, 4);
+    if (e < d / 2) {
+      dst[qs_offset(e, 4)] = packed[v * (d / 2) + e];
+    } else {
+      const int b = e - d / 2;
+      *(uint16_t *)(dst + b * kPq4BlockBytes) = float_to_half_bits(radius[v]);
+    }
+  }
+}
+
+__global__ void blocks_to_soa_kernel(const uint8_t *__restrict__ blocks, uint8_t *__restrict__ packed,
+                                     float *__restrict__ radius, int64_t n, int d) {
+  const int64_t per = d / 2 + 1;
+  const int64_t total = n * per;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t v = t / per;
+    const int e = (int)(t - v * per);
+    const uint8_t *src = blocks + v * (int64_t)vector_bytes(d, 4);
+    if (e < d / 2) packed[v * (d / 2) + e] = src[qs_offset(e, 4)];
+    else radius[v] = half_bits_to_float(*(const uint16_t *)src);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+static int grid_for(int64_t items, int per_block, int cap = 8192) {
+  int64_t g = (items + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return (int)g;
+}
+
+hipError_t launch_quantize_rotated(const float *x_rot, const float *codebook, int bits, uint8_t *blocks,
+                                   float *radius_out, int64_t n, int d, hipStream_t s) {
+  const int grid = grid_for(n, 4);
+#define PQKV_QR(DD, BB) \
+  quantize_rotated_kernel<DD, BB><<<grid, 256, 0, s>>>(x_rot, codebook, blocks, radius_out, n)
+  if (d == 128 && bits == 4) PQKV_QR(128, 4);
+  else if (d == 128 && bits == 2) PQKV_QR(128, 2);
+  else if (d == 64 && bits == 4) PQKV_QR(64, 4);
+  else PQKV_QR(64, 2);
+#undef PQKV_QR
+  return hipGetLastError();
+}
+
+template <int D, bool INV>
+static void rotate_dispatch(const void *x, int xt, const float *R, void *y, int yt, int64_t n, float sc,
+                            hipStream_t s) {
+  const int grid = grid_for(n, 256 / D, 4096);
+  if (xt == 0 && yt == 0)
+    rotate_kernel<D, INV, float, float><<<grid, 256, 0, s>>>((const float *)x, R, (float *)y, n, sc);
+  else if (xt == 0 && yt == 1)
+    rotate_kernel<D, INV, float, half_t><<<grid, 256, 0, s>>>((const float *)x, R, (half_t *)y, n, sc);
+  else if (xt == 1 && yt == 0)
+    rotate_kernel<D, INV, half_t, float><<<grid, 256, 0, s>>>((const half_t *)x, R, (float *)y, n, sc);
+  else
+    rotate_kernel<D, INV, half_t, half_t><<<grid, 256, 0, s>>>((const half_t *)x, R, (half_t *)y, n, sc);
+}
+
+hipError_t launch_rotate(const void *x, int x_dtype, const float *R, void *y, int y_dtype, int64_t n, int d,
+                         int inverse, float out_scale, hipStream_t s) {
+  if (d == 128) {
+    if (inverse) rotate_dispatch<128, true>(x, x_dtype, R, y, y_dtype, n, out_scale, s);
+    else rotate_dispatch<128, false>(x, x_dtype, R, y, y_dtype, n, out_scale, s);
+  } else {
+    if (inverse) rotate_dispatch<64, true>(x, x_dtype, R, y, y_dtype, n, out_scale, s);
+    else rotate_dispatch<64, false>(x, x_dtype, R, y, y_dtype, n, out_scale, s);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_encode_exact(const EncodeArgs &a, int x_dtype, hipStream_t s) {
+  const int64_t n = a.n_outer * a.n_inner;
+  const int grid = grid_for(n, 256 / a.d, 4096);
+#define PQKV_EE(DD, BB)                                                            \
+  do {                                                                             \
+    if (x_dtype == 0) encode_exact_kernel<DD, BB, float><<<grid, 256, 0, s>>>(a);  \
+    else encode_exact_kernel<DD, BB, half_t><<<grid, 256, 0, s>>>(a);              \
+  } while (0)
+  if (a.d == 128 && a.bits == 4) PQKV_EE(128, 4);
+  else if (a.d == 128 && a.bits == 2) PQKV_EE(128, 2);
+  else if (a.d == 64 && a.bits == 4) PQKV_EE(64, 4);
+  else PQKV_EE(64, 2);
+#undef PQKV_EE
+  return hipGetLastError();
+}
+
+hipError_t launch_encode_soa(const float *x, const float *R, const float *codebook, int n_levels, float *radius,
+                             uint8_t *packed, int64_t n, int d, hipStream_t s) {
+  const int grid = grid_for(n, 256 / d, 4096);
+  if (d == 128) encode_soa_kernel<128><<<grid, 256, 0, s>>>(x, R, codebook, n_levels, radius, packed, n);
+  else encode_soa_kernel<64><<<grid, 256, 0, s>>>(x, R, codebook, n_levels, radius, packed, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_soa_to_blocks(const uint8_t *packed, const float *radius, uint8_t *blocks, int64_t n, int d,
+                                hipStream_t s) {
+  const int64_t total = n * (d / 2 + d / 32);
+  soa_to_blocks_kernel<<<grid_for(total, 256), 256, 0, s>>>(packed, radius, blocks, n, d);
+  return hipGetLastError();
+}
+
+hipError_t launch_blocks_to_soa(const uint8_t *blocks, uint8_t *packed, float *radius, int64_t n, int d,
+                                hipStream_t s) {
+  const int64_t total = n * (d / 2 + 1);
+  blocks_to_soa_kernel<<<grid_for(total, 256), 256, 0, s>>>(blocks, packed, radius, n, d);
+  return hipGetLastError();
+}
+
+}  // namespace pqkv

@@ -1,0 +1,74 @@
+// Host-side launcher declarations shared by the C-ABI layer (pqkv_api.cpp)
+// and the kernel translation units. Arguments reaching these functions have
+// already been validated.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "pqkv_layout.h"
+
+namespace pqkv {
+
+constexpr int kMaxListHeads = 64;  // kv heads per launch when heads are listed
+
+struct EncodeArgs {
+  const void *x;
+  int64_t x_outer_stride;      // elements
+  const float *R;
+  const float *codebook;
+  int bits;
+  uint8_t *blocks;
+  int64_t blocks_outer_stride; // bytes
+  int64_t n_outer, n_inner;
+  int d;
+  const float *p_rot;          // [m][d] or null
+  int m;
+  uint8_t *qjl;                // or null
+  int64_t qjl_outer_stride;    // bytes
+};
+
+// One launch of the split-K decode kernel covers B x n_heads (batch, kv-head)
+// streams with the same K and V bit widths.
+struct DecodeArgs {
+  const uint16_t *q;             // [B][Hq][d] fp16, rotated, times scale*log2(e)
+  const uint8_t *k_cache, *v_cache;
+  int64_t k_batch_stride, v_batch_stride;   // bytes between batches
+  int64_t k_head_stride, v_head_stride;     // bytes between heads (uniform mode)
+  const float *k_cb, *v_cb;      // codebook(s)
+  int cb_head_stride;            // 0: one table; 16: per-head tables
+  const uint8_t *qjl;            // [B][Hkv][S_max][m/8] or null
+  const float *p_rot;            // [m][d] (QJL only)
+  float *part;                   // [B][Hq][splits][d + 2]
+  int B, Hq, Hkv, S, S_max, d;
+  int splits, tokens_per_split;
+  int n_heads;                   // heads in this launch
+  int listed;                    // 1: heads / offsets below are used
+  int16_t heads[kMaxListHeads];
+  int64_t k_head_off[kMaxListHeads], v_head_off[kMaxListHeads];
+};
+
+// Event brackets for the measurement hook (pqkv_profile_*): returns a token
+// for prof_end, or -1 when profiling is off.
+int prof_begin(const char *name, hipStream_t s);
+void prof_end(int token, hipStream_t s);
+
+hipError_t launch_quantize_rotated(const float *x_rot, const float *codebook, int bits, uint8_t *blocks,
+                                   float *radius_out, int64_t n, int d, hipStream_t s);
+hipError_t launch_rotate(const void *x, int x_dtype, const float *R, void *y, int y_dtype, int64_t n, int d,
+                         int inverse, float out_scale, hipStream_t s);
+hipError_t launch_encode_exact(const EncodeArgs &a, int x_dtype, hipStream_t s);
+hipError_t launch_encode_soa(const float *x, const float *R, const float *codebook, int n_levels, float *radius,
+                             uint8_t *packed, int64_t n, int d, hipStream_t s);
+hipError_t launch_soa_to_blocks(const uint8_t *packed, const float *radius, uint8_t *blocks, int64_t n, int d,
+                                hipStream_t s);
+hipError_t launch_blocks_to_soa(const uint8_t *blocks, uint8_t *packed, float *radius, int64_t n, int d,
+                                hipStream_t s);
+
+hipError_t launch_decode_split(const DecodeArgs &a, int k_bits, int v_bits, hipStream_t s);
+hipError_t launch_decode_merge(const float *part, const float *R, void *out, int out_dtype, int BHq, int splits,
+                               int d, hipStream_t s);
+hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t s);
+
+}  // namespace pqkv

@@ -1,0 +1,127 @@
+"""GPU parity of the encoder against the CPU oracle (bit-exact).
+
+The HIP rotation is the reference's fp32 FMA chain, so the whole encode is
+compared bit for bit with oracle.c_rotate_fma -> c_quantize_rotated ->
+c_pack_blocks on the same inputs."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as OC
+from oracle import oracle as O
+from polarquant_kv import _lib, quantizer, rotation
+from polarquant_kv.lloyd_max import padded_codebook_torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _inputs(n, d, seed, special=True):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((n, d)) * rng.lognormal(0, 1.5, (n, 1))).astype(np.float32)
+    if special:
+        x[0] = 0.0                                           # zero vector
+        x[1] = 1e-30                                         # radius below the 1e-30 guard
+        x[2] = 0.0
+        x[2, 5] = 3.0                                        # one-hot
+        x[3] = 1e4 * rng.standard_normal(d)                  # large
+        c = O.lloyd_max_codebook(d, 4)[0]
+        x[4] = c[rng.integers(0, 16, d)]                     # on the centroids
+    return x
+
+
+@pytest.mark.parametrize("d,bits", [(128, 4), (64, 4), (128, 2), (64, 2)])
+def test_quantize_rotated_bit_exact(d, bits):
+    print(f"quantize_rotated d={d} bits={bits}", flush=True)
+    x = _inputs(3000, d, 1 + d + bits)
+    cb = O.lloyd_max_codebook(d, bits)[0]
+    blocks, radius = quantizer.quantize_rotated(torch.from_numpy(x).to(DEV), padded_codebook_torch(d, bits, DEV), bits)
+    r_ref, idx_ref = OC.c_quantize_rotated(x, cb)
+    torch.cuda.synchronize()
+    assert np.array_equal(radius.cpu().numpy().view(np.uint32), r_ref.view(np.uint32))
+    assert np.array_equal(blocks.cpu().numpy(), OC.c_pack_blocks(r_ref, idx_ref, bits))
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("inverse", [False, True])
+def test_rotate_bit_exact(d, dtype, inverse):
+    x = _inputs(257, d, 5, special=False)
+    xt = torch.from_numpy(x).to(DEV).to(dtype)
+    R = O.rotation_matrix(d, 42).astype(np.float32)
+    Rt = torch.from_numpy(R).to(DEV)
+    y = (rotation.inverse_rotate if inverse else rotation.rotate)(xt, Rt)
+    ref = OC.c_rotate_fma(xt.float().cpu().numpy(), R, inverse=inverse)
+    if dtype == torch.float32:
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    else:
+        assert np.array_equal(y.cpu().numpy(), ref.astype(np.float16))
+
+
+def _oracle_encode(x, R32, bits):
+    d = x.shape[-1]
+    cb = O.lloyd_max_codebook(d, bits)[0]
+    y = OC.c_rotate_fma(x.reshape(-1, d).astype(np.float32), R32)
+    r, idx = OC.c_quantize_rotated(y, cb)
+    return OC.c_pack_blocks(r, idx, bits), y, r, idx, cb
+
+
+@pytest.mark.parametrize("d,bits", [(128, 4), (64, 4), (128, 2)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_encode_cache_bit_exact(d, bits, dtype):
+    print(f"encode d={d} bits={bits} dtype={dtype}", flush=True)
+    B, H, T = 2, 3, 45
+    rng = np.random.default_rng(d + bits)
+    x = (rng.standard_normal((B, H, T, d)) * 2).astype(np.float32)
+    xt = torch.from_numpy(x).to(DEV).to(dtype)
+    R32 = O.rotation_matrix(d, 42).astype(np.float32)
+    Rt = torch.from_numpy(R32).to(DEV)
+    # write positions 7..51 of a 60-position cache (append at an offset)
+    cache = quantizer.allocate_cache(B, H, 60, d, bits, DEV)
+    quantizer.compress_pq(xt, Rt, cache=cache, start=7)
+    assert cache.seq_len == 52
+    want, *_ = _oracle_encode(xt.float().cpu().numpy(), R32, bits)
+    got = cache.blocks.cpu().numpy()
+    assert np.array_equal(got[:, :, 7:52].reshape(-1, got.shape[-1]), want)
+    assert not got[:, :, :7].any() and not got[:, :, 52:].any()
+
+
+def test_encode_mixed_widths_bit_exact():
+    B, H, T, d = 2, 4, 33, 128
+    widths = (4, 2, 2, 4)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((B, H, T, d)).astype(np.float16)
+    R32 = O.rotation_matrix(d, 42).astype(np.float32)
+    cache = quantizer.allocate_cache(B, H, 40, d, widths, DEV)
+    quantizer.compress_pq(torch.from_numpy(x).to(DEV), torch.from_numpy(R32).to(DEV), cache=cache)
+    got = cache.blocks.cpu().numpy()
+    for h, bits in enumerate(widths):
+        want, *_ = _oracle_encode(x[:, h].astype(np.float32), R32, bits)
+        vb = O.vector_bytes(d, bits)
+        off = cache.head_offset(h)
+        seg = got[:, off:off + T * vb].reshape(B * T, vb)
+        assert np.array_equal(seg, want), f"head {h}"
+
+
+def test_encode_qjl_signs():
+    B, H, T, d = 1, 2, 200, 128
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((B, H, T, d)).astype(np.float16)
+    R = O.rotation_matrix(d, 42)
+    P = O.jl_matrix(d, d, 43)
+    P_rot = (P @ R.T).astype(np.float32)
+    cache = quantizer.allocate_cache(B, H, T, d, 4, DEV, jl_dim=d)
+    quantizer.compress_pq(torch.from_numpy(x).to(DEV), torch.from_numpy(R.astype(np.float32)).to(DEV),
+                          cache=cache, jl_rot=torch.from_numpy(P_rot).to(DEV))
+    blocks, y, r, idx, cb = _oracle_encode(x.astype(np.float32), R.astype(np.float32), 4)
+    assert np.array_equal(cache.blocks.cpu().numpy().reshape(-1, 72), blocks)
+    e = y.astype(np.float64) - r[:, None].astype(np.float64) * cb[idx].astype(np.float64)
+    proj = e @ P_rot.astype(np.float64).T
+    want = O.bit_unpack_lsb(O.bit_pack_lsb(proj >= 0), d)
+    got = O.bit_unpack_lsb(cache.qjl_signs.cpu().numpy().reshape(-1, d // 8), d)
+    # sign ties: projections within fp32 summation error of zero
+    tol = 1e-5 * np.linalg.norm(e, axis=1, keepdims=True) * np.linalg.norm(P_rot, axis=1)[None]
+    bad = (got != want) & (np.abs(proj) > tol)
+    assert not bad.any(), int(bad.sum())
+    assert (got != want).mean() < 1e-3

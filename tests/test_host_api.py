@@ -1,0 +1,85 @@
+"""Host-side parts of the polarquant_kv package (no GPU): codebook, rotation,
+JL matrix, layout helpers and the refusal of the GPU entry points to run on
+CPU tensors."""
+
+import numpy as np
+import pytest
+import torch
+
+from polarquant_kv import lloyd_max, qjl, rotation, types
+from polarquant_kv import _lib
+
+
+@pytest.mark.parametrize("d,bits", [(64, 2), (64, 4), (128, 2), (128, 3), (128, 4)])
+def test_codebook_matches_reference_golden(d, bits, golden_codebooks):
+    c, b = lloyd_max.build_lloyd_max_codebook(d, bits)
+    gc, gb = golden_codebooks[f"d{d}_b{bits}"]
+    assert np.array_equal(c, gc) and np.array_equal(b, gb)
+    t = lloyd_max.get_codebook_torch(d, bits, device="cpu")
+    assert t.dtype == torch.float32 and np.array_equal(t.numpy(), gc)
+    p = lloyd_max.padded_codebook_torch(d, bits, device="cpu")
+    assert p.shape == (16,) and np.array_equal(p[: 1 << bits].numpy(), gc)
+
+
+def test_quantize_with_codebook_first_minimum():
+    c = np.array([-1.0, 0.0, 1.0], np.float32)
+    v = np.array([-0.5, 0.5, 0.2, -2.0], np.float32)   # exact ties pick the lower index
+    assert list(lloyd_max.quantize_with_codebook(v, c)) == [0, 1, 1, 0]
+    assert np.array_equal(lloyd_max.dequantize_with_codebook(np.array([2, 0]), c), [1.0, -1.0])
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_rotation_matches_reference_golden(d, golden_R):
+    R = rotation.generate_rotation_matrix(d, seed=42)
+    assert np.array_equal(R, golden_R[d])
+    Rt = rotation.generate_rotation_matrix(d, seed=42, device="cpu")
+    assert Rt.dtype == torch.float32 and np.array_equal(Rt.numpy(), golden_R[d].astype(np.float32))
+    v = np.random.default_rng(0).standard_normal((4, d)).astype(np.float32)
+    np.testing.assert_allclose(rotation.inverse_rotate(rotation.rotate(v, R), R), v, atol=1e-5)
+
+
+def test_rotation_rejects_bad_dimensions():
+    # tests/test_rotation.py:87-103 of the reference
+    for bad in (0, -3):
+        with pytest.raises(ValueError):
+            rotation.generate_rotation_matrix(bad)
+    with pytest.raises(ValueError):
+        rotation.generate_rotation_matrix(2.5)
+    assert abs(rotation.generate_rotation_matrix(1, seed=0)[0, 0]) == 1.0
+
+
+def test_jl_matrix(golden_P):
+    assert np.array_equal(qjl.generate_jl_matrix(128, 128, seed=43), golden_P[(128, 128, 43)])
+    with pytest.raises(ValueError):
+        qjl.generate_jl_matrix(0, 64)
+    s = torch.rand(5, 20) > 0.5
+    assert torch.equal(qjl.bit_unpack(qjl.bit_pack(s), 20), s)
+
+
+def test_cache_layout_helpers():
+    assert types.vector_bytes(128, 4) == 72 and types.vector_bytes(64, 2) == 20
+    with pytest.raises(ValueError):
+        types.vector_bytes(100, 4)
+    c = types.PQCache(blocks=torch.zeros(2, 10), head_dim=128, n_bits=(4, 2, 4), seq_len=0, max_seq_len=5,
+                      codebooks=None)
+    assert c.mixed and c.num_heads == 3
+    assert c.head_offset(0) == 0 and c.head_offset(1) == 5 * 72 and c.head_offset(2) == 5 * 72 + 5 * 40
+
+
+def test_gpu_entry_points_refuse_cpu_tensors():
+    from polarquant_kv import attention, quantizer
+    x = torch.zeros(1, 1, 4, 128)
+    R = torch.eye(128)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        quantizer.compress_pq(x, R)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        rotation.rotate(x, R)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        attention.decode_attention(torch.zeros(1, 2, 128), None, None, R)
+
+
+def test_missing_library_fails_loudly(monkeypatch):
+    monkeypatch.setattr(_lib, "LIB_PATH", "/nonexistent/libpqkv_hip.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(ImportError, match="no CPU fallback"):
+        _lib.lib()
