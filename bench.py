@@ -163,7 +163,7 @@ def main() -> int:
     step_bytes = cache_bytes + qo_bytes
     value = step_bytes / (step_ms / 1e3) / 1e9
     kern_ms = split_ms / max(split_n, 1)
-    kern_bytes = cache_bytes + B * Hq * d * 2                      # compressed K+V + fp16 rotated query
+    kern_bytes = cache_bytes + B * Hq * d * 4                      # compressed K+V + fp32 rotated query
     achieved = kern_bytes / (kern_ms / 1e3) / 1e9
 
     cpu = None
@@ -179,7 +179,7 @@ def main() -> int:
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(step_ms, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "u4 codes, f16 dot2 -> f32 accumulate", "data": "synthetic",
+        "vs_baseline": None, "dtype": "u4 codes -> f32 FMA", "data": "synthetic",
         "config": {"workload": "config3: Llama-3-8B layer decode, B=8 Hq=32 Hkv=8 d=128 S=32768, PQ4 K+V "
                                "(block_pq4 72 B/vector), per-channel LogNormal(0,1) std + 1% x20 outliers",
                    "global_batch": B, "seq_len": S, "parallelism": "single GPU"},

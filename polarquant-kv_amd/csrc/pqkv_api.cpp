@@ -270,7 +270,7 @@ size_t pqkv_decode_workspace_bytes(int B, int Hq, int Hkv, int S, int d) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S < 0 || d <= 0) return 0;
   int splits = 1, tps = 0;
   decode_plan(B, Hkv, S > 0 ? S : 1, &splits, &tps);
-  return align256((size_t)B * Hq * d * 2) + align256((size_t)B * Hq * splits * (d + 2) * 4);
+  return align256((size_t)B * Hq * d * 4) + align256((size_t)B * Hq * splits * (d + 2) * 4);
 }
 
 int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *k_cache, const uint8_t *v_cache,
@@ -312,17 +312,17 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
   }
   int splits = 1, tps = 0;
   decode_plan(B, Hkv, S, &splits, &tps);
-  uint16_t *q16 = (uint16_t *)workspace;
-  float *part = (float *)((char *)workspace + align256((size_t)B * Hq * d * 2));
+  float *q32 = (float *)workspace;
+  float *part = (float *)((char *)workspace + align256((size_t)B * Hq * d * 4));
   const float kLog2e = 1.4426950408889634f;
   int tok = pqkv::prof_begin("decode_rotate", st);
-  hipError_t e = pqkv::launch_rotate(q, q_dtype, R, q16, PQKV_F16, (int64_t)B * Hq, d, 0, scale * kLog2e, st);
+  hipError_t e = pqkv::launch_rotate(q, q_dtype, R, q32, PQKV_F32, (int64_t)B * Hq, d, 0, scale * kLog2e, st);
   pqkv::prof_end(tok, st);
   if (e != hipSuccess) return hip_status(e, "decode query rotation");
 
   pqkv::DecodeArgs a;
   memset(&a, 0, sizeof(a));
-  a.q = q16;
+  a.q = q32;
   a.k_cache = k_cache;
   a.v_cache = v_cache;
   a.k_cb = k_codebooks;

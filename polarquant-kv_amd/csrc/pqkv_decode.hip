@@ -29,23 +29,20 @@ constexpr int kTile = 64;
 constexpr int kWaves = 4;
 
 template <int BITS>
-__device__ __forceinline__ void build_lut(uint32_t *lut, const float *cb, int tid) {
-  // 4-bit: lut[b] = half2(c[b & 15], c[b >> 4])
-  // 2-bit: lut[2b], lut[2b+1] = half2(c[b&3], c[(b>>2)&3]), half2(c[(b>>4)&3], c[b>>6])
+__device__ __forceinline__ void build_lut(float *lut, const float *cb, int tid) {
+  // byte -> codebook values of the codes it holds, lowest code first:
+  // 4-bit: lut[2b .. 2b+1] = c[b & 15], c[b >> 4]
+  // 2-bit: lut[4b .. 4b+3] = c[b & 3], c[(b >> 2) & 3], c[(b >> 4) & 3], c[b >> 6]
   if (tid < 256) {
     if (BITS == 4) {
-      half2_t v = {(half_t)cb[tid & 15], (half_t)cb[tid >> 4]};
-      lut[tid] = __builtin_bit_cast(uint32_t, v);
+      lut[2 * tid] = cb[tid & 15];
+      lut[2 * tid + 1] = cb[tid >> 4];
     } else {
-      half2_t v0 = {(half_t)cb[tid & 3], (half_t)cb[(tid >> 2) & 3]};
-      half2_t v1 = {(half_t)cb[(tid >> 4) & 3], (half_t)cb[tid >> 6]};
-      lut[2 * tid] = __builtin_bit_cast(uint32_t, v0);
-      lut[2 * tid + 1] = __builtin_bit_cast(uint32_t, v1);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) lut[4 * tid + k] = cb[(tid >> (2 * k)) & 3];
     }
   }
 }
-
-__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 
 // Copy nbytes (multiple of 4) from global to a wave-private LDS slot.
 __device__ __forceinline__ void load_tile(uint32_t *dst, const uint8_t *src, int nbytes, bool al16, int lane) {
@@ -63,6 +60,10 @@ __device__ __forceinline__ void load_tile(uint32_t *dst, const uint8_t *src, int
   }
 }
 
+// fp32 split-K decode. All arithmetic is fp32 FMA: the codebook values and
+// the query are kept in fp32, as the 2e-3 absolute output tolerance on
+// outlier-channel caches (outputs of magnitude ~1e2) leaves no room for fp16
+// rounding of either operand.
 template <int D, int G, int KB, int VBITS, bool QJL>
 __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
   constexpr int VBK = vector_bytes(D, KB), VBV = vector_bytes(D, VBITS);
@@ -71,15 +72,16 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
   constexpr int NQV = VBITS == 4 ? D / 8 : D / 16;          // V qs dwords per token
   constexpr int NG = kWave / NQV;                           // V token groups
   constexpr int CPL = VBITS == 4 ? 8 : 16;                  // V coords per lane
-  constexpr int LUTK = KB == 4 ? 256 : 512, LUTV = VBITS == 4 ? 256 : 512;
+  constexpr int KPB = KB == 4 ? 2 : 4, VPB = VBITS == 4 ? 2 : 4;  // codes per byte
   constexpr int TILE_DW = kTile * (KW + VW);
   constexpr int M = D;                                      // QJL projections
+  constexpr int GP = (G + 3) & ~3;                          // padded head count
 
-  __shared__ uint32_t lut_k[LUTK];
-  __shared__ uint32_t lut_v[LUTV];
-  __shared__ uint32_t q_lds[G][D / 2];
-  __shared__ uint32_t tiles[kWaves * TILE_DW + 4];
-  __shared__ uint32_t pr_lds[kWaves][G][kTile / 2];
+  __shared__ __attribute__((aligned(16))) float lut_k[256 * KPB];
+  __shared__ __attribute__((aligned(16))) float lut_v[256 * VPB];
+  __shared__ __attribute__((aligned(16))) float q_lds[G][D];
+  __shared__ __attribute__((aligned(16))) uint32_t tiles[kWaves * TILE_DW + 4];
+  __shared__ __attribute__((aligned(16))) float pr_lds[kWaves][kTile][GP];
   __shared__ float pq_lds[QJL ? G : 1][QJL ? M : 1];
   __shared__ float red_m[kWaves][G], red_l[kWaves][G];
 
@@ -103,9 +105,9 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
 
   build_lut<KB>(lut_k, a.k_cb + h * a.cb_head_stride, tid);
   build_lut<VBITS>(lut_v, a.v_cb + h * a.cb_head_stride, tid);
-  for (int i = tid; i < G * D / 2; i += 256) {
-    const int hh = i / (D / 2), p = i - hh * (D / 2);
-    q_lds[hh][p] = ((const uint32_t *)a.q)[((int64_t)(b * a.Hq + h * G + hh) * D) / 2 + p];
+  for (int i = tid; i < G * D; i += 256) {
+    const int hh = i / D, p = i - hh * D;
+    q_lds[hh][p] = a.q[(int64_t)(b * a.Hq + h * G + hh) * D + p];
   }
   __syncthreads();
   if (QJL) {
@@ -114,11 +116,7 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
       const int hh = i / M, r = i - hh * M;
       float acc = 0.0f;
       const float *pr = a.p_rot + (int64_t)r * D;
-      for (int k = 0; k < D / 2; ++k) {
-        const half2_t qq = as_h2(q_lds[hh][k]);
-        acc = __builtin_fmaf(pr[2 * k], (float)qq.x, acc);
-        acc = __builtin_fmaf(pr[2 * k + 1], (float)qq.y, acc);
-      }
+      for (int k = 0; k < D; ++k) acc = __builtin_fmaf(pr[k], q_lds[hh][k], acc);
       pq_lds[hh][r] = acc * (1.0f / M);
     }
     __syncthreads();
@@ -136,7 +134,7 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
     for (int c = 0; c < CPL; ++c) o[hh][c] = 0.0f;
   }
 
-  // V-phase lane roles.
+  // V-phase lane roles: qs dword vw of tokens vg, vg + NG, ...
   const int vw = lane % NQV, vg = lane / NQV;
   const int vob = VBITS == 4 ? (vw >> 2) * kPq4BlockBytes + 2 + 4 * (vw & 3)
                              : (vw >> 1) * kPq2BlockBytes + 2 + 4 * (vw & 1);
@@ -167,28 +165,27 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
       const int ob = KB == 4 ? (k >> 2) * kPq4BlockBytes + 2 + 4 * (k & 3)
                              : (k >> 1) * kPq2BlockBytes + 2 + 4 * (k & 1);
       const uint32_t w = (ob & 3) ? align_bytes(W[(ob >> 2) + 1], W[ob >> 2], 2) : W[ob >> 2];
-      if (KB == 4) {
-        const half2_t c0 = as_h2(lut_k[w & 0xFF]), c1 = as_h2(lut_k[(w >> 8) & 0xFF]);
-        const half2_t c2 = as_h2(lut_k[(w >> 16) & 0xFF]), c3 = as_h2(lut_k[w >> 24]);
 #pragma unroll
-        for (int hh = 0; hh < G; ++hh) {
-          const uint4 qv = *(const uint4 *)&q_lds[hh][4 * k];
-          s[hh] = fdot2(c0, as_h2(qv.x), s[hh]);
-          s[hh] = fdot2(c1, as_h2(qv.y), s[hh]);
-          s[hh] = fdot2(c2, as_h2(qv.z), s[hh]);
-          s[hh] = fdot2(c3, as_h2(qv.w), s[hh]);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t byte = (w >> (8 * j)) & 0xFF;
-          const uint2 e = *(const uint2 *)&lut_k[2 * byte];
-          const int p = 4 * k + j;  // coordinates 4p .. 4p+3
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t byte = (w >> (8 * j)) & 0xFF;
+        const int c0 = (4 * k + j) * KPB;  // first coordinate held by this byte
+        if (KB == 4) {
+          const float2 e = *(const float2 *)&lut_k[2 * byte];
 #pragma unroll
           for (int hh = 0; hh < G; ++hh) {
-            const uint2 qv = *(const uint2 *)&q_lds[hh][2 * p];
-            s[hh] = fdot2(as_h2(e.x), as_h2(qv.x), s[hh]);
-            s[hh] = fdot2(as_h2(e.y), as_h2(qv.y), s[hh]);
+            const float2 qq = *(const float2 *)&q_lds[hh][c0];
+            s[hh] = __builtin_fmaf(e.x, qq.x, s[hh]);
+            s[hh] = __builtin_fmaf(e.y, qq.y, s[hh]);
+          }
+        } else {
+          const float4 e = *(const float4 *)&lut_k[4 * byte];
+#pragma unroll
+          for (int hh = 0; hh < G; ++hh) {
+            const float4 qq = *(const float4 *)&q_lds[hh][c0];
+            s[hh] = __builtin_fmaf(e.x, qq.x, s[hh]);
+            s[hh] = __builtin_fmaf(e.y, qq.y, s[hh]);
+            s[hh] = __builtin_fmaf(e.z, qq.z, s[hh]);
+            s[hh] = __builtin_fmaf(e.w, qq.w, s[hh]);
           }
         }
       }
@@ -197,8 +194,9 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
     for (int hh = 0; hh < G; ++hh) s[hh] *= rk;
     if (QJL) {
       // + (1/m) sum_i (2 sign_i - 1) (P q)_i, skipped for zero keys.
-      const uint32_t *sg = (const uint32_t *)(a.qjl + (((int64_t)(b * a.Hkv + h) * a.S_max) + t0 + lane) * (M / 8));
       if (valid && rk > 0.0f) {
+        const uint32_t *sg =
+            (const uint32_t *)(a.qjl + (((int64_t)(b * a.Hkv + h) * a.S_max) + t0 + lane) * (M / 8));
 #pragma unroll
         for (int wd = 0; wd < M / 32; ++wd) {
           const uint32_t bits = sg[wd];
@@ -221,8 +219,7 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
       const float p = valid ? __builtin_amdgcn_exp2f(sv - mnew) : 0.0f;
       l_run[hh] = l_run[hh] * alpha[hh] + p;
       m_run[hh] = mnew;
-      const float pr = valid ? p * rv : 0.0f;
-      ((uint16_t *)&pr_lds[wave][hh][0])[lane] = float_to_half_bits(pr);
+      pr_lds[wave][lane][hh] = valid ? p * rv : 0.0f;
     }
 #pragma unroll
     for (int hh = 0; hh < G; ++hh)
@@ -232,42 +229,36 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // ---- values: lane = (token group vg, qs dword vw), token pairs ----
+    // ---- values: lane = (token group vg, qs dword vw) ----
 #pragma unroll 2
-    for (int j = 0; j < 32 / NG; ++j) {
-      const int pi = vg + NG * j;  // pair index: tokens 2pi, 2pi+1
-      const uint32_t *pa = vtile + (2 * pi) * VW, *pb = pa + VW;
-      const uint32_t wa = align_bytes(pa[vodw + 1], pa[vodw], vosh);
-      const uint32_t wb = align_bytes(pb[vodw + 1], pb[vodw], vosh);
-      half2_t pp[G];
+    for (int j = 0; j < kTile / NG; ++j) {
+      const int t = vg + NG * j;
+      const uint32_t *pt = vtile + t * VW;
+      const uint32_t w = align_bytes(pt[vodw + 1], pt[vodw], vosh);
+      float pw[GP];
 #pragma unroll
-      for (int hh = 0; hh < G; ++hh) pp[hh] = as_h2(pr_lds[wave][hh][pi]);
-      if (VBITS == 4) {
-        const uint32_t x = (wa & 0x0F0F0F0Fu) | ((wb << 4) & 0xF0F0F0F0u);
-        const uint32_t y = ((wa >> 4) & 0x0F0F0F0Fu) | (wb & 0xF0F0F0F0u);
+      for (int g4 = 0; g4 < GP; g4 += 4) {
+        const float4 v4 = *(const float4 *)&pr_lds[wave][t][g4];
+        pw[g4] = v4.x; pw[g4 + 1] = v4.y; pw[g4 + 2] = v4.z; pw[g4 + 3] = v4.w;
+      }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const half2_t cx = as_h2(lut_v[(x >> (8 * k)) & 0xFF]);
-          const half2_t cy = as_h2(lut_v[(y >> (8 * k)) & 0xFF]);
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t byte = (w >> (8 * k)) & 0xFF;
+        if (VBITS == 4) {
+          const float2 e = *(const float2 *)&lut_v[2 * byte];
 #pragma unroll
           for (int hh = 0; hh < G; ++hh) {
-            o[hh][2 * k] = fdot2(cx, pp[hh], o[hh][2 * k]);
-            o[hh][2 * k + 1] = fdot2(cy, pp[hh], o[hh][2 * k + 1]);
+            o[hh][2 * k] = __builtin_fmaf(pw[hh], e.x, o[hh][2 * k]);
+            o[hh][2 * k + 1] = __builtin_fmaf(pw[hh], e.y, o[hh][2 * k + 1]);
           }
-        }
-      } else {
-        const uint32_t x = (wa & 0x33333333u) | ((wb & 0x33333333u) << 2);
-        const uint32_t y = ((wa >> 2) & 0x33333333u) | (wb & 0xCCCCCCCCu);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint2 ex = *(const uint2 *)&lut_v[2 * ((x >> (8 * k)) & 0xFF)];
-          const uint2 ey = *(const uint2 *)&lut_v[2 * ((y >> (8 * k)) & 0xFF)];
+        } else {
+          const float4 e = *(const float4 *)&lut_v[4 * byte];
 #pragma unroll
           for (int hh = 0; hh < G; ++hh) {
-            o[hh][4 * k] = fdot2(as_h2(ex.x), pp[hh], o[hh][4 * k]);
-            o[hh][4 * k + 2] = fdot2(as_h2(ex.y), pp[hh], o[hh][4 * k + 2]);
-            o[hh][4 * k + 1] = fdot2(as_h2(ey.x), pp[hh], o[hh][4 * k + 1]);
-            o[hh][4 * k + 3] = fdot2(as_h2(ey.y), pp[hh], o[hh][4 * k + 3]);
+            o[hh][4 * k] = __builtin_fmaf(pw[hh], e.x, o[hh][4 * k]);
+            o[hh][4 * k + 1] = __builtin_fmaf(pw[hh], e.y, o[hh][4 * k + 1]);
+            o[hh][4 * k + 2] = __builtin_fmaf(pw[hh], e.z, o[hh][4 * k + 2]);
+            o[hh][4 * k + 3] = __builtin_fmaf(pw[hh], e.w, o[hh][4 * k + 3]);
           }
         }
       }

@@ -30,7 +30,10 @@ __device__ __forceinline__ float quantize_wave(float x0, float x1, const float *
   }
 #pragma unroll
   for (int s = 32; s > 0; s >>= 1) v = v + shfl_down_f(v, s);
-  const float r = __fsqrt_rn(__shfl(v, 0, kWave));
+  // Correctly rounded fp32 square root: v_sqrt_f32 alone is only within
+  // 1 ulp, so take the fp64 root (correctly rounded) and round once to fp32,
+  // which gives the correctly rounded fp32 root of an fp32 argument.
+  const float r = (float)__builtin_sqrt((double)__shfl(v, 0, kWave));
   const bool nz = r > 1e-30f;
   const float d0 = nz ? __fdiv_rn(x0, r) : 0.0f;
   const float d1 = nz ? __fdiv_rn(x1, r) : 0.0f;

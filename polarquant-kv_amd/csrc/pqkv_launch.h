@@ -32,7 +32,7 @@ struct EncodeArgs {
 // One launch of the split-K decode kernel covers B x n_heads (batch, kv-head)
 // streams with the same K and V bit widths.
 struct DecodeArgs {
-  const uint16_t *q;             // [B][Hq][d] fp16, rotated, times scale*log2(e)
+  const float *q;                // [B][Hq][d] fp32, rotated, times scale*log2(e)
   const uint8_t *k_cache, *v_cache;
   int64_t k_batch_stride, v_batch_stride;   // bytes between batches
   int64_t k_head_stride, v_head_stride;     // bytes between heads (uniform mode)

@@ -150,7 +150,7 @@ def test_decode_qjl_correction():
     _check(out.cpu().numpy(), ref)
     # the correction must matter: without it the result moves
     plain = _oracle(q, R, kc, vc, S)
-    assert np.abs(plain - ref).max() > 10 * MAX_ABS
+    assert np.abs(plain - ref).max() > 2 * MAX_ABS
 
 
 def test_compressed_attention_gpu_api():
