@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -34,6 +35,14 @@ int hip_status(hipError_t e, const char *what) {
 }
 
 bool supported_d(int d) { return d == 64 || d == 128; }
+
+// Decode kernel choice: the matrix-core kernel serves 4-bit K and V without
+// QJL; PQKV_DECODE_KERNEL=valu forces the fp32 VALU kernel everywhere.
+bool use_mfma(int k_bits, int v_bits, bool qjl) {
+  if (k_bits != 4 || v_bits != 4 || qjl) return false;
+  const char *e = getenv("PQKV_DECODE_KERNEL");
+  return !(e && strcmp(e, "valu") == 0);
+}
 bool supported_bits(int b) { return b == 2 || b == 4; }
 bool float_dtype(int t) { return t == PQKV_F32 || t == PQKV_F16; }
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -348,7 +357,8 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
     a.n_heads = Hkv;
     a.listed = 0;
     tok = pqkv::prof_begin("decode_split", st);
-    e = pqkv::launch_decode_split(a, k_bits, v_bits, st);
+    e = use_mfma(k_bits, v_bits, qjl_signs != nullptr) ? pqkv::launch_decode_mfma(a, st)
+                                                       : pqkv::launch_decode_split(a, k_bits, v_bits, st);
     pqkv::prof_end(tok, st);
     if (e != hipSuccess) return hip_status(e, "decode split launch");
   } else {
@@ -374,7 +384,8 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
         if (n == 0) continue;
         a.n_heads = n;
         tok = pqkv::prof_begin("decode_split", st);
-        e = pqkv::launch_decode_split(a, kbits, vbits, st);
+        e = use_mfma(kbits, vbits, qjl_signs != nullptr) ? pqkv::launch_decode_mfma(a, st)
+                                                         : pqkv::launch_decode_split(a, kbits, vbits, st);
         pqkv::prof_end(tok, st);
         if (e != hipSuccess) return hip_status(e, "decode split launch");
       }

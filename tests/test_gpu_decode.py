@@ -107,6 +107,34 @@ def test_decode_matches_oracle(case):
     _check(out.cpu().numpy(), ref)
 
 
+VALU_CASES = [c for c in CASES if c[5] == 4 and c[6] == 4][:4]
+
+
+@pytest.mark.parametrize("case", VALU_CASES, ids=lambda c: "B{}_Hq{}_Hkv{}_S{}_d{}_k{}v{}".format(*c))
+def test_decode_valu_kernel_matches_oracle(case, monkeypatch):
+    """The fp32 VALU kernel on 4-bit caches (the matrix-core kernel serves
+    them by default)."""
+    monkeypatch.setenv("PQKV_DECODE_KERNEL", "valu")
+    B, Hq, Hkv, S, d, kb, vb = case
+    q, R, Rt, kc, vc, _ = _setup(B, Hq, Hkv, S, d, kb, vb, seed=sum(case) + 1)
+    out = attention.decode_attention(torch.from_numpy(q).to(DEV), kc, vc, Rt, out_dtype=torch.float32)
+    _check(out.cpu().numpy(), _oracle(q, R, kc, vc, S))
+
+
+def test_decode_outlier_channels_both_kernels(monkeypatch):
+    """The metric config's data law (per-channel LogNormal std, 1 % of the
+    channels x20): outputs reach ~1e2, so this is the case that needs
+    fp32-grade arithmetic in both kernels."""
+    B, Hq, Hkv, S, d = 2, 32, 8, 700, 128
+    q, R, Rt, kc, vc, _ = _setup(B, Hq, Hkv, S, d, 4, 4, seed=77, kind="channel")
+    ref = _oracle(q, R, kc, vc, S)
+    assert np.abs(ref).max() > 10.0
+    for kernel in ("mfma", "valu"):
+        monkeypatch.setenv("PQKV_DECODE_KERNEL", kernel)
+        out = attention.decode_attention(torch.from_numpy(q).to(DEV), kc, vc, Rt, out_dtype=torch.float32)
+        _check(out.cpu().numpy(), ref)
+
+
 def test_decode_partial_cache_and_dtypes():
     # S < S_max, fp32 query, fp16 output
     q, R, Rt, kc, vc, _ = _setup(2, 8, 2, 700, 128, 4, 4, seed=5, S_max=1000)
