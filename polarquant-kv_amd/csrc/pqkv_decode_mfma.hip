@@ -18,14 +18,19 @@
 //
 // Layouts (16x16x32 f16; verified on the device): A lane l holds row l%16,
 // k = 8(l/16)+i; B lane l holds column l%16, k = 8(l/16)+i; D lane l holds
-// rows 4(l/16)+i, column l%16.
-//   scores  S[row][token]: B column = token, a lane's 8 k values = 4
-//           coordinates x (hi, lo) = two packed bytes, each read from a
-//           256-entry table of (c_hi, c_lo, c_hi', c_lo') for its two codes.
-//   values  O[row][coord]: B column = coordinate, a lane's 8 k values = 4
-//           tokens x (hi, lo); two tokens' nibbles of that coordinate are
-//           interleaved into one byte, so the same kind of table read gives
-//           both tokens' (hi, lo) values.
+// rows 4(l/16)+i, column l%16. Below col = l%16, grp = l/16.
+//   scores, transposed: S^T[token][col] = A(K codes) . B(q parts); a lane's
+//     A row is one token, its 8 k values 4 coordinates x (hi, lo) = two packed
+//     bytes, each read from a 256-entry table of (c_hi, c_lo, c_hi', c_lo').
+//     The result sits in D with token rows 4grp+i and head column col, which
+//     is exactly the A layout the value product needs for the softmax
+//     weights: no transposition through LDS.
+//   values: O[head row][coord] = A(p parts) . B(V codes); a lane's B column is
+//     one coordinate, its 8 k values 4 tokens x (hi, lo): two tokens' nibbles
+//     of that coordinate interleaved into one byte give both tokens' values
+//     with the same kind of table read.
+// Cross-lane steps use DPP row rotations and the gfx950 permlane16/32 swaps
+// (VALU), not LDS permutes; LDS carries only the chunk tiles and the tables.
 #include "pqkv_device.h"
 #include "pqkv_launch.h"
 
@@ -34,13 +39,19 @@ namespace pqkv {
 namespace {
 
 constexpr int kMWaves = 4;
-constexpr int kChunk = 32;          // tokens per wave iteration
-constexpr float kLoScale = 2048.0f; // 2^11
+constexpr int kSub = 16;             // tokens per MFMA tile
+constexpr int kChunk = 64;           // tokens per wave iteration
+constexpr float kLoScale = 2048.0f;  // 2^11
 
 __device__ __forceinline__ void split_hi_lo(float x, half_t *hi, half_t *lo) {
   const half_t h = (half_t)x;
   *hi = h;
   *lo = (half_t)__builtin_fmaf(x, kLoScale, -(float)h * kLoScale);
+}
+
+__device__ __forceinline__ uint32_t pack_h2(half_t a, half_t b) {
+  half2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // byte b -> halfs (c_hi[b & 15], c_lo[b & 15], c_hi[b >> 4], c_lo[b >> 4])
@@ -49,8 +60,7 @@ __device__ __forceinline__ void build_lut_pairs(uint2 *lut, const float *cb, int
     half_t h0, l0, h1, l1;
     split_hi_lo(cb[tid & 15], &h0, &l0);
     split_hi_lo(cb[tid >> 4], &h1, &l1);
-    half2_t a = {h0, l0}, c = {h1, l1};
-    lut[tid] = make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, c));
+    lut[tid] = make_uint2(pack_h2(h0, l0), pack_h2(h1, l1));
   }
 }
 
@@ -59,169 +69,108 @@ __device__ __forceinline__ half8_t pack8(uint2 a, uint2 b) {
   u32x4v v = {a.x, a.y, b.x, b.y};
   return __builtin_bit_cast(half8_t, v);
 }
+__device__ __forceinline__ half8_t pack8u(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  u32x4v v = {a, b, c, d};
+  return __builtin_bit_cast(half8_t, v);
+}
 
 __device__ __forceinline__ float4_t mfma16(half8_t a, half8_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Lane col of each 16-lane row receives lane (col + 8) % 16 (DPP row_ror:8).
+__device__ __forceinline__ uint32_t row_ror8(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float row_ror8f(float x) { return __builtin_bit_cast(float, row_ror8(__builtin_bit_cast(uint32_t, x))); }
+
+// Combine the same lane position of the four 16-lane rows (gfx950 swaps).
+__device__ __forceinline__ float rows_max(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x), false, false);
+  x = fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x), false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x), false, false);
+  x = __builtin_bit_cast(float, (uint32_t)a[0]) + __builtin_bit_cast(float, (uint32_t)a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x), false, false);
+  return __builtin_bit_cast(float, (uint32_t)b[0]) + __builtin_bit_cast(float, (uint32_t)b[1]);
 }
 
 // Raw buffer over one (batch, head) stream: loads past `bytes` return 0.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t stream_rsrc(const uint8_t *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
 }
-__device__ __forceinline__ uint32_t bld32(__amdgpu_buffer_rsrc_t r, int off) {
-  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-}
-__device__ __forceinline__ uint32_t bld16(__amdgpu_buffer_rsrc_t r, int off) {
-  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+__device__ __forceinline__ u32x4 bld128(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
-// Raw bytes of one 32-token chunk as this lane needs them.
+// One 64-token chunk of K and V as contiguous 16-byte pieces: lane l holds
+// pieces l + 64 j.
 template <int D>
 struct ChunkRegs {
-  uint32_t k[2][D / 16];   // per 16-token sub-tile: the two code bytes of MFMA step kk
-  uint32_t rk[2], rv[2];   // fp16 radius bits of the lane's score-side tokens
-  uint32_t v[8][2];        // value qs dword vw of tokens 4*grp + e (+16 for e >= 4), aligned pair
+  static constexpr int kBytes = kChunk * vector_bytes(D, 4);  // per stream
+  static constexpr int kPieces = kBytes / 16;
+  static constexpr int kPerLane = (kPieces + 63) / 64;
+  u32x4 k[kPerLane], v[kPerLane];
 };
 
 template <int D>
 __device__ __forceinline__ void load_chunk(ChunkRegs<D> &c, __amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
-                                           int t0, int col, int grp, int vob_al) {
-  constexpr int VB = vector_bytes(D, 4);
+                                           int t0, int lane) {
+  using CR = ChunkRegs<D>;
+  const int base = t0 * vector_bytes(D, 4);
 #pragma unroll
-  for (int st = 0; st < 2; ++st) {
-    const int base = (t0 + 16 * st + col) * VB;
-    c.rk[st] = bld16(kr, base);
-    c.rv[st] = bld16(vr, base);
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk)  // qs bytes 8kk + 2grp, +1
-      c.k[st][kk] = bld16(kr, base + (kk >> 1) * kPq4BlockBytes + 2 + 8 * (kk & 1) + 2 * grp);
+  for (int j = 0; j < CR::kPerLane; ++j) {
+    const int piece = lane + 64 * j;
+    if (j < CR::kPerLane - 1 || piece < CR::kPieces) {
+      c.k[j] = bld128(kr, base + 16 * piece);
+      c.v[j] = bld128(vr, base + 16 * piece);
+    }
   }
+}
+
+// LDS tiles keep the HBM byte layout; 8-byte stores run at full LDS rate.
+template <int D>
+__device__ __forceinline__ void stage_chunk(const ChunkRegs<D> &c, uint8_t *ktile, uint8_t *vtile, int lane) {
+  using CR = ChunkRegs<D>;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int off = (t0 + 16 * (e >> 2) + 4 * grp + (e & 3)) * VB + vob_al;
-    c.v[e][0] = bld32(vr, off);
-    c.v[e][1] = bld32(vr, off + 4);
+  for (int j = 0; j < CR::kPerLane; ++j) {
+    const int piece = lane + 64 * j;
+    if (j < CR::kPerLane - 1 || piece < CR::kPieces) {
+      *(uint2 *)(ktile + 16 * piece) = make_uint2(c.k[j].x, c.k[j].y);
+      *(uint2 *)(ktile + 16 * piece + 8) = make_uint2(c.k[j].z, c.k[j].w);
+      *(uint2 *)(vtile + 16 * piece) = make_uint2(c.v[j].x, c.v[j].y);
+      *(uint2 *)(vtile + 16 * piece + 8) = make_uint2(c.v[j].z, c.v[j].w);
+    }
   }
+}
+
+// qs dword holding coordinates 32m + 8*sub .. +7 (sub = 0..3) of one vector:
+// byte offset 18m + 2 + 4 sub, misaligned by two bytes when m is even.
+__device__ __forceinline__ uint32_t qs_dword(const uint8_t *vec, int m, int sub) {
+  const int off = m * kPq4BlockBytes + 2 + 4 * sub;
+  if (m & 1) return *(const uint32_t *)(vec + off);
+  const uint32_t *p = (const uint32_t *)(vec + off - 2);
+  return align_bytes(p[1], p[0], 2);
 }
 
 }  // namespace
 
 template <int D, int G>
-__device__ __forceinline__ void process_chunk(const ChunkRegs<D> &cur, int t0, int t_end, int col, int grp, int wave,
-                                              int vsh, int vpar, const uint2 *lut_k, const uint2 *lut_v,
-                                              half_t (*p_lds)[kChunk][2], const half8_t *qa, float (&m_run)[4],
-                                              float (&l_run)[4], float4_t *oacc) {
-  constexpr int KK = D / 16;     // score MFMAs per 16-token sub-tile
-  constexpr int NB = D / 16;     // value n-tiles
-  const int shead0 = 4 * (grp & 1);
-  const int ntok = min(kChunk, t_end - t0);
-
-  // ---------------- scores ----------------
-  float4_t sacc[2];
-#pragma unroll
-  for (int st = 0; st < 2; ++st) {
-    sacc[st] = (float4_t){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      const uint32_t u = cur.k[st][kk];
-      sacc[st] = mfma16(qa[kk], pack8(lut_k[u & 0xFF], lut_k[(u >> 8) & 0xFF]), sacc[st]);
-    }
-  }
-
-  // ---------------- online softmax (rows 0-7 = heads) ----------------
-  float s[2][4];
-#pragma unroll
-  for (int st = 0; st < 2; ++st) {
-    const float rk = half_bits_to_float(cur.rk[st]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float cross = shfl_xor_f(sacc[st][i], 32);
-      const bool ok = (16 * st + col) < ntok && grp < 2 && (shead0 + i) < G;
-      s[st][i] = ok ? __builtin_fmaf(cross, 1.0f / kLoScale, sacc[st][i]) * rk : -INFINITY;
-    }
-  }
-  float alpha[4];
-  bool moved = false;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float mx = fmaxf(s[0][i], s[1][i]);
-#pragma unroll
-    for (int sft = 1; sft < 16; sft <<= 1) mx = fmaxf(mx, shfl_xor_f(mx, sft));
-    const float mnew = fmaxf(m_run[i], mx);
-    // a head with no valid score yet keeps m = -inf; avoid inf - inf
-    alpha[i] = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run[i] - mnew);
-    moved |= mnew != m_run[i];
-    float psum = 0.0f;
-#pragma unroll
-    for (int st = 0; st < 2; ++st) {
-      const float p = s[st][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[st][i] - mnew);
-      psum += p;
-      const int head = shead0 + i;
-      if (grp < 2 && head < G) {
-        half_t ph, pl;
-        split_hi_lo(p * half_bits_to_float(cur.rv[st]), &ph, &pl);
-        const half2_t top = {ph, (half_t)0.0f}, bot = {pl, ph};
-        *(half2_t *)&p_lds[head][16 * st + col][0] = top;
-        *(half2_t *)&p_lds[8 + head][16 * st + col][0] = bot;
-      }
-    }
-    l_run[i] = l_run[i] * alpha[i] + psum;
-    m_run[i] = mnew;
-  }
-  // O rows 4*grp + i belong to head 4*(grp & 1) + i: lanes 32-63 take the
-  // factors of lanes 0-31. Skipped when no running max moved.
-  if (__ballot(moved) != 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float other = shfl_xor_f(alpha[i], 32);
-      const float f = grp < 2 ? alpha[i] : other;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) oacc[nb][i] *= f;
-    }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-  // ---------------- values: two 16-token k-blocks ----------------
-#pragma unroll
-  for (int kb2 = 0; kb2 < 2; ++kb2) {
-    const half8_t pa = *(const half8_t *)&p_lds[col][16 * kb2 + 4 * grp][0];
-    const uint32_t w0 = align_bytes(cur.v[4 * kb2 + 0][1], cur.v[4 * kb2 + 0][0], vsh);
-    const uint32_t w1 = align_bytes(cur.v[4 * kb2 + 1][1], cur.v[4 * kb2 + 1][0], vsh);
-    const uint32_t w2 = align_bytes(cur.v[4 * kb2 + 2][1], cur.v[4 * kb2 + 2][0], vsh);
-    const uint32_t w3 = align_bytes(cur.v[4 * kb2 + 3][1], cur.v[4 * kb2 + 3][0], vsh);
-    // token pairs (0,1), (2,3): byte k of x = even coordinate 2k, of y = odd 2k+1
-    const uint32_t x01 = (w0 & 0x0F0F0F0Fu) | ((w1 << 4) & 0xF0F0F0F0u);
-    const uint32_t y01 = ((w0 >> 4) & 0x0F0F0F0Fu) | (w1 & 0xF0F0F0F0u);
-    const uint32_t x23 = (w2 & 0x0F0F0F0Fu) | ((w3 << 4) & 0xF0F0F0F0u);
-    const uint32_t y23 = ((w2 >> 4) & 0x0F0F0F0Fu) | (w3 & 0xF0F0F0F0u);
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      // D = 128: n-tile nb is nibble nb of dword col (coordinate 8*col + nb).
-      // D = 64: n-tile nb is coordinate 8*(col & 7) + 2*nb + (col >> 3).
-      const int par = D == 128 ? (nb & 1) : vpar;
-      const int byte = D == 128 ? (nb >> 1) : nb;
-      const uint32_t i01 = ((par ? y01 : x01) >> (8 * byte)) & 0xFF;
-      const uint32_t i23 = ((par ? y23 : x23) >> (8 * byte)) & 0xFF;
-      oacc[nb] = mfma16(pa, pack8(lut_v[i01], lut_v[i23]), oacc[nb]);
-    }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-template <int D, int G>
 __global__ void __launch_bounds__(256, 2) decode_mfma_kernel(const DecodeArgs a) {
-  constexpr int KK = D / 16;
-  constexpr int NB = D / 16;
+  constexpr int VB = vector_bytes(D, 4);
+  constexpr int KK = D / 16;     // score MFMAs per 16-token tile
+  constexpr int NB = D / 16;     // value n-tiles
+  constexpr int NSUB = kChunk / kSub;
+  constexpr int TILE = kChunk * VB;
 
   __shared__ uint2 lut_k[256], lut_v[256];
-  // per wave: P as (hi, 0) in rows 0-7 and (lo, hi) in rows 8-15, per token
-  __shared__ __attribute__((aligned(16))) half_t p_lds[kMWaves][16][kChunk][2];
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[kMWaves][2][TILE + 16];
+  __shared__ __attribute__((aligned(8))) uint16_t rad[kMWaves][2][kChunk];
   __shared__ float red_m[kMWaves][8], red_l[kMWaves][8];
-  __shared__ float red_o[kMWaves][8][D];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
@@ -239,94 +188,193 @@ __global__ void __launch_bounds__(256, 2) decode_mfma_kernel(const DecodeArgs a)
     kstream = a.k_cache + b * a.k_batch_stride + h * a.k_head_stride;
     vstream = a.v_cache + b * a.v_batch_stride + h * a.v_head_stride;
   }
-  const uint32_t valid_bytes = (uint32_t)a.S * (uint32_t)vector_bytes(D, 4);
+  const uint32_t valid_bytes = (uint32_t)a.S * (uint32_t)VB;
   const __amdgpu_buffer_rsrc_t kres = stream_rsrc(kstream, valid_bytes);
   const __amdgpu_buffer_rsrc_t vres = stream_rsrc(vstream, valid_bytes);
 
   build_lut_pairs(lut_k, a.k_cb + h * a.cb_head_stride, tid);
   build_lut_pairs(lut_v, a.v_cb + h * a.cb_head_stride, tid);
-  for (int i = tid; i < kMWaves * 16 * kChunk * 2; i += 256) (&p_lds[0][0][0][0])[i] = (half_t)0.0f;
 
-  // Query fragments: row col = (head col & 7, part col >> 3); k = 8grp + i is
-  // (coordinate 16kk + 4grp + i/2, part i%2).
-  const int ahead = col & 7;
-  const bool arow_lo = col >= 8;
-  const float qmask = ahead < G ? 1.0f : 0.0f;
-  half8_t qa[KK];
-  const float *qrow = a.q + (int64_t)(b * a.Hq + h * G + (ahead < G ? ahead : 0)) * D;
+  // q as the B operand of the score product: column col = (head col & 7,
+  // part col >> 3); step kk, k = 8grp + i covers coordinate
+  // 32(kk/2) + 8grp + 4(kk%2) + i/2, part i%2:
+  //   col < 8 : (q_hi, 0)        col >= 8 : (q_lo, q_hi)
+  const int qh = col & 7;
+  const bool qlo = col >= 8;
+  const float qmask = qh < G ? 1.0f : 0.0f;
+  const float *qrow = a.q + (int64_t)(b * a.Hq + h * G + (qh < G ? qh : 0)) * D;
+  half8_t qb[KK];
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       half_t vh, vl;
-      split_hi_lo(qrow[16 * kk + 4 * grp + j] * qmask, &vh, &vl);
-      qa[kk][2 * j] = arow_lo ? vl : vh;
-      qa[kk][2 * j + 1] = arow_lo ? vh : (half_t)0.0f;
+      split_hi_lo(qrow[32 * (kk >> 1) + 8 * grp + 4 * (kk & 1) + j] * qmask, &vh, &vl);
+      qb[kk][2 * j] = qlo ? vl : vh;
+      qb[kk][2 * j + 1] = qlo ? vh : (half_t)0.0f;
     }
   }
 
-  float m_run[4], l_run[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m_run[i] = -INFINITY;
-    l_run[i] = 0.0f;
-  }
+  // Running softmax state: lanes with col < 8 own head col (replicated over
+  // the four rows).
+  float m_run = -INFINITY, l_run = 0.0f;
   float4_t oacc[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) oacc[nb] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
-  // Value-side lane roles: qs dword vw of a lane's tokens.
+  // Value side: lane's coordinate group (qs dword) and, for D = 64, parity.
   const int vw = D == 128 ? col : (col & 7);
-  const int vpar = D == 128 ? 0 : (col >> 3);   // D = 64: even / odd coordinates
+  const int vpar = D == 128 ? 0 : (col >> 3);
   const int vob = (vw >> 2) * kPq4BlockBytes + 2 + 4 * (vw & 3);
   const int vob_al = vob & ~3, vsh = vob & 3;
+  const bool head_ok = col < 8 && col < G;
+
+  uint8_t *ktile = tiles[wave][0], *vtile = tiles[wave][1];
+  uint16_t *rk_lds = rad[wave][0], *rv_lds = rad[wave][1];
   __syncthreads();
 
-  // Two register sets alternate: one is consumed while the next chunk of
-  // this wave streams into the other.
-  ChunkRegs<D> ra, rb;
+  ChunkRegs<D> cr;
   constexpr int kStep = kMWaves * kChunk;
   int t0 = t_begin + wave * kChunk;
-  if (t0 < t_end) load_chunk<D>(ra, kres, vres, t0, col, grp, vob_al);
-  while (t0 < t_end) {
-    if (t0 + kStep < t_end) load_chunk<D>(rb, kres, vres, t0 + kStep, col, grp, vob_al);
-    process_chunk<D, G>(ra, t0, t_end, col, grp, wave, vsh, vpar, lut_k, lut_v, p_lds[wave], qa, m_run, l_run,
-                        oacc);
-    t0 += kStep;
-    if (t0 >= t_end) break;
-    if (t0 + kStep < t_end) load_chunk<D>(ra, kres, vres, t0 + kStep, col, grp, vob_al);
-    process_chunk<D, G>(rb, t0, t_end, col, grp, wave, vsh, vpar, lut_k, lut_v, p_lds[wave], qa, m_run, l_run,
-                        oacc);
-    t0 += kStep;
+  if (t0 < t_end) load_chunk<D>(cr, kres, vres, t0, lane);
+  for (; t0 < t_end; t0 += kStep) {
+    const int ntok = min(kChunk, t_end - t0);
+    stage_chunk<D>(cr, ktile, vtile, lane);
+    if (t0 + kStep < t_end) load_chunk<D>(cr, kres, vres, t0 + kStep, lane);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // radii of the chunk's tokens, gathered so a lane reads 4 with one load
+    rk_lds[lane] = *(const uint16_t *)(ktile + lane * VB);
+    rv_lds[lane] = *(const uint16_t *)(vtile + lane * VB);
+
+    // ---------------- scores: S^T[token][col] per 16-token tile ----------------
+    float4_t sacc[NSUB];
+#pragma unroll
+    for (int st = 0; st < NSUB; ++st) {
+      sacc[st] = (float4_t){0.f, 0.f, 0.f, 0.f};
+      const uint8_t *kv = ktile + (kSub * st + col) * VB;
+#pragma unroll
+      for (int m = 0; m < KK / 2; ++m) {
+        const uint32_t w = qs_dword(kv, m, grp);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const uint32_t b0 = (w >> (16 * e)) & 0xFF, b1 = (w >> (16 * e + 8)) & 0xFF;
+          sacc[st] = mfma16(pack8(lut_k[b0], lut_k[b1]), qb[2 * m + e], sacc[st]);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---------------- softmax over the chunk ----------------
+    // s = D[t][h] + 2^-11 D[t][h + 8] in lanes col < 8; token 16st + 4grp + i.
+    float sv[NSUB][4];
+    float cmax = -INFINITY;
+#pragma unroll
+    for (int st = 0; st < NSUB; ++st) {
+      const uint2 rk4 = *(const uint2 *)&rk_lds[kSub * st + 4 * grp];
+      const uint32_t rkw[2] = {rk4.x, rk4.y};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float cross = row_ror8f(sacc[st][i]);
+        const float rk = half_bits_to_float(rkw[i >> 1] >> (16 * (i & 1)));
+        const bool ok = head_ok && (kSub * st + 4 * grp + i) < ntok;
+        sv[st][i] = ok ? __builtin_fmaf(cross, 1.0f / kLoScale, sacc[st][i]) * rk : -INFINITY;
+        cmax = fmaxf(cmax, sv[st][i]);
+      }
+    }
+    cmax = rows_max(cmax);
+    const float mnew = fmaxf(m_run, cmax);
+    // a head with no valid score yet keeps m = -inf; avoid inf - inf
+    const float alpha = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - mnew);
+    m_run = mnew;
+
+    // rescale the running output: lane (col, grp) holds rows 4grp + i, i.e.
+    // head 4(grp & 1) + i (hi part for grp < 2, cross part for grp >= 2);
+    // alpha of head hh sits in lane hh.
+    {
+      float al[8];
+#pragma unroll
+      for (int hh = 0; hh < 8; ++hh)
+        al[hh] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), hh));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float f = (grp & 1) ? al[4 + i] : al[i];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) oacc[nb][i] *= f;
+      }
+    }
+
+    // ---------------- values, one 16-token k-block per tile ----------------
+    float psum = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < NSUB; ++kb) {
+      // weights p * r_v in the A layout: col < 8 -> (p_hi, 0), col >= 8 ->
+      // (p_lo, p_hi) of head col - 8, taken from lane col - 8.
+      const uint2 rv4 = *(const uint2 *)&rv_lds[kSub * kb + 4 * grp];
+      const uint32_t rvw[2] = {rv4.x, rv4.y};
+      uint32_t pa[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = sv[kb][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[kb][i] - mnew);
+        psum += p;
+        half_t ph, pl;
+        split_hi_lo(p * half_bits_to_float(rvw[i >> 1] >> (16 * (i & 1))), &ph, &pl);
+        const uint32_t top = pack_h2(ph, (half_t)0.0f);
+        const uint32_t bot = row_ror8(pack_h2(pl, ph));
+        pa[i] = col < 8 ? top : bot;
+      }
+      const half8_t pav = pack8u(pa[0], pa[1], pa[2], pa[3]);
+      uint32_t wv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t *pv = (const uint32_t *)(vtile + (kSub * kb + 4 * grp + e) * VB + vob_al);
+        wv[e] = align_bytes(pv[1], pv[0], vsh);
+      }
+      // token pairs (0,1), (2,3): byte k of x = even coordinate 2k, of y = odd
+      const uint32_t x01 = (wv[0] & 0x0F0F0F0Fu) | ((wv[1] << 4) & 0xF0F0F0F0u);
+      const uint32_t y01 = ((wv[0] >> 4) & 0x0F0F0F0Fu) | (wv[1] & 0xF0F0F0F0u);
+      const uint32_t x23 = (wv[2] & 0x0F0F0F0Fu) | ((wv[3] << 4) & 0xF0F0F0F0u);
+      const uint32_t y23 = ((wv[2] >> 4) & 0x0F0F0F0Fu) | (wv[3] & 0xF0F0F0F0u);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        // D = 128: n-tile nb is nibble nb of dword col (coordinate 8*col + nb).
+        // D = 64: n-tile nb is coordinate 8*(col & 7) + 2*nb + (col >> 3).
+        const int par = D == 128 ? (nb & 1) : vpar;
+        const int byte = D == 128 ? (nb >> 1) : nb;
+        const uint32_t i01 = ((par ? y01 : x01) >> (8 * byte)) & 0xFF;
+        const uint32_t i23 = ((par ? y23 : x23) >> (8 * byte)) & 0xFF;
+        oacc[nb] = mfma16(pav, pack8(lut_v[i01], lut_v[i23]), oacc[nb]);
+      }
+    }
+    l_run = l_run * alpha + psum;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 
   // ---------------- per-wave results ----------------
-  const int shead0 = 4 * (grp & 1);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float l = l_run[i];
-#pragma unroll
-    for (int sft = 1; sft < 16; sft <<= 1) l += shfl_xor_f(l, sft);
-    l_run[i] = l;
+  // l: sum over the four rows of lane col; m is already row-uniform.
+  l_run = rows_sum(l_run);
+  if (lane < G) {
+    red_m[wave][lane] = m_run;
+    red_l[wave][lane] = l_run;
   }
-  if (grp < 2 && col == 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (shead0 + i < G) {
-        red_m[wave][shead0 + i] = m_run[i];
-        red_l[wave][shead0 + i] = l_run[i];
-      }
-    }
-  }
+  // O[head][coord] = D[head] + 2^-11 D[head + 8]: rows 8-15 sit 32 lanes up.
+  float *red_o = (float *)tiles[wave][0];  // this wave's tile is free now
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      // (once per block: a plain cross-lane read; hipcc 7.2 picks the wrong
+      // source register for permlane32_swap on extracted vector elements)
       const float cross = shfl_xor_f(oacc[nb][i], 32);
-      const int head = shead0 + i;
+      const int head = 4 * grp + i;
       if (grp < 2 && head < G) {
         const int coord = D == 128 ? 8 * col + nb : 8 * (col & 7) + 2 * nb + (col >> 3);
-        red_o[wave][head][coord] = __builtin_fmaf(cross, 1.0f / kLoScale, oacc[nb][i]);
+        red_o[head * D + coord] = __builtin_fmaf(cross, 1.0f / kLoScale, oacc[nb][i]);
       }
     }
   __syncthreads();
@@ -340,7 +388,7 @@ __global__ void __launch_bounds__(256, 2) decode_mfma_kernel(const DecodeArgs a)
     for (int w = 0; w < kMWaves; ++w) {
       const float sc = red_m[w][hh] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w][hh] - mx);
       L += red_l[w][hh] * sc;
-      O += red_o[w][hh][c] * sc;
+      O += ((const float *)tiles[w][0])[hh * D + c] * sc;
     }
     float *dst = a.part + (((int64_t)(b * a.Hq + h * G + hh) * a.splits) + split) * (D + 2);
     if (c == 0) {
