@@ -14,9 +14,15 @@ the timed region.
 
 value = algorithmic bytes per step (compressed K+V read once, query read,
 output written) / step time. roofline: the split-K decode kernel's algorithmic
-bytes per launch over its mean duration, timed with hipEvents recorded by the
-library on the launch stream. cpu_baseline: the CPU oracle (float64 numpy
-decode, single thread) on one (batch, kv-head) stream of the same cache.
+bytes per launch over its mean duration, timed with hipEvents that the library
+records on the launch stream in a second loop of `--steps` calls (the timed
+loop runs without them); roofline.traffic is the HBM bytes per launch of
+that kernel from the committed rocprofv3 counter summary
+(profiles/decode_mfma_config3_hbm_traffic.md: FETCH_SIZE and WRITE_SIZE, each
+scaled by the same counter's reading on a plain 1 GiB device copy, which
+`--calibrate` adds after the timed region). cpu_baseline: the CPU oracle
+(float64 numpy decode, one thread) over whole (batch, kv-head) streams of the
+same cache for about 8 s, and the C oracle's encoder for about 4 s.
 """
 
 from __future__ import annotations
@@ -33,6 +39,7 @@ for _p in (os.path.join(ROOT, "polarquant-kv_amd"), ROOT):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_mfma_config3_hbm_traffic.md")
 METRIC = "PQ4 decode-attn GB/s & % HBM peak; encode tokens/s; at 1 MI355X, 32K ctx"
 
 
@@ -50,33 +57,40 @@ def synth_channel_kv(torch, B, H, S, d, seed, dev):
     return (x * std).clamp_(-65504, 65504).to(torch.float16)
 
 
-def cpu_baseline(kc, vc, q, R, d, b=0, h=0):
-    """Time the CPU oracle's decode on one (batch, kv-head) stream."""
+def cpu_baseline(kc, vc, q, R, d, budget_s=8.0):
+    """Time the CPU oracle's decode (float64 numpy, one thread) over whole
+    (batch, kv-head) streams of the same cache until `budget_s` has elapsed.
+    Returns (GB/s of compressed cache + query/output bytes, streams, seconds)."""
     import numpy as np
     from threadpoolctl import threadpool_limits
 
     from oracle import oracle as O
 
-    G = q.shape[1] // kc.num_heads
-    kb = kc.blocks[b:b + 1, h:h + 1].cpu().numpy()
-    vb = vc.blocks[b:b + 1, h:h + 1].cpu().numpy()
-    qs = q[b:b + 1, G * h:G * (h + 1)].float().cpu().numpy().astype(np.float64)
+    B, Hkv = kc.batch, kc.num_heads
+    G = q.shape[1] // Hkv
+    kb_all = kc.blocks.cpu().numpy()
+    vb_all = vc.blocks.cpu().numpy()
+    q_all = q.float().cpu().numpy().astype(np.float64)
     cb = O.lloyd_max_codebook(d, 4)[0]
     Rn = R.cpu().numpy().astype(np.float64)
-    times = []
+    done_bytes, streams, elapsed = 0, 0, 0.0
     with threadpool_limits(limits=1):
-        O.decode_attention(qs, kb[:, :, :256], vb[:, :, :256], Rn, cb, cb)  # warm-up
-        for _ in range(3):
+        O.decode_attention(q_all[:1, :G], kb_all[:1, :1, :256], vb_all[:1, :1, :256], Rn, cb, cb)  # warm-up
+        while elapsed < budget_s and streams < B * Hkv * 8:
+            b, h = divmod(streams % (B * Hkv), Hkv)
+            kb, vb = kb_all[b:b + 1, h:h + 1], vb_all[b:b + 1, h:h + 1]
+            qs = q_all[b:b + 1, G * h:G * (h + 1)]
             t0 = time.perf_counter()
             O.decode_attention(qs, kb, vb, Rn, cb, cb)
-            times.append(time.perf_counter() - t0)
-    t = sorted(times)[len(times) // 2]
-    sample_bytes = kb.nbytes + vb.nbytes + qs.size * 2 + qs.size * 2
-    return sample_bytes / t / 1e9, t
+            elapsed += time.perf_counter() - t0
+            done_bytes += kb.nbytes + vb.nbytes + qs.size * 2 * 2
+            streams += 1
+    return done_bytes / elapsed / 1e9, streams, elapsed
 
 
-def cpu_encode_baseline(d, n=4096):
-    """C oracle (single thread): FMA-chain rotation + quantiser + packing."""
+def cpu_encode_baseline(d, budget_s=4.0, n=4096):
+    """C oracle (single thread): FMA-chain rotation + quantiser + packing of
+    n-vector batches until `budget_s` has elapsed. Returns vectors/s."""
     import numpy as np
 
     import oracle as OC
@@ -86,11 +100,48 @@ def cpu_encode_baseline(d, n=4096):
     R = O.rotation_matrix(d, 42).astype(np.float32)
     cb = O.lloyd_max_codebook(d, 4)[0]
     OC.c_rotate_fma(x[:64], R)
-    t0 = time.perf_counter()
-    y = OC.c_rotate_fma(x, R)
-    r, idx = OC.c_quantize_rotated(y, cb)
-    OC.c_pack_blocks(r, idx, 4)
-    return n / (time.perf_counter() - t0)
+    vectors, elapsed = 0, 0.0
+    while elapsed < budget_s:
+        t0 = time.perf_counter()
+        y = OC.c_rotate_fma(x, R)
+        r, idx = OC.c_quantize_rotated(y, cb)
+        OC.c_pack_blocks(r, idx, 4)
+        elapsed += time.perf_counter() - t0
+        vectors += n
+    return vectors / elapsed
+
+
+def decode_kernel_name(d: int) -> str:
+    """The split kernel pqkv_decode_attn launches for a uniform PQ4 cache."""
+    if os.environ.get("PQKV_DECODE_KERNEL", "") == "valu":
+        return f"decode_split_kernel<{d},4,4,4>"
+    return f"decode_mfma_kernel<{d},4>"
+
+
+def committed_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary, or
+    None when the summary is absent or covers another kernel."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            fields = dict(line.split("=", 1) for line in f.read().splitlines() if line.startswith("- ") and "=" in line)
+    except OSError:
+        return None
+    fields = {k[2:].strip(): v.strip().strip("`") for k, v in fields.items()}
+    if fields.get("kernel") != kernel:
+        return None
+    return int(float(fields["traffic_bytes_per_launch"]))
+
+
+def calibrate(torch, dev):
+    """Untimed: a plain 1 GiB device-to-device copy (the runtime's copy
+    kernel, 16-byte loads and stores like the decode kernel) whose FETCH_SIZE
+    and WRITE_SIZE readings scale those counters to bytes."""
+    x = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    y = torch.empty_like(x)
+    x.fill_(1)
+    y.copy_(x)
+    torch.cuda.synchronize()
+    del x, y
 
 
 def main() -> int:
@@ -100,6 +151,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--encode-iters", type=int, default=3)
+    ap.add_argument("--calibrate", action="store_true",
+                    help="after the timed region, run a plain 1 GiB device copy (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the path shards by (batch, kv-head) with no exchange); "
@@ -139,12 +192,15 @@ def main() -> int:
     del K, V
 
     # ---- decode ----
+    # Timed region: library event hooks off (each hook pair costs ~6 us of
+    # stream time). A second loop of the same length then records the hooks'
+    # hipEvents on the launch stream for the per-kernel means.
+    _lib.profile_enable(False)
     q = torch.randn(B, Hq, d, device=dev, dtype=torch.float16)
     ws = torch.empty(_lib.lib().pqkv_decode_workspace_bytes(B, Hq, Hkv, S, d), dtype=torch.uint8, device=dev)
     for _ in range(args.warmup):
         attention.decode_attention(q, kc, vc, R, workspace=ws)
     torch.cuda.synchronize()
-    _lib.profile_collect("")
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
     for _ in range(args.steps):
@@ -152,6 +208,11 @@ def main() -> int:
     t1.record()
     torch.cuda.synchronize()
     step_ms = t0.elapsed_time(t1) / args.steps
+    _lib.profile_enable(True)
+    _lib.profile_collect("")
+    for _ in range(args.steps):
+        attention.decode_attention(q, kc, vc, R, workspace=ws)
+    torch.cuda.synchronize()
     split_ms, split_n = _lib.profile_collect("decode_split")
     merge_ms, merge_n = _lib.profile_collect("decode_merge")
     rot_ms, rot_n = _lib.profile_collect("decode_rotate")
@@ -166,27 +227,32 @@ def main() -> int:
     kern_bytes = cache_bytes + B * Hq * d * 4                      # compressed K+V + fp32 rotated query
     achieved = kern_bytes / (kern_ms / 1e3) / 1e9
 
+    if args.calibrate:
+        calibrate(torch, dev)
+
+    kernel = decode_kernel_name(d)
+    traffic = committed_traffic(kernel)
     cpu = None
     if not args.no_cpu:
-        gbs, t = cpu_baseline(kc, vc, q, R, d)
+        gbs, streams, t = cpu_baseline(kc, vc, q, R, d)
         enc_vs = cpu_encode_baseline(d)
         cpu = {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"oracle float64 decode of one (batch, kv-head) stream of the same cache "
-                         f"(S=32768, 4 query heads, 1/64 of the step), median of 3 runs, {t:.2f} s each; "
-                         f"encode: C oracle FMA rotation + quantiser on 4096 vectors = "
-                         f"{enc_vs / (2 * Hkv):.0f} tokens/s"}
+               "sample": f"oracle float64 numpy decode, one thread, of {streams} whole (batch, kv-head) streams "
+                         f"of the same cache (S=32768, {Hq // Hkv} query heads each; 64 streams = one step) "
+                         f"in {t:.1f} s; encode: C oracle FMA rotation + quantiser + packing, one thread, "
+                         f"{enc_vs:.0f} vectors/s = {enc_vs / (2 * Hkv):.0f} tokens/s (K+V of {Hkv} kv heads)"}
 
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(step_ms, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "u4 codes -> f32 FMA", "data": "synthetic",
+        "vs_baseline": None, "dtype": "u4 codes; f16 hi/lo MFMA, f32 accumulate", "data": "synthetic",
         "config": {"workload": "config3: Llama-3-8B layer decode, B=8 Hq=32 Hkv=8 d=128 S=32768, PQ4 K+V "
                                "(block_pq4 72 B/vector), per-channel LogNormal(0,1) std + 1% x20 outliers",
                    "global_batch": B, "seq_len": S, "parallelism": "single GPU"},
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode_split_kernel<128,4,4,4>", "kernel_ms": round(kern_ms, 5),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": kernel, "kernel_ms": round(kern_ms, 5),
                      "bytes_per_launch": kern_bytes},
         "stages_ms": {"query_rotate": round(rot_ms / max(rot_n, 1), 5), "split": round(kern_ms, 5),
                       "merge": round(merge_ms / max(merge_n, 1), 5)},

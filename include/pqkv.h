@@ -68,7 +68,8 @@ int pqkv_lloyd_max_codebook(int d, int n_bits, int n_iterations, int grid_size,
  * chain over j in increasing order, the arithmetic of the reference's
  * rotate kernels (integration/polarquant-kv.patch:395-437,
  * csrc/polarquant_full.cu:25-40,125-140) and of its encode kernel
- * (csrc/flash_turboquant.cu:132-137). d <= 256. */
+ * (csrc/flash_turboquant.cu:132-137). d in {64, 128}; R is device fp32
+ * [d][d], 16-byte aligned. */
 int pqkv_rotate(const void *x, int x_dtype, const float *R, void *y, int y_dtype,
                 int64_t n, int d, int inverse, void *stream);
 
@@ -113,7 +114,8 @@ int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride,
  * per-head tables, or one table when the *_head_bits pointer is NULL.
  * Replaces turboquant_full_attention (csrc/flash_turboquant.cu:180-211),
  * polarquant_fused_attention_cuda (patch:469-506) plus the query and output
- * rotations around them (patch:395-437). S = 0 writes zeros. */
+ * rotations around them (patch:395-437). R is device fp32 [d][d], 16-byte
+ * aligned. S = 0 writes zeros. */
 size_t pqkv_decode_workspace_bytes(int B, int Hq, int Hkv, int S, int d);
 
 int pqkv_decode_attn(const void *q, int q_dtype, const float *R,

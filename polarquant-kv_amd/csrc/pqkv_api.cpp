@@ -47,7 +47,8 @@ bool supported_bits(int b) { return b == 2 || b == 4; }
 bool float_dtype(int t) { return t == PQKV_F32 || t == PQKV_F16; }
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Split-K plan: about 1024 workgroups, whole 64-token tiles per wave.
+// Split-K plan: about 1024 workgroups, whole 64-token tiles per wave; at most
+// 1024 splits per stream (the merge kernel's weight table).
 void decode_plan(int B, int Hkv, int S, int *splits, int *tps) {
   const int64_t streams = (int64_t)B * Hkv;
   int64_t want = (1024 + streams - 1) / streams;
@@ -234,6 +235,7 @@ int pqkv_rotate(const void *x, int x_dtype, const float *R, void *y, int y_dtype
     return fail(PQKV_ERR_UNSUPPORTED, "rotate: dtypes %d -> %d", x_dtype, y_dtype);
   if (n == 0) return PQKV_OK;
   if (!x || !R || !y) return fail(PQKV_ERR_INVALID, "rotate: null pointer");
+  if ((uintptr_t)R % 16) return fail(PQKV_ERR_INVALID, "rotate: R must be 16-byte aligned");
   return hip_status(pqkv::launch_rotate(x, x_dtype, R, y, y_dtype, n, d, inverse ? 1 : 0, 1.0f,
                                         (hipStream_t)stream),
                     "rotate launch");
@@ -307,6 +309,7 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
   if (qjl_signs && m != d) return fail(PQKV_ERR_UNSUPPORTED, "decode: QJL needs m == d");
   if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(PQKV_ERR_INVALID, "decode: scale must be > 0");
   if (!q || !R || !out) return fail(PQKV_ERR_INVALID, "decode: null pointer");
+  if ((uintptr_t)R % 16) return fail(PQKV_ERR_INVALID, "decode: R must be 16-byte aligned");
   const size_t need = pqkv_decode_workspace_bytes(B, Hq, Hkv, S, d);
   if (S > 0) {
     if (!k_cache || !v_cache || !k_codebooks || !v_codebooks)

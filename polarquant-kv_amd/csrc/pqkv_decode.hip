@@ -315,29 +315,71 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
   }
 }
 
-// Combine splits, normalise and rotate back: out = (sum_s w_s o_s / L) R.
+// Combine splits, normalise and rotate back: out = R^T (sum_s w_s o_s / L).
+// Four query heads per block (one wave each for the split weights); R is
+// staged once per block in LDS with padded rows, so the column reads
+// R[k][j] across lanes j are conflict-free.
 template <int D, typename TOUT>
-__global__ void __launch_bounds__(D) decode_merge_kernel(const float *__restrict__ part,
-                                                         const float *__restrict__ R,
-                                                         TOUT *__restrict__ out, int splits) {
-  __shared__ float os[D];
-  const int j = threadIdx.x;
-  const float *p = part + (int64_t)blockIdx.x * splits * (D + 2);
-  float mx = -INFINITY;
-  for (int s = 0; s < splits; ++s) mx = fmaxf(mx, p[s * (D + 2)]);
-  float L = 0.0f, O = 0.0f;
-  for (int s = 0; s < splits; ++s) {
-    const float ms = p[s * (D + 2)];
-    const float sc = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - mx);
-    L += p[s * (D + 2) + 1] * sc;
-    O += p[s * (D + 2) + 2 + j] * sc;
+__global__ void __launch_bounds__(256) decode_merge_kernel(const float *__restrict__ part,
+                                                          const float *__restrict__ R,
+                                                          TOUT *__restrict__ out, int BHq, int splits) {
+  constexpr int NH = kMergeHeads;
+  constexpr int RP = D + 1;
+  constexpr int PER = NH * D / 256;  // outputs per thread
+  __shared__ float rs[D * RP];
+  __shared__ float os[NH * D];
+  __shared__ float wts[NH][kMaxSplits];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int head0 = blockIdx.x * NH;
+  stage_matrix_padded<D>(R, rs, tid);
+  {
+    const int hq = head0 + wave;
+    if (hq < BHq) {
+      const float *p = part + (int64_t)hq * splits * (D + 2);
+      float mx = -INFINITY;
+      for (int sp = lane; sp < splits; sp += 64) mx = fmaxf(mx, p[(int64_t)sp * (D + 2)]);
+      mx = wave_max(mx);
+      float L = 0.0f;
+      for (int sp = lane; sp < splits; sp += 64) {
+        const float ms = p[(int64_t)sp * (D + 2)];
+        const float e = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - mx);
+        wts[wave][sp] = e;
+        L = __builtin_fmaf(e, p[(int64_t)sp * (D + 2) + 1], L);
+      }
+      L = wave_sum(L);
+      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+      for (int sp = lane; sp < splits; sp += 64) wts[wave][sp] *= inv;
+    }
   }
-  os[j] = L > 0.0f ? O / L : 0.0f;
   __syncthreads();
-  float acc = 0.0f;
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = tid + 256 * u, hh = i / D, c = i % D;
+    const int hq = head0 + hh;
+    float o = 0.0f;
+    if (hq < BHq) {
+      const float *p = part + (int64_t)hq * splits * (D + 2) + 2 + c;
 #pragma unroll 8
-  for (int k = 0; k < D; ++k) acc = __builtin_fmaf(os[k], R[k * D + j], acc);
-  out[(int64_t)blockIdx.x * D + j] = (TOUT)acc;
+      for (int sp = 0; sp < splits; ++sp) o = __builtin_fmaf(wts[hh][sp], p[(int64_t)sp * (D + 2)], o);
+    }
+    os[i] = o;
+  }
+  __syncthreads();
+  float acc[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) acc[u] = 0.0f;
+  const int j = tid % D;
+#pragma unroll 8
+  for (int k = 0; k < D; ++k) {
+    const float r = rs[k * RP + j];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) acc[u] = __builtin_fmaf(os[((tid + 256 * u) / D) * D + k], r, acc[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int hq = head0 + (tid + 256 * u) / D;
+    if (hq < BHq) out[(int64_t)hq * D + j] = (TOUT)acc[u];
+  }
 }
 
 __global__ void fill_zero_kernel(uint32_t *p, int64_t n) {
@@ -385,12 +427,14 @@ hipError_t launch_decode_split(const DecodeArgs &a, int k_bits, int v_bits, hipS
 
 hipError_t launch_decode_merge(const float *part, const float *R, void *out, int out_dtype, int BHq, int splits,
                                int d, hipStream_t s) {
+  if (splits < 1 || splits > kMaxSplits) return hipErrorInvalidValue;
+  const int grid = (BHq + kMergeHeads - 1) / kMergeHeads;
   if (d == 128) {
-    if (out_dtype == 0) decode_merge_kernel<128, float><<<BHq, 128, 0, s>>>(part, R, (float *)out, splits);
-    else decode_merge_kernel<128, half_t><<<BHq, 128, 0, s>>>(part, R, (half_t *)out, splits);
+    if (out_dtype == 0) decode_merge_kernel<128, float><<<grid, 256, 0, s>>>(part, R, (float *)out, BHq, splits);
+    else decode_merge_kernel<128, half_t><<<grid, 256, 0, s>>>(part, R, (half_t *)out, BHq, splits);
   } else {
-    if (out_dtype == 0) decode_merge_kernel<64, float><<<BHq, 64, 0, s>>>(part, R, (float *)out, splits);
-    else decode_merge_kernel<64, half_t><<<BHq, 64, 0, s>>>(part, R, (half_t *)out, splits);
+    if (out_dtype == 0) decode_merge_kernel<64, float><<<grid, 256, 0, s>>>(part, R, (float *)out, BHq, splits);
+    else decode_merge_kernel<64, half_t><<<grid, 256, 0, s>>>(part, R, (half_t *)out, BHq, splits);
   }
   return hipGetLastError();
 }

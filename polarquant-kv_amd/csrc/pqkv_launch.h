@@ -12,6 +12,8 @@
 namespace pqkv {
 
 constexpr int kMaxListHeads = 64;  // kv heads per launch when heads are listed
+constexpr int kMaxSplits = 1024;   // split-K partitions per (batch, kv head)
+constexpr int kMergeHeads = 4;     // query heads per merge workgroup
 
 struct EncodeArgs {
   const void *x;
