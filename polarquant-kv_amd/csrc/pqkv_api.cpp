@@ -47,17 +47,39 @@ bool supported_bits(int b) { return b == 2 || b == 4; }
 bool float_dtype(int t) { return t == PQKV_F32 || t == PQKV_F16; }
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Split-K plan: about 1024 workgroups, whole 64-token tiles per wave; at most
-// 1024 splits per stream (the merge kernel's weight table).
-void decode_plan(int B, int Hkv, int S, int *splits, int *tps) {
+// Split-K plan: about `target` workgroups, whole 64-token tiles per wave, at
+// least one tile per wave; at most 1024 splits per stream (the merge kernel's
+// weight table). More target never means fewer splits, so the workspace is
+// sized with the largest target any launch uses (kPlanMaxTarget).
+constexpr int kPlanMaxTarget = 2048;
+constexpr int kValuTarget = 1024;
+void decode_plan(int B, int Hkv, int S, int target, int *splits, int *tps) {
   const int64_t streams = (int64_t)B * Hkv;
-  int64_t want = (1024 + streams - 1) / streams;
+  if (target > kPlanMaxTarget) target = kPlanMaxTarget;
+  int64_t want = (target + streams - 1) / streams;
   int64_t t = (S + want - 1) / want;
   if (t < 256) t = 256;
   t = (t + 63) / 64 * 64;
   *tps = (int)t;
   *splits = (int)((S + t - 1) / t);
   if (*splits < 1) *splits = 1;
+}
+
+// Workgroups resident at once for the matrix-core decode kernel: compute
+// units x workgroups per CU (the kernel's launch bounds and LDS use allow
+// pqkv::kMfmaBlocksPerCU), so one launch is one balanced round.
+int mfma_target() {
+  static std::mutex mu;
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kValuTarget;
+  std::lock_guard<std::mutex> lk(mu);
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev] * pqkv::kMfmaBlocksPerCU;
 }
 
 struct ProfRecord {
@@ -280,7 +302,7 @@ int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride, const float 
 size_t pqkv_decode_workspace_bytes(int B, int Hq, int Hkv, int S, int d) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S < 0 || d <= 0) return 0;
   int splits = 1, tps = 0;
-  decode_plan(B, Hkv, S > 0 ? S : 1, &splits, &tps);
+  decode_plan(B, Hkv, S > 0 ? S : 1, kPlanMaxTarget, &splits, &tps);
   return align256((size_t)B * Hq * d * 4) + align256((size_t)B * Hq * splits * (d + 2) * 4);
 }
 
@@ -323,7 +345,8 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
     return hip_status(pqkv::launch_fill_zero(out, ob, st), "decode zero fill");
   }
   int splits = 1, tps = 0;
-  decode_plan(B, Hkv, S, &splits, &tps);
+  const bool all_mfma = !mixed && use_mfma(k_bits, v_bits, qjl_signs != nullptr);
+  decode_plan(B, Hkv, S, all_mfma ? mfma_target() : kValuTarget, &splits, &tps);
   float *q32 = (float *)workspace;
   float *part = (float *)((char *)workspace + align256((size_t)B * Hq * d * 4));
   const float kLog2e = 1.4426950408889634f;

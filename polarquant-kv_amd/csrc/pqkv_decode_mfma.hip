@@ -107,6 +107,12 @@ __device__ __forceinline__ u32x4 bld128(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) volatile u32x2 lds_u32x2;
+
+// 8-byte LDS store the compiler neither merges nor turns into a flat store.
+__device__ __forceinline__ void lds_store8(uint8_t *p, u32x2 v) { *(lds_u32x2 *)p = v; }
+
 // One 64-token chunk of K and V as contiguous 16-byte pieces: lane l holds
 // pieces l + 64 j.
 template <int D>
@@ -132,7 +138,8 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<D> &c, __amdgpu_buffer_rsrc
   }
 }
 
-// LDS tiles keep the HBM byte layout; 8-byte stores run at full LDS rate.
+// LDS tiles keep the HBM byte layout. 8-byte stores run at the full LDS rate
+// (16-byte ones at half); volatile keeps the compiler from merging them.
 template <int D>
 __device__ __forceinline__ void stage_chunk(const ChunkRegs<D> &c, uint8_t *ktile, uint8_t *vtile, int lane) {
   using CR = ChunkRegs<D>;
@@ -140,10 +147,10 @@ __device__ __forceinline__ void stage_chunk(const ChunkRegs<D> &c, uint8_t *ktil
   for (int j = 0; j < CR::kPerLane; ++j) {
     const int piece = lane + 64 * j;
     if (j < CR::kPerLane - 1 || piece < CR::kPieces) {
-      *(uint2 *)(ktile + 16 * piece) = make_uint2(c.k[j].x, c.k[j].y);
-      *(uint2 *)(ktile + 16 * piece + 8) = make_uint2(c.k[j].z, c.k[j].w);
-      *(uint2 *)(vtile + 16 * piece) = make_uint2(c.v[j].x, c.v[j].y);
-      *(uint2 *)(vtile + 16 * piece + 8) = make_uint2(c.v[j].z, c.v[j].w);
+      lds_store8(ktile + 16 * piece, c.k[j].xy);
+      lds_store8(ktile + 16 * piece + 8, c.k[j].zw);
+      lds_store8(vtile + 16 * piece, c.v[j].xy);
+      lds_store8(vtile + 16 * piece + 8, c.v[j].zw);
     }
   }
 }
@@ -160,7 +167,7 @@ __device__ __forceinline__ uint32_t qs_dword(const uint8_t *vec, int m, int sub)
 }  // namespace
 
 template <int D, int G>
-__global__ void __launch_bounds__(256, 2) decode_mfma_kernel(const DecodeArgs a) {
+__global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(const DecodeArgs a) {
   constexpr int VB = vector_bytes(D, 4);
   constexpr int KK = D / 16;     // score MFMAs per 16-token tile
   constexpr int NB = D / 16;     // value n-tiles
@@ -227,7 +234,6 @@ __global__ void __launch_bounds__(256, 2) decode_mfma_kernel(const DecodeArgs a)
   const int vpar = D == 128 ? 0 : (col >> 3);
   const int vob = (vw >> 2) * kPq4BlockBytes + 2 + 4 * (vw & 3);
   const int vob_al = vob & ~3, vsh = vob & 3;
-  const bool head_ok = col < 8 && col < G;
 
   uint8_t *ktile = tiles[wave][0], *vtile = tiles[wave][1];
   uint16_t *rk_lds = rad[wave][0], *rv_lds = rad[wave][1];
@@ -249,29 +255,62 @@ __global__ void __launch_bounds__(256, 2) decode_mfma_kernel(const DecodeArgs a)
     rv_lds[lane] = *(const uint16_t *)(vtile + lane * VB);
 
     // ---------------- scores: S^T[token][col] per 16-token tile ----------------
-    float4_t sacc[NSUB];
-#pragma unroll
-    for (int st = 0; st < NSUB; ++st) {
-      sacc[st] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    // Table entries of sub-tile st + 1 are requested before the MFMAs of
+    // sub-tile st, so LDS latency overlaps matrix work within the wave.
+    auto k_tables = [&](int st, uint2 (&t)[KK][2]) {
       const uint8_t *kv = ktile + (kSub * st + col) * VB;
 #pragma unroll
       for (int m = 0; m < KK / 2; ++m) {
         const uint32_t w = qs_dword(kv, m, grp);
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          const uint32_t b0 = (w >> (16 * e)) & 0xFF, b1 = (w >> (16 * e + 8)) & 0xFF;
-          sacc[st] = mfma16(pack8(lut_k[b0], lut_k[b1]), qb[2 * m + e], sacc[st]);
+          t[2 * m + e][0] = lut_k[(w >> (16 * e)) & 0xFF];
+          t[2 * m + e][1] = lut_k[(w >> (16 * e + 8)) & 0xFF];
         }
       }
+    };
+    // Value-side entries of k-block kb: two tokens' nibbles of the lane's
+    // coordinate interleaved into one byte (token pairs (0,1) and (2,3)).
+    auto v_tables = [&](int kb, uint2 (&t)[NB][2]) {
+      uint32_t wv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t *pv = (const uint32_t *)(vtile + (kSub * kb + 4 * grp + e) * VB + vob_al);
+        wv[e] = align_bytes(pv[1], pv[0], vsh);
+      }
+      // byte k of x = even coordinate 2k of both tokens, of y = odd 2k + 1
+      const uint32_t x01 = (wv[0] & 0x0F0F0F0Fu) | ((wv[1] << 4) & 0xF0F0F0F0u);
+      const uint32_t y01 = ((wv[0] >> 4) & 0x0F0F0F0Fu) | (wv[1] & 0xF0F0F0F0u);
+      const uint32_t x23 = (wv[2] & 0x0F0F0F0Fu) | ((wv[3] << 4) & 0xF0F0F0F0u);
+      const uint32_t y23 = ((wv[2] >> 4) & 0x0F0F0F0Fu) | (wv[3] & 0xF0F0F0F0u);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        // D = 128: n-tile nb is nibble nb of dword col (coordinate 8*col + nb).
+        // D = 64: n-tile nb is coordinate 8*(col & 7) + 2*nb + (col >> 3).
+        const int par = D == 128 ? (nb & 1) : vpar;
+        const int byte = D == 128 ? (nb >> 1) : nb;
+        t[nb][0] = lut_v[((par ? y01 : x01) >> (8 * byte)) & 0xFF];
+        t[nb][1] = lut_v[((par ? y23 : x23) >> (8 * byte)) & 0xFF];
+      }
+    };
+    float4_t sacc[NSUB];
+    uint2 kt[2][KK][2];
+    k_tables(0, kt[0]);
+#pragma unroll
+    for (int st = 0; st < NSUB; ++st) {
+      if (st + 1 < NSUB) k_tables(st + 1, kt[(st + 1) & 1]);
+      sacc[st] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) sacc[st] = mfma16(pack8(kt[st & 1][kk][0], kt[st & 1][kk][1]), qb[kk], sacc[st]);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint2 vt[2][NB][2];
+    v_tables(0, vt[0]);
 
     // ---------------- softmax over the chunk ----------------
-    // s = D[t][h] + 2^-11 D[t][h + 8] in lanes col < 8; token 16st + 4grp + i.
+    // s = D[t][h] + 2^-11 D[t][h + 8] for token 16st + 4grp + i, meaningful
+    // in lanes col < G. Lanes of absent heads (q = 0) and the cross lanes
+    // (col >= 8) carry finite values that only reach discarded output rows.
     float sv[NSUB][4];
-    float cmax = -INFINITY;
 #pragma unroll
     for (int st = 0; st < NSUB; ++st) {
       const uint2 rk4 = *(const uint2 *)&rk_lds[kSub * st + 4 * grp];
@@ -280,15 +319,26 @@ __global__ void __launch_bounds__(256, 2) decode_mfma_kernel(const DecodeArgs a)
       for (int i = 0; i < 4; ++i) {
         const float cross = row_ror8f(sacc[st][i]);
         const float rk = half_bits_to_float(rkw[i >> 1] >> (16 * (i & 1)));
-        const bool ok = head_ok && (kSub * st + 4 * grp + i) < ntok;
-        sv[st][i] = ok ? __builtin_fmaf(cross, 1.0f / kLoScale, sacc[st][i]) * rk : -INFINITY;
-        cmax = fmaxf(cmax, sv[st][i]);
+        sv[st][i] = __builtin_fmaf(cross, 1.0f / kLoScale, sacc[st][i]) * rk;
       }
     }
+    if (ntok < kChunk) {  // wave-uniform: only the last chunk of a split
+#pragma unroll
+      for (int st = 0; st < NSUB; ++st)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (kSub * st + 4 * grp + i >= ntok) sv[st][i] = -INFINITY;
+    }
+    float cmax = sv[0][0];
+#pragma unroll
+    for (int st = 0; st < NSUB; ++st)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cmax = fmaxf(cmax, sv[st][i]);
+    // token 0 of the chunk is valid, so after the row reduction every lane's
+    // max is finite; the first chunk has m_run = -inf and alpha = 0.
     cmax = rows_max(cmax);
     const float mnew = fmaxf(m_run, cmax);
-    // a head with no valid score yet keeps m = -inf; avoid inf - inf
-    const float alpha = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - mnew);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
     m_run = mnew;
 
     // rescale the running output: lane (col, grp) holds rows 4grp + i, i.e.
@@ -311,6 +361,7 @@ __global__ void __launch_bounds__(256, 2) decode_mfma_kernel(const DecodeArgs a)
     float psum = 0.0f;
 #pragma unroll
     for (int kb = 0; kb < NSUB; ++kb) {
+      if (kb + 1 < NSUB) v_tables(kb + 1, vt[(kb + 1) & 1]);
       // weights p * r_v in the A layout: col < 8 -> (p_hi, 0), col >= 8 ->
       // (p_lo, p_hi) of head col - 8, taken from lane col - 8.
       const uint2 rv4 = *(const uint2 *)&rv_lds[kSub * kb + 4 * grp];
@@ -318,7 +369,7 @@ __global__ void __launch_bounds__(256, 2) decode_mfma_kernel(const DecodeArgs a)
       uint32_t pa[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = sv[kb][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[kb][i] - mnew);
+        const float p = __builtin_amdgcn_exp2f(sv[kb][i] - mnew);
         psum += p;
         half_t ph, pl;
         split_hi_lo(p * half_bits_to_float(rvw[i >> 1] >> (16 * (i & 1))), &ph, &pl);
@@ -327,27 +378,8 @@ __global__ void __launch_bounds__(256, 2) decode_mfma_kernel(const DecodeArgs a)
         pa[i] = col < 8 ? top : bot;
       }
       const half8_t pav = pack8u(pa[0], pa[1], pa[2], pa[3]);
-      uint32_t wv[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t *pv = (const uint32_t *)(vtile + (kSub * kb + 4 * grp + e) * VB + vob_al);
-        wv[e] = align_bytes(pv[1], pv[0], vsh);
-      }
-      // token pairs (0,1), (2,3): byte k of x = even coordinate 2k, of y = odd
-      const uint32_t x01 = (wv[0] & 0x0F0F0F0Fu) | ((wv[1] << 4) & 0xF0F0F0F0u);
-      const uint32_t y01 = ((wv[0] >> 4) & 0x0F0F0F0Fu) | (wv[1] & 0xF0F0F0F0u);
-      const uint32_t x23 = (wv[2] & 0x0F0F0F0Fu) | ((wv[3] << 4) & 0xF0F0F0F0u);
-      const uint32_t y23 = ((wv[2] >> 4) & 0x0F0F0F0Fu) | (wv[3] & 0xF0F0F0F0u);
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        // D = 128: n-tile nb is nibble nb of dword col (coordinate 8*col + nb).
-        // D = 64: n-tile nb is coordinate 8*(col & 7) + 2*nb + (col >> 3).
-        const int par = D == 128 ? (nb & 1) : vpar;
-        const int byte = D == 128 ? (nb >> 1) : nb;
-        const uint32_t i01 = ((par ? y01 : x01) >> (8 * byte)) & 0xFF;
-        const uint32_t i23 = ((par ? y23 : x23) >> (8 * byte)) & 0xFF;
-        oacc[nb] = mfma16(pav, pack8(lut_v[i01], lut_v[i23]), oacc[nb]);
-      }
+      for (int nb = 0; nb < NB; ++nb) oacc[nb] = mfma16(pav, pack8(vt[kb & 1][nb][0], vt[kb & 1][nb][1]), oacc[nb]);
     }
     l_run = l_run * alpha + psum;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -14,6 +14,7 @@ namespace pqkv {
 constexpr int kMaxListHeads = 64;  // kv heads per launch when heads are listed
 constexpr int kMaxSplits = 1024;   // split-K partitions per (batch, kv head)
 constexpr int kMergeHeads = 4;     // query heads per merge workgroup
+constexpr int kMfmaBlocksPerCU = 2;  // decode_mfma_kernel workgroups resident per CU
 
 struct EncodeArgs {
   const void *x;
