@@ -423,19 +423,79 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
 }
 
 size_t pqkv_prefill_workspace_bytes(int B, int Hq, int Hkv, int Sq, int S, int d) {
-  (void)B; (void)Hq; (void)Hkv; (void)Sq; (void)S; (void)d;
-  return 0;
+  (void)Hkv;
+  (void)S;
+  if (B <= 0 || Hq <= 0 || Sq <= 0 || d <= 0) return 0;
+  // rotated queries and rotated outputs, fp32 [B][Hq][Sq][d] each
+  return 2 * align256((size_t)B * Hq * Sq * d * 4);
 }
 
 int pqkv_prefill_attn(const void *q, int q_dtype, const float *R, const uint8_t *k_cache, const uint8_t *v_cache,
                       const float *k_codebook, const float *v_codebook, int k_bits, int v_bits, int B, int Hq,
                       int Hkv, int Sq, int q_start, int S, int S_max, int d, float scale, int causal, void *out,
                       int out_dtype, void *workspace, size_t workspace_bytes, void *stream) {
-  (void)q; (void)q_dtype; (void)R; (void)k_cache; (void)v_cache; (void)k_codebook; (void)v_codebook;
-  (void)k_bits; (void)v_bits; (void)B; (void)Hq; (void)Hkv; (void)Sq; (void)q_start; (void)S; (void)S_max;
-  (void)d; (void)scale; (void)causal; (void)out; (void)out_dtype; (void)workspace; (void)workspace_bytes;
-  (void)stream;
-  return fail(PQKV_ERR_UNSUPPORTED, "prefill: not built yet");
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || S < 0 || S_max < S || q_start < 0)
+    return fail(PQKV_ERR_INVALID, "prefill: B=%d Hq=%d Hkv=%d Sq=%d S=%d S_max=%d q_start=%d", B, Hq, Hkv, Sq, S,
+                S_max, q_start);
+  if (Hq % Hkv) return fail(PQKV_ERR_INVALID, "prefill: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
+  if (Hq / Hkv > pqkv::prefill_rows_per_block())
+    return fail(PQKV_ERR_UNSUPPORTED, "prefill: group size %d", Hq / Hkv);
+  if (causal && (int64_t)q_start + Sq > S)
+    return fail(PQKV_ERR_INVALID, "prefill: causal queries at %d..%d are not all in the cache (S=%d)", q_start,
+                q_start + Sq - 1, S);
+  if (!supported_d(d)) return fail(PQKV_ERR_UNSUPPORTED, "prefill: d=%d", d);
+  if (k_bits != 4 || v_bits != 4) return fail(PQKV_ERR_UNSUPPORTED, "prefill: widths k=%d v=%d (4-bit only)", k_bits, v_bits);
+  if (!float_dtype(q_dtype) || !float_dtype(out_dtype)) return fail(PQKV_ERR_UNSUPPORTED, "prefill: dtype");
+  if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(PQKV_ERR_INVALID, "prefill: scale must be > 0");
+  if (Sq == 0) return PQKV_OK;
+  if (!q || !R || !out) return fail(PQKV_ERR_INVALID, "prefill: null pointer");
+  if ((uintptr_t)R % 16) return fail(PQKV_ERR_INVALID, "prefill: R must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  if (S == 0) {
+    const size_t ob = (size_t)B * Hq * Sq * d * (out_dtype == PQKV_F32 ? 4 : 2);
+    return hip_status(pqkv::launch_fill_zero(out, ob, st), "prefill zero fill");
+  }
+  if (!k_cache || !v_cache || !k_codebook || !v_codebook) return fail(PQKV_ERR_INVALID, "prefill: null cache or codebook");
+  const size_t need = pqkv_prefill_workspace_bytes(B, Hq, Hkv, Sq, S, d);
+  if (!workspace || workspace_bytes < need)
+    return fail(PQKV_ERR_WORKSPACE, "prefill: workspace %zu < %zu bytes", workspace_bytes, need);
+  const int64_t nvec = (int64_t)B * Hq * Sq;
+  float *q32 = (float *)workspace;
+  float *o32 = (float *)((char *)workspace + align256((size_t)nvec * d * 4));
+  const float kLog2e = 1.4426950408889634f;
+  int tok = pqkv::prof_begin("prefill_rotate", st);
+  hipError_t e = pqkv::launch_rotate(q, q_dtype, R, q32, PQKV_F32, nvec, d, 0, scale * kLog2e, st);
+  pqkv::prof_end(tok, st);
+  if (e != hipSuccess) return hip_status(e, "prefill query rotation");
+  pqkv::PrefillArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = q32;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.head_stride = (int64_t)S_max * pqkv_vector_bytes(d, 4);
+  a.batch_stride = a.head_stride * Hkv;
+  a.k_cb = k_codebook;
+  a.v_cb = v_codebook;
+  a.o = o32;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.G = Hq / Hkv;
+  a.Sq = Sq;
+  a.q_start = q_start;
+  a.S = S;
+  a.S_max = S_max;
+  a.d = d;
+  a.causal = causal ? 1 : 0;
+  a.qt = pqkv::prefill_rows_per_block() / a.G;
+  tok = pqkv::prof_begin("prefill_attn", st);
+  e = pqkv::launch_prefill(a, st);
+  pqkv::prof_end(tok, st);
+  if (e != hipSuccess) return hip_status(e, "prefill launch");
+  tok = pqkv::prof_begin("prefill_out_rotate", st);
+  e = pqkv::launch_rotate(o32, PQKV_F32, R, out, out_dtype, nvec, d, 1, 1.0f, st);
+  pqkv::prof_end(tok, st);
+  return hip_status(e, "prefill output rotation");
 }
 
 int pqkv_soa_to_blocks(const uint8_t *packed, const float *radius, uint8_t *blocks, int64_t n, int d,

@@ -52,6 +52,18 @@ struct DecodeArgs {
   int64_t k_head_off[kMaxListHeads], v_head_off[kMaxListHeads];
 };
 
+// One launch of the chunked-prefill kernel: workgroups of 256 query rows
+// (qt tokens x G heads) of one (batch, kv-head); 4-bit K and V.
+struct PrefillArgs {
+  const float *q;                // [B][Hq][Sq][d] fp32, rotated, times scale*log2(e)
+  const uint8_t *k_cache, *v_cache;
+  int64_t batch_stride, head_stride;        // bytes (both caches: block_pq4, S_max vectors)
+  const float *k_cb, *v_cb;      // [16]
+  float *o;                      // [B][Hq][Sq][d] fp32, rotated, normalised
+  int B, Hq, Hkv, G, Sq, q_start, S, S_max, d, causal;
+  int qt;                        // query tokens per workgroup (rows / G)
+};
+
 // Event brackets for the measurement hook (pqkv_profile_*): returns a token
 // for prof_end, or -1 when profiling is off.
 int prof_begin(const char *name, hipStream_t s);
@@ -75,5 +87,7 @@ hipError_t launch_decode_mfma(const DecodeArgs &a, hipStream_t s);
 hipError_t launch_decode_merge(const float *part, const float *R, void *out, int out_dtype, int BHq, int splits,
                                int d, hipStream_t s);
 hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t s);
+hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s);
+int prefill_rows_per_block();
 
 }  // namespace pqkv

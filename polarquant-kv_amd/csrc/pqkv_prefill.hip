@@ -1,0 +1,407 @@
+// Chunked-prefill attention on the matrix cores (gfx950 v_mfma_f32_16x16x32_f16)
+// over block_pq4 keys and values.
+//
+// Sq query tokens per sequence, at absolute positions q_start.., attend to a
+// cache that already holds them (append-then-attend). With causal set, query
+// i sees cache positions <= q_start + i.
+//
+// Work split: one workgroup = 8 waves = 256 query rows of one (batch, kv-head),
+// a row being (query token, head of the group): row r -> token r / G, head
+// r % G. Each wave owns 32 rows (two 16-row tiles). The KV cache is walked in
+// 64-token tiles. Each tile is decoded once per workgroup into LDS, as fp16
+// planes in the exact order the MFMA operands want, so that every operand
+// read is a conflict-free run of 8-byte loads. Tiles are double-buffered:
+// the codes of tile i+1 are fetched from HBM before tile i's matrix work and
+// decoded after it.
+//
+// Scores are computed transposed, S^T[token][row] = K^ . Q^T: K^ (16 tokens x
+// 32 coordinates) is the A operand and the rotated queries the B operand, so
+// the result lands in the D layout with tokens on rows and query rows on
+// columns. That is the A layout of the P . V^ product, so the softmax weights
+// never leave the lanes (the same trick as the decode kernel).
+//
+// Precision: every fp32 operand x is split as x_hi = fp16(x),
+// x_lo = fp16(x - x_hi) (fp16 subnormals included, which the f16 MFMA keeps),
+// and each product is hi.hi + hi.lo + lo.hi in one fp32 accumulator: three
+// MFMAs per tile product, relative error ~2^-21 per term.
+#include "pqkv_device.h"
+#include "pqkv_launch.h"
+
+namespace pqkv {
+
+namespace {
+
+constexpr int kPW = 8;                    // waves per workgroup
+constexpr int kPRowsWave = 32;            // query rows per wave
+constexpr int kPT = 64;                   // kv tokens per tile
+constexpr int kSegBytes = 64 * 8;         // one operand segment: 64 lanes x 8 bytes
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
+typedef __attribute__((address_space(3))) const u32x2 lds_cu32x2;
+
+__device__ __forceinline__ void lds_put8(uint8_t *p, uint32_t a, uint32_t b) { *(lds_u32x2 *)p = (u32x2){a, b}; }
+__device__ __forceinline__ u32x2 lds_get8(const uint8_t *p) { return *(lds_cu32x2 *)p; }
+
+__device__ __forceinline__ void split2(float x, half_t *hi, half_t *lo) {
+  const half_t h = (half_t)x;
+  *hi = h;
+  *lo = (half_t)(x - (float)h);
+}
+
+__device__ __forceinline__ uint32_t pack_h2(half_t a, half_t b) {
+  half2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ half8_t pack8u(u32x2 a, u32x2 b) {
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  u32x4v v = {a.x, a.y, b.x, b.y};
+  return __builtin_bit_cast(half8_t, v);
+}
+
+__device__ __forceinline__ float4_t mfma16(half8_t a, half8_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float rows_max(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x), false, false);
+  x = fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x), false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x), false, false);
+  x = __builtin_bit_cast(float, (uint32_t)a[0]) + __builtin_bit_cast(float, (uint32_t)a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x), false, false);
+  return __builtin_bit_cast(float, (uint32_t)b[0]) + __builtin_bit_cast(float, (uint32_t)b[1]);
+}
+
+// Value of lane `row` (0..15) for output row 4 grp + i: the 16 values are
+// read once into scalars, then each lane picks by its lane group.
+__device__ __forceinline__ void per_row(float v, int grp, float (&f)[4]) {
+  float s[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), r));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) f[i] = grp == 0 ? s[i] : grp == 1 ? s[4 + i] : grp == 2 ? s[8 + i] : s[12 + i];
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t stream_rsrc(const uint8_t *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint32_t bld32(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t bld16(__amdgpu_buffer_rsrc_t r, int off) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+}
+
+// The code dword holding coordinates 8 g8 .. 8 g8 + 7 of vector `t`
+// (block g8 / 4, qs bytes 4 (g8 % 4) ..): two aligned loads and a byte shift.
+template <int VB>
+__device__ __forceinline__ uint32_t load_code_dword(__amdgpu_buffer_rsrc_t r, int t, int g8) {
+  const int off = t * VB + (g8 >> 2) * kPq4BlockBytes + 2 + 4 * (g8 & 3);
+  const int al = off & ~3;
+  return align_bytes(bld32(r, al + 4), bld32(r, al), off & 3);
+}
+
+}  // namespace
+
+template <int D>
+struct PrefillTile {
+  static constexpr int KS = D / 32;              // k-steps of the score product
+  static constexpr int NB = D / 16;              // n-tiles of the value product
+  static constexpr int KSEG = 4 * KS * 2 * 2;    // K segments: (tt, ks, plane, half)
+  static constexpr int VSEG = NB * 2 * 2 * 2;    // V segments: (nb, kk, plane, half)
+  static constexpr int BYTES = (KSEG + VSEG) * kSegBytes;
+  static constexpr int KITEMS = kPT * (D / 8);   // (token, 8-coordinate group)
+  static constexpr int VITEMS = (kPT / 4) * (D / 8);  // (4-token group, 8-coordinate group)
+  __device__ static int kseg(int tt, int ks, int plane, int h) { return ((tt * KS + ks) * 2 + plane) * 2 + h; }
+  __device__ static int vseg(int nb, int kk, int plane, int h) { return KSEG + ((nb * 2 + kk) * 2 + plane) * 2 + h; }
+};
+
+// Codes of one 64-token tile, held in registers between fetch and decode.
+template <int D>
+struct TileCodes {
+  static constexpr int KPER = PrefillTile<D>::KITEMS / (kPW * 64);
+  uint32_t k[KPER];
+  uint32_t v[4];
+  uint32_t r;
+};
+
+template <int D>
+__device__ __forceinline__ void fetch_tile(TileCodes<D> &c, __amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
+                                           int t0, int tid) {
+  using PT = PrefillTile<D>;
+  constexpr int VB = vector_bytes(D, 4);
+#pragma unroll
+  for (int u = 0; u < TileCodes<D>::KPER; ++u) {
+    const int item = tid + kPW * 64 * u;
+    c.k[u] = load_code_dword<VB>(kr, t0 + item / (D / 8), item % (D / 8));
+  }
+  if (tid < PT::VITEMS) {
+    const int q4 = tid / (D / 8), g8 = tid % (D / 8);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c.v[j] = load_code_dword<VB>(vr, t0 + 4 * q4 + j, g8);
+  }
+  if (tid < kPT) c.r = bld16(kr, (t0 + tid) * VB);            // wave 0: key radii
+  else if (tid < 2 * kPT) c.r = bld16(vr, (t0 + tid - kPT) * VB);  // wave 1: value radii
+}
+
+// Decode a fetched tile into LDS: K^ and V^ hi / lo planes in operand order,
+// and fp32 radii.
+template <int D>
+__device__ __forceinline__ void decode_tile(const TileCodes<D> &c, uint8_t *tile, float *rad, const uint2 *lut_k,
+                                            const uint2 *lut_v, int tid) {
+  using PT = PrefillTile<D>;
+#pragma unroll
+  for (int u = 0; u < TileCodes<D>::KPER; ++u) {
+    const int item = tid + kPW * 64 * u;
+    const int t = item / (D / 8), g8 = item % (D / 8);
+    const int lane = 16 * (g8 & 3) + (t & 15);
+    const uint32_t w = c.k[u];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      // coordinates 8 g8 + 4h .. +3: bytes 2h, 2h + 1 of w
+      const uint2 a = lut_k[(w >> (16 * h)) & 0xFF], b = lut_k[(w >> (16 * h + 8)) & 0xFF];
+      const uint32_t hi0 = __builtin_amdgcn_perm(a.y, a.x, 0x05040100u), hi1 = __builtin_amdgcn_perm(b.y, b.x, 0x05040100u);
+      const uint32_t lo0 = __builtin_amdgcn_perm(a.y, a.x, 0x07060302u), lo1 = __builtin_amdgcn_perm(b.y, b.x, 0x07060302u);
+      lds_put8(tile + PT::kseg(t >> 4, g8 >> 2, 0, h) * kSegBytes + lane * 8, hi0, hi1);
+      lds_put8(tile + PT::kseg(t >> 4, g8 >> 2, 1, h) * kSegBytes + lane * 8, lo0, lo1);
+    }
+  }
+  if (tid < PT::VITEMS) {
+    const int q4 = tid / (D / 8), g8 = tid % (D / 8);
+    const int tt = q4 >> 2, kk = tt >> 1, h = tt & 1, grp = q4 & 3;
+    // token pairs (0,1), (2,3): byte k of x = coordinate 2k of both tokens, of y = 2k + 1
+    const uint32_t x01 = (c.v[0] & 0x0F0F0F0Fu) | ((c.v[1] << 4) & 0xF0F0F0F0u);
+    const uint32_t y01 = ((c.v[0] >> 4) & 0x0F0F0F0Fu) | (c.v[1] & 0xF0F0F0F0u);
+    const uint32_t x23 = (c.v[2] & 0x0F0F0F0Fu) | ((c.v[3] << 4) & 0xF0F0F0F0u);
+    const uint32_t y23 = ((c.v[2] >> 4) & 0x0F0F0F0Fu) | (c.v[3] & 0xF0F0F0F0u);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int dcoord = 8 * g8 + e;
+      const int k = e >> 1;
+      const uint32_t s01 = (e & 1) ? y01 : x01, s23 = (e & 1) ? y23 : x23;
+      const uint2 a = lut_v[(s01 >> (8 * k)) & 0xFF], b = lut_v[(s23 >> (8 * k)) & 0xFF];
+      const int lane = 16 * grp + (dcoord & 15);
+      const uint32_t hi01 = __builtin_amdgcn_perm(a.y, a.x, 0x05040100u), hi23 = __builtin_amdgcn_perm(b.y, b.x, 0x05040100u);
+      const uint32_t lo01 = __builtin_amdgcn_perm(a.y, a.x, 0x07060302u), lo23 = __builtin_amdgcn_perm(b.y, b.x, 0x07060302u);
+      lds_put8(tile + PT::vseg(dcoord >> 4, kk, 0, h) * kSegBytes + lane * 8, hi01, hi23);
+      lds_put8(tile + PT::vseg(dcoord >> 4, kk, 1, h) * kSegBytes + lane * 8, lo01, lo23);
+    }
+  }
+  if (tid < 2 * kPT) rad[tid] = half_bits_to_float(c.r);
+}
+
+template <int D>
+__global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const PrefillArgs a) {
+  using PT = PrefillTile<D>;
+  constexpr int KS = PT::KS, NB = PT::NB;
+  constexpr int VB = vector_bytes(D, 4);
+  __shared__ uint2 lut_k[256], lut_v[256];
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[2][PT::BYTES];
+  __shared__ __attribute__((aligned(16))) float rads[2][2 * kPT];  // [buf][k radii | v radii]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int G = a.G;
+  const int qtile = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / a.Hkv, h = bh - b * a.Hkv;
+  const int q0 = qtile * a.qt;                       // first query token of the block
+  const int q_last = min(a.Sq, q0 + a.qt) - 1;       // last valid query token
+  const int kv_end = a.causal ? min(a.S, a.q_start + q_last + 1) : a.S;
+
+  const uint8_t *kstream = a.k_cache + b * a.batch_stride + h * a.head_stride;
+  const uint8_t *vstream = a.v_cache + b * a.batch_stride + h * a.head_stride;
+  const uint32_t valid_bytes = (uint32_t)a.S * (uint32_t)VB;
+  const __amdgpu_buffer_rsrc_t kres = stream_rsrc(kstream, valid_bytes);
+  const __amdgpu_buffer_rsrc_t vres = stream_rsrc(vstream, valid_bytes);
+
+  if (tid < 256) {  // byte -> (c_hi, c_lo) of its low and high nibble codes
+    half_t h0, l0, h1, l1;
+    split2(a.k_cb[tid & 15], &h0, &l0);
+    split2(a.k_cb[tid >> 4], &h1, &l1);
+    lut_k[tid] = make_uint2(pack_h2(h0, l0), pack_h2(h1, l1));
+    split2(a.v_cb[tid & 15], &h0, &l0);
+    split2(a.v_cb[tid >> 4], &h1, &l1);
+    lut_v[tid] = make_uint2(pack_h2(h0, l0), pack_h2(h1, l1));
+  }
+
+  // Queries as the B operand: column col = row 32 wave + 16 rt + col; step ks,
+  // k = 8 grp + i covers coordinate 32 ks + 8 grp + i.
+  half8_t qh[2][KS], ql[2][KS];
+  int row_pos[2];
+  bool row_ok[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int row = 32 * wave + 16 * rt + col;
+    const int tok = q0 + row / G, head = row % G;
+    row_ok[rt] = row < a.qt * G && tok < a.Sq;
+    row_pos[rt] = a.q_start + tok;
+    const float *qr = a.q + (((int64_t)(b * a.Hq + h * G + head) * a.Sq) + (row_ok[rt] ? tok : 0)) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        half_t vh, vl;
+        split2(row_ok[rt] ? qr[32 * ks + 8 * grp + i] : 0.0f, &vh, &vl);
+        qh[rt][ks][i] = vh;
+        ql[rt][ks][i] = vl;
+      }
+  }
+
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
+  float4_t oacc[2][NB];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) oacc[rt][nb] = (float4_t){0.f, 0.f, 0.f, 0.f};
+
+  const int ntiles = (kv_end + kPT - 1) / kPT;
+  TileCodes<D> codes;
+  __syncthreads();  // tables ready
+  if (ntiles > 0) {
+    fetch_tile<D>(codes, kres, vres, 0, tid);
+    decode_tile<D>(codes, tiles[0], rads[0], lut_k, lut_v, tid);
+  }
+  for (int it = 0; it < ntiles; ++it) {
+    const int t0 = it * kPT;
+    __syncthreads();  // tile it decoded; the other buffer is free
+    if (it + 1 < ntiles) fetch_tile<D>(codes, kres, vres, t0 + kPT, tid);
+    const uint8_t *tile = tiles[it & 1];
+    const float *rk = rads[it & 1], *rv = rads[it & 1] + kPT;
+
+    // ---------------- scores S^T[token][row] ----------------
+    float4_t sacc[2][4];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) sacc[rt][tt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const half8_t ah = pack8u(lds_get8(tile + PT::kseg(tt, ks, 0, 0) * kSegBytes + lane * 8),
+                                  lds_get8(tile + PT::kseg(tt, ks, 0, 1) * kSegBytes + lane * 8));
+        const half8_t al = pack8u(lds_get8(tile + PT::kseg(tt, ks, 1, 0) * kSegBytes + lane * 8),
+                                  lds_get8(tile + PT::kseg(tt, ks, 1, 1) * kSegBytes + lane * 8));
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          sacc[rt][tt] = mfma16(ah, qh[rt][ks], sacc[rt][tt]);
+          sacc[rt][tt] = mfma16(al, qh[rt][ks], sacc[rt][tt]);
+          sacc[rt][tt] = mfma16(ah, ql[rt][ks], sacc[rt][tt]);
+        }
+      }
+
+    // ---------------- online softmax, per row (lane col) ----------------
+    const bool need_mask = t0 + kPT > a.S || (a.causal && t0 + kPT - 1 > a.q_start + q0);
+    half8_t ph[2][2], pl[2][2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float s[4][4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const float4 r4 = *(const float4 *)&rk[16 * tt + 4 * grp];
+        const float rr[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[tt][i] = sacc[rt][tt][i] * rr[i];
+      }
+      if (need_mask) {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int t = t0 + 16 * tt + 4 * grp + i;
+            if (t >= a.S || (a.causal && t > row_pos[rt])) s[tt][i] = -INFINITY;
+          }
+      }
+      float cmax = s[0][0];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cmax = fmaxf(cmax, s[tt][i]);
+      cmax = rows_max(cmax);
+      // token 0 is valid for every row, so m_run is finite after the first tile
+      const float mnew = fmaxf(m_run[rt], cmax);
+      const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - mnew);
+      m_run[rt] = mnew;
+      float psum = 0.0f;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const float4 r4 = *(const float4 *)&rv[16 * tt + 4 * grp];
+        const float rr[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = __builtin_amdgcn_exp2f(s[tt][i] - mnew);
+          psum += p;
+          half_t vh, vl;
+          split2(p * rr[i], &vh, &vl);
+          // A operand of the value product: k = 8 grp + i' <-> token tile
+          // 2 kk + i' / 4, token 4 grp + i' % 4
+          ph[rt][tt >> 1][4 * (tt & 1) + i] = vh;
+          pl[rt][tt >> 1][4 * (tt & 1) + i] = vl;
+        }
+      }
+      l_run[rt] = l_run[rt] * alpha + psum;
+      float f[4];
+      per_row(alpha, grp, f);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) oacc[rt][nb][i] *= f[i];
+    }
+
+    // ---------------- values O[row][coord] += P . V^ ----------------
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const half8_t bh = pack8u(lds_get8(tile + PT::vseg(nb, kk, 0, 0) * kSegBytes + lane * 8),
+                                  lds_get8(tile + PT::vseg(nb, kk, 0, 1) * kSegBytes + lane * 8));
+        const half8_t bl = pack8u(lds_get8(tile + PT::vseg(nb, kk, 1, 0) * kSegBytes + lane * 8),
+                                  lds_get8(tile + PT::vseg(nb, kk, 1, 1) * kSegBytes + lane * 8));
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          oacc[rt][nb] = mfma16(ph[rt][kk], bh, oacc[rt][nb]);
+          oacc[rt][nb] = mfma16(ph[rt][kk], bl, oacc[rt][nb]);
+          oacc[rt][nb] = mfma16(pl[rt][kk], bh, oacc[rt][nb]);
+        }
+      }
+
+    if (it + 1 < ntiles) decode_tile<D>(codes, tiles[(it + 1) & 1], rads[(it + 1) & 1], lut_k, lut_v, tid);
+  }
+
+  // ---------------- normalise and write o_rot ----------------
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const float l = rows_sum(l_run[rt]);
+    float f[4];
+    per_row(l > 0.0f ? 1.0f / l : 0.0f, grp, f);
+    // output rows 4 grp + i of this row tile
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 32 * wave + 16 * rt + 4 * grp + i;
+      const int tok = q0 + row / G, head = row % G;
+      if (row < a.qt * G && tok < a.Sq) {
+        float *dst = a.o + (((int64_t)(b * a.Hq + h * G + head) * a.Sq) + tok) * D;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) dst[16 * nb + col] = oacc[rt][nb][i] * f[i];
+      }
+    }
+  }
+}
+
+hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s) {
+  const int qtiles = (a.Sq + a.qt - 1) / a.qt;
+  dim3 grid(qtiles, a.B * a.Hkv);
+  if (a.d == 128) prefill_mfma_kernel<128><<<grid, kPW * 64, 0, s>>>(a);
+  else prefill_mfma_kernel<64><<<grid, kPW * 64, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+int prefill_rows_per_block() { return kPW * kPRowsWave; }
+
+}  // namespace pqkv
