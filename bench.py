@@ -259,7 +259,11 @@ def main() -> int:
         "encode": {"tokens_per_s": round(enc_tokens_s), "ms": round(enc_ms, 4),
                    "kernel_ms": round(enc_kernel_ms / max(enc_launches, 1), 4), "GB_per_s": round(
                        enc_bytes / (enc_ms / 1e3) / 1e9, 2), "vectors": 2 * B * Hkv * S,
-                   "kernel": "encode_exact_kernel (fp32 FMA-chain rotation)"},
+                   "kernel": "encode_mfma_kernel (matrix-core rotation, bit-exact quantiser)",
+                   "roofline": {"bound": "hbm", "bytes": enc_bytes, "achieved_GBps": round(
+                       enc_bytes / (enc_kernel_ms / max(enc_launches, 1) * 2 / 1e3) / 1e9, 2),
+                       "frac": round(enc_bytes / (enc_kernel_ms / max(enc_launches, 1) * 2 / 1e3) / 1e9
+                                     / HBM_PEAK_GBS, 4)}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

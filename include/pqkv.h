@@ -91,6 +91,9 @@ int pqkv_quantize_rotated(const float *x_rot, const float *codebook, int n_bits,
  * m = d): signs at qjl + o * qjl_outer_stride + i * (m/8), bit i of the
  * sketch = (p_rot[i] . (x_rot - r c[idx]) >= 0), LSB first
  * (src/polarquant_kv_cuda/compress_kernel.py:166-175, qjl_kernel.py:6-37).
+ * fp16 input without QJL (x rows and R 16-byte aligned) runs on the
+ * matrix-core encoder of pqkv_encode_mfma; PQKV_ENCODE_KERNEL=exact in the
+ * environment forces the FMA-chain rotation of pqkv_rotate everywhere.
  * Replaces turboquant_compress (csrc/flash_turboquant.cu:213-225) and
  * polarquant_compress_cuda (patch:443-467). */
 int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride,
@@ -99,6 +102,21 @@ int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride,
                 int64_t n_outer, int64_t n_inner, int d,
                 const float *p_rot, int m, uint8_t *qjl, int64_t qjl_outer_stride,
                 void *stream);
+
+/* Matrix-core encoder (no counterpart in the reference: a second, faster
+ * implementation of pqkv_encode for fp16 input without QJL, which
+ * pqkv_encode uses whenever its conditions hold unless the environment sets
+ * PQKV_ENCODE_KERNEL=exact). x must be 16-byte aligned with a row stride that
+ * is a multiple of 8 elements, R 16-byte aligned; otherwise
+ * PQKV_ERR_UNSUPPORTED. The rotation runs on the matrix cores with fp32-grade
+ * products but not the reference's FMA-chain rounding; the quantiser is
+ * bit-exact on the rotated values it computes, which rot_out (nullable,
+ * fp32 [n_outer * n_inner][d]) receives. */
+int pqkv_encode_mfma(const void *x, int x_dtype, int64_t x_outer_stride,
+                     const float *R, const float *codebook, int n_bits,
+                     uint8_t *blocks, int64_t blocks_outer_stride,
+                     int64_t n_outer, int64_t n_inner, int d,
+                     float *rot_out, void *stream);
 
 /* ---- decode attention ----------------------------------------------------
  * One query token per sequence against a block-encoded cache:

@@ -275,9 +275,11 @@ int pqkv_quantize_rotated(const float *x_rot, const float *codebook, int n_bits,
                     "quantize_rotated launch");
 }
 
-int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride, const float *R, const float *codebook,
-                int n_bits, uint8_t *blocks, int64_t blocks_outer_stride, int64_t n_outer, int64_t n_inner, int d,
-                const float *p_rot, int m, uint8_t *qjl, int64_t qjl_outer_stride, void *stream) {
+namespace {
+
+int encode_validate(const void *x, int x_dtype, int64_t x_outer_stride, const float *R, const float *codebook,
+                    int n_bits, uint8_t *blocks, int64_t blocks_outer_stride, int64_t n_outer, int64_t n_inner, int d,
+                    const float *p_rot, int m, uint8_t *qjl, int64_t qjl_outer_stride) {
   if (n_outer < 0 || n_inner < 0) return fail(PQKV_ERR_INVALID, "encode: negative count");
   if (!supported_d(d) || !supported_bits(n_bits))
     return fail(PQKV_ERR_UNSUPPORTED, "encode: d=%d bits=%d", d, n_bits);
@@ -291,12 +293,60 @@ int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride, const float 
     return fail(PQKV_ERR_INVALID, "encode: outer strides overlap rows");
   if (qjl && n_outer > 1 && qjl_outer_stride < n_inner * (m / 8))
     return fail(PQKV_ERR_INVALID, "encode: qjl outer stride overlaps rows");
+  return 1;  // valid, work to do
+}
+
+// The matrix-core encoder takes fp16 input without QJL whose rows and R allow
+// 16-byte loads.
+bool fast_encode_ok(const void *x, int x_dtype, int64_t x_outer_stride, int64_t n_outer, const float *R,
+                    const uint8_t *qjl) {
+  if (x_dtype != PQKV_F16 || qjl != nullptr) return false;
+  if ((uintptr_t)x % 16 || (uintptr_t)R % 16) return false;
+  return n_outer <= 1 || x_outer_stride % 8 == 0;
+}
+
+}  // namespace
+
+// Encoder choice: the matrix-core encoder wherever fast_encode_ok holds;
+// PQKV_ENCODE_KERNEL=exact forces the FMA-chain encoder (the reference
+// kernel's rotation rounding) everywhere.
+int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride, const float *R, const float *codebook,
+                int n_bits, uint8_t *blocks, int64_t blocks_outer_stride, int64_t n_outer, int64_t n_inner, int d,
+                const float *p_rot, int m, uint8_t *qjl, int64_t qjl_outer_stride, void *stream) {
+  const int v = encode_validate(x, x_dtype, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride, n_outer,
+                                n_inner, d, p_rot, m, qjl, qjl_outer_stride);
+  if (v <= 0) return v;
   pqkv::EncodeArgs a{x, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride, n_outer, n_inner,
                      d, p_rot, m, qjl, qjl_outer_stride};
-  const int tok = pqkv::prof_begin("encode_exact", (hipStream_t)stream);
-  const hipError_t e = pqkv::launch_encode_exact(a, x_dtype, (hipStream_t)stream);
-  pqkv::prof_end(tok, (hipStream_t)stream);
+  const char *env = getenv("PQKV_ENCODE_KERNEL");
+  const bool exact = env && strcmp(env, "exact") == 0;
+  hipError_t e;
+  if (!exact && fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, R, qjl)) {
+    const int tok = pqkv::prof_begin("encode_mfma", (hipStream_t)stream);
+    e = pqkv::launch_encode_mfma(a, nullptr, (hipStream_t)stream);
+    pqkv::prof_end(tok, (hipStream_t)stream);
+  } else {
+    const int tok = pqkv::prof_begin("encode_exact", (hipStream_t)stream);
+    e = pqkv::launch_encode_exact(a, x_dtype, (hipStream_t)stream);
+    pqkv::prof_end(tok, (hipStream_t)stream);
+  }
   return hip_status(e, "encode launch");
+}
+
+int pqkv_encode_mfma(const void *x, int x_dtype, int64_t x_outer_stride, const float *R, const float *codebook,
+                     int n_bits, uint8_t *blocks, int64_t blocks_outer_stride, int64_t n_outer, int64_t n_inner,
+                     int d, float *rot_out, void *stream) {
+  const int v = encode_validate(x, x_dtype, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride, n_outer,
+                                n_inner, d, nullptr, 0, nullptr, 0);
+  if (v <= 0) return v;
+  if (!fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, R, nullptr))
+    return fail(PQKV_ERR_UNSUPPORTED, "encode_mfma: needs fp16 x, 16-byte aligned x rows and R");
+  pqkv::EncodeArgs a{x, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride, n_outer, n_inner,
+                     d, nullptr, 0, nullptr, 0};
+  const int tok = pqkv::prof_begin("encode_mfma", (hipStream_t)stream);
+  const hipError_t e = pqkv::launch_encode_mfma(a, rot_out, (hipStream_t)stream);
+  pqkv::prof_end(tok, (hipStream_t)stream);
+  return hip_status(e, "encode_mfma launch");
 }
 
 size_t pqkv_decode_workspace_bytes(int B, int Hq, int Hkv, int S, int d) {

@@ -1,8 +1,15 @@
-"""GPU parity of the encoder against the CPU oracle (bit-exact).
+"""GPU parity of the encoders against the CPU oracle (bit-exact).
 
-The HIP rotation is the reference's fp32 FMA chain, so the whole encode is
-compared bit for bit with oracle.c_rotate_fma -> c_quantize_rotated ->
-c_pack_blocks on the same inputs."""
+Two encoders sit behind pqkv_encode:
+  * the exact encoder (PQKV_ENCODE_KERNEL=exact, and always for fp32 input or
+    QJL): its rotation is the reference's fp32 FMA chain, so the whole encode
+    is compared bit for bit with oracle.c_rotate_fma -> c_quantize_rotated ->
+    c_pack_blocks on the same inputs;
+  * the matrix-core encoder (fp16 input without QJL, the default there): its
+    rotation has fp32-grade products with another rounding, so its quantiser
+    is compared bit for bit with the oracle on the rotated values it returns
+    (pqkv_encode_mfma's rot_out), and its rotation is checked against the FMA
+    chain within fp32 rounding."""
 
 import numpy as np
 import pytest
@@ -69,8 +76,9 @@ def _oracle_encode(x, R32, bits):
 
 @pytest.mark.parametrize("d,bits", [(128, 4), (64, 4), (128, 2)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
-def test_encode_cache_bit_exact(d, bits, dtype):
+def test_encode_cache_bit_exact(d, bits, dtype, monkeypatch):
     print(f"encode d={d} bits={bits} dtype={dtype}", flush=True)
+    monkeypatch.setenv("PQKV_ENCODE_KERNEL", "exact")
     B, H, T = 2, 3, 45
     rng = np.random.default_rng(d + bits)
     x = (rng.standard_normal((B, H, T, d)) * 2).astype(np.float32)
@@ -87,7 +95,8 @@ def test_encode_cache_bit_exact(d, bits, dtype):
     assert not got[:, :, :7].any() and not got[:, :, 52:].any()
 
 
-def test_encode_mixed_widths_bit_exact():
+def test_encode_mixed_widths_bit_exact(monkeypatch):
+    monkeypatch.setenv("PQKV_ENCODE_KERNEL", "exact")
     B, H, T, d = 2, 4, 33, 128
     widths = (4, 2, 2, 4)
     rng = np.random.default_rng(3)
@@ -125,3 +134,102 @@ def test_encode_qjl_signs():
     bad = (got != want) & (np.abs(proj) > tol)
     assert not bad.any(), int(bad.sum())
     assert (got != want).mean() < 1e-3
+
+
+# ---------------------------------------------------------------------------
+# matrix-core encoder
+# ---------------------------------------------------------------------------
+
+def _fp16_inputs(n, d, seed, kind):
+    rng = np.random.default_rng(seed)
+    if kind == "normal":
+        x = rng.standard_normal((n, d))
+    elif kind == "channel":
+        std = np.exp(rng.standard_normal(d))
+        std[rng.permutation(d)[:2]] *= 20
+        x = rng.standard_normal((n, d)) * std
+    else:  # special vectors among lognormal-scaled ones
+        x = rng.standard_normal((n, d)) * rng.lognormal(0, 1.5, (n, 1))
+        x[0] = 0.0                                           # zero vector
+        x[1] = 0.0
+        x[1, 3] = 6e-8                                       # fp16 subnormal, one coordinate
+        x[2] = 0.0
+        x[2, 5] = 3.0                                        # one-hot
+        x[3] = 1e4 * rng.standard_normal(d)                  # large
+        x[4] = 1.0                                           # constant
+    return x.astype(np.float16)
+
+
+def _encode_mfma(x16, R32, cb_t, bits, d, n_outer=1):
+    n = x16.shape[0]
+    vb = O.vector_bytes(d, bits)
+    xt = torch.from_numpy(x16).to(DEV)
+    Rt = torch.from_numpy(R32).to(DEV)
+    blocks = torch.zeros(n, vb, dtype=torch.uint8, device=DEV)
+    rot = torch.empty(n, d, dtype=torch.float32, device=DEV)
+    n_inner = n // n_outer
+    _lib.check(_lib.lib().pqkv_encode_mfma(xt.data_ptr(), _lib.F16, n_inner * d, Rt.data_ptr(), cb_t.data_ptr(),
+                                           bits, blocks.data_ptr(), n_inner * vb, n_outer, n_inner, d,
+                                           rot.data_ptr(), _lib.stream_of(xt)))
+    torch.cuda.synchronize()
+    return blocks.cpu().numpy(), rot.cpu().numpy()
+
+
+@pytest.mark.parametrize("d,bits", [(128, 4), (64, 4), (128, 2), (64, 2)])
+@pytest.mark.parametrize("kind", ["normal", "channel", "special"])
+def test_mfma_encoder_quantiser_bit_exact_on_its_rotation(d, bits, kind):
+    print(f"encode_mfma d={d} bits={bits} kind={kind}", flush=True)
+    x = _fp16_inputs(3001, d, d + bits, kind)              # not a multiple of the 64-vector tile
+    R32 = O.rotation_matrix(d, 42).astype(np.float32)
+    blocks, rot = _encode_mfma(x, R32, padded_codebook_torch(d, bits, DEV), bits, d, n_outer=3001 if kind == "normal" else 1)
+    cb = O.lloyd_max_codebook(d, bits)[0]
+    r_ref, idx_ref = OC.c_quantize_rotated(rot, cb)
+    assert np.array_equal(blocks, OC.c_pack_blocks(r_ref, idx_ref, bits))
+    if kind == "special":
+        assert not blocks[0, :2].any() and r_ref[0] == 0.0  # zero vector: radius 0, code argmin |c|
+
+
+@pytest.mark.parametrize("d,bits", [(128, 4), (64, 2)])
+def test_mfma_rotation_within_fp32_rounding_of_fma_chain(d, bits):
+    x = _fp16_inputs(4096, d, 7, "channel")
+    R32 = O.rotation_matrix(d, 42).astype(np.float32)
+    blocks, rot = _encode_mfma(x, R32, padded_codebook_torch(d, bits, DEV), bits, d)
+    ref = OC.c_rotate_fma(x.astype(np.float32), R32)
+    scale = np.abs(x.astype(np.float64)) @ np.abs(R32.astype(np.float64)).T   # sum |x_k R_jk|
+    # both are fp32 sums of 128 products in different orders; dropping R's lo
+    # half would leave ~2^-12 of the scale, far above this bound
+    err = np.abs(rot.astype(np.float64) - ref) / scale
+    assert err.max() <= 64 * 2.0 ** -24, err.max()
+    cb = O.lloyd_max_codebook(d, bits)[0]
+    r_ref, idx_ref = OC.c_quantize_rotated(ref, cb)
+    r_got, idx_got = OC.c_quantize_rotated(rot, cb)
+    assert (idx_got == idx_ref).mean() > 0.9999            # codes flip only at exact boundary cases
+    assert (np.abs(r_got.astype(np.float64) / r_ref - 1) < 1e-6).all()
+
+
+def test_mfma_encoder_unsorted_codebook_uses_the_scan():
+    d, bits = 128, 4
+    x = _fp16_inputs(700, d, 3, "normal")
+    R32 = O.rotation_matrix(d, 42).astype(np.float32)
+    cb = O.lloyd_max_codebook(d, bits)[0]
+    perm = np.random.default_rng(0).permutation(16)
+    cbp = cb[perm].astype(np.float32)
+    blocks, rot = _encode_mfma(x, R32, torch.from_numpy(cbp).to(DEV), bits, d)
+    r_ref, idx_ref = OC.c_quantize_rotated(rot, cbp)
+    assert np.array_equal(blocks, OC.c_pack_blocks(r_ref, idx_ref, bits))
+
+
+def test_compress_pq_fp16_takes_the_mfma_encoder(monkeypatch):
+    B, H, T, d = 2, 3, 150, 128
+    x = _fp16_inputs(B * H * T, d, 9, "normal").reshape(B, H, T, d)
+    R32 = O.rotation_matrix(d, 42).astype(np.float32)
+    Rt = torch.from_numpy(R32).to(DEV)
+    cache = quantizer.allocate_cache(B, H, 160, d, 4, DEV)
+    quantizer.compress_pq(torch.from_numpy(x).to(DEV), Rt, cache=cache)
+    got = cache.blocks.cpu().numpy()[:, :, :T].reshape(-1, 72)
+    want, _ = _encode_mfma(x.reshape(-1, d), R32, padded_codebook_torch(d, 4, DEV), 4, d)
+    assert np.array_equal(got, want)
+    monkeypatch.setenv("PQKV_ENCODE_KERNEL", "exact")
+    quantizer.compress_pq(torch.from_numpy(x).to(DEV), Rt, cache=cache, start=0)
+    want_exact, *_ = _oracle_encode(x.astype(np.float32), R32, 4)
+    assert np.array_equal(cache.blocks.cpu().numpy()[:, :, :T].reshape(-1, 72), want_exact)
