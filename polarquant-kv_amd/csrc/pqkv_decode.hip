@@ -316,22 +316,31 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
 }
 
 // Combine splits, normalise and rotate back: out = R^T (sum_s w_s o_s / L).
-// Four query heads per block (one wave each for the split weights); R is
-// staged once per block in LDS with padded rows, so the column reads
-// R[k][j] across lanes j are conflict-free.
+// Workgroup (hg, cg): kMergeHeads query heads x 32 output columns. One wave
+// per head computes the split weights; every workgroup of a head group forms
+// the full normalised o_rot (cheap, L2-resident partials) and then its 32
+// outputs from the matching 32 columns of R, staged as [32][D + 1].
 template <int D, typename TOUT>
 __global__ void __launch_bounds__(256) decode_merge_kernel(const float *__restrict__ part,
                                                           const float *__restrict__ R,
                                                           TOUT *__restrict__ out, int BHq, int splits) {
   constexpr int NH = kMergeHeads;
+  constexpr int NC = 32;           // output columns per workgroup
   constexpr int RP = D + 1;
-  constexpr int PER = NH * D / 256;  // outputs per thread
-  __shared__ float rs[D * RP];
+  __shared__ float rs[NC * RP];    // rs[jj][k] = R[k][c0 + jj]
   __shared__ float os[NH * D];
   __shared__ float wts[NH][kMaxSplits];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int head0 = blockIdx.x * NH;
-  stage_matrix_padded<D>(R, rs, tid);
+  const int head0 = blockIdx.x * NH, c0 = blockIdx.y * NC;
+#pragma unroll
+  for (int u = 0; u < NC * D / 4 / 256; ++u) {
+    const int i = tid + 256 * u, k = i / (NC / 4), j4 = i % (NC / 4);
+    const float4 v = *(const float4 *)(R + (int64_t)k * D + c0 + 4 * j4);
+    rs[(4 * j4 + 0) * RP + k] = v.x;
+    rs[(4 * j4 + 1) * RP + k] = v.y;
+    rs[(4 * j4 + 2) * RP + k] = v.z;
+    rs[(4 * j4 + 3) * RP + k] = v.w;
+  }
   {
     const int hq = head0 + wave;
     if (hq < BHq) {
@@ -353,7 +362,7 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const float *__restri
   }
   __syncthreads();
 #pragma unroll
-  for (int u = 0; u < PER; ++u) {
+  for (int u = 0; u < NH * D / 256; ++u) {
     const int i = tid + 256 * u, hh = i / D, c = i % D;
     const int hq = head0 + hh;
     float o = 0.0f;
@@ -365,20 +374,13 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const float *__restri
     os[i] = o;
   }
   __syncthreads();
-  float acc[PER];
-#pragma unroll
-  for (int u = 0; u < PER; ++u) acc[u] = 0.0f;
-  const int j = tid % D;
-#pragma unroll 8
-  for (int k = 0; k < D; ++k) {
-    const float r = rs[k * RP + j];
-#pragma unroll
-    for (int u = 0; u < PER; ++u) acc[u] = __builtin_fmaf(os[((tid + 256 * u) / D) * D + k], r, acc[u]);
-  }
-#pragma unroll
-  for (int u = 0; u < PER; ++u) {
-    const int hq = head0 + (tid + 256 * u) / D;
-    if (hq < BHq) out[(int64_t)hq * D + j] = (TOUT)acc[u];
+  if (tid < NH * NC) {
+    const int hh = tid / NC, jj = tid % NC;
+    float acc = 0.0f;
+#pragma unroll 16
+    for (int k = 0; k < D; ++k) acc = __builtin_fmaf(os[hh * D + k], rs[jj * RP + k], acc);
+    const int hq = head0 + hh;
+    if (hq < BHq) out[(int64_t)hq * D + c0 + jj] = (TOUT)acc;
   }
 }
 
@@ -428,7 +430,7 @@ hipError_t launch_decode_split(const DecodeArgs &a, int k_bits, int v_bits, hipS
 hipError_t launch_decode_merge(const float *part, const float *R, void *out, int out_dtype, int BHq, int splits,
                                int d, hipStream_t s) {
   if (splits < 1 || splits > kMaxSplits) return hipErrorInvalidValue;
-  const int grid = (BHq + kMergeHeads - 1) / kMergeHeads;
+  const dim3 grid((BHq + kMergeHeads - 1) / kMergeHeads, d / 32);
   if (d == 128) {
     if (out_dtype == 0) decode_merge_kernel<128, float><<<grid, 256, 0, s>>>(part, R, (float *)out, BHq, splits);
     else decode_merge_kernel<128, half_t><<<grid, 256, 0, s>>>(part, R, (half_t *)out, BHq, splits);

@@ -52,24 +52,4 @@ __device__ __forceinline__ float fdot2(half2_t a, half2_t b, float c) {
   return __builtin_amdgcn_fdot2(a, b, c, false);
 }
 
-// Copy a D x D fp32 matrix into LDS with rows padded to D + 1 floats, using
-// a 256-thread block; all of a thread's 16-byte loads are issued before any
-// LDS store so they overlap.
-template <int D>
-__device__ __forceinline__ void stage_matrix_padded(const float *__restrict__ m, float *lds, int tid) {
-  constexpr int kPer = D * D / 4 / 256;
-  float4 v[kPer];
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) v[u] = ((const float4 *)m)[tid + 256 * u];
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) {
-    const int i = 4 * (tid + 256 * u), row = i / D, col = i % D;
-    float *dst = lds + row * (D + 1) + col;
-    dst[0] = v[u].x;
-    dst[1] = v[u].y;
-    dst[2] = v[u].z;
-    dst[3] = v[u].w;
-  }
-}
-
 }  // namespace pqkv

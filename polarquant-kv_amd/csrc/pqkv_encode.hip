@@ -147,43 +147,57 @@ __device__ __forceinline__ float load_as_float(const T *p) { return (float)*p; }
 
 // y = R x (forward) or R^T x (inverse) for n vectors, each output one fp32
 // FMA chain over k ascending (the encoder's order, so both agree bit for bit).
-// R is staged once per block in LDS with a padded row ([D][D + 1]): lanes
-// reading R[j][k] (forward, stride D + 1) or R[k][j] (inverse, stride 1) hit
-// distinct banks (70 KB of LDS for D = 128; gfx950 allows 160 KB per
-// workgroup). 256 threads = 256 / D column groups, 4 vectors per thread.
-template <int D>
-constexpr int rotate_vectors_per_block() { return 4 * (256 / D); }
+// Workgroup (vg, cg): 8 vectors x 32 output columns, one output per thread.
+// The 32 rows (forward) or columns (inverse) of R it needs are staged in LDS
+// as [32][D + 1] (padded: the per-lane reads r[jj][k] hit distinct banks).
+constexpr int kRotVec = 8;   // vectors per workgroup iteration
+constexpr int kRotCols = 32; // output columns per workgroup
 
 template <int D, bool INVERSE, typename TIN, typename TOUT>
 __global__ void __launch_bounds__(256) rotate_kernel(const TIN *__restrict__ x, const float *__restrict__ R,
                                                      TOUT *__restrict__ y, int64_t n, float out_scale) {
-  constexpr int NV = rotate_vectors_per_block<D>();
   constexpr int RP = D + 1;
-  __shared__ float rs[D * RP];   // R, padded rows
-  __shared__ float xs[NV * D];   // this iteration's vectors
+  __shared__ float rs[kRotCols * RP];
+  __shared__ float xs[kRotVec * D];
   const int tid = threadIdx.x;
-  stage_matrix_padded<D>(R, rs, tid);
-  const int j = tid % D, g = tid / D;
-  for (int64_t base = (int64_t)blockIdx.x * NV; base < n; base += (int64_t)gridDim.x * NV) {
+  const int c0 = blockIdx.y * kRotCols;
+  // rs[jj][k] = R[c0 + jj][k] (forward) or R[k][c0 + jj] (inverse)
+  if (!INVERSE) {
 #pragma unroll
-    for (int u = 0; u < NV * D / 256; ++u) {
+    for (int u = 0; u < kRotCols * D / 4 / 256; ++u) {
+      const int i = tid + 256 * u, jj = i / (D / 4), k4 = i % (D / 4);
+      const float4 v = *(const float4 *)(R + (int64_t)(c0 + jj) * D + 4 * k4);
+      float *dst = rs + jj * RP + 4 * k4;
+      dst[0] = v.x;
+      dst[1] = v.y;
+      dst[2] = v.z;
+      dst[3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < kRotCols * D / 4 / 256; ++u) {
+      const int i = tid + 256 * u, k = i / (kRotCols / 4), j4 = i % (kRotCols / 4);
+      const float4 v = *(const float4 *)(R + (int64_t)k * D + c0 + 4 * j4);
+      rs[(4 * j4 + 0) * RP + k] = v.x;
+      rs[(4 * j4 + 1) * RP + k] = v.y;
+      rs[(4 * j4 + 2) * RP + k] = v.z;
+      rs[(4 * j4 + 3) * RP + k] = v.w;
+    }
+  }
+  const int jj = tid % kRotCols, g = tid / kRotCols;   // g: vector of the group
+  for (int64_t base = (int64_t)blockIdx.x * kRotVec; base < n; base += (int64_t)gridDim.x * kRotVec) {
+#pragma unroll
+    for (int u = 0; u < kRotVec * D / 256; ++u) {
       const int i = tid + 256 * u;
       const int64_t v = base + i / D;
       xs[i] = v < n ? load_as_float(x + v * D + (i % D)) : 0.0f;
     }
     __syncthreads();
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 8
-    for (int k = 0; k < D; ++k) {
-      const float r = INVERSE ? rs[k * RP + j] : rs[j * RP + k];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) acc[u] = __builtin_fmaf(xs[(4 * g + u) * D + k], r, acc[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t v = base + 4 * g + u;
-      if (v < n) y[v * D + j] = (TOUT)(acc[u] * out_scale);
-    }
+    float acc = 0.0f;
+#pragma unroll 16
+    for (int k = 0; k < D; ++k) acc = __builtin_fmaf(xs[g * D + k], rs[jj * RP + k], acc);
+    const int64_t v = base + g;
+    if (v < n) y[v * D + c0 + jj] = (TOUT)(acc * out_scale);
     __syncthreads();
   }
 }
@@ -371,7 +385,7 @@ hipError_t launch_quantize_rotated(const float *x_rot, const float *codebook, in
 template <int D, bool INV>
 static void rotate_dispatch(const void *x, int xt, const float *R, void *y, int yt, int64_t n, float sc,
                             hipStream_t s) {
-  const int grid = grid_for(n, rotate_vectors_per_block<D>(), 1024);
+  const dim3 grid(grid_for(n, kRotVec, 2048), D / kRotCols);
   if (xt == 0 && yt == 0)
     rotate_kernel<D, INV, float, float><<<grid, 256, 0, s>>>((const float *)x, R, (float *)y, n, sc);
   else if (xt == 0 && yt == 1)
