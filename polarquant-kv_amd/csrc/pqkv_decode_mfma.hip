@@ -174,10 +174,22 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   constexpr int NSUB = kChunk / kSub;
   constexpr int TILE = kChunk * VB;
 
-  __shared__ uint2 lut_k[256], lut_v[256];
-  __shared__ __attribute__((aligned(16))) uint8_t tiles[kMWaves][2][TILE + 16];
-  __shared__ __attribute__((aligned(8))) uint16_t rad[kMWaves][2][kChunk];
-  __shared__ float red_m[kMWaves][8], red_l[kMWaves][8];
+  // One LDS block with the tables first, so their addresses fit the 16-bit
+  // immediate offset of ds_read (the whole block is 80 KB). Per wave: two
+  // chunk buffers (the chunk being finished and the next one), each a K and a
+  // V tile plus their gathered radii.
+  struct Smem {
+    uint2 lut_k[256], lut_v[256];
+    float red_m[kMWaves][8], red_l[kMWaves][8];
+    uint16_t rad[kMWaves][2][2][kChunk];
+    __attribute__((aligned(16))) uint8_t tiles[kMWaves][2][2][TILE + 16];
+  };
+  __shared__ Smem sm;
+  uint2 *lut_k = sm.lut_k, *lut_v = sm.lut_v;
+  auto &tiles = sm.tiles;
+  auto &rad = sm.rad;
+  auto &red_m = sm.red_m;
+  auto &red_l = sm.red_l;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
@@ -235,78 +247,41 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   const int vob = (vw >> 2) * kPq4BlockBytes + 2 + 4 * (vw & 3);
   const int vob_al = vob & ~3, vsh = vob & 3;
 
-  uint8_t *ktile = tiles[wave][0], *vtile = tiles[wave][1];
-  uint16_t *rk_lds = rad[wave][0], *rv_lds = rad[wave][1];
+  ChunkRegs<D> cr_;
   __syncthreads();
 
-  ChunkRegs<D> cr;
-  constexpr int kStep = kMWaves * kChunk;
-  int t0 = t_begin + wave * kChunk;
-  if (t0 < t_end) load_chunk<D>(cr, kres, vres, t0, lane);
-  for (; t0 < t_end; t0 += kStep) {
-    const int ntok = min(kChunk, t_end - t0);
-    stage_chunk<D>(cr, ktile, vtile, lane);
-    if (t0 + kStep < t_end) load_chunk<D>(cr, kres, vres, t0 + kStep, lane);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // radii of the chunk's tokens, gathered so a lane reads 4 with one load
-    rk_lds[lane] = *(const uint16_t *)(ktile + lane * VB);
-    rv_lds[lane] = *(const uint16_t *)(vtile + lane * VB);
-
-    // ---------------- scores: S^T[token][col] per 16-token tile ----------------
-    // Table entries of sub-tile st + 1 are requested before the MFMAs of
-    // sub-tile st, so LDS latency overlaps matrix work within the wave.
-    auto k_tables = [&](int st, uint2 (&t)[KK][2]) {
+  // Stage a chunk (held in registers) into buffer `buf` and gather its radii.
+  auto stage = [&](int buf) {
+    stage_chunk<D>(cr_, tiles[wave][buf][0], tiles[wave][buf][1], lane);
+    rad[wave][buf][0][lane] = *(const uint16_t *)(tiles[wave][buf][0] + lane * VB);
+    rad[wave][buf][1][lane] = *(const uint16_t *)(tiles[wave][buf][1] + lane * VB);
+  };
+  // Scores of the chunk in buffer `buf`: S^T[token][col] per 16-token tile.
+  auto scores = [&](int buf, float4_t (&sacc)[NSUB]) {
+    const uint8_t *ktile = tiles[wave][buf][0];
+#pragma unroll
+    for (int st = 0; st < NSUB; ++st) {
       const uint8_t *kv = ktile + (kSub * st + col) * VB;
+      uint2 kt[KK][2];
 #pragma unroll
       for (int m = 0; m < KK / 2; ++m) {
         const uint32_t w = qs_dword(kv, m, grp);
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          t[2 * m + e][0] = lut_k[(w >> (16 * e)) & 0xFF];
-          t[2 * m + e][1] = lut_k[(w >> (16 * e + 8)) & 0xFF];
+          kt[2 * m + e][0] = lut_k[(w >> (16 * e)) & 0xFF];
+          kt[2 * m + e][1] = lut_k[(w >> (16 * e + 8)) & 0xFF];
         }
       }
-    };
-    // Value-side entries of k-block kb: two tokens' nibbles of the lane's
-    // coordinate interleaved into one byte (token pairs (0,1) and (2,3)).
-    auto v_tables = [&](int kb, uint2 (&t)[NB][2]) {
-      uint32_t wv[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t *pv = (const uint32_t *)(vtile + (kSub * kb + 4 * grp + e) * VB + vob_al);
-        wv[e] = align_bytes(pv[1], pv[0], vsh);
-      }
-      // byte k of x = even coordinate 2k of both tokens, of y = odd 2k + 1
-      const uint32_t x01 = (wv[0] & 0x0F0F0F0Fu) | ((wv[1] << 4) & 0xF0F0F0F0u);
-      const uint32_t y01 = ((wv[0] >> 4) & 0x0F0F0F0Fu) | (wv[1] & 0xF0F0F0F0u);
-      const uint32_t x23 = (wv[2] & 0x0F0F0F0Fu) | ((wv[3] << 4) & 0xF0F0F0F0u);
-      const uint32_t y23 = ((wv[2] >> 4) & 0x0F0F0F0Fu) | (wv[3] & 0xF0F0F0F0u);
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        // D = 128: n-tile nb is nibble nb of dword col (coordinate 8*col + nb).
-        // D = 64: n-tile nb is coordinate 8*(col & 7) + 2*nb + (col >> 3).
-        const int par = D == 128 ? (nb & 1) : vpar;
-        const int byte = D == 128 ? (nb >> 1) : nb;
-        t[nb][0] = lut_v[((par ? y01 : x01) >> (8 * byte)) & 0xFF];
-        t[nb][1] = lut_v[((par ? y23 : x23) >> (8 * byte)) & 0xFF];
-      }
-    };
-    float4_t sacc[NSUB];
-    uint2 kt[2][KK][2];
-    k_tables(0, kt[0]);
-#pragma unroll
-    for (int st = 0; st < NSUB; ++st) {
-      if (st + 1 < NSUB) k_tables(st + 1, kt[(st + 1) & 1]);
       sacc[st] = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) sacc[st] = mfma16(pack8(kt[st & 1][kk][0], kt[st & 1][kk][1]), qb[kk], sacc[st]);
+      for (int kk = 0; kk < KK; ++kk) sacc[st] = mfma16(pack8(kt[kk][0], kt[kk][1]), qb[kk], sacc[st]);
     }
-    uint2 vt[2][NB][2];
-    v_tables(0, vt[0]);
-
-    // ---------------- softmax over the chunk ----------------
+  };
+  // Softmax update and value product of the chunk in buffer `buf` whose
+  // scores are `sacc`; tokens >= ntok of the chunk are masked.
+  auto finish = [&](int buf, const float4_t (&sacc)[NSUB], int ntok, bool partial) {
+    const uint8_t *vtile = tiles[wave][buf][1];
+    const uint16_t *rk_lds = rad[wave][buf][0], *rv_lds = rad[wave][buf][1];
     // s = D[t][h] + 2^-11 D[t][h + 8] for token 16st + 4grp + i, meaningful
     // in lanes col < G. Lanes of absent heads (q = 0) and the cross lanes
     // (col >= 8) carry finite values that only reach discarded output rows.
@@ -322,7 +297,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
         sv[st][i] = __builtin_fmaf(cross, 1.0f / kLoScale, sacc[st][i]) * rk;
       }
     }
-    if (ntok < kChunk) {  // wave-uniform: only the last chunk of a split
+    if (partial) {
 #pragma unroll
       for (int st = 0; st < NSUB; ++st)
 #pragma unroll
@@ -340,11 +315,11 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     const float mnew = fmaxf(m_run, cmax);
     const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
     m_run = mnew;
-
     // rescale the running output: lane (col, grp) holds rows 4grp + i, i.e.
     // head 4(grp & 1) + i (hi part for grp < 2, cross part for grp >= 2);
-    // alpha of head hh sits in lane hh.
-    {
+    // alpha of head hh sits in lane hh. Skipped (wave-uniform) when no head's
+    // maximum moved, the common case once the first chunks are in.
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) & 0xFFull) {
       float al[8];
 #pragma unroll
       for (int hh = 0; hh < 8; ++hh)
@@ -356,12 +331,33 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
         for (int nb = 0; nb < NB; ++nb) oacc[nb][i] *= f;
       }
     }
-
-    // ---------------- values, one 16-token k-block per tile ----------------
+    // values, one 16-token k-block per MFMA step
     float psum = 0.0f;
 #pragma unroll
     for (int kb = 0; kb < NSUB; ++kb) {
-      if (kb + 1 < NSUB) v_tables(kb + 1, vt[(kb + 1) & 1]);
+      // value-side entries: two tokens' nibbles of the lane's coordinate
+      // interleaved into one byte (token pairs (0,1) and (2,3))
+      uint32_t wv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t *pv = (const uint32_t *)(vtile + (kSub * kb + 4 * grp + e) * VB + vob_al);
+        wv[e] = align_bytes(pv[1], pv[0], vsh);
+      }
+      // byte k of x = even coordinate 2k of both tokens, of y = odd 2k + 1
+      const uint32_t x01 = (wv[0] & 0x0F0F0F0Fu) | ((wv[1] << 4) & 0xF0F0F0F0u);
+      const uint32_t y01 = ((wv[0] >> 4) & 0x0F0F0F0Fu) | (wv[1] & 0xF0F0F0F0u);
+      const uint32_t x23 = (wv[2] & 0x0F0F0F0Fu) | ((wv[3] << 4) & 0xF0F0F0F0u);
+      const uint32_t y23 = ((wv[2] >> 4) & 0x0F0F0F0Fu) | (wv[3] & 0xF0F0F0F0u);
+      uint2 vt[NB][2];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        // D = 128: n-tile nb is nibble nb of dword col (coordinate 8*col + nb).
+        // D = 64: n-tile nb is coordinate 8*(col & 7) + 2*nb + (col >> 3).
+        const int par = D == 128 ? (nb & 1) : vpar;
+        const int byte = D == 128 ? (nb >> 1) : nb;
+        vt[nb][0] = lut_v[((par ? y01 : x01) >> (8 * byte)) & 0xFF];
+        vt[nb][1] = lut_v[((par ? y23 : x23) >> (8 * byte)) & 0xFF];
+      }
       // weights p * r_v in the A layout: col < 8 -> (p_hi, 0), col >= 8 ->
       // (p_lo, p_hi) of head col - 8, taken from lane col - 8.
       const uint2 rv4 = *(const uint2 *)&rv_lds[kSub * kb + 4 * grp];
@@ -379,12 +375,39 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
       }
       const half8_t pav = pack8u(pa[0], pa[1], pa[2], pa[3]);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) oacc[nb] = mfma16(pav, pack8(vt[kb & 1][nb][0], vt[kb & 1][nb][1]), oacc[nb]);
+      for (int nb = 0; nb < NB; ++nb) oacc[nb] = mfma16(pav, pack8(vt[nb][0], vt[nb][1]), oacc[nb]);
     }
     l_run = l_run * alpha + psum;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  // The wave's chunks start at first + i * kStep. Iteration i finishes chunk
+  // i (softmax + values) and computes the scores of chunk i + 1 in the same
+  // straight-line block, so each one's LDS latency hides behind the other's
+  // work; the chunk i + 2 codes are in flight meanwhile. Only the last chunk
+  // can be partial; it is finished after the loop.
+  constexpr int kStep = kMWaves * kChunk;
+  const int first = t_begin + wave * kChunk;
+  const int nch = first < t_end ? (t_end - first + kStep - 1) / kStep : 0;
+  if (nch > 0) {
+    load_chunk<D>(cr_, kres, vres, first, lane);
+    stage(0);
+    if (nch > 1) load_chunk<D>(cr_, kres, vres, first + kStep, lane);
+    float4_t sacc[NSUB];
+    scores(0, sacc);
+    for (int i = 0; i + 1 < nch; ++i) {
+      const int nxt = (i + 1) & 1;
+      stage(nxt);
+      // chunk i + 2 (a repeat of the last chunk past the end: an L2 hit)
+      const int tl = first + min(i + 2, nch - 1) * kStep;
+      load_chunk<D>(cr_, kres, vres, tl, lane);
+      float4_t snext[NSUB];
+      scores(nxt, snext);
+      finish(i & 1, sacc, kChunk, false);
+#pragma unroll
+      for (int st = 0; st < NSUB; ++st) sacc[st] = snext[st];
+    }
+    const int tlast = first + (nch - 1) * kStep;
+    finish((nch - 1) & 1, sacc, min(kChunk, t_end - tlast), true);
   }
 
   // ---------------- per-wave results ----------------
