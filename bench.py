@@ -146,6 +146,9 @@ def calibrate(torch, dev):
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--workload", choices=("config3", "config4", "config5"), default="config3",
+                    help="config3 (default): the metric line; config4 / config5: the low-bit + QJL decode and "
+                         "the chunked-prefill configurations, for their own measurement lines")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
@@ -159,6 +162,14 @@ def main() -> int:
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
 
+    if args.workload == "config4":
+        return run_config4(args)
+    if args.workload == "config5":
+        return run_config5(args)
+    return run_config3(args)
+
+
+def run_config3(args) -> int:
     import torch
 
     from polarquant_kv import _lib, attention, quantizer
@@ -265,6 +276,153 @@ def main() -> int:
                        "frac": round(enc_bytes / (enc_kernel_ms / max(enc_launches, 1) * 2 / 1e3) / 1e9
                                      / HBM_PEAK_GBS, 4)}},
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+def _timed(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        out = fn()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps, out
+
+
+def _kernel_means(torch, _lib, fn, steps, names):
+    """Kernel time per step (all launches of a kernel in one step summed),
+    from the library's hipEvents on the launch stream."""
+    _lib.profile_enable(True)
+    _lib.profile_collect("")
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    res = {}
+    for n in names:
+        ms, _ = _lib.profile_collect(n)
+        res[n] = ms / steps
+    _lib.profile_enable(False)
+    return res
+
+
+def run_config4(args) -> int:
+    """Low-bit decode: B=4, 32 q / 8 kv heads, d=128, S=16384, keys with the
+    QJL sign sketch (m = d, P seed 43); (i) 2-bit K and V, (ii) kv heads 0-3
+    at 4 bits and 4-7 at 2 bits. value = variant (i)'s algorithmic GB/s."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+    from polarquant_kv import _lib, attention, quantizer
+
+    dev = "cuda:0"
+    B, Hq, Hkv, S, d = 4, 32, 8, 16384, 128
+    R64 = O.rotation_matrix(d, 42)
+    R = torch.from_numpy(R64.astype("float32")).to(dev)
+    P_rot = torch.from_numpy((O.jl_matrix(d, d, 43) @ R64.T).astype("float32")).to(dev)
+    K = synth_channel_kv(torch, B, Hkv, S, d, 4321, dev)
+    V = synth_channel_kv(torch, B, Hkv, S, d, 8765, dev)
+    q = torch.randn(B, Hq, d, device=dev, dtype=torch.float16)
+    variants = {"2bit": 2, "mixed": (4, 4, 4, 4, 2, 2, 2, 2)}
+    res = {}
+    for name, bits in variants.items():
+        kc = quantizer.allocate_cache(B, Hkv, S, d, bits, dev, jl_dim=d)
+        vc = quantizer.allocate_cache(B, Hkv, S, d, bits, dev)
+        quantizer.compress_pq(K, R, cache=kc, jl_rot=P_rot)
+        quantizer.compress_pq(V, R, cache=vc)
+        ws = torch.empty(_lib.lib().pqkv_decode_workspace_bytes(B, Hq, Hkv, S, d), dtype=torch.uint8, device=dev)
+
+        def step():
+            return attention.decode_attention(q, kc, vc, R, jl_rot=P_rot, workspace=ws)
+
+        _lib.profile_enable(False)
+        step_ms, out = _timed(torch, step, args.steps, args.warmup)
+        assert torch.isfinite(out.float()).all()
+        km = _kernel_means(torch, _lib, step, args.steps, ("decode_split", "decode_merge", "decode_rotate"))
+        cache_bytes = kc.blocks.numel() + vc.blocks.numel() + kc.qjl_signs.numel()
+        step_bytes = cache_bytes + B * Hq * d * 2 * 2
+        kern_bytes = cache_bytes + B * Hq * d * 4 + d * d * 4
+        res[name] = {"ms_per_step": round(step_ms, 5), "GB_per_s": round(step_bytes / (step_ms / 1e3) / 1e9, 2),
+                     "bytes_per_step": step_bytes, "split_ms": round(km["decode_split"], 5),
+                     "split_GB_per_s": round(kern_bytes / (km["decode_split"] / 1e3) / 1e9, 2),
+                     "merge_ms": round(km["decode_merge"], 5), "rotate_ms": round(km["decode_rotate"], 5)}
+        del kc, vc
+    v = res["2bit"]
+    line = {
+        "metric": "decode-attn GB/s at 1 MI355X (low-bit + QJL)", "value": v["GB_per_s"], "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": v["ms_per_step"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u2/u4 codes + 1-bit QJL signs; f32 FMA", "data": "synthetic",
+        "config": {"workload": "config4: Llama-3-8B layer decode, B=4 Hq=32 Hkv=8 d=128 S=16384, QJL keys m=128 "
+                               "(P seed 43); variants 2bit (block_pq2 K+V) and mixed (kv heads 0-3 PQ4, 4-7 PQ2)",
+                   "global_batch": B, "seq_len": S, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": v["split_GB_per_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(v["split_GB_per_s"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "decode_split_kernel<128,4,2,2,qjl>", "kernel_ms": v["split_ms"]},
+        "variants": res, "cpu_baseline": None,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+def run_config5(args) -> int:
+    """Chunked prefill: B=1, 64 q / 8 kv heads, d=128, 131072 cached PQ4
+    tokens + a 2048-token fp16 chunk, causal. A step encodes the chunk's K
+    and V into the cache and runs prefill attention for the chunk. value =
+    algorithmic TFLOP/s of the attention (64 (2048 131072 + 2048 2049 / 2) 4 128)."""
+    import torch
+
+    from oracle import oracle as O
+    from polarquant_kv import _lib, attention, quantizer
+
+    dev = "cuda:0"
+    B, Hq, Hkv, d = 1, 64, 8, 128
+    S_cache, Sq = 131072, 2048
+    S = S_cache + Sq
+    R = torch.from_numpy(O.rotation_matrix(d, 42).astype("float32")).to(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    kc = quantizer.allocate_cache(B, Hkv, S, d, 4, dev)
+    vc = quantizer.allocate_cache(B, Hkv, S, d, 4, dev)
+    quantizer.compress_pq(torch.randn(B, Hkv, S_cache, d, generator=g, device=dev).half(), R, cache=kc)
+    quantizer.compress_pq(torch.randn(B, Hkv, S_cache, d, generator=g, device=dev).half(), R, cache=vc)
+    k_new = torch.randn(B, Hkv, Sq, d, generator=g, device=dev).half()
+    v_new = torch.randn(B, Hkv, Sq, d, generator=g, device=dev).half()
+    q = torch.randn(B, Hq, Sq, d, generator=g, device=dev).half()
+
+    def step():
+        quantizer.compress_pq(k_new, R, cache=kc, start=S_cache)
+        quantizer.compress_pq(v_new, R, cache=vc, start=S_cache)
+        return attention.prefill_attention(q, kc, vc, R, q_start=S_cache, causal=True)
+
+    steps = max(1, min(args.steps, 20))
+    _lib.profile_enable(False)
+    step_ms, out = _timed(torch, step, steps, max(1, min(args.warmup, 3)))
+    assert torch.isfinite(out.float()).all()
+    km = _kernel_means(torch, _lib, step, steps, ("prefill_attn", "prefill_rotate", "prefill_out_rotate", "encode"))
+    flops = 64 * (Sq * S_cache + Sq * (Sq + 1) / 2) * 4 * d
+    tflops = flops / (step_ms / 1e3) / 1e12
+    kern_tflops = flops / (km["prefill_attn"] / 1e3) / 1e12
+    line = {
+        "metric": "chunked-prefill attention TFLOP/s at 1 MI355X", "value": round(tflops, 2), "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": steps, "warmup": max(1, min(args.warmup, 3)), "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u4 codes; f16 hi/lo MFMA (3 products), f32 accumulate", "data": "synthetic",
+        "config": {"workload": "config5: 70B-shaped layer prefill, B=1 Hq=64 Hkv=8 d=128, 131072 cached PQ4 "
+                               "tokens + 2048-token fp16 chunk (encoded into the cache each step), causal; "
+                               "K/V/Q N(0,1)",
+                   "global_batch": B, "seq_len": S, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(kern_tflops / 2500.0, 4), "traffic": None, "kernel": "prefill_mfma_kernel<128>",
+                     "kernel_ms": round(km["prefill_attn"], 4), "flops_per_launch": flops,
+                     "note": "fp32-grade products cost 3 fp16 MFMAs each: this arithmetic tops out at 1/3"},
+        "stages_ms": {k: round(v, 4) for k, v in km.items()},
+        "cpu_baseline": None,
     }
     print(json.dumps(line))
     return 0
