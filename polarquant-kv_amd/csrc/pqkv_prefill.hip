@@ -11,8 +11,9 @@
 // 64-token tiles. Each tile is decoded once per workgroup into LDS, as fp16
 // planes in the exact order the MFMA operands want, so that every operand
 // read is a conflict-free run of 8-byte loads. Tiles are double-buffered:
-// the codes of tile i+1 are fetched from HBM before tile i's matrix work and
-// decoded after it.
+// the codes of tile i+1 are fetched from HBM an iteration ahead and decoded
+// by half the waves before, and by the other half after, tile i's matrix
+// work.
 //
 // Scores are computed transposed, S^T[token][row] = K^ . Q^T: K^ (16 tokens x
 // 32 coordinates) is the A operand and the rotated queries the B operand, so
@@ -263,18 +264,31 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
   const int ntiles = (kv_end + kPT - 1) / kPT;
   TileCodes<D> codes;
   __syncthreads();  // tables ready
+  // The two waves sharing a SIMD (w and w + 4) run each iteration in
+  // opposite phase order: waves 4..7 decode the next tile before their matrix
+  // work, waves 0..3 after it, so one wave's MFMAs overlap the other's table
+  // decode and softmax instead of both waves contending for the same unit.
+  // The codes of tile it + 1 are fetched one iteration ahead.
+  const bool decode_first = wave >= kPW / 2;
   if (ntiles > 0) {
     fetch_tile<D>(codes, kres, vres, 0, tid);
     decode_tile<D>(codes, tiles[0], rads[0], lut_k, lut_v, tid);
+    if (ntiles > 1) fetch_tile<D>(codes, kres, vres, kPT, tid);
   }
   for (int it = 0; it < ntiles; ++it) {
     const int t0 = it * kPT;
     __syncthreads();  // tile it decoded; the other buffer is free
-    if (it + 1 < ntiles) fetch_tile<D>(codes, kres, vres, t0 + kPT, tid);
+    if (decode_first && it + 1 < ntiles) {
+      decode_tile<D>(codes, tiles[(it + 1) & 1], rads[(it + 1) & 1], lut_k, lut_v, tid);
+      if (it + 2 < ntiles) fetch_tile<D>(codes, kres, vres, t0 + 2 * kPT, tid);
+    }
     const uint8_t *tile = tiles[it & 1];
     const float *rk = rads[it & 1], *rv = rads[it & 1] + kPT;
 
     // ---------------- scores S^T[token][row] ----------------
+    // Matrix bursts run at raised wave priority, so the SIMD arbiter keeps
+    // them back to back while the other wave's VALU work fills the gaps.
+    __builtin_amdgcn_s_setprio(1);
     float4_t sacc[2][4];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
@@ -296,6 +310,7 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
         }
       }
 
+    __builtin_amdgcn_s_setprio(0);
     // ---------------- online softmax, per row (lane col) ----------------
     const bool need_mask = t0 + kPT > a.S || (a.causal && t0 + kPT - 1 > a.q_start + q0);
     half8_t ph[2][2], pl[2][2];
@@ -355,6 +370,7 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
     }
 
     // ---------------- values O[row][coord] += P . V^ ----------------
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -371,7 +387,11 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
         }
       }
 
-    if (it + 1 < ntiles) decode_tile<D>(codes, tiles[(it + 1) & 1], rads[(it + 1) & 1], lut_k, lut_v, tid);
+    __builtin_amdgcn_s_setprio(0);
+    if (!decode_first && it + 1 < ntiles) {
+      decode_tile<D>(codes, tiles[(it + 1) & 1], rads[(it + 1) & 1], lut_k, lut_v, tid);
+      if (it + 2 < ntiles) fetch_tile<D>(codes, kres, vres, t0 + 2 * kPT, tid);
+    }
   }
 
   // ---------------- normalise and write o_rot ----------------
