@@ -259,6 +259,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   // Scores of the chunk in buffer `buf`: S^T[token][col] per 16-token tile.
   auto scores = [&](int buf, float4_t (&sacc)[NSUB]) {
     const uint8_t *ktile = tiles[wave][buf][0];
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int st = 0; st < NSUB; ++st) {
       const uint8_t *kv = ktile + (kSub * st + col) * VB;
@@ -276,6 +277,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) sacc[st] = mfma16(pack8(kt[kk][0], kt[kk][1]), qb[kk], sacc[st]);
     }
+    __builtin_amdgcn_s_setprio(0);
   };
   // Softmax update and value product of the chunk in buffer `buf` whose
   // scores are `sacc`; tokens >= ntok of the chunk are masked.
