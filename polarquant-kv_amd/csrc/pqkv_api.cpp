@@ -6,6 +6,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -52,11 +53,11 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // weight table). More target never means fewer splits, so the workspace is
 // sized with the largest target any launch uses (kPlanMaxTarget).
 constexpr int kPlanMaxTarget = 2048;
-constexpr int kValuTarget = 1024;
-void decode_plan(int B, int Hkv, int S, int target, int *splits, int *tps) {
-  const int64_t streams = (int64_t)B * Hkv;
+constexpr int kValuTarget = 512;
+void decode_plan(int64_t streams, int S, int target, int *splits, int *tps) {
   if (target > kPlanMaxTarget) target = kPlanMaxTarget;
   int64_t want = (target + streams - 1) / streams;
+  if (want > pqkv::kMaxSplits) want = pqkv::kMaxSplits;
   int64_t t = (S + want - 1) / want;
   if (t < 256) t = 256;
   t = (t + 63) / 64 * 64;
@@ -352,8 +353,12 @@ int pqkv_encode_mfma(const void *x, int x_dtype, int64_t x_outer_stride, const f
 size_t pqkv_decode_workspace_bytes(int B, int Hq, int Hkv, int S, int d) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S < 0 || d <= 0) return 0;
   int splits = 1, tps = 0;
-  decode_plan(B, Hkv, S > 0 ? S : 1, kPlanMaxTarget, &splits, &tps);
-  return align256((size_t)B * Hq * d * 4) + align256((size_t)B * Hq * splits * (d + 2) * 4);
+  // bound over every plan a call can make: fewest streams per launch (B),
+  // largest target
+  decode_plan(B, S > 0 ? S : 1, kPlanMaxTarget, &splits, &tps);
+  // rotated queries, split partials, and the QJL projections P_rot q_rot / m
+  return align256((size_t)B * Hq * d * 4) + align256((size_t)B * Hq * splits * (d + 2) * 4) +
+         align256((size_t)B * Hq * d * 4);
 }
 
 int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *k_cache, const uint8_t *v_cache,
@@ -394,14 +399,27 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
     const size_t ob = (size_t)B * Hq * d * (out_dtype == PQKV_F32 ? 4 : 2);
     return hip_status(pqkv::launch_fill_zero(out, ob, st), "decode zero fill");
   }
+  // One split plan serves every launch (they share the partials layout); it
+  // is sized for the largest launch: all kv heads, or with mixed widths the
+  // largest group of heads sharing (k bits, v bits).
+  int group = Hkv;
+  if (mixed) {
+    int count[2][2] = {{0, 0}, {0, 0}};
+    for (int h = 0; h < Hkv; ++h) ++count[kb[h] == 4][vb[h] == 4];
+    group = std::max(std::max(count[0][0], count[0][1]), std::max(count[1][0], count[1][1]));
+  }
   int splits = 1, tps = 0;
   const bool all_mfma = !mixed && use_mfma(k_bits, v_bits, qjl_signs != nullptr);
-  decode_plan(B, Hkv, S, all_mfma ? mfma_target() : kValuTarget, &splits, &tps);
+  decode_plan((int64_t)B * group, S, all_mfma ? mfma_target() : kValuTarget, &splits, &tps);
   float *q32 = (float *)workspace;
   float *part = (float *)((char *)workspace + align256((size_t)B * Hq * d * 4));
+  float *pq32 = (float *)((char *)part + align256((size_t)B * Hq * splits * (d + 2) * 4));
   const float kLog2e = 1.4426950408889634f;
   int tok = pqkv::prof_begin("decode_rotate", st);
   hipError_t e = pqkv::launch_rotate(q, q_dtype, R, q32, PQKV_F32, (int64_t)B * Hq, d, 0, scale * kLog2e, st);
+  // QJL: P_rot q_rot / m once per query head (m == d), for every split
+  if (e == hipSuccess && qjl_signs) e = pqkv::launch_rotate(q32, PQKV_F32, p_rot, pq32, PQKV_F32, (int64_t)B * Hq, d, 0,
+                                                            1.0f / (float)m, st);
   pqkv::prof_end(tok, st);
   if (e != hipSuccess) return hip_status(e, "decode query rotation");
 
@@ -415,6 +433,7 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
   a.cb_head_stride = mixed ? 16 : 0;
   a.qjl = qjl_signs;
   a.p_rot = p_rot;
+  a.pq = qjl_signs ? pq32 : nullptr;
   a.part = part;
   a.B = B;
   a.Hq = Hq;

@@ -83,6 +83,10 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t tiles[kWaves * TILE_DW + 4];
   __shared__ __attribute__((aligned(16))) float pr_lds[kWaves][kTile][GP];
   __shared__ float pq_lds[QJL ? G : 1][QJL ? M : 1];
+  // QJL partial sums per 4-bit slice of the sign vector: qt[p][v][h] =
+  // sum_j (bit j of v ? +1 : -1) pq[h][4p + j], so a key's correction is
+  // M/4 table reads instead of M sign multiplies per head.
+  __shared__ __attribute__((aligned(16))) float qt[QJL ? M / 4 : 1][16][GP];
   __shared__ float red_m[kWaves][G], red_l[kWaves][G];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -111,13 +115,21 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
   }
   __syncthreads();
   if (QJL) {
-    // pq[h][i] = (p_rot[i] . q_h) / m, q already carries scale * log2(e).
+    // pq[h][i] = (p_rot[i] . q_h) / m (q already carries scale * log2(e)),
+    // computed once per call for every query head
     for (int i = tid; i < G * M; i += 256) {
       const int hh = i / M, r = i - hh * M;
+      pq_lds[hh][r] = a.pq[(int64_t)(b * a.Hq + h * G + hh) * M + r];
+    }
+    __syncthreads();
+    for (int i = tid; i < (M / 4) * 16 * GP; i += 256) {
+      const int hh = i % GP, v = (i / GP) & 15, pp = i / (16 * GP);
       float acc = 0.0f;
-      const float *pr = a.p_rot + (int64_t)r * D;
-      for (int k = 0; k < D; ++k) acc = __builtin_fmaf(pr[k], q_lds[hh][k], acc);
-      pq_lds[hh][r] = acc * (1.0f / M);
+      if (hh < G) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc += ((v >> j) & 1) ? pq_lds[hh][4 * pp + j] : -pq_lds[hh][4 * pp + j];
+      }
+      qt[pp][v][hh] = acc;
     }
     __syncthreads();
   }
@@ -144,6 +156,17 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
     const int t0 = t_begin + tile * kTile;
     if (t0 >= t_end) break;
     const int ntok = min(kTile, t_end - t0);
+    // this lane's key signs (QJL), requested before the tile so the load
+    // overlaps the score work; lanes past the tile read zeros
+    uint32_t sg[QJL ? M / 32 : 1];
+    if (QJL) {
+      const uint8_t *sb = a.qjl + ((int64_t)(b * a.Hkv + h) * a.S_max + t0) * (M / 8);
+      const __amdgpu_buffer_rsrc_t sr =
+          __builtin_amdgcn_make_buffer_rsrc((void *)sb, (short)0, ntok * (M / 8), 0x00020000);
+#pragma unroll
+      for (int wd = 0; wd < M / 32; ++wd)
+        sg[wd] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(sr, lane * (M / 8) + 4 * wd, 0, 0));
+    }
     load_tile(ktile, kstream + (int64_t)t0 * VBK, ntok * VBK, kal, lane);
     load_tile(vtile, vstream + (int64_t)t0 * VBV, ntok * VBV, val, lane);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -195,16 +218,20 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
     if (QJL) {
       // + (1/m) sum_i (2 sign_i - 1) (P q)_i, skipped for zero keys.
       if (valid && rk > 0.0f) {
-        const uint32_t *sg =
-            (const uint32_t *)(a.qjl + (((int64_t)(b * a.Hkv + h) * a.S_max) + t0 + lane) * (M / 8));
 #pragma unroll
         for (int wd = 0; wd < M / 32; ++wd) {
           const uint32_t bits = sg[wd];
 #pragma unroll
-          for (int i = 0; i < 32; ++i) {
-            const float sgn = ((bits >> i) & 1u) ? 1.0f : -1.0f;
+          for (int nb = 0; nb < 8; ++nb) {
+            const float *e = qt[8 * wd + nb][(bits >> (4 * nb)) & 15];
 #pragma unroll
-            for (int hh = 0; hh < G; ++hh) s[hh] = __builtin_fmaf(sgn, pq_lds[hh][32 * wd + i], s[hh]);
+            for (int h4 = 0; h4 < GP; h4 += 4) {
+              const float4 v4 = *(const float4 *)(e + h4);
+              const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+              for (int u = 0; u < 4; ++u)
+                if (h4 + u < G) s[h4 + u] += vv[u];
+            }
           }
         }
       }

@@ -43,6 +43,7 @@ struct DecodeArgs {
   int cb_head_stride;            // 0: one table; 16: per-head tables
   const uint8_t *qjl;            // [B][Hkv][S_max][m/8] or null
   const float *p_rot;            // [m][d] (QJL only)
+  const float *pq;               // [B][Hq][m] = P_rot q / m (QJL only)
   float *part;                   // [B][Hq][splits][d + 2]
   int B, Hq, Hkv, S, S_max, d;
   int splits, tokens_per_split;
