@@ -66,22 +66,26 @@ void decode_plan(int64_t streams, int S, int target, int *splits, int *tps) {
   if (*splits < 1) *splits = 1;
 }
 
-// Workgroups resident at once for the matrix-core decode kernel: compute
-// units x workgroups per CU (the kernel's launch bounds and LDS use allow
-// pqkv::kMfmaBlocksPerCU), so one launch is one balanced round.
-int mfma_target() {
+// Compute units of the current device (cached per device; 256 if the query
+// fails).
+int device_cus() {
   static std::mutex mu;
   static int cus[64] = {0};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kValuTarget;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
   std::lock_guard<std::mutex> lk(mu);
   if (cus[dev] == 0) {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
     cus[dev] = n;
   }
-  return cus[dev] * pqkv::kMfmaBlocksPerCU;
+  return cus[dev];
 }
+
+// Workgroups resident at once for the matrix-core decode kernel: compute
+// units x workgroups per CU (the kernel's launch bounds and LDS use allow
+// pqkv::kMfmaBlocksPerCU), so one launch is one balanced round.
+int mfma_target() { return device_cus() * pqkv::kMfmaBlocksPerCU; }
 
 struct ProfRecord {
   std::string name;
@@ -299,11 +303,28 @@ int encode_validate(const void *x, int x_dtype, int64_t x_outer_stride, const fl
 
 // The matrix-core encoder takes fp16 input without QJL whose rows and R allow
 // 16-byte loads.
-bool fast_encode_ok(const void *x, int x_dtype, int64_t x_outer_stride, int64_t n_outer, const float *R,
-                    const uint8_t *qjl) {
+bool fast_encode_ok(const void *x, int x_dtype, int64_t x_outer_stride, int64_t n_outer, int64_t n_inner,
+                    const float *R, const uint8_t *qjl) {
   if (x_dtype != PQKV_F16 || qjl != nullptr) return false;
   if ((uintptr_t)x % 16 || (uintptr_t)R % 16) return false;
+  if (n_outer * n_inner > ((int64_t)1 << 32) - 64) return false;  // 32-bit vector indices
   return n_outer <= 1 || x_outer_stride % 8 == 0;
+}
+
+// Rows that follow each other with no gap in x, the blocks and the signs are
+// one run of vectors: a single row lets the kernels skip the row split.
+pqkv::EncodeArgs encode_args(const void *x, int64_t x_outer_stride, const float *R, const float *codebook,
+                             int n_bits, uint8_t *blocks, int64_t blocks_outer_stride, int64_t n_outer,
+                             int64_t n_inner, int d, const float *p_rot, int m, uint8_t *qjl,
+                             int64_t qjl_outer_stride) {
+  const int64_t vb = pqkv_vector_bytes(d, n_bits);
+  if (n_outer > 1 && x_outer_stride == n_inner * d && blocks_outer_stride == n_inner * vb &&
+      (qjl == nullptr || qjl_outer_stride == n_inner * (m / 8))) {
+    n_inner *= n_outer;
+    n_outer = 1;
+  }
+  return pqkv::EncodeArgs{x, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride, n_outer, n_inner,
+                          d, p_rot, m, qjl, qjl_outer_stride};
 }
 
 }  // namespace
@@ -317,14 +338,14 @@ int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride, const float 
   const int v = encode_validate(x, x_dtype, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride, n_outer,
                                 n_inner, d, p_rot, m, qjl, qjl_outer_stride);
   if (v <= 0) return v;
-  pqkv::EncodeArgs a{x, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride, n_outer, n_inner,
-                     d, p_rot, m, qjl, qjl_outer_stride};
+  const pqkv::EncodeArgs a = encode_args(x, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride,
+                                         n_outer, n_inner, d, p_rot, m, qjl, qjl_outer_stride);
   const char *env = getenv("PQKV_ENCODE_KERNEL");
   const bool exact = env && strcmp(env, "exact") == 0;
   hipError_t e;
-  if (!exact && fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, R, qjl)) {
+  if (!exact && fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, n_inner, R, qjl)) {
     const int tok = pqkv::prof_begin("encode_mfma", (hipStream_t)stream);
-    e = pqkv::launch_encode_mfma(a, nullptr, (hipStream_t)stream);
+    e = pqkv::launch_encode_mfma(a, nullptr, device_cus(), (hipStream_t)stream);
     pqkv::prof_end(tok, (hipStream_t)stream);
   } else {
     const int tok = pqkv::prof_begin("encode_exact", (hipStream_t)stream);
@@ -340,12 +361,12 @@ int pqkv_encode_mfma(const void *x, int x_dtype, int64_t x_outer_stride, const f
   const int v = encode_validate(x, x_dtype, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride, n_outer,
                                 n_inner, d, nullptr, 0, nullptr, 0);
   if (v <= 0) return v;
-  if (!fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, R, nullptr))
-    return fail(PQKV_ERR_UNSUPPORTED, "encode_mfma: needs fp16 x, 16-byte aligned x rows and R");
-  pqkv::EncodeArgs a{x, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride, n_outer, n_inner,
-                     d, nullptr, 0, nullptr, 0};
+  if (!fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, n_inner, R, nullptr))
+    return fail(PQKV_ERR_UNSUPPORTED, "encode_mfma: needs fp16 x, 16-byte aligned x rows and R, < 2^32 vectors");
+  const pqkv::EncodeArgs a = encode_args(x, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride,
+                                         n_outer, n_inner, d, nullptr, 0, nullptr, 0);
   const int tok = pqkv::prof_begin("encode_mfma", (hipStream_t)stream);
-  const hipError_t e = pqkv::launch_encode_mfma(a, rot_out, (hipStream_t)stream);
+  const hipError_t e = pqkv::launch_encode_mfma(a, rot_out, device_cus(), (hipStream_t)stream);
   pqkv::prof_end(tok, (hipStream_t)stream);
   return hip_status(e, "encode_mfma launch");
 }

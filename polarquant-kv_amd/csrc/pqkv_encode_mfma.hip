@@ -23,8 +23,19 @@
 // switch points by bisection over fp32 values with the scan itself, then
 // builds a table over 1024 direction cells holding (index at the cell start,
 // the switch point inside the cell): one LDS read and one compare per
-// coordinate. A codebook that is not strictly increasing, or with two switch
-// points in one cell, falls back to the scan.
+// coordinate. A codebook that is not strictly increasing, with two switch
+// points in one cell, or with a switch point below 2^-60 in magnitude, falls
+// back to the scan.
+//
+// Direction on the table path: dir = q0 + e * inv with inv = RN(1 / r) (one
+// correctly rounded division per vector), q0 = RN(y * inv) and the residual
+// e = fma(-r, q0, y). By Markstein's theorem this is RN(y / r), the
+// reference's division, whenever e is exact, which holds when
+// exp(r) + exp(q0) - 46 >= -149. The fast form is taken per 16-vector tile
+// when every radius is finite and >= 2^-40 (or zero-like, dir = 0): then every
+// direction within a factor of two of a switch point (>= 2^-60) is exact, and a
+// direction off by an ulp elsewhere crosses no switch point, so the index is
+// the reference's. Tiles with other radii divide per coordinate.
 #include "pqkv_device.h"
 #include "pqkv_launch.h"
 
@@ -33,7 +44,8 @@ namespace pqkv {
 namespace {
 
 constexpr int kEW = 4;              // waves per workgroup
-constexpr int kECells = 1024;       // direction cells over [-1, 1]
+constexpr int kECells = 1024;       // direction cells over [-1, 1], 1/512 wide
+constexpr int kECellSlots = kECells + 3;  // cell u covers [u - 513, u - 512) / 512
 constexpr int kESeg = 64 * 8;       // one operand segment: 64 lanes x 8 bytes
 constexpr int kEVec = 64;           // vectors per wave iteration (4 tiles of 16)
 
@@ -86,13 +98,56 @@ __device__ __forceinline__ int scan_index(float d, const float *cb, int nl) {
   return b;
 }
 
-// Direction cell, monotone in d (the table is built with the same function).
-__device__ __forceinline__ int dir_cell(float d) {
+// The same scan as a rolled loop over the LDS codebook: the fallback path's
+// form, which keeps the codebook out of registers.
+__device__ __forceinline__ int scan_index_rolled(float d, const float *cb, int nl) {
 #pragma clang fp contract(off)
-  const float t = (d + 1.0f) * (float)(kECells / 2);
-  const int u = (int)t;
-  return min(max(u, 0), kECells);
+  int b = 0;
+  float m = 1e30f;
+#pragma nounroll
+  for (int i = 0; i < nl; ++i) {
+    const float e = fabsf(d - cb[i]);
+    if (e < m) {
+      m = e;
+      b = i;
+    }
+  }
+  return b;
 }
+
+// Direction cell, monotone in d (the table is built with the same function;
+// a rounded fma of a monotone exact function is monotone). For |d| <= 1 + 2^-9
+// the clamp never acts: dir_cell_unclamped is the same function there.
+__device__ __forceinline__ int dir_cell_unclamped(float d) {
+  return (int)__builtin_fmaf(d, (float)(kECells / 2), (float)(kECells / 2 + 1));
+}
+__device__ __forceinline__ int dir_cell(float d) {
+  return min(max(dir_cell_unclamped(d), 0), kECellSlots - 1);
+}
+
+// Unsigned division by a divisor fixed per launch (Granlund and Montgomery,
+// "Division by invariant integers using multiplication", 1994, round-up
+// multiplier with the add-back step): exact for every 32-bit numerator.
+struct FastDiv {
+  uint32_t d, m;
+  int s1, s2;
+  __device__ explicit FastDiv(uint32_t div) : d(div) {
+    int l = 0;
+    while (l < 32 && (1ull << l) < div) ++l;
+    m = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << l) - div)) / div + 1);
+    s1 = l < 1 ? l : 1;
+    s2 = l > 1 ? l - 1 : 0;
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    const uint32_t t = __umulhi(m, n);
+    return (t + ((n - t) >> s1)) >> s2;
+  }
+};
+
+template <bool B>
+struct TableFlag {
+  static constexpr bool on = B;
+};
 
 // Order-preserving map between fp32 values and integers.
 __device__ __forceinline__ int64_t fkey(float f) {
@@ -113,7 +168,7 @@ __global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeAr
   constexpr int VB = vector_bytes(D, BITS);
   constexpr int SEGS = MT * KS * 2 * 2; // (mt, ks, plane, half)
   __shared__ __attribute__((aligned(16))) uint8_t rl[SEGS * kESeg];
-  __shared__ uint2 cells[kECells + 1];  // (index at the cell start, switch point bits or +inf)
+  __shared__ uint2 cells[kECellSlots];  // (index at the cell start, switch point bits or +inf)
   __shared__ float cb[16], thr[16];
   __shared__ int ucell[16];
   __shared__ int table_ok;
@@ -142,25 +197,44 @@ __global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeAr
   if (tid < 16) cb[tid] = tid < NL ? a.codebook[tid] : 0.0f;
   if (tid == 0) table_ok = 1;
   __syncthreads();
-  // ---- switch points: lane i of wave 0 bisects between c_i and c_{i+1} ----
-  if (tid < NL - 1) {
-    const int i = tid;
-    if (!(cb[i] < cb[i + 1])) {
-      table_ok = 0;
-    } else {
-      int64_t lo = fkey(cb[i]), hi = fkey(cb[i + 1]);
-      if (scan_index(cb[i], cb, NL) > i || scan_index(cb[i + 1], cb, NL) < i + 1) table_ok = 0;
-      while (hi - lo > 1) {
-        const int64_t mid = lo + (hi - lo) / 2;
-        if (scan_index(kfloat(mid), cb, NL) >= i + 1) hi = mid;
-        else lo = mid;
+  // ---- switch points: 16 lanes per point i search (c_i, c_{i+1}] 16-ary:
+  // lane j tests the (j + 1)/16 point of the range, the first that the scan
+  // maps to i + 1 or more closes it. Keys of fp32 values differ by < 2^33,
+  // so 9 steps reach a range of one. ----
+  {
+    const int i = tid >> 4, j = tid & 15;
+    const bool act = i < NL - 1;
+    bool ok = act;
+    int64_t lo = 0, hi = 0;
+    if (act) {
+      ok = cb[i] < cb[i + 1] && scan_index(cb[i], cb, NL) <= i && scan_index(cb[i + 1], cb, NL) >= i + 1;
+      lo = fkey(cb[i]);
+      hi = fkey(cb[i + 1]);
+    }
+    for (int step = 0; step < 10; ++step) {
+      const int64_t span = hi - lo;
+      const int64_t cand = j == 15 ? hi : lo + ((span * (j + 1)) >> 4);
+      const bool p = ok && span > 1 && scan_index(kfloat(cand), cb, NL) >= i + 1;
+      const uint32_t gm = (uint32_t)(__builtin_amdgcn_ballot_w64(p) >> (16 * (i & 3))) & 0xFFFFu;
+      const int k = gm ? __builtin_ctz(gm) : 15;
+      if (ok && span > 1) {
+        const int64_t nhi = k == 15 ? hi : lo + ((span * (k + 1)) >> 4);
+        lo = k == 0 ? lo : lo + ((span * k) >> 4);
+        hi = nhi;
       }
-      thr[i] = kfloat(hi);
-      ucell[i] = dir_cell(kfloat(hi));
+    }
+    if (act && j == 0) {
+      if (!ok || hi - lo != 1) {
+        table_ok = 0;
+      } else {
+        thr[i] = kfloat(hi);
+        ucell[i] = dir_cell(kfloat(hi));
+        if (!(fabsf(thr[i]) >= 0x1p-60f)) table_ok = 0;
+      }
     }
   }
   __syncthreads();
-  for (int u = tid; u <= kECells; u += kEW * 64) {
+  for (int u = tid; u < kECellSlots; u += kEW * 64) {
     int base = 0, inside = -1, count = 0;
     for (int i = 0; i < NL - 1; ++i) {
       if (ucell[i] < u) ++base;
@@ -173,26 +247,28 @@ __global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeAr
     cells[u] = make_uint2((uint32_t)base, inside >= 0 ? __builtin_bit_cast(uint32_t, thr[inside]) : 0x7F800000u);
   }
   __syncthreads();
-  const bool use_table = table_ok != 0;
 
   const half_t *x = (const half_t *)a.x;
-  const int64_t n = a.n_outer * a.n_inner;
-  const int64_t groups = (n + kEVec - 1) / kEVec;
-  for (int64_t g = (int64_t)blockIdx.x * kEW + wave; g < groups; g += (int64_t)gridDim.x * kEW) {
-    // ---- B operand: lane (col, grp), tile c holds vector 64 g + 16 c + col,
-    // input coordinates 32 ks + 8 grp .. + 7 ----
-    half8_t xb[4][KS];
-    int64_t vout[4];
+  // vector v = n_inner * vo + vi; the host keeps n below 2^32
+  const uint32_t n = (uint32_t)(a.n_outer * a.n_inner);
+  const int64_t groups = ((int64_t)n + kEVec - 1) / kEVec;
+  const FastDiv by_inner((uint32_t)a.n_inner);
+  const bool rows = a.n_outer > 1;
+  auto split = [&](uint32_t v, uint32_t &vo, uint32_t &vi) {
+    vo = rows ? by_inner.div(v) : 0u;
+    vi = v - vo * (uint32_t)a.n_inner;
+  };
+  // The table test is uniform per workgroup: one copy of the loop per path,
+  // so no branch sits between the per-coordinate table reads.
+  // B operand: lane (col, grp), tile c holds vector 64 g + 16 c + col, input
+  // coordinates 32 ks + 8 grp .. + 7 (zeros past the end).
+  auto load_x = [&](int64_t g, half8_t (&xb)[4][KS]) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const int64_t v = g * kEVec + 16 * c + col;
-      int64_t vo = 0, vi = v;
-      if (a.n_outer > 1) {
-        vo = v / a.n_inner;
-        vi = v - vo * a.n_inner;
-      }
-      vout[c] = v < n ? vo * a.blocks_outer_stride + vi * VB : -1;
-      const half_t *xv = x + vo * a.x_outer_stride + vi * D;
+      const uint32_t v = (uint32_t)g * kEVec + 16 * c + col;
+      uint32_t vo, vi;
+      split(v, vo, vi);
+      const half_t *xv = x + (int64_t)vo * a.x_outer_stride + (int64_t)vi * D;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         if (v < n) {
@@ -203,6 +279,14 @@ __global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeAr
         }
       }
     }
+  };
+  const int64_t g_step = (int64_t)gridDim.x * kEW;
+  auto run = [&](auto flag) {
+  constexpr bool kTable = decltype(flag)::on;
+  half8_t xb[4][KS];
+  int64_t g = (int64_t)blockIdx.x * kEW + wave;
+  if (g < groups) load_x(g, xb);
+  for (; g < groups; g += g_step) {
     float4_t acc[4][MT];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
@@ -221,6 +305,8 @@ __global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeAr
           acc[c][mt] = mfma16(al, xb[c][ks], acc[c][mt]);
         }
       }
+    // The next group's input streams in while this one is quantised.
+    if (g + g_step < groups) load_x(g + g_step, xb);
 
     // ---- per vector: radius tree, direction, index, packing ----
 #pragma unroll
@@ -230,9 +316,15 @@ __global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeAr
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) y[mt][i] = acc[c][mt][i];
-      const int64_t vo_bytes = vout[c];
+      int64_t vo_bytes;
+      {
+        const uint32_t v = (uint32_t)g * kEVec + 16 * c + col;
+        uint32_t vo, vi;
+        split(v, vo, vi);
+        vo_bytes = v < n ? (int64_t)vo * a.blocks_outer_stride + (int64_t)vi * VB : -1;
+      }
       if (rot_out != nullptr && vo_bytes >= 0) {
-        const int64_t v = g * kEVec + 16 * c + col;
+        const int64_t v = (int64_t)g * kEVec + 16 * c + col;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -270,18 +362,49 @@ __global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeAr
       }
       const bool nz = r > 1e-30f;
       int code[MT][4];
+      if constexpr (kTable) {
+        // Fast form for the tile when every radius is zero-like (dir = 0,
+        // reached through inv = 0 on finite y) or finite and >= 2^-40
+        // (Markstein quotient exact, |dir| <= 1 + 11 ulp so the cell needs no
+        // clamp). A NaN radius (dir = 0 by the reference, but y * 0 is NaN)
+        // takes the per-coordinate form.
+        const bool fast = r <= 1e-30f || (r >= 0x1p-40f && r < __builtin_inff());
+        if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
+          const float inv = nz ? __fdiv_rn(1.0f, r) : 0.0f;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+          for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float d = nz ? __fdiv_rn(y[mt][i], r) : 0.0f;
-          if (use_table) {
-            const uint2 e = cells[dir_cell(d)];
-            code[mt][i] = (int)e.x + (d >= __builtin_bit_cast(float, e.y) ? 1 : 0);
-          } else {
-            code[mt][i] = scan_index(d, cb, NL);
-          }
+            for (int i = 0; i < 4; ++i) {
+              float d;
+              {
+#pragma clang fp contract(off)
+                const float q0 = y[mt][i] * inv;
+                const float e = __builtin_fmaf(-r, q0, y[mt][i]);
+                d = __builtin_fmaf(e, inv, q0);
+              }
+              const uint2 ce = cells[dir_cell_unclamped(d)];
+              code[mt][i] = (int)ce.x + (d >= __builtin_bit_cast(float, ce.y) ? 1 : 0);
+            }
+        } else {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float d = nz ? __fdiv_rn(y[mt][i], r) : 0.0f;
+              d = d == d ? d : -2.0f;  // NaN: index 0, as the scan gives
+              const uint2 ce = cells[dir_cell(d)];
+              code[mt][i] = (int)ce.x + (d >= __builtin_bit_cast(float, ce.y) ? 1 : 0);
+            }
         }
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float d = nz ? __fdiv_rn(y[mt][i], r) : 0.0f;
+            code[mt][i] = scan_index_rolled(d, cb, NL);
+          }
+      }
       if (vo_bytes >= 0) {
         uint8_t *out = a.blocks + vo_bytes;
         if (BITS == 4) {
@@ -303,13 +426,18 @@ __global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeAr
       }
     }
   }
+  };
+  if (table_ok != 0) run(TableFlag<true>{});
+  else run(TableFlag<false>{});
 }
 
-hipError_t launch_encode_mfma(const EncodeArgs &a, float *rot_out, hipStream_t s) {
+hipError_t launch_encode_mfma(const EncodeArgs &a, float *rot_out, int cus, hipStream_t s) {
   const int64_t n = a.n_outer * a.n_inner;
   const int64_t groups = (n + kEVec - 1) / kEVec;
+  // each workgroup builds its R operand and centroid table once, so one
+  // resident round (the launch bounds give two per CU) loops over the groups
   int64_t grid = (groups + kEW - 1) / kEW;
-  if (grid > 1024) grid = 1024;
+  if (grid > 2 * (int64_t)cus) grid = 2 * (int64_t)cus;
   if (grid < 1) grid = 1;
 #define PQKV_EM(DD, BB) encode_mfma_kernel<DD, BB><<<(int)grid, kEW * 64, 0, s>>>(a, rot_out)
   if (a.d == 128 && a.bits == 4) PQKV_EM(128, 4);

@@ -77,7 +77,8 @@ hipError_t launch_rotate(const void *x, int x_dtype, const float *R, void *y, in
 hipError_t launch_encode_exact(const EncodeArgs &a, int x_dtype, hipStream_t s);
 // Matrix-core encoder for fp16 input without QJL; rot_out (nullable) receives
 // the fp32 rotated vectors the quantiser saw, [n][d].
-hipError_t launch_encode_mfma(const EncodeArgs &a, float *rot_out, hipStream_t s);
+// One round of workgroups (two per compute unit) loops over the vectors.
+hipError_t launch_encode_mfma(const EncodeArgs &a, float *rot_out, int cus, hipStream_t s);
 hipError_t launch_encode_soa(const float *x, const float *R, const float *codebook, int n_levels, float *radius,
                              uint8_t *packed, int64_t n, int d, hipStream_t s);
 hipError_t launch_soa_to_blocks(const uint8_t *packed, const float *radius, uint8_t *blocks, int64_t n, int d,

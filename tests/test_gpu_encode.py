@@ -207,6 +207,57 @@ def test_mfma_rotation_within_fp32_rounding_of_fma_chain(d, bits):
     assert (np.abs(r_got.astype(np.float64) / r_ref - 1) < 1e-6).all()
 
 
+@pytest.mark.parametrize("n_inner", [1, 7, 64, 333])
+def test_mfma_encoder_strided_rows(n_inner):
+    """Rows with gaps in x and in the blocks (no flattening): the per-vector
+    row split must land every vector where the contiguous encode puts it."""
+    d, bits, n_outer = 128, 4, 37
+    print(f"encode_mfma strided rows n_inner={n_inner}", flush=True)
+    vb = O.vector_bytes(d, bits)
+    x = _fp16_inputs(n_outer * n_inner, d, n_inner, "channel")
+    R32 = O.rotation_matrix(d, 42).astype(np.float32)
+    cb_t = padded_codebook_torch(d, bits, DEV)
+    want, _ = _encode_mfma(x, R32, cb_t, bits, d)
+    xs, bs = n_inner + 3, n_inner + 5                      # row strides in vectors
+    xpad = np.zeros((n_outer, xs, d), np.float16)
+    xpad[:, :n_inner] = x.reshape(n_outer, n_inner, d)
+    xt = torch.from_numpy(xpad).to(DEV)
+    Rt = torch.from_numpy(R32).to(DEV)
+    blocks = torch.full((n_outer, bs, vb), 0xAB, dtype=torch.uint8, device=DEV)
+    _lib.check(_lib.lib().pqkv_encode_mfma(xt.data_ptr(), _lib.F16, xs * d, Rt.data_ptr(), cb_t.data_ptr(), bits,
+                                           blocks.data_ptr(), bs * vb, n_outer, n_inner, d, None,
+                                           _lib.stream_of(xt)))
+    torch.cuda.synchronize()
+    got = blocks.cpu().numpy()
+    assert np.array_equal(got[:, :n_inner].reshape(-1, vb), want)
+    assert (got[:, n_inner:] == 0xAB).all()                 # gaps untouched
+
+
+def test_mfma_encoder_nonfinite_rows():
+    """inf / NaN coordinates take the per-coordinate division form for their
+    tile; the quantiser still matches the reference's on the rotated values."""
+    d, bits = 128, 4
+    x = _fp16_inputs(200, d, 11, "normal")
+    x[5, 7] = np.inf
+    x[20, 0] = -np.inf
+    x[21, :] = np.inf
+    x[40, 9] = np.nan
+    x[70, 3], x[70, 4] = np.inf, -np.inf
+    R32 = O.rotation_matrix(d, 42).astype(np.float32)
+    blocks, rot = _encode_mfma(x, R32, padded_codebook_torch(d, bits, DEV), bits, d)
+    cb = O.lloyd_max_codebook(d, bits)[0]
+    r_ref, idx_ref = OC.c_quantize_rotated(rot, cb)
+    want = OC.c_pack_blocks(r_ref, idx_ref, bits)
+    codes = np.concatenate([np.arange(2, 18), np.arange(20, 36), np.arange(38, 54), np.arange(56, 72)])
+    assert np.array_equal(blocks[:, codes], want[:, codes])  # index bytes
+    rad_got = blocks[:, [0, 1, 18, 19, 36, 37, 54, 55]].copy().view(np.float16).astype(np.float32)
+    rad_want = want[:, [0, 1, 18, 19, 36, 37, 54, 55]].copy().view(np.float16).astype(np.float32)
+    assert np.array_equal(np.isnan(rad_got), np.isnan(rad_want))
+    ok = ~np.isnan(rad_want)
+    assert np.array_equal(rad_got[ok], rad_want[ok])
+    assert np.isnan(rot[40]).any() and not np.isfinite(rad_want[40]).all()
+
+
 def test_mfma_encoder_unsorted_codebook_uses_the_scan():
     d, bits = 128, 4
     x = _fp16_inputs(700, d, 3, "normal")
