@@ -10,10 +10,10 @@
 // r % G. Each wave owns 32 rows (two 16-row tiles). The KV cache is walked in
 // 64-token tiles. Each tile is decoded once per workgroup into LDS, as fp16
 // planes in the exact order the MFMA operands want, so that every operand
-// read is a conflict-free run of 8-byte loads. Tiles are double-buffered:
-// the codes of tile i+1 are fetched from HBM an iteration ahead and decoded
-// by half the waves before, and by the other half after, tile i's matrix
-// work.
+// read is a conflict-free run of 8-byte loads. Tiles are double-buffered.
+// The waves run a two-group ping-pong schedule (matrix stage against softmax
+// and decode stage, one group a stage behind the other), described at the
+// main loop.
 //
 // Scores are computed transposed, S^T[token][row] = K^ . Q^T: K^ (16 tokens x
 // 32 coordinates) is the A operand and the rotated queries the B operand, so
@@ -122,46 +122,73 @@ struct PrefillTile {
   __device__ static int vseg(int nb, int kk, int plane, int h) { return KSEG + ((nb * 2 + kk) * 2 + plane) * 2 + h; }
 };
 
-// Codes of one 64-token tile, held in registers between fetch and decode.
+// Raw block_pq4 bytes of one 64-token tile of one stream, staged in LDS by
+// buffer-to-LDS loads (1 KB per wave instruction) so that no code registers
+// stay live across the schedule's stages.
 template <int D>
-struct TileCodes {
-  static constexpr int KPER = PrefillTile<D>::KITEMS / (kPW * 64);
-  uint32_t k[KPER];
-  uint32_t v[4];
-  uint32_t r;
+struct RawTile {
+  static constexpr int kBytes = kPT * vector_bytes(D, 4);
+  static constexpr int kPieces = (kBytes + 1023) / 1024;
+  static constexpr int kAlloc = kPieces * 1024;
 };
 
+// One group's four waves copy tile t0 of a stream into `raw`; bytes past the
+// stream's end arrive as zeros.
 template <int D>
-__device__ __forceinline__ void fetch_tile(TileCodes<D> &c, __amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
-                                           int t0, int tid) {
-  using PT = PrefillTile<D>;
+__device__ __forceinline__ void dma_raw(__amdgpu_buffer_rsrc_t r, uint8_t *raw, int t0, int gw, int lane) {
   constexpr int VB = vector_bytes(D, 4);
 #pragma unroll
-  for (int u = 0; u < TileCodes<D>::KPER; ++u) {
-    const int item = tid + kPW * 64 * u;
-    c.k[u] = load_code_dword<VB>(kr, t0 + item / (D / 8), item % (D / 8));
+  for (int j = 0; j < (RawTile<D>::kPieces + 3) / 4; ++j) {
+    const int p = gw + 4 * j;
+    if (p < RawTile<D>::kPieces)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)(raw + 1024 * p), 16,
+                                               t0 * VB + 1024 * p + 16 * lane, 0, 0, 0);
   }
-  if (tid < PT::VITEMS) {
-    const int q4 = tid / (D / 8), g8 = tid % (D / 8);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) c.v[j] = load_code_dword<VB>(vr, t0 + 4 * q4 + j, g8);
-  }
-  if (tid < kPT) c.r = bld16(kr, (t0 + tid) * VB);            // wave 0: key radii
-  else if (tid < 2 * kPT) c.r = bld16(vr, (t0 + tid - kPT) * VB);  // wave 1: value radii
 }
 
-// Decode a fetched tile into LDS: K^ and V^ hi / lo planes in operand order,
-// and fp32 radii.
+// The code dword holding coordinates 8 g8 .. 8 g8 + 7 of tile vector t in LDS.
+template <int VB>
+__device__ __forceinline__ uint32_t raw_code_dword(const uint8_t *raw, int t, int g8) {
+  const int off = t * VB + (g8 >> 2) * kPq4BlockBytes + 2 + 4 * (g8 & 3);
+  const uint32_t *p = (const uint32_t *)(raw + (off & ~3));
+  return align_bytes(p[1], p[0], off & 3);
+}
+
+// The thread index passed through an opaque move: the decode addresses
+// derived from it are then recomputed in each stage (a few VALU operations)
+// instead of being hoisted out of the tile loop and spilled.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// K items: item i is operand lane L = i % 64 of segment pair (tt, ks) =
+// (i / 64) / KS, (i / 64) % KS: token 16 tt + L % 16, coordinates
+// 32 ks + 8 (L / 16) .. + 7. A wave's items are one (tt, ks) with L = its
+// lane, so its LDS writes are contiguous runs.
 template <int D>
-__device__ __forceinline__ void decode_tile(const TileCodes<D> &c, uint8_t *tile, float *rad, const uint2 *lut_k,
-                                            const uint2 *lut_v, int tid) {
+__device__ __forceinline__ void k_item(int item, int &t, int &g8) {
+  constexpr int KS = PrefillTile<D>::KS;
+  const int tk = item >> 6, L = item & 63;
+  t = 16 * (tk / KS) + (L & 15);
+  g8 = 4 * (tk % KS) + (L >> 4);
+}
+
+// Decode a staged K tile into LDS: K^ hi / lo planes in operand order, and
+// fp32 key radii. Run by group 0 (gtid 0..255).
+template <int D>
+__device__ __forceinline__ void decode_k(const uint8_t *raw, uint8_t *tile, float *rad, const uint2 *lut_k,
+                                         int gtid) {
   using PT = PrefillTile<D>;
+  constexpr int VB = vector_bytes(D, 4);
+  constexpr int KPER = PT::KITEMS / (kPW / 2 * 64);  // 4 (d = 128) or 2
+  gtid = opaque(gtid);
 #pragma unroll
-  for (int u = 0; u < TileCodes<D>::KPER; ++u) {
-    const int item = tid + kPW * 64 * u;
-    const int t = item / (D / 8), g8 = item % (D / 8);
-    const int lane = 16 * (g8 & 3) + (t & 15);
-    const uint32_t w = c.k[u];
+  for (int u = 0; u < KPER; ++u) {
+    int t, g8;
+    k_item<D>(gtid + (kPW / 2) * 64 * u, t, g8);
+    const int lane = 16 * (g8 & 3) + (t & 15);  // = the writing thread's lane
+    const uint32_t w = raw_code_dword<VB>(raw, t, g8);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       // coordinates 8 g8 + 4h .. +3: bytes 2h, 2h + 1 of w
@@ -172,20 +199,38 @@ __device__ __forceinline__ void decode_tile(const TileCodes<D> &c, uint8_t *tile
       lds_put8(tile + PT::kseg(t >> 4, g8 >> 2, 1, h) * kSegBytes + lane * 8, lo0, lo1);
     }
   }
-  if (tid < PT::VITEMS) {
-    const int q4 = tid / (D / 8), g8 = tid % (D / 8);
+  if (gtid < kPT) rad[gtid] = half_bits_to_float(*(const uint16_t *)(raw + gtid * VB));
+}
+
+// Decode a staged V tile: V^ hi / lo planes in operand order, fp32 value
+// radii. Run by group 1 (gtid 0..255).
+template <int D>
+__device__ __forceinline__ void decode_v(const uint8_t *raw, uint8_t *tile, float *rad, const uint2 *lut_v,
+                                         int gtid) {
+  using PT = PrefillTile<D>;
+  constexpr int VB = vector_bytes(D, 4);
+  gtid = opaque(gtid);
+  if (gtid < PT::VITEMS) {
+    const int q4 = gtid / (D / 8), g8 = gtid % (D / 8);
     const int tt = q4 >> 2, kk = tt >> 1, h = tt & 1, grp = q4 & 3;
-    // token pairs (0,1), (2,3): byte k of x = coordinate 2k of both tokens, of y = 2k + 1
-    const uint32_t x01 = (c.v[0] & 0x0F0F0F0Fu) | ((c.v[1] << 4) & 0xF0F0F0F0u);
-    const uint32_t y01 = ((c.v[0] >> 4) & 0x0F0F0F0Fu) | (c.v[1] & 0xF0F0F0F0u);
-    const uint32_t x23 = (c.v[2] & 0x0F0F0F0Fu) | ((c.v[3] << 4) & 0xF0F0F0F0u);
-    const uint32_t y23 = ((c.v[2] >> 4) & 0x0F0F0F0Fu) | (c.v[3] & 0xF0F0F0F0u);
+    uint32_t c[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int j = 0; j < 4; ++j) c[j] = raw_code_dword<VB>(raw, 4 * q4 + j, g8);
+    // token pairs (0,1), (2,3): byte k of x = coordinate 2k of both tokens, of y = 2k + 1
+    const uint32_t x01 = (c[0] & 0x0F0F0F0Fu) | ((c[1] << 4) & 0xF0F0F0F0u);
+    const uint32_t y01 = ((c[0] >> 4) & 0x0F0F0F0Fu) | (c[1] & 0xF0F0F0F0u);
+    const uint32_t x23 = (c[2] & 0x0F0F0F0Fu) | ((c[3] << 4) & 0xF0F0F0F0u);
+    const uint32_t y23 = ((c[2] >> 4) & 0x0F0F0F0Fu) | (c[3] & 0xF0F0F0F0u);
+    // Coordinate order rotated by g8 / 2: the 64 writes of one step then
+    // cover 32 bank pairs (two per pair, the minimum for 512 bytes) instead
+    // of sharing four.
+#pragma unroll
+    for (int step = 0; step < 8; ++step) {
+      const int e = (step + (g8 >> 1)) & 7;
       const int dcoord = 8 * g8 + e;
       const int k = e >> 1;
       const uint32_t s01 = (e & 1) ? y01 : x01, s23 = (e & 1) ? y23 : x23;
-      const uint2 a = lut_v[(s01 >> (8 * k)) & 0xFF], b = lut_v[(s23 >> (8 * k)) & 0xFF];
+      const uint2 a = lut_v[__builtin_amdgcn_ubfe(s01, 8 * k, 8)], b = lut_v[__builtin_amdgcn_ubfe(s23, 8 * k, 8)];
       const int lane = 16 * grp + (dcoord & 15);
       const uint32_t hi01 = __builtin_amdgcn_perm(a.y, a.x, 0x05040100u), hi23 = __builtin_amdgcn_perm(b.y, b.x, 0x05040100u);
       const uint32_t lo01 = __builtin_amdgcn_perm(a.y, a.x, 0x07060302u), lo23 = __builtin_amdgcn_perm(b.y, b.x, 0x07060302u);
@@ -193,7 +238,7 @@ __device__ __forceinline__ void decode_tile(const TileCodes<D> &c, uint8_t *tile
       lds_put8(tile + PT::vseg(dcoord >> 4, kk, 1, h) * kSegBytes + lane * 8, lo01, lo23);
     }
   }
-  if (tid < 2 * kPT) rad[tid] = half_bits_to_float(c.r);
+  if (gtid < kPT) rad[kPT + gtid] = half_bits_to_float(*(const uint16_t *)(raw + gtid * VB));
 }
 
 template <int D>
@@ -204,9 +249,15 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
   __shared__ uint2 lut_k[256], lut_v[256];
   __shared__ __attribute__((aligned(16))) uint8_t tiles[2][PT::BYTES];
   __shared__ __attribute__((aligned(16))) float rads[2][2 * kPT];  // [buf][k radii | v radii]
+  // raw codes of the tiles being staged: group 0's stream K, group 1's V
+  __shared__ __attribute__((aligned(16))) uint8_t raw[2][2][RawTile<D>::kAlloc];  // [group][buf]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
+  // Two groups of four waves; wave w and w + 4 share a SIMD.
+  const int group = __builtin_amdgcn_readfirstlane(wave) >= kPW / 2 ? 1 : 0;  // wave-uniform
+  const int gtid = tid - group * (kPW / 2) * 64;
+  const int gw = __builtin_amdgcn_readfirstlane(wave) - group * (kPW / 2);
   const int G = a.G;
   const int qtile = blockIdx.x;
   const int bh = blockIdx.y;
@@ -235,20 +286,19 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
   // k = 8 grp + i covers coordinate 32 ks + 8 grp + i.
   half8_t qh[2][KS], ql[2][KS];
   int row_pos[2];
-  bool row_ok[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     const int row = 32 * wave + 16 * rt + col;
     const int tok = q0 + row / G, head = row % G;
-    row_ok[rt] = row < a.qt * G && tok < a.Sq;
+    const bool row_ok = row < a.qt * G && tok < a.Sq;
     row_pos[rt] = a.q_start + tok;
-    const float *qr = a.q + (((int64_t)(b * a.Hq + h * G + head) * a.Sq) + (row_ok[rt] ? tok : 0)) * D;
+    const float *qr = a.q + (((int64_t)(b * a.Hq + h * G + head) * a.Sq) + (row_ok ? tok : 0)) * D;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         half_t vh, vl;
-        split2(row_ok[rt] ? qr[32 * ks + 8 * grp + i] : 0.0f, &vh, &vl);
+        split2(row_ok ? qr[32 * ks + 8 * grp + i] : 0.0f, &vh, &vl);
         qh[rt][ks][i] = vh;
         ql[rt][ks][i] = vl;
       }
@@ -260,36 +310,13 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) oacc[rt][nb] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  float4_t sacc[2][4];                 // scores of the tile between X and Y
+  half8_t ph[2][2], pl[2][2];          // softmax weights between Y and the next X
 
-  const int ntiles = (kv_end + kPT - 1) / kPT;
-  TileCodes<D> codes;
-  __syncthreads();  // tables ready
-  // The two waves sharing a SIMD (w and w + 4) run each iteration in
-  // opposite phase order: waves 4..7 decode the next tile before their matrix
-  // work, waves 0..3 after it, so one wave's MFMAs overlap the other's table
-  // decode and softmax instead of both waves contending for the same unit.
-  // The codes of tile it + 1 are fetched one iteration ahead.
-  const bool decode_first = wave >= kPW / 2;
-  if (ntiles > 0) {
-    fetch_tile<D>(codes, kres, vres, 0, tid);
-    decode_tile<D>(codes, tiles[0], rads[0], lut_k, lut_v, tid);
-    if (ntiles > 1) fetch_tile<D>(codes, kres, vres, kPT, tid);
-  }
-  for (int it = 0; it < ntiles; ++it) {
-    const int t0 = it * kPT;
-    __syncthreads();  // tile it decoded; the other buffer is free
-    if (decode_first && it + 1 < ntiles) {
-      decode_tile<D>(codes, tiles[(it + 1) & 1], rads[(it + 1) & 1], lut_k, lut_v, tid);
-      if (it + 2 < ntiles) fetch_tile<D>(codes, kres, vres, t0 + 2 * kPT, tid);
-    }
+  // ---- stage bodies ----
+  // scores S^T[token][row] of tile it
+  auto scores = [&](int it) {
     const uint8_t *tile = tiles[it & 1];
-    const float *rk = rads[it & 1], *rv = rads[it & 1] + kPT;
-
-    // ---------------- scores S^T[token][row] ----------------
-    // Matrix bursts run at raised wave priority, so the SIMD arbiter keeps
-    // them back to back while the other wave's VALU work fills the gaps.
-    __builtin_amdgcn_s_setprio(1);
-    float4_t sacc[2][4];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
@@ -309,11 +336,31 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
           sacc[rt][tt] = mfma16(ah, ql[rt][ks], sacc[rt][tt]);
         }
       }
-
-    __builtin_amdgcn_s_setprio(0);
-    // ---------------- online softmax, per row (lane col) ----------------
+  };
+  // O[row][coord] += P . V^ of tile it
+  auto values = [&](int it) {
+    const uint8_t *tile = tiles[it & 1];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const half8_t bh = pack8u(lds_get8(tile + PT::vseg(nb, kk, 0, 0) * kSegBytes + lane * 8),
+                                  lds_get8(tile + PT::vseg(nb, kk, 0, 1) * kSegBytes + lane * 8));
+        const half8_t bl = pack8u(lds_get8(tile + PT::vseg(nb, kk, 1, 0) * kSegBytes + lane * 8),
+                                  lds_get8(tile + PT::vseg(nb, kk, 1, 1) * kSegBytes + lane * 8));
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          oacc[rt][nb] = mfma16(ph[rt][kk], bh, oacc[rt][nb]);
+          oacc[rt][nb] = mfma16(ph[rt][kk], bl, oacc[rt][nb]);
+          oacc[rt][nb] = mfma16(pl[rt][kk], bh, oacc[rt][nb]);
+        }
+      }
+  };
+  // online softmax of tile it's scores -> weights p * r_v as the A operand
+  auto softmax = [&](int it) {
+    const int t0 = it * kPT;
+    const float *rk = rads[it & 1], *rv = rads[it & 1] + kPT;
     const bool need_mask = t0 + kPT > a.S || (a.causal && t0 + kPT - 1 > a.q_start + q0);
-    half8_t ph[2][2], pl[2][2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       float s[4][4];
@@ -361,6 +408,8 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
         }
       }
       l_run[rt] = l_run[rt] * alpha + psum;
+      // the running output holds tiles < it here (tile it's values come in
+      // the next X stage), so the rescale applies now
       float f[4];
       per_row(alpha, grp, f);
 #pragma unroll
@@ -368,29 +417,76 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
 #pragma unroll
         for (int i = 0; i < 4; ++i) oacc[rt][nb][i] *= f[i];
     }
+  };
 
-    // ---------------- values O[row][coord] += P . V^ ----------------
+  // ---- ping-pong schedule ----
+  // Each tile takes two stages per wave: X(it) = values of tile it - 1 and
+  // scores of tile it (matrix work), Y(it) = softmax of tile it plus one half
+  // of tile it + 1's table decode (VALU and LDS work). Group 1 runs one stage
+  // behind group 0 with a block barrier after every stage, so the two waves
+  // sharing a SIMD are always in opposite stages: one's MFMA bursts overlap
+  // the other's softmax and decode.
+  // Tile it lives in buffer it & 1. Group 0 decodes K(it + 1) in its Y(it)
+  // (stage 2 it + 1), after both groups' last read of K(it - 1) (stage
+  // 2 it - 1); group 1 decodes V(it + 1) in its Y(it) (stage 2 it + 2), after
+  // group 1's values of tile it - 1 (stage 2 it + 1). Each is read from the
+  // stage after its decode on, and radii follow their half.
+  const int ntiles = (kv_end + kPT - 1) / kPT;
+  const __amdgpu_buffer_rsrc_t gres = group == 0 ? kres : vres;  // this group's stream
+  uint8_t(&graw)[2][RawTile<D>::kAlloc] = raw[group];
+  auto decode = [&](int it) {  // this group's half of tile it, from graw[it & 1]
+    if (group == 0) decode_k<D>(graw[it & 1], tiles[it & 1], rads[it & 1], lut_k, gtid);
+    else decode_v<D>(graw[it & 1], tiles[it & 1], rads[it & 1], lut_v, gtid);
+  };
+  auto wait_dma = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
+  // Block barrier for LDS hand-offs only: __syncthreads' release fence would
+  // also wait for the raw-tile copies still in flight.
+  auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+  if (ntiles > 0) dma_raw<D>(gres, graw[0], 0, gw, lane);
+  if (ntiles > 1) dma_raw<D>(gres, graw[1], kPT, gw, lane);
+  wait_dma();
+  __syncthreads();  // tables and the first two raw tiles ready
+  if (ntiles > 0) decode(0);
+  __syncthreads();  // tile 0 decoded
+
+  // One loop per group (the compiler then sees that the scores and the
+  // weights are never live together); both make 2 ntiles + 2 barrier calls.
+  // Raw tile it + 2 streams into LDS from Y(it) on (after tile it + 1's
+  // decode freed nothing it needs: it overwrites tile it's raw buffer); each
+  // wave waits for its copies before the barrier that ends its next X stage.
+  auto x_stage = [&](int it) {
     __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const half8_t bh = pack8u(lds_get8(tile + PT::vseg(nb, kk, 0, 0) * kSegBytes + lane * 8),
-                                  lds_get8(tile + PT::vseg(nb, kk, 0, 1) * kSegBytes + lane * 8));
-        const half8_t bl = pack8u(lds_get8(tile + PT::vseg(nb, kk, 1, 0) * kSegBytes + lane * 8),
-                                  lds_get8(tile + PT::vseg(nb, kk, 1, 1) * kSegBytes + lane * 8));
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-          oacc[rt][nb] = mfma16(ph[rt][kk], bh, oacc[rt][nb]);
-          oacc[rt][nb] = mfma16(ph[rt][kk], bl, oacc[rt][nb]);
-          oacc[rt][nb] = mfma16(pl[rt][kk], bh, oacc[rt][nb]);
+    if (it >= 1) values(it - 1);
+    __builtin_amdgcn_sched_barrier(0);  // weights die before the scores start
+    if (it < ntiles) scores(it);
+    __builtin_amdgcn_s_setprio(0);
+    wait_dma();
+  };
+  auto y_stage = [&](int it) {
+    softmax(it);
+    if (it + 1 < ntiles) {
+      decode(it + 1);
+      if (it + 2 < ntiles) dma_raw<D>(gres, graw[it & 1], (it + 2) * kPT, gw, lane);
+    }
+  };
+  if (ntiles > 0) {
+    if (group == 0) {
+      for (int it = 0; it <= ntiles; ++it) {
+        x_stage(it);                                   // stage 2 it
+        barrier();
+        if (it < ntiles) y_stage(it);                  // stage 2 it + 1
+        barrier();
+      }
+    } else {
+      barrier();                                 // stage 0
+      for (int it = 0; it <= ntiles; ++it) {
+        x_stage(it);                                   // stage 2 it + 1
+        barrier();
+        if (it < ntiles) {                             // stage 2 it + 2
+          y_stage(it);
+          barrier();
         }
       }
-
-    __builtin_amdgcn_s_setprio(0);
-    if (!decode_first && it + 1 < ntiles) {
-      decode_tile<D>(codes, tiles[(it + 1) & 1], rads[(it + 1) & 1], lut_k, lut_v, tid);
-      if (it + 2 < ntiles) fetch_tile<D>(codes, kres, vres, t0 + 2 * kPT, tid);
     }
   }
 
