@@ -78,14 +78,12 @@ __device__ __forceinline__ float rows_sum(float x) {
   return __builtin_bit_cast(float, (uint32_t)b[0]) + __builtin_bit_cast(float, (uint32_t)b[1]);
 }
 
-// Value of lane `row` (0..15) for output row 4 grp + i: the 16 values are
-// read once into scalars, then each lane picks by its lane group.
+// Value of lane `row` (0..15) for output row 4 grp + i (v is the same in
+// the four lanes of a column): one lane gather per i.
 __device__ __forceinline__ void per_row(float v, int grp, float (&f)[4]) {
-  float s[16];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) s[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), r));
-#pragma unroll
-  for (int i = 0; i < 4; ++i) f[i] = grp == 0 ? s[i] : grp == 1 ? s[4 + i] : grp == 2 ? s[8 + i] : s[12 + i];
+  for (int i = 0; i < 4; ++i)
+    f[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * (4 * grp + i), __builtin_bit_cast(int, v)));
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t stream_rsrc(const uint8_t *base, uint32_t bytes) {
@@ -193,10 +191,8 @@ __device__ __forceinline__ void decode_k(const uint8_t *raw, uint8_t *tile, floa
     for (int h = 0; h < 2; ++h) {
       // coordinates 8 g8 + 4h .. +3: bytes 2h, 2h + 1 of w
       const uint2 a = lut_k[(w >> (16 * h)) & 0xFF], b = lut_k[(w >> (16 * h + 8)) & 0xFF];
-      const uint32_t hi0 = __builtin_amdgcn_perm(a.y, a.x, 0x05040100u), hi1 = __builtin_amdgcn_perm(b.y, b.x, 0x05040100u);
-      const uint32_t lo0 = __builtin_amdgcn_perm(a.y, a.x, 0x07060302u), lo1 = __builtin_amdgcn_perm(b.y, b.x, 0x07060302u);
-      lds_put8(tile + PT::kseg(t >> 4, g8 >> 2, 0, h) * kSegBytes + lane * 8, hi0, hi1);
-      lds_put8(tile + PT::kseg(t >> 4, g8 >> 2, 1, h) * kSegBytes + lane * 8, lo0, lo1);
+      lds_put8(tile + PT::kseg(t >> 4, g8 >> 2, 0, h) * kSegBytes + lane * 8, a.x, b.x);
+      lds_put8(tile + PT::kseg(t >> 4, g8 >> 2, 1, h) * kSegBytes + lane * 8, a.y, b.y);
     }
   }
   if (gtid < kPT) rad[gtid] = half_bits_to_float(*(const uint16_t *)(raw + gtid * VB));
@@ -232,10 +228,8 @@ __device__ __forceinline__ void decode_v(const uint8_t *raw, uint8_t *tile, floa
       const uint32_t s01 = (e & 1) ? y01 : x01, s23 = (e & 1) ? y23 : x23;
       const uint2 a = lut_v[__builtin_amdgcn_ubfe(s01, 8 * k, 8)], b = lut_v[__builtin_amdgcn_ubfe(s23, 8 * k, 8)];
       const int lane = 16 * grp + (dcoord & 15);
-      const uint32_t hi01 = __builtin_amdgcn_perm(a.y, a.x, 0x05040100u), hi23 = __builtin_amdgcn_perm(b.y, b.x, 0x05040100u);
-      const uint32_t lo01 = __builtin_amdgcn_perm(a.y, a.x, 0x07060302u), lo23 = __builtin_amdgcn_perm(b.y, b.x, 0x07060302u);
-      lds_put8(tile + PT::vseg(dcoord >> 4, kk, 0, h) * kSegBytes + lane * 8, hi01, hi23);
-      lds_put8(tile + PT::vseg(dcoord >> 4, kk, 1, h) * kSegBytes + lane * 8, lo01, lo23);
+      lds_put8(tile + PT::vseg(dcoord >> 4, kk, 0, h) * kSegBytes + lane * 8, a.x, b.x);
+      lds_put8(tile + PT::vseg(dcoord >> 4, kk, 1, h) * kSegBytes + lane * 8, a.y, b.y);
     }
   }
   if (gtid < kPT) rad[kPT + gtid] = half_bits_to_float(*(const uint16_t *)(raw + gtid * VB));
@@ -272,14 +266,14 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
   const __amdgpu_buffer_rsrc_t kres = stream_rsrc(kstream, valid_bytes);
   const __amdgpu_buffer_rsrc_t vres = stream_rsrc(vstream, valid_bytes);
 
-  if (tid < 256) {  // byte -> (c_hi, c_lo) of its low and high nibble codes
+  if (tid < 256) {  // byte -> (c_hi, c_hi' | c_lo, c_lo') of its low and high nibble codes
     half_t h0, l0, h1, l1;
     split2(a.k_cb[tid & 15], &h0, &l0);
     split2(a.k_cb[tid >> 4], &h1, &l1);
-    lut_k[tid] = make_uint2(pack_h2(h0, l0), pack_h2(h1, l1));
+    lut_k[tid] = make_uint2(pack_h2(h0, h1), pack_h2(l0, l1));
     split2(a.v_cb[tid & 15], &h0, &l0);
     split2(a.v_cb[tid >> 4], &h1, &l1);
-    lut_v[tid] = make_uint2(pack_h2(h0, l0), pack_h2(h1, l1));
+    lut_v[tid] = make_uint2(pack_h2(h0, h1), pack_h2(l0, l1));
   }
 
   // Queries as the B operand: column col = row 32 wave + 16 rt + col; step ks,
@@ -314,47 +308,67 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
   half8_t ph[2][2], pl[2][2];          // softmax weights between Y and the next X
 
   // ---- stage bodies ----
-  // scores S^T[token][row] of tile it
+  // scores S^T[token][row] of tile it. The operands of step n + 1 are read
+  // before step n's products (the fence keeps them there), so the LDS
+  // latency hides behind six MFMAs.
   auto scores = [&](int it) {
     const uint8_t *tile = tiles[it & 1];
+    auto kop = [&](int n, int plane) {
+      const int tt = n / KS, ks = n % KS;
+      return pack8u(lds_get8(tile + PT::kseg(tt, ks, plane, 0) * kSegBytes + lane * 8),
+                    lds_get8(tile + PT::kseg(tt, ks, plane, 1) * kSegBytes + lane * 8));
+    };
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) sacc[rt][tt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    half8_t ah = kop(0, 0), al = kop(0, 1);
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const half8_t ah = pack8u(lds_get8(tile + PT::kseg(tt, ks, 0, 0) * kSegBytes + lane * 8),
-                                  lds_get8(tile + PT::kseg(tt, ks, 0, 1) * kSegBytes + lane * 8));
-        const half8_t al = pack8u(lds_get8(tile + PT::kseg(tt, ks, 1, 0) * kSegBytes + lane * 8),
-                                  lds_get8(tile + PT::kseg(tt, ks, 1, 1) * kSegBytes + lane * 8));
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-          sacc[rt][tt] = mfma16(ah, qh[rt][ks], sacc[rt][tt]);
-          sacc[rt][tt] = mfma16(al, qh[rt][ks], sacc[rt][tt]);
-          sacc[rt][tt] = mfma16(ah, ql[rt][ks], sacc[rt][tt]);
-        }
+    for (int n = 0; n < 4 * KS; ++n) {
+      const int tt = n / KS, ks = n % KS;
+      half8_t ah_n = ah, al_n = al;
+      if (n + 1 < 4 * KS) {
+        ah_n = kop(n + 1, 0);
+        al_n = kop(n + 1, 1);
       }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        sacc[rt][tt] = mfma16(ah, qh[rt][ks], sacc[rt][tt]);
+        sacc[rt][tt] = mfma16(al, qh[rt][ks], sacc[rt][tt]);
+        sacc[rt][tt] = mfma16(ah, ql[rt][ks], sacc[rt][tt]);
+      }
+      ah = ah_n;
+      al = al_n;
+    }
   };
-  // O[row][coord] += P . V^ of tile it
+  // O[row][coord] += P . V^ of tile it, operands read one step ahead
   auto values = [&](int it) {
     const uint8_t *tile = tiles[it & 1];
+    auto vop = [&](int n, int plane) {
+      const int nb = n >> 1, kk = n & 1;
+      return pack8u(lds_get8(tile + PT::vseg(nb, kk, plane, 0) * kSegBytes + lane * 8),
+                    lds_get8(tile + PT::vseg(nb, kk, plane, 1) * kSegBytes + lane * 8));
+    };
+    half8_t bh = vop(0, 0), bl = vop(0, 1);
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const half8_t bh = pack8u(lds_get8(tile + PT::vseg(nb, kk, 0, 0) * kSegBytes + lane * 8),
-                                  lds_get8(tile + PT::vseg(nb, kk, 0, 1) * kSegBytes + lane * 8));
-        const half8_t bl = pack8u(lds_get8(tile + PT::vseg(nb, kk, 1, 0) * kSegBytes + lane * 8),
-                                  lds_get8(tile + PT::vseg(nb, kk, 1, 1) * kSegBytes + lane * 8));
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-          oacc[rt][nb] = mfma16(ph[rt][kk], bh, oacc[rt][nb]);
-          oacc[rt][nb] = mfma16(ph[rt][kk], bl, oacc[rt][nb]);
-          oacc[rt][nb] = mfma16(pl[rt][kk], bh, oacc[rt][nb]);
-        }
+    for (int n = 0; n < 2 * NB; ++n) {
+      const int nb = n >> 1, kk = n & 1;
+      half8_t bh_n = bh, bl_n = bl;
+      if (n + 1 < 2 * NB) {
+        bh_n = vop(n + 1, 0);
+        bl_n = vop(n + 1, 1);
       }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        oacc[rt][nb] = mfma16(ph[rt][kk], bh, oacc[rt][nb]);
+        oacc[rt][nb] = mfma16(ph[rt][kk], bl, oacc[rt][nb]);
+        oacc[rt][nb] = mfma16(pl[rt][kk], bh, oacc[rt][nb]);
+      }
+      bh = bh_n;
+      bl = bl_n;
+    }
   };
   // online softmax of tile it's scores -> weights p * r_v as the A operand
   auto softmax = [&](int it) {
@@ -409,13 +423,16 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
       }
       l_run[rt] = l_run[rt] * alpha + psum;
       // the running output holds tiles < it here (tile it's values come in
-      // the next X stage), so the rescale applies now
-      float f[4];
-      per_row(alpha, grp, f);
+      // the next X stage), so the rescale applies now; skipped (wave-uniform)
+      // when no row's maximum moved, the common case after the first tiles
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+        float f[4];
+        per_row(alpha, grp, f);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+        for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) oacc[rt][nb][i] *= f[i];
+          for (int i = 0; i < 4; ++i) oacc[rt][nb][i] *= f[i];
+      }
     }
   };
 
