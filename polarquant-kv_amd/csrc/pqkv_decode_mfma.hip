@@ -322,13 +322,12 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     // alpha of head hh sits in lane hh. Skipped (wave-uniform) when no head's
     // maximum moved, the common case once the first chunks are in.
     if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) & 0xFFull) {
-      float al[8];
-#pragma unroll
-      for (int hh = 0; hh < 8; ++hh)
-        al[hh] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), hh));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float f = (grp & 1) ? al[4 + i] : al[i];
+        // lane gather (a select between two read-lanes becomes a scratch
+        // array indexed by the lane group)
+        const float f = __builtin_bit_cast(
+            float, __builtin_amdgcn_ds_bpermute(4 * (4 * (grp & 1) + i), __builtin_bit_cast(int, alpha)));
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) oacc[nb][i] *= f;
       }
