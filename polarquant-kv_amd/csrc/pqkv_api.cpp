@@ -37,10 +37,9 @@ int hip_status(hipError_t e, const char *what) {
 
 bool supported_d(int d) { return d == 64 || d == 128; }
 
-// Decode kernel choice: the matrix-core kernel serves 4-bit K and V without
-// QJL; PQKV_DECODE_KERNEL=valu forces the fp32 VALU kernel everywhere.
-bool use_mfma(int k_bits, int v_bits, bool qjl) {
-  if (k_bits != 4 || v_bits != 4 || qjl) return false;
+// Decode kernel choice: the matrix-core kernel serves every width pair, with
+// or without QJL; PQKV_DECODE_KERNEL=valu forces the fp32 VALU kernel.
+bool use_mfma() {
   const char *e = getenv("PQKV_DECODE_KERNEL");
   return !(e && strcmp(e, "valu") == 0);
 }
@@ -430,8 +429,8 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
     group = std::max(std::max(count[0][0], count[0][1]), std::max(count[1][0], count[1][1]));
   }
   int splits = 1, tps = 0;
-  const bool all_mfma = !mixed && use_mfma(k_bits, v_bits, qjl_signs != nullptr);
-  decode_plan((int64_t)B * group, S, all_mfma ? mfma_target() : kValuTarget, &splits, &tps);
+  const bool mfma = use_mfma();
+  decode_plan((int64_t)B * group, S, mfma ? mfma_target() : kValuTarget, &splits, &tps);
   float *q32 = (float *)workspace;
   float *part = (float *)((char *)workspace + align256((size_t)B * Hq * d * 4));
   float *pq32 = (float *)((char *)part + align256((size_t)B * Hq * splits * (d + 2) * 4));
@@ -473,8 +472,7 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
     a.n_heads = Hkv;
     a.listed = 0;
     tok = pqkv::prof_begin("decode_split", st);
-    e = use_mfma(k_bits, v_bits, qjl_signs != nullptr) ? pqkv::launch_decode_mfma(a, st)
-                                                       : pqkv::launch_decode_split(a, k_bits, v_bits, st);
+    e = mfma ? pqkv::launch_decode_mfma(a, k_bits, v_bits, st) : pqkv::launch_decode_split(a, k_bits, v_bits, st);
     pqkv::prof_end(tok, st);
     if (e != hipSuccess) return hip_status(e, "decode split launch");
   } else {
@@ -500,8 +498,7 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
         if (n == 0) continue;
         a.n_heads = n;
         tok = pqkv::prof_begin("decode_split", st);
-        e = use_mfma(kbits, vbits, qjl_signs != nullptr) ? pqkv::launch_decode_mfma(a, st)
-                                                         : pqkv::launch_decode_split(a, kbits, vbits, st);
+        e = mfma ? pqkv::launch_decode_mfma(a, kbits, vbits, st) : pqkv::launch_decode_split(a, kbits, vbits, st);
         pqkv::prof_end(tok, st);
         if (e != hipSuccess) return hip_status(e, "decode split launch");
       }

@@ -1,5 +1,6 @@
 // Split-K decode attention on the matrix cores (gfx950 v_mfma_f32_16x16x32_f16)
-// for block_pq4 keys and values.
+// for block_pq4 / block_pq2 keys and values, optionally with the QJL sign
+// correction on the keys.
 //
 // Same contract and workspace format as decode_split_kernel (pqkv_decode.hip):
 // scores q_rot . c[idx] * r_k, online softmax in the exp2 domain, values
@@ -29,8 +30,16 @@
 //     one coordinate, its 8 k values 4 tokens x (hi, lo): two tokens' nibbles
 //     of that coordinate interleaved into one byte give both tokens' values
 //     with the same kind of table read.
+// 2-bit codes: a nibble holds two codes, so the same operand shapes come from
+// 16-entry tables (nibble -> (c_hi, c_lo, c_hi', c_lo')); value tokens pair
+// up as two crumbs per nibble.
+// QJL: s += [r_k > 0] sum_i (2 sign_i - 1) pq_i with pq = P_rot q / m, a
+// second product on the matrix cores: A = the signs as +-1 (a 16-entry table
+// maps 4 sign bits to 4 halves), B = pq as (hi | lo) columns, 32 projections
+// per MFMA.
 // Cross-lane steps use DPP row rotations and the gfx950 permlane16/32 swaps
-// (VALU), not LDS permutes; LDS carries only the chunk tiles and the tables.
+// (VALU); LDS carries the chunk tiles and the tables, and ds_bpermute moves
+// the sign bytes (and the rare rescale factors) between lanes.
 #include "pqkv_device.h"
 #include "pqkv_launch.h"
 
@@ -54,13 +63,26 @@ __device__ __forceinline__ uint32_t pack_h2(half_t a, half_t b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// byte b -> halfs (c_hi[b & 15], c_lo[b & 15], c_hi[b >> 4], c_lo[b >> 4])
+// 4-bit: byte b -> halfs (c_hi[b & 15], c_lo[b & 15], c_hi[b >> 4], c_lo[b >> 4]);
+// 2-bit: nibble n -> the same for codes n & 3 and n >> 2.
+template <int BITS>
 __device__ __forceinline__ void build_lut_pairs(uint2 *lut, const float *cb, int tid) {
-  if (tid < 256) {
+  constexpr int N = BITS == 4 ? 256 : 16, SH = BITS == 4 ? 4 : 2, MASK = BITS == 4 ? 15 : 3;
+  if (tid < N) {
     half_t h0, l0, h1, l1;
-    split_hi_lo(cb[tid & 15], &h0, &l0);
-    split_hi_lo(cb[tid >> 4], &h1, &l1);
+    split_hi_lo(cb[tid & MASK], &h0, &l0);
+    split_hi_lo(cb[tid >> SH], &h1, &l1);
     lut[tid] = make_uint2(pack_h2(h0, l0), pack_h2(h1, l1));
+  }
+}
+
+// QJL: 4 sign bits -> the halfs (2 bit_j - 1), j = 0..3.
+__device__ __forceinline__ void build_sign_lut(uint2 *lut, int tid) {
+  if (tid < 16) {
+    uint32_t h[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) h[j] = ((tid >> j) & 1) ? 0x3C00u : 0xBC00u;  // +1.0 / -1.0 fp16
+    lut[tid] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
   }
 }
 
@@ -114,41 +136,57 @@ typedef __attribute__((address_space(3))) volatile u32x2 lds_u32x2;
 __device__ __forceinline__ void lds_store8(uint8_t *p, u32x2 v) { *(lds_u32x2 *)p = v; }
 
 // One 64-token chunk of K and V as contiguous 16-byte pieces: lane l holds
-// pieces l + 64 j.
-template <int D>
+// pieces l + 64 j of each; with QJL, also token l's sign bytes.
+template <int D, int KB, int VBITS, bool QJL>
 struct ChunkRegs {
-  static constexpr int kBytes = kChunk * vector_bytes(D, 4);  // per stream
-  static constexpr int kPieces = kBytes / 16;
-  static constexpr int kPerLane = (kPieces + 63) / 64;
-  u32x4 k[kPerLane], v[kPerLane];
+  static constexpr int kBytesK = kChunk * vector_bytes(D, KB);
+  static constexpr int kBytesV = kChunk * vector_bytes(D, VBITS);
+  static constexpr int kPiecesK = kBytesK / 16, kPiecesV = kBytesV / 16;
+  static constexpr int kPerLaneK = (kPiecesK + 63) / 64, kPerLaneV = (kPiecesV + 63) / 64;
+  static constexpr int kSignDw = QJL ? D / 32 : 1;  // m = d sign bits per token
+  u32x4 k[kPerLaneK], v[kPerLaneV];
+  uint32_t sg[kSignDw];
 };
 
-template <int D>
-__device__ __forceinline__ void load_chunk(ChunkRegs<D> &c, __amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
-                                           int t0, int lane) {
-  using CR = ChunkRegs<D>;
-  const int base = t0 * vector_bytes(D, 4);
+template <int D, int KB, int VBITS, bool QJL>
+__device__ __forceinline__ void load_chunk(ChunkRegs<D, KB, VBITS, QJL> &c, __amdgpu_buffer_rsrc_t kr,
+                                           __amdgpu_buffer_rsrc_t vr, __amdgpu_buffer_rsrc_t sr, int t0, int lane) {
+  using CR = ChunkRegs<D, KB, VBITS, QJL>;
+  const int kbase = t0 * vector_bytes(D, KB), vbase = t0 * vector_bytes(D, VBITS);
+  // Every lane loads its last piece too, also past the chunk (the next
+  // tokens' bytes, or zeros past the stream): a conditional load here makes
+  // the compiler keep the piece array in scratch. Only the LDS stores are
+  // limited to the chunk.
 #pragma unroll
-  for (int j = 0; j < CR::kPerLane; ++j) {
-    const int piece = lane + 64 * j;
-    if (j < CR::kPerLane - 1 || piece < CR::kPieces) {
-      c.k[j] = bld128(kr, base + 16 * piece);
-      c.v[j] = bld128(vr, base + 16 * piece);
-    }
+  for (int j = 0; j < CR::kPerLaneK; ++j) c.k[j] = bld128(kr, kbase + 16 * (lane + 64 * j));
+#pragma unroll
+  for (int j = 0; j < CR::kPerLaneV; ++j) c.v[j] = bld128(vr, vbase + 16 * (lane + 64 * j));
+  if constexpr (QJL) {
+    const int sbase = (t0 + lane) * (D / 8);
+#pragma unroll
+    for (int j = 0; j < CR::kSignDw; ++j)
+      c.sg[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(sr, sbase + 4 * j, 0, 0));
   }
 }
 
 // LDS tiles keep the HBM byte layout. 8-byte stores run at the full LDS rate
 // (16-byte ones at half); volatile keeps the compiler from merging them.
-template <int D>
-__device__ __forceinline__ void stage_chunk(const ChunkRegs<D> &c, uint8_t *ktile, uint8_t *vtile, int lane) {
-  using CR = ChunkRegs<D>;
+template <int D, int KB, int VBITS, bool QJL>
+__device__ __forceinline__ void stage_chunk(const ChunkRegs<D, KB, VBITS, QJL> &c, uint8_t *ktile, uint8_t *vtile,
+                                            int lane) {
+  using CR = ChunkRegs<D, KB, VBITS, QJL>;
 #pragma unroll
-  for (int j = 0; j < CR::kPerLane; ++j) {
+  for (int j = 0; j < CR::kPerLaneK; ++j) {
     const int piece = lane + 64 * j;
-    if (j < CR::kPerLane - 1 || piece < CR::kPieces) {
+    if (j < CR::kPerLaneK - 1 || piece < CR::kPiecesK) {
       lds_store8(ktile + 16 * piece, c.k[j].xy);
       lds_store8(ktile + 16 * piece + 8, c.k[j].zw);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < CR::kPerLaneV; ++j) {
+    const int piece = lane + 64 * j;
+    if (j < CR::kPerLaneV - 1 || piece < CR::kPiecesV) {
       lds_store8(vtile + 16 * piece, c.v[j].xy);
       lds_store8(vtile + 16 * piece + 8, c.v[j].zw);
     }
@@ -166,30 +204,34 @@ __device__ __forceinline__ uint32_t qs_dword(const uint8_t *vec, int m, int sub)
 
 }  // namespace
 
-template <int D, int G>
+template <int D, int G, int KB, int VBITS, bool QJL>
 __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(const DecodeArgs a) {
-  constexpr int VB = vector_bytes(D, 4);
+  constexpr int VBK = vector_bytes(D, KB), VBV = vector_bytes(D, VBITS);
   constexpr int KK = D / 16;     // score MFMAs per 16-token tile
   constexpr int NB = D / 16;     // value n-tiles
   constexpr int NSUB = kChunk / kSub;
-  constexpr int TILE = kChunk * VB;
+  constexpr int TILE_K = kChunk * VBK, TILE_V = kChunk * VBV;
+  constexpr int NLK = KB == 4 ? 256 : 16, NLV = VBITS == 4 ? 256 : 16;
+  constexpr int KQ = D / 32;     // QJL MFMAs per 16-token tile (m = d projections)
+  using CR = ChunkRegs<D, KB, VBITS, QJL>;
 
   // One LDS block with the tables first, so their addresses fit the 16-bit
-  // immediate offset of ds_read (the whole block is 80 KB). Per wave: two
+  // immediate offset of ds_read (the 4-bit block is 80 KB). Per wave: two
   // chunk buffers (the chunk being finished and the next one), each a K and a
   // V tile plus their gathered radii.
   struct Smem {
-    uint2 lut_k[256], lut_v[256];
+    uint2 lut_k[NLK], lut_v[NLV], lut_s[QJL ? 16 : 1];
     float red_m[kMWaves][8], red_l[kMWaves][8];
     uint16_t rad[kMWaves][2][2][kChunk];
-    __attribute__((aligned(16))) uint8_t tiles[kMWaves][2][2][TILE + 16];
+    __attribute__((aligned(16))) uint8_t tiles[kMWaves][2][TILE_K + TILE_V + 32];
   };
   __shared__ Smem sm;
-  uint2 *lut_k = sm.lut_k, *lut_v = sm.lut_v;
-  auto &tiles = sm.tiles;
+  uint2 *lut_k = sm.lut_k, *lut_v = sm.lut_v, *lut_s = sm.lut_s;
   auto &rad = sm.rad;
   auto &red_m = sm.red_m;
   auto &red_l = sm.red_l;
+  auto ktile_of = [&](int w, int buf) { return sm.tiles[w][buf]; };
+  auto vtile_of = [&](int w, int buf) { return sm.tiles[w][buf] + TILE_K + 16; };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
@@ -207,12 +249,15 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     kstream = a.k_cache + b * a.k_batch_stride + h * a.k_head_stride;
     vstream = a.v_cache + b * a.v_batch_stride + h * a.v_head_stride;
   }
-  const uint32_t valid_bytes = (uint32_t)a.S * (uint32_t)VB;
-  const __amdgpu_buffer_rsrc_t kres = stream_rsrc(kstream, valid_bytes);
-  const __amdgpu_buffer_rsrc_t vres = stream_rsrc(vstream, valid_bytes);
+  const __amdgpu_buffer_rsrc_t kres = stream_rsrc(kstream, (uint32_t)a.S * (uint32_t)VBK);
+  const __amdgpu_buffer_rsrc_t vres = stream_rsrc(vstream, (uint32_t)a.S * (uint32_t)VBV);
+  __amdgpu_buffer_rsrc_t sres = kres;
+  if constexpr (QJL)
+    sres = stream_rsrc(a.qjl + ((int64_t)(b * a.Hkv + h) * a.S_max) * (D / 8), (uint32_t)a.S * (uint32_t)(D / 8));
 
-  build_lut_pairs(lut_k, a.k_cb + h * a.cb_head_stride, tid);
-  build_lut_pairs(lut_v, a.v_cb + h * a.cb_head_stride, tid);
+  build_lut_pairs<KB>(lut_k, a.k_cb + h * a.cb_head_stride, tid);
+  build_lut_pairs<VBITS>(lut_v, a.v_cb + h * a.cb_head_stride, tid);
+  if constexpr (QJL) build_sign_lut(lut_s, tid);
 
   // q as the B operand of the score product: column col = (head col & 7,
   // part col >> 3); step kk, k = 8grp + i covers coordinate
@@ -221,7 +266,8 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   const int qh = col & 7;
   const bool qlo = col >= 8;
   const float qmask = qh < G ? 1.0f : 0.0f;
-  const float *qrow = a.q + (int64_t)(b * a.Hq + h * G + (qh < G ? qh : 0)) * D;
+  const int64_t qrow_i = (int64_t)(b * a.Hq + h * G + (qh < G ? qh : 0));
+  const float *qrow = a.q + qrow_i * D;
   half8_t qb[KK];
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk) {
@@ -233,6 +279,21 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
       qb[kk][2 * j + 1] = qlo ? vh : (half_t)0.0f;
     }
   }
+  // QJL: pq = P_rot q / m as the B operand of the sign product: step kq,
+  // k = 8grp + i covers projection 32 kq + 8 grp + i; column col < 8 holds
+  // pq_hi of head col, col >= 8 holds pq_lo (x 2^11) of head col - 8.
+  half8_t pb[QJL ? KQ : 1];
+  if constexpr (QJL) {
+    const float *pqrow = a.pq + qrow_i * D;
+#pragma unroll
+    for (int kq = 0; kq < KQ; ++kq)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        half_t vh, vl;
+        split_hi_lo(pqrow[32 * kq + 8 * grp + i] * qmask, &vh, &vl);
+        pb[kq][i] = qlo ? vl : vh;
+      }
+  }
 
   // Running softmax state: lanes with col < 8 own head col (replicated over
   // the four rows).
@@ -241,64 +302,109 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) oacc[nb] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
-  // Value side: lane's coordinate group (qs dword) and, for D = 64, parity.
+  // Value side: the lane's 8 coordinates (D = 128: 8 col .. + 7; D = 64:
+  // 8 (col & 7) .. + 7 with parity col >> 3) as a qs dword (4-bit) or half
+  // dword (2-bit) of each token.
   const int vw = D == 128 ? col : (col & 7);
   const int vpar = D == 128 ? 0 : (col >> 3);
-  const int vob = (vw >> 2) * kPq4BlockBytes + 2 + 4 * (vw & 3);
+  const int vob = VBITS == 4 ? (vw >> 2) * kPq4BlockBytes + 2 + 4 * (vw & 3)
+                             : (vw >> 2) * kPq2BlockBytes + 2 + 2 * (vw & 3);
   const int vob_al = vob & ~3, vsh = vob & 3;
 
-  ChunkRegs<D> cr_;
+  CR cr_;
+  uint32_t sgA[QJL ? NSUB : 1];  // QJL sign bytes of the chunk being scored, in the A layout
   __syncthreads();
 
-  // Stage a chunk (held in registers) into buffer `buf` and gather its radii.
+  // Stage a chunk (held in registers) into buffer `buf`, gather its radii,
+  // and (QJL) move its sign bytes into the A layout: lane (col, grp) of
+  // sub-tile st holds bytes 4 kq + grp of token 16 st + col.
   auto stage = [&](int buf) {
-    stage_chunk<D>(cr_, tiles[wave][buf][0], tiles[wave][buf][1], lane);
-    rad[wave][buf][0][lane] = *(const uint16_t *)(tiles[wave][buf][0] + lane * VB);
-    rad[wave][buf][1][lane] = *(const uint16_t *)(tiles[wave][buf][1] + lane * VB);
+    uint8_t *kt = ktile_of(wave, buf), *vt = vtile_of(wave, buf);
+    stage_chunk<D, KB, VBITS, QJL>(cr_, kt, vt, lane);
+    rad[wave][buf][0][lane] = *(const uint16_t *)(kt + lane * VBK);
+    rad[wave][buf][1][lane] = *(const uint16_t *)(vt + lane * VBV);
+    if constexpr (QJL) {
+#pragma unroll
+      for (int st = 0; st < NSUB; ++st) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int kq = 0; kq < KQ; ++kq) {
+          const uint32_t dw = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (kSub * st + col), (int)cr_.sg[kq]);
+          packed |= ((dw >> (8 * grp)) & 0xFFu) << (8 * kq);
+        }
+        sgA[st] = packed;
+      }
+    }
   };
-  // Scores of the chunk in buffer `buf`: S^T[token][col] per 16-token tile.
-  auto scores = [&](int buf, float4_t (&sacc)[NSUB]) {
-    const uint8_t *ktile = tiles[wave][buf][0];
+  // Scores of the chunk in buffer `buf`, finished to the exp2-domain logit:
+  // s = (D[t][h] + 2^-11 D[t][h + 8]) r_k (+ the QJL term when r_k > 0) for
+  // token 16st + 4grp + i, meaningful in lanes col < G. Lanes of absent heads
+  // (q = 0) and the cross lanes (col >= 8) carry finite values that only
+  // reach discarded output rows.
+  auto scores = [&](int buf, float4_t (&sc)[NSUB]) {
+    const uint8_t *ktile = ktile_of(wave, buf);
+    const uint16_t *rk_lds = rad[wave][buf][0];
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int st = 0; st < NSUB; ++st) {
-      const uint8_t *kv = ktile + (kSub * st + col) * VB;
+      const uint8_t *kv = ktile + (kSub * st + col) * VBK;
       uint2 kt[KK][2];
 #pragma unroll
       for (int m = 0; m < KK / 2; ++m) {
-        const uint32_t w = qs_dword(kv, m, grp);
+        if constexpr (KB == 4) {
+          const uint32_t w = qs_dword(kv, m, grp);
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          kt[2 * m + e][0] = lut_k[(w >> (16 * e)) & 0xFF];
-          kt[2 * m + e][1] = lut_k[(w >> (16 * e + 8)) & 0xFF];
+          for (int e = 0; e < 2; ++e) {
+            kt[2 * m + e][0] = lut_k[(w >> (16 * e)) & 0xFF];
+            kt[2 * m + e][1] = lut_k[(w >> (16 * e + 8)) & 0xFF];
+          }
+        } else {
+          // coordinates 32m + 8grp + 4e .. + 3 are byte e of the qs half
+          // dword at 10m + 2 + 2grp
+          const uint32_t w = *(const uint16_t *)(kv + m * kPq2BlockBytes + 2 + 2 * grp);
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            kt[2 * m + e][0] = lut_k[(w >> (8 * e)) & 0xF];
+            kt[2 * m + e][1] = lut_k[(w >> (8 * e + 4)) & 0xF];
+          }
         }
       }
-      sacc[st] = (float4_t){0.f, 0.f, 0.f, 0.f};
+      float4_t acc = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) sacc[st] = mfma16(pack8(kt[kk][0], kt[kk][1]), qb[kk], sacc[st]);
-    }
-    __builtin_amdgcn_s_setprio(0);
-  };
-  // Softmax update and value product of the chunk in buffer `buf` whose
-  // scores are `sacc`; tokens >= ntok of the chunk are masked.
-  auto finish = [&](int buf, const float4_t (&sacc)[NSUB], int ntok, bool partial) {
-    const uint8_t *vtile = tiles[wave][buf][1];
-    const uint16_t *rk_lds = rad[wave][buf][0], *rv_lds = rad[wave][buf][1];
-    // s = D[t][h] + 2^-11 D[t][h + 8] for token 16st + 4grp + i, meaningful
-    // in lanes col < G. Lanes of absent heads (q = 0) and the cross lanes
-    // (col >= 8) carry finite values that only reach discarded output rows.
-    float sv[NSUB][4];
+      for (int kk = 0; kk < KK; ++kk) acc = mfma16(pack8(kt[kk][0], kt[kk][1]), qb[kk], acc);
+      float4_t accq = (float4_t){0.f, 0.f, 0.f, 0.f};
+      if constexpr (QJL) {
 #pragma unroll
-    for (int st = 0; st < NSUB; ++st) {
+        for (int kq = 0; kq < KQ; ++kq) {
+          const uint32_t byte = (sgA[st] >> (8 * kq)) & 0xFF;
+          accq = mfma16(pack8(lut_s[byte & 15], lut_s[byte >> 4]), pb[kq], accq);
+        }
+      }
       const uint2 rk4 = *(const uint2 *)&rk_lds[kSub * st + 4 * grp];
       const uint32_t rkw[2] = {rk4.x, rk4.y};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float cross = row_ror8f(sacc[st][i]);
         const float rk = half_bits_to_float(rkw[i >> 1] >> (16 * (i & 1)));
-        sv[st][i] = __builtin_fmaf(cross, 1.0f / kLoScale, sacc[st][i]) * rk;
+        float v = __builtin_fmaf(row_ror8f(acc[i]), 1.0f / kLoScale, acc[i]) * rk;
+        if constexpr (QJL) {
+          const float q = __builtin_fmaf(row_ror8f(accq[i]), 1.0f / kLoScale, accq[i]);
+          v = rk > 0.0f ? v + q : v;  // zero keys get no correction
+        }
+        sc[st][i] = v;
       }
     }
+    __builtin_amdgcn_s_setprio(0);
+  };
+  // Softmax update and value product of the chunk in buffer `buf` whose
+  // logits are `sc`; tokens >= ntok of the chunk are masked.
+  auto finish = [&](int buf, const float4_t (&sc)[NSUB], int ntok, bool partial) {
+    const uint8_t *vtile = vtile_of(wave, buf);
+    const uint16_t *rv_lds = rad[wave][buf][1];
+    float sv[NSUB][4];
+#pragma unroll
+    for (int st = 0; st < NSUB; ++st)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[st][i] = sc[st][i];
     if (partial) {
 #pragma unroll
       for (int st = 0; st < NSUB; ++st)
@@ -336,28 +442,46 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     float psum = 0.0f;
 #pragma unroll
     for (int kb = 0; kb < NSUB; ++kb) {
-      // value-side entries: two tokens' nibbles of the lane's coordinate
-      // interleaved into one byte (token pairs (0,1) and (2,3))
-      uint32_t wv[4];
+      // value-side entries: two tokens' codes of the lane's coordinate
+      // interleaved into one byte (4-bit) or nibble (2-bit), token pairs
+      // (0,1) and (2,3)
+      uint32_t x01, y01, x23, y23;
+      if constexpr (VBITS == 4) {
+        uint32_t wv[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t *pv = (const uint32_t *)(vtile + (kSub * kb + 4 * grp + e) * VB + vob_al);
-        wv[e] = align_bytes(pv[1], pv[0], vsh);
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t *pv = (const uint32_t *)(vtile + (kSub * kb + 4 * grp + e) * VBV + vob_al);
+          wv[e] = align_bytes(pv[1], pv[0], vsh);
+        }
+        // byte k of x = even coordinate 2k of both tokens, of y = odd 2k + 1
+        x01 = (wv[0] & 0x0F0F0F0Fu) | ((wv[1] << 4) & 0xF0F0F0F0u);
+        y01 = ((wv[0] >> 4) & 0x0F0F0F0Fu) | (wv[1] & 0xF0F0F0F0u);
+        x23 = (wv[2] & 0x0F0F0F0Fu) | ((wv[3] << 4) & 0xF0F0F0F0u);
+        y23 = ((wv[2] >> 4) & 0x0F0F0F0Fu) | (wv[3] & 0xF0F0F0F0u);
+      } else {
+        uint32_t wv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wv[e] = *(const uint16_t *)(vtile + (kSub * kb + 4 * grp + e) * VBV + vob);
+        // nibble k of x = even coordinate 2k of both tokens, of y = odd 2k + 1
+        x01 = (wv[0] & 0x3333u) | ((wv[1] << 2) & 0xCCCCu);
+        y01 = ((wv[0] >> 2) & 0x3333u) | (wv[1] & 0xCCCCu);
+        x23 = (wv[2] & 0x3333u) | ((wv[3] << 2) & 0xCCCCu);
+        y23 = ((wv[2] >> 2) & 0x3333u) | (wv[3] & 0xCCCCu);
       }
-      // byte k of x = even coordinate 2k of both tokens, of y = odd 2k + 1
-      const uint32_t x01 = (wv[0] & 0x0F0F0F0Fu) | ((wv[1] << 4) & 0xF0F0F0F0u);
-      const uint32_t y01 = ((wv[0] >> 4) & 0x0F0F0F0Fu) | (wv[1] & 0xF0F0F0F0u);
-      const uint32_t x23 = (wv[2] & 0x0F0F0F0Fu) | ((wv[3] << 4) & 0xF0F0F0F0u);
-      const uint32_t y23 = ((wv[2] >> 4) & 0x0F0F0F0Fu) | (wv[3] & 0xF0F0F0F0u);
       uint2 vt[NB][2];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        // D = 128: n-tile nb is nibble nb of dword col (coordinate 8*col + nb).
+        // D = 128: n-tile nb is coordinate 8*col + nb of the lane's group.
         // D = 64: n-tile nb is coordinate 8*(col & 7) + 2*nb + (col >> 3).
         const int par = D == 128 ? (nb & 1) : vpar;
-        const int byte = D == 128 ? (nb >> 1) : nb;
-        vt[nb][0] = lut_v[((par ? y01 : x01) >> (8 * byte)) & 0xFF];
-        vt[nb][1] = lut_v[((par ? y23 : x23) >> (8 * byte)) & 0xFF];
+        const int sub = D == 128 ? (nb >> 1) : nb;
+        if constexpr (VBITS == 4) {
+          vt[nb][0] = lut_v[((par ? y01 : x01) >> (8 * sub)) & 0xFF];
+          vt[nb][1] = lut_v[((par ? y23 : x23) >> (8 * sub)) & 0xFF];
+        } else {
+          vt[nb][0] = lut_v[((par ? y01 : x01) >> (4 * sub)) & 0xF];
+          vt[nb][1] = lut_v[((par ? y23 : x23) >> (4 * sub)) & 0xF];
+        }
       }
       // weights p * r_v in the A layout: col < 8 -> (p_hi, 0), col >= 8 ->
       // (p_lo, p_hi) of head col - 8, taken from lane col - 8.
@@ -390,9 +514,9 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   const int first = t_begin + wave * kChunk;
   const int nch = first < t_end ? (t_end - first + kStep - 1) / kStep : 0;
   if (nch > 0) {
-    load_chunk<D>(cr_, kres, vres, first, lane);
+    load_chunk<D, KB, VBITS, QJL>(cr_, kres, vres, sres, first, lane);
     stage(0);
-    if (nch > 1) load_chunk<D>(cr_, kres, vres, first + kStep, lane);
+    if (nch > 1) load_chunk<D, KB, VBITS, QJL>(cr_, kres, vres, sres, first + kStep, lane);
     float4_t sacc[NSUB];
     scores(0, sacc);
     for (int i = 0; i + 1 < nch; ++i) {
@@ -400,7 +524,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
       stage(nxt);
       // chunk i + 2 (a repeat of the last chunk past the end: an L2 hit)
       const int tl = first + min(i + 2, nch - 1) * kStep;
-      load_chunk<D>(cr_, kres, vres, tl, lane);
+      load_chunk<D, KB, VBITS, QJL>(cr_, kres, vres, sres, tl, lane);
       float4_t snext[NSUB];
       scores(nxt, snext);
       finish(i & 1, sacc, kChunk, false);
@@ -419,7 +543,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     red_l[wave][lane] = l_run;
   }
   // O[head][coord] = D[head] + 2^-11 D[head + 8]: rows 8-15 sit 32 lanes up.
-  float *red_o = (float *)tiles[wave][0];  // this wave's tile is free now
+  float *red_o = (float *)ktile_of(wave, 0);  // this wave's tile is free now
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -444,7 +568,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     for (int w = 0; w < kMWaves; ++w) {
       const float sc = red_m[w][hh] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w][hh] - mx);
       L += red_l[w][hh] * sc;
-      O += ((const float *)tiles[w][0])[hh * D + c] * sc;
+      O += ((const float *)ktile_of(w, 0))[hh * D + c] * sc;
     }
     float *dst = a.part + (((int64_t)(b * a.Hq + h * G + hh) * a.splits) + split) * (D + 2);
     if (c == 0) {
@@ -455,25 +579,39 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   }
 }
 
-template <int D>
+template <int D, int KB, int VBITS, bool QJL>
 static void launch_dm(const DecodeArgs &a, int G, hipStream_t s) {
   dim3 grid(a.splits, a.B * a.n_heads);
   switch (G) {
-    case 1: decode_mfma_kernel<D, 1><<<grid, 256, 0, s>>>(a); break;
-    case 2: decode_mfma_kernel<D, 2><<<grid, 256, 0, s>>>(a); break;
-    case 3: decode_mfma_kernel<D, 3><<<grid, 256, 0, s>>>(a); break;
-    case 4: decode_mfma_kernel<D, 4><<<grid, 256, 0, s>>>(a); break;
-    case 5: decode_mfma_kernel<D, 5><<<grid, 256, 0, s>>>(a); break;
-    case 6: decode_mfma_kernel<D, 6><<<grid, 256, 0, s>>>(a); break;
-    case 7: decode_mfma_kernel<D, 7><<<grid, 256, 0, s>>>(a); break;
-    default: decode_mfma_kernel<D, 8><<<grid, 256, 0, s>>>(a); break;
+    case 1: decode_mfma_kernel<D, 1, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
+    case 2: decode_mfma_kernel<D, 2, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
+    case 3: decode_mfma_kernel<D, 3, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
+    case 4: decode_mfma_kernel<D, 4, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
+    case 5: decode_mfma_kernel<D, 5, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
+    case 6: decode_mfma_kernel<D, 6, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
+    case 7: decode_mfma_kernel<D, 7, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
+    default: decode_mfma_kernel<D, 8, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
   }
 }
 
-hipError_t launch_decode_mfma(const DecodeArgs &a, hipStream_t s) {
+template <int D, int KB, int VBITS>
+static void launch_dm_q(const DecodeArgs &a, int G, hipStream_t s) {
+  if (a.qjl != nullptr) launch_dm<D, KB, VBITS, true>(a, G, s);
+  else launch_dm<D, KB, VBITS, false>(a, G, s);
+}
+
+template <int D>
+static void launch_dm_w(const DecodeArgs &a, int k_bits, int v_bits, int G, hipStream_t s) {
+  if (k_bits == 4 && v_bits == 4) launch_dm_q<D, 4, 4>(a, G, s);
+  else if (k_bits == 4) launch_dm_q<D, 4, 2>(a, G, s);
+  else if (v_bits == 4) launch_dm_q<D, 2, 4>(a, G, s);
+  else launch_dm_q<D, 2, 2>(a, G, s);
+}
+
+hipError_t launch_decode_mfma(const DecodeArgs &a, int k_bits, int v_bits, hipStream_t s) {
   const int G = a.Hq / a.Hkv;
-  if (a.d == 128) launch_dm<128>(a, G, s);
-  else launch_dm<64>(a, G, s);
+  if (a.d == 128) launch_dm_w<128>(a, k_bits, v_bits, G, s);
+  else launch_dm_w<64>(a, k_bits, v_bits, G, s);
   return hipGetLastError();
 }
 

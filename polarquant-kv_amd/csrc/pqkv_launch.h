@@ -87,8 +87,9 @@ hipError_t launch_blocks_to_soa(const uint8_t *blocks, uint8_t *packed, float *r
                                 hipStream_t s);
 
 hipError_t launch_decode_split(const DecodeArgs &a, int k_bits, int v_bits, hipStream_t s);
-// Matrix-core variant for 4-bit keys and values without QJL (same workspace).
-hipError_t launch_decode_mfma(const DecodeArgs &a, hipStream_t s);
+// Matrix-core variant for 2- and 4-bit keys and values, with or without QJL
+// (same workspace).
+hipError_t launch_decode_mfma(const DecodeArgs &a, int k_bits, int v_bits, hipStream_t s);
 hipError_t launch_decode_merge(const float *part, const float *R, void *out, int out_dtype, int BHq, int splits,
                                int d, hipStream_t s);
 hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t s);
