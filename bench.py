@@ -115,7 +115,7 @@ def decode_kernel_name(d: int) -> str:
     """The split kernel pqkv_decode_attn launches for a uniform PQ4 cache."""
     if os.environ.get("PQKV_DECODE_KERNEL", "") == "valu":
         return f"decode_split_kernel<{d},4,4,4>"
-    return f"decode_mfma_kernel<{d},4>"
+    return f"decode_mfma_kernel<{d},4,4,4>"
 
 
 def committed_traffic(kernel: str):
@@ -357,13 +357,13 @@ def run_config4(args) -> int:
         "metric": "decode-attn GB/s at 1 MI355X (low-bit + QJL)", "value": v["GB_per_s"], "unit": "GB/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": v["ms_per_step"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "u2/u4 codes + 1-bit QJL signs; f32 FMA", "data": "synthetic",
+        "dtype": "u2/u4 codes + 1-bit QJL signs; f16 hi/lo MFMA, f32 accumulate", "data": "synthetic",
         "config": {"workload": "config4: Llama-3-8B layer decode, B=4 Hq=32 Hkv=8 d=128 S=16384, QJL keys m=128 "
                                "(P seed 43); variants 2bit (block_pq2 K+V) and mixed (kv heads 0-3 PQ4, 4-7 PQ2)",
                    "global_batch": B, "seq_len": S, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": v["split_GB_per_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(v["split_GB_per_s"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode_split_kernel<128,4,2,2,qjl>", "kernel_ms": v["split_ms"]},
+                     "kernel": "decode_mfma_kernel<128,4,2,2,qjl>", "kernel_ms": v["split_ms"]},
         "variants": res, "cpu_baseline": None,
     }
     print(json.dumps(line))
