@@ -37,9 +37,13 @@
 // second product on the matrix cores: A = the signs as +-1 (a 16-entry table
 // maps 4 sign bits to 4 halves), B = pq as (hi | lo) columns, 32 projections
 // per MFMA.
-// Cross-lane steps use DPP row rotations and the gfx950 permlane16/32 swaps
-// (VALU); LDS carries the chunk tiles and the tables, and ds_bpermute moves
-// the sign bytes (and the rare rescale factors) between lanes.
+// Operands come straight from HBM in MFMA lane order (no LDS staging): a key
+// lane loads its lane group's qs bytes of one token (lane group grp owns
+// coordinates grp*D/4 .. grp*D/4 + D/4 - 1, so they are contiguous), a value
+// lane its qs word of four tokens, and each lane one radius that DPP row
+// broadcasts hand to the lanes of its score rows. LDS holds only the code
+// tables. Cross-lane steps use DPP row rotations / broadcasts and the gfx950
+// permlane16/32 swaps (VALU); ds_bpermute moves the rare rescale factors.
 #include "pqkv_device.h"
 #include "pqkv_launch.h"
 
@@ -125,82 +129,77 @@ __device__ __forceinline__ float rows_sum(float x) {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t stream_rsrc(const uint8_t *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
 }
-__device__ __forceinline__ u32x4 bld128(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+__device__ __forceinline__ uint32_t bld32(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t bld16(__amdgpu_buffer_rsrc_t r, int off) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
 }
 
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) volatile u32x2 lds_u32x2;
+// N consecutive dwords at the dword-aligned byte offset `off`.
+template <int N>
+__device__ __forceinline__ void load_words(__amdgpu_buffer_rsrc_t r, int off, uint32_t (&w)[N]) {
+  typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+  typedef uint32_t u32x3v __attribute__((ext_vector_type(3)));
+  if constexpr (N == 5) {
+    const u32x4 x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
+    w[4] = bld32(r, off + 16);
+  } else if constexpr (N == 3) {
+    const u32x3v x = __builtin_bit_cast(u32x3v, __builtin_amdgcn_raw_buffer_load_b96(r, off, 0, 0));
+    w[0] = x.x; w[1] = x.y; w[2] = x.z;
+  } else {
+    static_assert(N == 2, "operand word count");
+    const u32x2v x = __builtin_bit_cast(u32x2v, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+    w[0] = x.x; w[1] = x.y;
+  }
+}
 
-// 8-byte LDS store the compiler neither merges nor turns into a flat store.
-__device__ __forceinline__ void lds_store8(uint8_t *p, u32x2 v) { *(lds_u32x2 *)p = v; }
+// Lane n of each 16-lane row to the whole row (DPP row_newbcast:n); n must
+// fold to a constant after unrolling.
+template <int N>
+__device__ __forceinline__ float row_bcast_c(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x150 + N, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_bcast(float x, int n) {
+  switch (n) {
+    case 0: return row_bcast_c<0>(x);   case 1: return row_bcast_c<1>(x);
+    case 2: return row_bcast_c<2>(x);   case 3: return row_bcast_c<3>(x);
+    case 4: return row_bcast_c<4>(x);   case 5: return row_bcast_c<5>(x);
+    case 6: return row_bcast_c<6>(x);   case 7: return row_bcast_c<7>(x);
+    case 8: return row_bcast_c<8>(x);   case 9: return row_bcast_c<9>(x);
+    case 10: return row_bcast_c<10>(x); case 11: return row_bcast_c<11>(x);
+    case 12: return row_bcast_c<12>(x); case 13: return row_bcast_c<13>(x);
+    case 14: return row_bcast_c<14>(x); default: return row_bcast_c<15>(x);
+  }
+}
 
-// One 64-token chunk of K and V as contiguous 16-byte pieces: lane l holds
-// pieces l + 64 j of each; with QJL, also token l's sign bytes.
-template <int D, int KB, int VBITS, bool QJL>
-struct ChunkRegs {
-  static constexpr int kBytesK = kChunk * vector_bytes(D, KB);
-  static constexpr int kBytesV = kChunk * vector_bytes(D, VBITS);
-  static constexpr int kPiecesK = kBytesK / 16, kPiecesV = kBytesV / 16;
-  static constexpr int kPerLaneK = (kPiecesK + 63) / 64, kPerLaneV = (kPiecesV + 63) / 64;
-  static constexpr int kSignDw = QJL ? D / 32 : 1;  // m = d sign bits per token
-  u32x4 k[kPerLaneK], v[kPerLaneV];
-  uint32_t sg[kSignDw];
+constexpr int kNSub = kChunk / kSub;
+
+// One 64-token chunk of keys in operand order, straight from HBM. For
+// sub-tile st, lane (col, grp) holds the qs bytes of coordinates
+// grp*D/4 .. grp*D/4 + D/4 - 1 of token 16 st + col: kWords dwords that start
+// 2 bytes (qs start 2 mod 4) or 4 bytes (qs start dword-aligned) before them,
+// so every load stays inside its own vector and one byte permute per word
+// aligns them. r: the radius of token 16 (col / 4) + 4 grp + col % 4 (row
+// broadcasts hand each lane those of its score rows). sg (QJL): sign bytes
+// grp*D/32 .. of token 16 st + col.
+template <int D, int KB, bool QJL>
+struct ChunkK {
+  static constexpr int kWords = D * KB / 128 + 1;
+  uint32_t w[kNSub][kWords];
+  uint32_t r;
+  uint32_t sg[QJL ? kNSub : 1];
 };
-
-template <int D, int KB, int VBITS, bool QJL>
-__device__ __forceinline__ void load_chunk(ChunkRegs<D, KB, VBITS, QJL> &c, __amdgpu_buffer_rsrc_t kr,
-                                           __amdgpu_buffer_rsrc_t vr, __amdgpu_buffer_rsrc_t sr, int t0, int lane) {
-  using CR = ChunkRegs<D, KB, VBITS, QJL>;
-  const int kbase = t0 * vector_bytes(D, KB), vbase = t0 * vector_bytes(D, VBITS);
-  // Every lane loads its last piece too, also past the chunk (the next
-  // tokens' bytes, or zeros past the stream): a conditional load here makes
-  // the compiler keep the piece array in scratch. Only the LDS stores are
-  // limited to the chunk.
-#pragma unroll
-  for (int j = 0; j < CR::kPerLaneK; ++j) c.k[j] = bld128(kr, kbase + 16 * (lane + 64 * j));
-#pragma unroll
-  for (int j = 0; j < CR::kPerLaneV; ++j) c.v[j] = bld128(vr, vbase + 16 * (lane + 64 * j));
-  if constexpr (QJL) {
-    const int sbase = (t0 + lane) * (D / 8);
-#pragma unroll
-    for (int j = 0; j < CR::kSignDw; ++j)
-      c.sg[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(sr, sbase + 4 * j, 0, 0));
-  }
-}
-
-// LDS tiles keep the HBM byte layout. 8-byte stores run at the full LDS rate
-// (16-byte ones at half); volatile keeps the compiler from merging them.
-template <int D, int KB, int VBITS, bool QJL>
-__device__ __forceinline__ void stage_chunk(const ChunkRegs<D, KB, VBITS, QJL> &c, uint8_t *ktile, uint8_t *vtile,
-                                            int lane) {
-  using CR = ChunkRegs<D, KB, VBITS, QJL>;
-#pragma unroll
-  for (int j = 0; j < CR::kPerLaneK; ++j) {
-    const int piece = lane + 64 * j;
-    if (j < CR::kPerLaneK - 1 || piece < CR::kPiecesK) {
-      lds_store8(ktile + 16 * piece, c.k[j].xy);
-      lds_store8(ktile + 16 * piece + 8, c.k[j].zw);
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < CR::kPerLaneV; ++j) {
-    const int piece = lane + 64 * j;
-    if (j < CR::kPerLaneV - 1 || piece < CR::kPiecesV) {
-      lds_store8(vtile + 16 * piece, c.v[j].xy);
-      lds_store8(vtile + 16 * piece + 8, c.v[j].zw);
-    }
-  }
-}
-
-// qs dword holding coordinates 32m + 8*sub .. +7 (sub = 0..3) of one vector:
-// byte offset 18m + 2 + 4 sub, misaligned by two bytes when m is even.
-__device__ __forceinline__ uint32_t qs_dword(const uint8_t *vec, int m, int sub) {
-  const int off = m * kPq4BlockBytes + 2 + 4 * sub;
-  if (m & 1) return *(const uint32_t *)(vec + off);
-  const uint32_t *p = (const uint32_t *)(vec + off - 2);
-  return align_bytes(p[1], p[0], 2);
-}
+// Values: for sub-tile kb and e = 0..3, the lane's qs word of token
+// 16 kb + 4 grp + e (4-bit: the two dwords around it, aligned as for keys;
+// 2-bit: the half dword). r as for keys.
+template <int VBITS>
+struct ChunkV {
+  static constexpr int kWords = VBITS == 4 ? 2 : 1;
+  uint32_t w[kNSub][4][kWords];
+  uint32_t r;
+};
 
 }  // namespace
 
@@ -209,29 +208,23 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   constexpr int VBK = vector_bytes(D, KB), VBV = vector_bytes(D, VBITS);
   constexpr int KK = D / 16;     // score MFMAs per 16-token tile
   constexpr int NB = D / 16;     // value n-tiles
-  constexpr int NSUB = kChunk / kSub;
-  constexpr int TILE_K = kChunk * VBK, TILE_V = kChunk * VBV;
+  constexpr int NSUB = kNSub;
   constexpr int NLK = KB == 4 ? 256 : 16, NLV = VBITS == 4 ? 256 : 16;
   constexpr int KQ = D / 32;     // QJL MFMAs per 16-token tile (m = d projections)
-  using CR = ChunkRegs<D, KB, VBITS, QJL>;
+  using CK = ChunkK<D, KB, QJL>;
+  using CV = ChunkV<VBITS>;
 
-  // One LDS block with the tables first, so their addresses fit the 16-bit
-  // immediate offset of ds_read (the 4-bit block is 80 KB). Per wave: two
-  // chunk buffers (the chunk being finished and the next one), each a K and a
-  // V tile plus their gathered radii.
+  // LDS holds only the code tables and the end-of-split reduction: the
+  // operands come straight from HBM in the lane order the MFMAs want.
   struct Smem {
     uint2 lut_k[NLK], lut_v[NLV], lut_s[QJL ? 16 : 1];
     float red_m[kMWaves][8], red_l[kMWaves][8];
-    uint16_t rad[kMWaves][2][2][kChunk];
-    __attribute__((aligned(16))) uint8_t tiles[kMWaves][2][TILE_K + TILE_V + 32];
+    float red_o[kMWaves][G * D];
   };
   __shared__ Smem sm;
   uint2 *lut_k = sm.lut_k, *lut_v = sm.lut_v, *lut_s = sm.lut_s;
-  auto &rad = sm.rad;
   auto &red_m = sm.red_m;
   auto &red_l = sm.red_l;
-  auto ktile_of = [&](int w, int buf) { return sm.tiles[w][buf]; };
-  auto vtile_of = [&](int w, int buf) { return sm.tiles[w][buf] + TILE_K + 16; };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
@@ -261,7 +254,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
 
   // q as the B operand of the score product: column col = (head col & 7,
   // part col >> 3); step kk, k = 8grp + i covers coordinate
-  // 32(kk/2) + 8grp + 4(kk%2) + i/2, part i%2:
+  // grp*D/4 + 4kk + i/2 (the lane group's coordinate range), part i%2:
   //   col < 8 : (q_hi, 0)        col >= 8 : (q_lo, q_hi)
   const int qh = col & 7;
   const bool qlo = col >= 8;
@@ -274,14 +267,15 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       half_t vh, vl;
-      split_hi_lo(qrow[32 * (kk >> 1) + 8 * grp + 4 * (kk & 1) + j] * qmask, &vh, &vl);
+      split_hi_lo(qrow[grp * (D / 4) + 4 * kk + j] * qmask, &vh, &vl);
       qb[kk][2 * j] = qlo ? vl : vh;
       qb[kk][2 * j + 1] = qlo ? vh : (half_t)0.0f;
     }
   }
   // QJL: pq = P_rot q / m as the B operand of the sign product: step kq,
-  // k = 8grp + i covers projection 32 kq + 8 grp + i; column col < 8 holds
-  // pq_hi of head col, col >= 8 holds pq_lo (x 2^11) of head col - 8.
+  // k = 8grp + i covers projection grp*D/4 + 8 kq + i (sign byte kq of the
+  // lane's piece); column col < 8 holds pq_hi of head col, col >= 8 holds
+  // pq_lo (x 2^11) of head col - 8.
   half8_t pb[QJL ? KQ : 1];
   if constexpr (QJL) {
     const float *pqrow = a.pq + qrow_i * D;
@@ -290,7 +284,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         half_t vh, vl;
-        split_hi_lo(pqrow[32 * kq + 8 * grp + i] * qmask, &vh, &vl);
+        split_hi_lo(pqrow[grp * (D / 4) + 8 * kq + i] * qmask, &vh, &vl);
         pb[kq][i] = qlo ? vl : vh;
       }
   }
@@ -302,6 +296,13 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) oacc[nb] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
+  // Key side: the lane group's qs bytes start kphys bytes into the vector
+  // (2 mod 4 or 0 mod 4); the loaded words start 2 or 4 bytes earlier and
+  // a byte permute with ksel aligns them.
+  const int kc0 = grp * (D / 4);
+  const int kphys = (kc0 / kBlock) * block_bytes(KB) + 2 + (kc0 % kBlock) * KB / 8;
+  const int koff = kphys - ((kphys & 3) ? 2 : 4);
+  const uint32_t ksel = (kphys & 3) ? 0x05040302u : 0x07060504u;
   // Value side: the lane's 8 coordinates (D = 128: 8 col .. + 7; D = 64:
   // 8 (col & 7) .. + 7 with parity col >> 3) as a qs dword (4-bit) or half
   // dword (2-bit) of each token.
@@ -309,64 +310,66 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   const int vpar = D == 128 ? 0 : (col >> 3);
   const int vob = VBITS == 4 ? (vw >> 2) * kPq4BlockBytes + 2 + 4 * (vw & 3)
                              : (vw >> 2) * kPq2BlockBytes + 2 + 2 * (vw & 3);
-  const int vob_al = vob & ~3, vsh = vob & 3;
+  const int voff = VBITS == 4 ? vob - ((vob & 3) ? 2 : 4) : vob;
+  const uint32_t vsel = (vob & 3) ? 0x05040302u : 0x07060504u;
+  // token (relative to the chunk) whose radii this lane loads
+  const int rtok = kSub * (col >> 2) + 4 * grp + (col & 3);
 
-  CR cr_;
-  uint32_t sgA[QJL ? NSUB : 1];  // QJL sign bytes of the chunk being scored, in the A layout
-  __syncthreads();
-
-  // Stage a chunk (held in registers) into buffer `buf`, gather its radii,
-  // and (QJL) move its sign bytes into the A layout: lane (col, grp) of
-  // sub-tile st holds bytes 4 kq + grp of token 16 st + col.
-  auto stage = [&](int buf) {
-    uint8_t *kt = ktile_of(wave, buf), *vt = vtile_of(wave, buf);
-    stage_chunk<D, KB, VBITS, QJL>(cr_, kt, vt, lane);
-    rad[wave][buf][0][lane] = *(const uint16_t *)(kt + lane * VBK);
-    rad[wave][buf][1][lane] = *(const uint16_t *)(vt + lane * VBV);
+  // Every load is unconditional (tokens past S read zeros); a conditional
+  // load makes the compiler keep the register array in scratch.
+  auto load_k = [&](CK &c, int t0) {
+#pragma unroll
+    for (int st = 0; st < NSUB; ++st) load_words(kres, (t0 + kSub * st + col) * VBK + koff, c.w[st]);
+    c.r = bld16(kres, (t0 + rtok) * VBK);
     if constexpr (QJL) {
 #pragma unroll
       for (int st = 0; st < NSUB; ++st) {
-        uint32_t packed = 0;
-#pragma unroll
-        for (int kq = 0; kq < KQ; ++kq) {
-          const uint32_t dw = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (kSub * st + col), (int)cr_.sg[kq]);
-          packed |= ((dw >> (8 * grp)) & 0xFFu) << (8 * kq);
-        }
-        sgA[st] = packed;
+        const int so = (t0 + kSub * st + col) * (D / 8) + grp * (D / 32);
+        c.sg[st] = D == 128 ? bld32(sres, so) : bld16(sres, so);
       }
     }
   };
-  // Scores of the chunk in buffer `buf`, finished to the exp2-domain logit:
+  auto load_v = [&](CV &c, int t0) {
+#pragma unroll
+    for (int kb = 0; kb < NSUB; ++kb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int off = (t0 + kSub * kb + 4 * grp + e) * VBV + voff;
+        if constexpr (VBITS == 4) load_words(vres, off, c.w[kb][e]);
+        else c.w[kb][e][0] = bld16(vres, off);
+      }
+    c.r = bld16(vres, (t0 + rtok) * VBV);
+  };
+  __syncthreads();
+
+  // Scores of the chunk held in `k`, finished to the exp2-domain logit:
   // s = (D[t][h] + 2^-11 D[t][h + 8]) r_k (+ the QJL term when r_k > 0) for
   // token 16st + 4grp + i, meaningful in lanes col < G. Lanes of absent heads
   // (q = 0) and the cross lanes (col >= 8) carry finite values that only
   // reach discarded output rows.
-  auto scores = [&](int buf, float4_t (&sc)[NSUB]) {
-    const uint8_t *ktile = ktile_of(wave, buf);
-    const uint16_t *rk_lds = rad[wave][buf][0];
+  auto scores = [&](const CK &k, float4_t (&sc)[NSUB]) {
+    const float rkl = half_bits_to_float(k.r);
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int st = 0; st < NSUB; ++st) {
-      const uint8_t *kv = ktile + (kSub * st + col) * VBK;
+      // the lane group's qs words of token 16st + col
+      uint32_t qw[CK::kWords - 1];
+#pragma unroll
+      for (int i = 0; i + 1 < CK::kWords; ++i) qw[i] = __builtin_amdgcn_perm(k.w[st][i + 1], k.w[st][i], ksel);
       uint2 kt[KK][2];
 #pragma unroll
-      for (int m = 0; m < KK / 2; ++m) {
+      for (int kk = 0; kk < KK; ++kk) {
+        // step kk: coordinates 4kk .. 4kk + 3 of the lane group's range
         if constexpr (KB == 4) {
-          const uint32_t w = qs_dword(kv, m, grp);
-#pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            kt[2 * m + e][0] = lut_k[(w >> (16 * e)) & 0xFF];
-            kt[2 * m + e][1] = lut_k[(w >> (16 * e + 8)) & 0xFF];
-          }
+          const uint32_t w = qw[kk >> 1];
+          const int e = kk & 1;
+          kt[kk][0] = lut_k[(w >> (16 * e)) & 0xFF];
+          kt[kk][1] = lut_k[(w >> (16 * e + 8)) & 0xFF];
         } else {
-          // coordinates 32m + 8grp + 4e .. + 3 are byte e of the qs half
-          // dword at 10m + 2 + 2grp
-          const uint32_t w = *(const uint16_t *)(kv + m * kPq2BlockBytes + 2 + 2 * grp);
-#pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            kt[2 * m + e][0] = lut_k[(w >> (8 * e)) & 0xF];
-            kt[2 * m + e][1] = lut_k[(w >> (8 * e + 4)) & 0xF];
-          }
+          const uint32_t w = qw[kk >> 2];
+          const int e = kk & 3;
+          kt[kk][0] = lut_k[(w >> (8 * e)) & 0xF];
+          kt[kk][1] = lut_k[(w >> (8 * e + 4)) & 0xF];
         }
       }
       float4_t acc = (float4_t){0.f, 0.f, 0.f, 0.f};
@@ -376,15 +379,13 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
       if constexpr (QJL) {
 #pragma unroll
         for (int kq = 0; kq < KQ; ++kq) {
-          const uint32_t byte = (sgA[st] >> (8 * kq)) & 0xFF;
+          const uint32_t byte = (k.sg[st] >> (8 * kq)) & 0xFF;
           accq = mfma16(pack8(lut_s[byte & 15], lut_s[byte >> 4]), pb[kq], accq);
         }
       }
-      const uint2 rk4 = *(const uint2 *)&rk_lds[kSub * st + 4 * grp];
-      const uint32_t rkw[2] = {rk4.x, rk4.y};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float rk = half_bits_to_float(rkw[i >> 1] >> (16 * (i & 1)));
+        const float rk = row_bcast(rkl, 4 * st + i);  // radius of token 16st + 4grp + i
         float v = __builtin_fmaf(row_ror8f(acc[i]), 1.0f / kLoScale, acc[i]) * rk;
         if constexpr (QJL) {
           const float q = __builtin_fmaf(row_ror8f(accq[i]), 1.0f / kLoScale, accq[i]);
@@ -395,11 +396,10 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     }
     __builtin_amdgcn_s_setprio(0);
   };
-  // Softmax update and value product of the chunk in buffer `buf` whose
-  // logits are `sc`; tokens >= ntok of the chunk are masked.
-  auto finish = [&](int buf, const float4_t (&sc)[NSUB], int ntok, bool partial) {
-    const uint8_t *vtile = vtile_of(wave, buf);
-    const uint16_t *rv_lds = rad[wave][buf][1];
+  // Softmax update and value product of the chunk whose values are in `v`
+  // and whose logits are `sc`; tokens >= ntok of the chunk are masked.
+  auto finish = [&](const CV &v, const float4_t (&sc)[NSUB], int ntok, bool partial) {
+    const float rvl = half_bits_to_float(v.r);
     float sv[NSUB][4];
 #pragma unroll
     for (int st = 0; st < NSUB; ++st)
@@ -449,10 +449,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
       if constexpr (VBITS == 4) {
         uint32_t wv[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t *pv = (const uint32_t *)(vtile + (kSub * kb + 4 * grp + e) * VBV + vob_al);
-          wv[e] = align_bytes(pv[1], pv[0], vsh);
-        }
+        for (int e = 0; e < 4; ++e) wv[e] = __builtin_amdgcn_perm(v.w[kb][e][1], v.w[kb][e][0], vsel);
         // byte k of x = even coordinate 2k of both tokens, of y = odd 2k + 1
         x01 = (wv[0] & 0x0F0F0F0Fu) | ((wv[1] << 4) & 0xF0F0F0F0u);
         y01 = ((wv[0] >> 4) & 0x0F0F0F0Fu) | (wv[1] & 0xF0F0F0F0u);
@@ -461,7 +458,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
       } else {
         uint32_t wv[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) wv[e] = *(const uint16_t *)(vtile + (kSub * kb + 4 * grp + e) * VBV + vob);
+        for (int e = 0; e < 4; ++e) wv[e] = v.w[kb][e][0];
         // nibble k of x = even coordinate 2k of both tokens, of y = odd 2k + 1
         x01 = (wv[0] & 0x3333u) | ((wv[1] << 2) & 0xCCCCu);
         y01 = ((wv[0] >> 2) & 0x3333u) | (wv[1] & 0xCCCCu);
@@ -485,15 +482,13 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
       }
       // weights p * r_v in the A layout: col < 8 -> (p_hi, 0), col >= 8 ->
       // (p_lo, p_hi) of head col - 8, taken from lane col - 8.
-      const uint2 rv4 = *(const uint2 *)&rv_lds[kSub * kb + 4 * grp];
-      const uint32_t rvw[2] = {rv4.x, rv4.y};
       uint32_t pa[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float p = __builtin_amdgcn_exp2f(sv[kb][i] - mnew);
         psum += p;
         half_t ph, pl;
-        split_hi_lo(p * half_bits_to_float(rvw[i >> 1] >> (16 * (i & 1))), &ph, &pl);
+        split_hi_lo(p * row_bcast(rvl, 4 * kb + i), &ph, &pl);  // r_v of token 16kb + 4grp + i
         const uint32_t top = pack_h2(ph, (half_t)0.0f);
         const uint32_t bot = row_ror8(pack_h2(pl, ph));
         pa[i] = col < 8 ? top : bot;
@@ -505,34 +500,36 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     l_run = l_run * alpha + psum;
   };
 
-  // The wave's chunks start at first + i * kStep. Iteration i finishes chunk
-  // i (softmax + values) and computes the scores of chunk i + 1 in the same
-  // straight-line block, so each one's LDS latency hides behind the other's
-  // work; the chunk i + 2 codes are in flight meanwhile. Only the last chunk
-  // can be partial; it is finished after the loop.
+  // The wave's chunks start at first + i * kStep. Iteration i computes the
+  // scores of chunk i + 1 and finishes chunk i (softmax + values) in one
+  // straight-line block, so each one's table-read latency hides behind the
+  // other's work. A chunk's key registers are reloaded (chunk i + 2) as soon
+  // as its scores are done, its value registers (chunk i + 1) as soon as it
+  // is finished: each load has half an iteration to land. Only the last
+  // chunk can be partial; it is finished after the loop.
   constexpr int kStep = kMWaves * kChunk;
   const int first = t_begin + wave * kChunk;
   const int nch = first < t_end ? (t_end - first + kStep - 1) / kStep : 0;
   if (nch > 0) {
-    load_chunk<D, KB, VBITS, QJL>(cr_, kres, vres, sres, first, lane);
-    stage(0);
-    if (nch > 1) load_chunk<D, KB, VBITS, QJL>(cr_, kres, vres, sres, first + kStep, lane);
+    CK ck;
+    CV cv;
+    load_k(ck, first);
+    load_v(cv, first);
     float4_t sacc[NSUB];
-    scores(0, sacc);
+    scores(ck, sacc);
+    // chunk 1 (a repeat of chunk 0 when there is none: an L2 hit)
+    load_k(ck, first + min(1, nch - 1) * kStep);
     for (int i = 0; i + 1 < nch; ++i) {
-      const int nxt = (i + 1) & 1;
-      stage(nxt);
-      // chunk i + 2 (a repeat of the last chunk past the end: an L2 hit)
-      const int tl = first + min(i + 2, nch - 1) * kStep;
-      load_chunk<D, KB, VBITS, QJL>(cr_, kres, vres, sres, tl, lane);
       float4_t snext[NSUB];
-      scores(nxt, snext);
-      finish(i & 1, sacc, kChunk, false);
+      scores(ck, snext);
+      load_k(ck, first + min(i + 2, nch - 1) * kStep);
+      finish(cv, sacc, kChunk, false);
+      load_v(cv, first + (i + 1) * kStep);
 #pragma unroll
       for (int st = 0; st < NSUB; ++st) sacc[st] = snext[st];
     }
     const int tlast = first + (nch - 1) * kStep;
-    finish((nch - 1) & 1, sacc, min(kChunk, t_end - tlast), true);
+    finish(cv, sacc, min(kChunk, t_end - tlast), true);
   }
 
   // ---------------- per-wave results ----------------
@@ -543,7 +540,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     red_l[wave][lane] = l_run;
   }
   // O[head][coord] = D[head] + 2^-11 D[head + 8]: rows 8-15 sit 32 lanes up.
-  float *red_o = (float *)ktile_of(wave, 0);  // this wave's tile is free now
+  float *red_o = sm.red_o[wave];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -568,7 +565,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     for (int w = 0; w < kMWaves; ++w) {
       const float sc = red_m[w][hh] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w][hh] - mx);
       L += red_l[w][hh] * sc;
-      O += ((const float *)ktile_of(w, 0))[hh * D + c] * sc;
+      O += sm.red_o[w][hh * D + c] * sc;
     }
     float *dst = a.part + (((int64_t)(b * a.Hq + h * G + hh) * a.splits) + split) * (D + 2);
     if (c == 0) {
