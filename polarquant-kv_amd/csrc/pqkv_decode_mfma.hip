@@ -106,8 +106,10 @@ __device__ __forceinline__ float4_t mfma16(half8_t a, half8_t b, float4_t c) {
 }
 
 // Lane col of each 16-lane row receives lane (col + 8) % 16 (DPP row_ror:8).
+// Every lane has a source, so no "old" value is needed (mov_dpp with
+// bound_ctrl: no zero-initialised copy, and the move can fold into its user).
 __device__ __forceinline__ uint32_t row_ror8(uint32_t x) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, false);
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xF, 0xF, true);
 }
 __device__ __forceinline__ float row_ror8f(float x) { return __builtin_bit_cast(float, row_ror8(__builtin_bit_cast(uint32_t, x))); }
 
@@ -159,7 +161,7 @@ __device__ __forceinline__ void load_words(__amdgpu_buffer_rsrc_t r, int off, ui
 // fold to a constant after unrolling.
 template <int N>
 __device__ __forceinline__ float row_bcast_c(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x150 + N, 0xF, 0xF, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x150 + N, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float row_bcast(float x, int n) {
   switch (n) {
@@ -342,65 +344,115 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   };
   __syncthreads();
 
-  // Scores of the chunk held in `k`, finished to the exp2-domain logit:
+  // ---- building blocks of one chunk ----
+  // Table reads of key sub-tile st: per score step kk, 4 codes x (hi, lo)
+  // (two 8-byte entries); QJL adds the sign-table reads.
+  struct KTile {
+    uint2 t[KK][2];
+    uint2 s[QJL ? KQ : 1][2];
+  };
+  auto kread = [&](const CK &k, int st, KTile &kt) {
+    // the lane group's qs words of token 16st + col
+    uint32_t qw[CK::kWords - 1];
+#pragma unroll
+    for (int i = 0; i + 1 < CK::kWords; ++i) qw[i] = __builtin_amdgcn_perm(k.w[st][i + 1], k.w[st][i], ksel);
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      // step kk: coordinates 4kk .. 4kk + 3 of the lane group's range
+      if constexpr (KB == 4) {
+        const uint32_t w = qw[kk >> 1];
+        const int e = kk & 1;
+        kt.t[kk][0] = lut_k[(w >> (16 * e)) & 0xFF];
+        kt.t[kk][1] = lut_k[(w >> (16 * e + 8)) & 0xFF];
+      } else {
+        const uint32_t w = qw[kk >> 2];
+        const int e = kk & 3;
+        kt.t[kk][0] = lut_k[(w >> (8 * e)) & 0xF];
+        kt.t[kk][1] = lut_k[(w >> (8 * e + 4)) & 0xF];
+      }
+    }
+    if constexpr (QJL) {
+#pragma unroll
+      for (int kq = 0; kq < KQ; ++kq) {
+        const uint32_t byte = (k.sg[st] >> (8 * kq)) & 0xFF;
+        kt.s[kq][0] = lut_s[byte & 15];
+        kt.s[kq][1] = lut_s[byte >> 4];
+      }
+    }
+  };
+  // Score products of key sub-tile st, finished to the exp2-domain logit:
   // s = (D[t][h] + 2^-11 D[t][h + 8]) r_k (+ the QJL term when r_k > 0) for
   // token 16st + 4grp + i, meaningful in lanes col < G. Lanes of absent heads
   // (q = 0) and the cross lanes (col >= 8) carry finite values that only
-  // reach discarded output rows.
-  auto scores = [&](const CK &k, float4_t (&sc)[NSUB]) {
-    const float rkl = half_bits_to_float(k.r);
-    __builtin_amdgcn_s_setprio(1);
+  // reach discarded output rows. rkl: this lane's loaded radius.
+  auto kmma = [&](const KTile &kt, float rkl, int st, float4_t &out) {
+    float4_t acc = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int st = 0; st < NSUB; ++st) {
-      // the lane group's qs words of token 16st + col
-      uint32_t qw[CK::kWords - 1];
+    for (int kk = 0; kk < KK; ++kk) acc = mfma16(pack8(kt.t[kk][0], kt.t[kk][1]), qb[kk], acc);
+    float4_t accq = (float4_t){0.f, 0.f, 0.f, 0.f};
+    if constexpr (QJL) {
 #pragma unroll
-      for (int i = 0; i + 1 < CK::kWords; ++i) qw[i] = __builtin_amdgcn_perm(k.w[st][i + 1], k.w[st][i], ksel);
-      uint2 kt[KK][2];
+      for (int kq = 0; kq < KQ; ++kq) accq = mfma16(pack8(kt.s[kq][0], kt.s[kq][1]), pb[kq], accq);
+    }
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        // step kk: coordinates 4kk .. 4kk + 3 of the lane group's range
-        if constexpr (KB == 4) {
-          const uint32_t w = qw[kk >> 1];
-          const int e = kk & 1;
-          kt[kk][0] = lut_k[(w >> (16 * e)) & 0xFF];
-          kt[kk][1] = lut_k[(w >> (16 * e + 8)) & 0xFF];
-        } else {
-          const uint32_t w = qw[kk >> 2];
-          const int e = kk & 3;
-          kt[kk][0] = lut_k[(w >> (8 * e)) & 0xF];
-          kt[kk][1] = lut_k[(w >> (8 * e + 4)) & 0xF];
-        }
-      }
-      float4_t acc = (float4_t){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) acc = mfma16(pack8(kt[kk][0], kt[kk][1]), qb[kk], acc);
-      float4_t accq = (float4_t){0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < 4; ++i) {
+      const float rk = row_bcast(rkl, 4 * st + i);  // radius of token 16st + 4grp + i
+      float v = __builtin_fmaf(row_ror8f(acc[i]), 1.0f / kLoScale, acc[i]) * rk;
       if constexpr (QJL) {
-#pragma unroll
-        for (int kq = 0; kq < KQ; ++kq) {
-          const uint32_t byte = (k.sg[st] >> (8 * kq)) & 0xFF;
-          accq = mfma16(pack8(lut_s[byte & 15], lut_s[byte >> 4]), pb[kq], accq);
-        }
+        const float q = __builtin_fmaf(row_ror8f(accq[i]), 1.0f / kLoScale, accq[i]);
+        v = rk > 0.0f ? v + q : v;  // zero keys get no correction
       }
+      out[i] = v;
+    }
+  };
+  // Table reads of value k-block kb: two tokens' codes of the lane's
+  // coordinate interleaved into one byte (4-bit) or nibble (2-bit), token
+  // pairs (0,1) and (2,3).
+  struct VTile {
+    uint2 t[NB][2];
+  };
+  auto vread = [&](const CV &v, int kb, VTile &vt) {
+    uint32_t x01, y01, x23, y23;
+    if constexpr (VBITS == 4) {
+      uint32_t wv[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float rk = row_bcast(rkl, 4 * st + i);  // radius of token 16st + 4grp + i
-        float v = __builtin_fmaf(row_ror8f(acc[i]), 1.0f / kLoScale, acc[i]) * rk;
-        if constexpr (QJL) {
-          const float q = __builtin_fmaf(row_ror8f(accq[i]), 1.0f / kLoScale, accq[i]);
-          v = rk > 0.0f ? v + q : v;  // zero keys get no correction
-        }
-        sc[st][i] = v;
+      for (int e = 0; e < 4; ++e) wv[e] = __builtin_amdgcn_perm(v.w[kb][e][1], v.w[kb][e][0], vsel);
+      // byte k of x = even coordinate 2k of both tokens, of y = odd 2k + 1
+      x01 = (wv[0] & 0x0F0F0F0Fu) | ((wv[1] << 4) & 0xF0F0F0F0u);
+      y01 = ((wv[0] >> 4) & 0x0F0F0F0Fu) | (wv[1] & 0xF0F0F0F0u);
+      x23 = (wv[2] & 0x0F0F0F0Fu) | ((wv[3] << 4) & 0xF0F0F0F0u);
+      y23 = ((wv[2] >> 4) & 0x0F0F0F0Fu) | (wv[3] & 0xF0F0F0F0u);
+    } else {
+      uint32_t wv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wv[e] = v.w[kb][e][0];
+      // nibble k of x = even coordinate 2k of both tokens, of y = odd 2k + 1
+      x01 = (wv[0] & 0x3333u) | ((wv[1] << 2) & 0xCCCCu);
+      y01 = ((wv[0] >> 2) & 0x3333u) | (wv[1] & 0xCCCCu);
+      x23 = (wv[2] & 0x3333u) | ((wv[3] << 2) & 0xCCCCu);
+      y23 = ((wv[2] >> 2) & 0x3333u) | (wv[3] & 0xCCCCu);
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      // D = 128: n-tile nb is coordinate 8*col + nb of the lane's group.
+      // D = 64: n-tile nb is coordinate 8*(col & 7) + 2*nb + (col >> 3).
+      const int par = D == 128 ? (nb & 1) : vpar;
+      const int sub = D == 128 ? (nb >> 1) : nb;
+      if constexpr (VBITS == 4) {
+        vt.t[nb][0] = lut_v[((par ? y01 : x01) >> (8 * sub)) & 0xFF];
+        vt.t[nb][1] = lut_v[((par ? y23 : x23) >> (8 * sub)) & 0xFF];
+      } else {
+        vt.t[nb][0] = lut_v[((par ? y01 : x01) >> (4 * sub)) & 0xF];
+        vt.t[nb][1] = lut_v[((par ? y23 : x23) >> (4 * sub)) & 0xF];
       }
     }
-    __builtin_amdgcn_s_setprio(0);
   };
-  // Softmax update and value product of the chunk whose values are in `v`
-  // and whose logits are `sc`; tokens >= ntok of the chunk are masked.
-  auto finish = [&](const CV &v, const float4_t (&sc)[NSUB], int ntok, bool partial) {
-    const float rvl = half_bits_to_float(v.r);
-    float sv[NSUB][4];
+  // Softmax bookkeeping of one chunk: logits sv (tokens >= ntok masked when
+  // partial), the new running max, the rescale of the running output.
+  struct FState {
+    float mnew, alpha, psum;
+  };
+  auto fbegin = [&](float (&sv)[NSUB][4], const float4_t (&sc)[NSUB], int ntok, bool partial) {
 #pragma unroll
     for (int st = 0; st < NSUB; ++st)
 #pragma unroll
@@ -420,92 +472,105 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     // token 0 of the chunk is valid, so after the row reduction every lane's
     // max is finite; the first chunk has m_run = -inf and alpha = 0.
     cmax = rows_max(cmax);
-    const float mnew = fmaxf(m_run, cmax);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
-    m_run = mnew;
+    FState f;
+    f.mnew = fmaxf(m_run, cmax);
+    f.alpha = __builtin_amdgcn_exp2f(m_run - f.mnew);
+    f.psum = 0.0f;
+    m_run = f.mnew;
     // rescale the running output: lane (col, grp) holds rows 4grp + i, i.e.
     // head 4(grp & 1) + i (hi part for grp < 2, cross part for grp >= 2);
     // alpha of head hh sits in lane hh. Skipped (wave-uniform) when no head's
     // maximum moved, the common case once the first chunks are in.
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) & 0xFFull) {
+    if (__builtin_amdgcn_ballot_w64(f.alpha != 1.0f) & 0xFFull) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         // lane gather (a select between two read-lanes becomes a scratch
         // array indexed by the lane group)
-        const float f = __builtin_bit_cast(
-            float, __builtin_amdgcn_ds_bpermute(4 * (4 * (grp & 1) + i), __builtin_bit_cast(int, alpha)));
+        const float fi = __builtin_bit_cast(
+            float, __builtin_amdgcn_ds_bpermute(4 * (4 * (grp & 1) + i), __builtin_bit_cast(int, f.alpha)));
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) oacc[nb][i] *= f;
+        for (int nb = 0; nb < NB; ++nb) oacc[nb][i] *= fi;
       }
     }
-    // values, one 16-token k-block per MFMA step
-    float psum = 0.0f;
+    return f;
+  };
+  // Weights p * r_v of k-block kb in the A layout: col < 8 -> (p_hi, 0),
+  // col >= 8 -> (p_lo, p_hi) of head col - 8, taken from lane col - 8.
+  auto fweights = [&](const float (&svk)[4], float rvl, int kb, FState &f) {
+    uint32_t pa[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = __builtin_amdgcn_exp2f(svk[i] - f.mnew);
+      f.psum += p;
+      half_t ph, pl;
+      split_hi_lo(p * row_bcast(rvl, 4 * kb + i), &ph, &pl);  // r_v of token 16kb + 4grp + i
+      const uint32_t top = pack_h2(ph, (half_t)0.0f);
+      const uint32_t bot = row_ror8(pack_h2(pl, ph));
+      pa[i] = col < 8 ? top : bot;
+    }
+    return pack8u(pa[0], pa[1], pa[2], pa[3]);
+  };
+  auto vmma = [&](half8_t pav, const VTile &vt) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) oacc[nb] = mfma16(pav, pack8(vt.t[nb][0], vt.t[nb][1]), oacc[nb]);
+  };
+
+  // Scores of a whole chunk (the first one): reads one sub-tile ahead.
+  auto scores = [&](const CK &k, float4_t (&sc)[NSUB]) {
+    const float rkl = half_bits_to_float(k.r);
+    KTile kt[2];
+    kread(k, 0, kt[0]);
+#pragma unroll
+    for (int st = 0; st < NSUB; ++st) {
+      if (st + 1 < NSUB) kread(k, st + 1, kt[(st + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      kmma(kt[st & 1], rkl, st, sc[st]);
+    }
+  };
+  // Softmax update and value product of a whole chunk (the last one).
+  auto finish = [&](const CV &v, const float4_t (&sc)[NSUB], int ntok, bool partial) {
+    float sv[NSUB][4];
+    FState f = fbegin(sv, sc, ntok, partial);
+    const float rvl = half_bits_to_float(v.r);
+    VTile vt[2];
+    vread(v, 0, vt[0]);
 #pragma unroll
     for (int kb = 0; kb < NSUB; ++kb) {
-      // value-side entries: two tokens' codes of the lane's coordinate
-      // interleaved into one byte (4-bit) or nibble (2-bit), token pairs
-      // (0,1) and (2,3)
-      uint32_t x01, y01, x23, y23;
-      if constexpr (VBITS == 4) {
-        uint32_t wv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) wv[e] = __builtin_amdgcn_perm(v.w[kb][e][1], v.w[kb][e][0], vsel);
-        // byte k of x = even coordinate 2k of both tokens, of y = odd 2k + 1
-        x01 = (wv[0] & 0x0F0F0F0Fu) | ((wv[1] << 4) & 0xF0F0F0F0u);
-        y01 = ((wv[0] >> 4) & 0x0F0F0F0Fu) | (wv[1] & 0xF0F0F0F0u);
-        x23 = (wv[2] & 0x0F0F0F0Fu) | ((wv[3] << 4) & 0xF0F0F0F0u);
-        y23 = ((wv[2] >> 4) & 0x0F0F0F0Fu) | (wv[3] & 0xF0F0F0F0u);
-      } else {
-        uint32_t wv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) wv[e] = v.w[kb][e][0];
-        // nibble k of x = even coordinate 2k of both tokens, of y = odd 2k + 1
-        x01 = (wv[0] & 0x3333u) | ((wv[1] << 2) & 0xCCCCu);
-        y01 = ((wv[0] >> 2) & 0x3333u) | (wv[1] & 0xCCCCu);
-        x23 = (wv[2] & 0x3333u) | ((wv[3] << 2) & 0xCCCCu);
-        y23 = ((wv[2] >> 2) & 0x3333u) | (wv[3] & 0xCCCCu);
-      }
-      uint2 vt[NB][2];
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        // D = 128: n-tile nb is coordinate 8*col + nb of the lane's group.
-        // D = 64: n-tile nb is coordinate 8*(col & 7) + 2*nb + (col >> 3).
-        const int par = D == 128 ? (nb & 1) : vpar;
-        const int sub = D == 128 ? (nb >> 1) : nb;
-        if constexpr (VBITS == 4) {
-          vt[nb][0] = lut_v[((par ? y01 : x01) >> (8 * sub)) & 0xFF];
-          vt[nb][1] = lut_v[((par ? y23 : x23) >> (8 * sub)) & 0xFF];
-        } else {
-          vt[nb][0] = lut_v[((par ? y01 : x01) >> (4 * sub)) & 0xF];
-          vt[nb][1] = lut_v[((par ? y23 : x23) >> (4 * sub)) & 0xF];
-        }
-      }
-      // weights p * r_v in the A layout: col < 8 -> (p_hi, 0), col >= 8 ->
-      // (p_lo, p_hi) of head col - 8, taken from lane col - 8.
-      uint32_t pa[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = __builtin_amdgcn_exp2f(sv[kb][i] - mnew);
-        psum += p;
-        half_t ph, pl;
-        split_hi_lo(p * row_bcast(rvl, 4 * kb + i), &ph, &pl);  // r_v of token 16kb + 4grp + i
-        const uint32_t top = pack_h2(ph, (half_t)0.0f);
-        const uint32_t bot = row_ror8(pack_h2(pl, ph));
-        pa[i] = col < 8 ? top : bot;
-      }
-      const half8_t pav = pack8u(pa[0], pa[1], pa[2], pa[3]);
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) oacc[nb] = mfma16(pav, pack8(vt[nb][0], vt[nb][1]), oacc[nb]);
+      if (kb + 1 < NSUB) vread(v, kb + 1, vt[(kb + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      vmma(fweights(sv[kb], rvl, kb, f), vt[kb & 1]);
     }
-    l_run = l_run * alpha + psum;
+    l_run = l_run * f.alpha + f.psum;
+  };
+  // One steady-state iteration: scores of the chunk in k (into sn) and the
+  // finish of the chunk in v with logits sc, sub-tile by sub-tile: both
+  // tiles' table reads are issued first, the softmax weights are computed
+  // while they are in flight, then the two products run.
+  auto step = [&](const CK &k, const CV &v, const float4_t (&sc)[NSUB], float4_t (&sn)[NSUB]) {
+    float sv[NSUB][4];
+    FState f = fbegin(sv, sc, kChunk, false);
+    const float rkl = half_bits_to_float(k.r), rvl = half_bits_to_float(v.r);
+#pragma unroll
+    for (int j = 0; j < NSUB; ++j) {
+      KTile kt;
+      VTile vt;
+      kread(k, j, kt);
+      vread(v, j, vt);
+      __builtin_amdgcn_sched_barrier(0);
+      const half8_t pav = fweights(sv[j], rvl, j, f);
+      __builtin_amdgcn_sched_barrier(0);
+      kmma(kt, rkl, j, sn[j]);
+      vmma(pav, vt);
+    }
+    l_run = l_run * f.alpha + f.psum;
   };
 
   // The wave's chunks start at first + i * kStep. Iteration i computes the
-  // scores of chunk i + 1 and finishes chunk i (softmax + values) in one
-  // straight-line block, so each one's table-read latency hides behind the
-  // other's work. A chunk's key registers are reloaded (chunk i + 2) as soon
-  // as its scores are done, its value registers (chunk i + 1) as soon as it
-  // is finished: each load has half an iteration to land. Only the last
+  // scores of chunk i + 1 and finishes chunk i (softmax + values), sub-tile
+  // by sub-tile, so each one's table-read latency hides behind the other's
+  // work. A chunk's key registers are reloaded (chunk i + 2) as soon as its
+  // scores are done, its value registers (chunk i + 1) as soon as it is
+  // finished: each load has most of an iteration to land. Only the last
   // chunk can be partial; it is finished after the loop.
   constexpr int kStep = kMWaves * kChunk;
   const int first = t_begin + wave * kChunk;
@@ -521,9 +586,8 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     load_k(ck, first + min(1, nch - 1) * kStep);
     for (int i = 0; i + 1 < nch; ++i) {
       float4_t snext[NSUB];
-      scores(ck, snext);
+      step(ck, cv, sacc, snext);
       load_k(ck, first + min(i + 2, nch - 1) * kStep);
-      finish(cv, sacc, kChunk, false);
       load_v(cv, first + (i + 1) * kStep);
 #pragma unroll
       for (int st = 0; st < NSUB; ++st) sacc[st] = snext[st];
