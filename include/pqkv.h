@@ -132,8 +132,8 @@ int pqkv_encode_mfma(const void *x, int x_dtype, int64_t x_outer_stride,
  * per-head tables, or one table when the *_head_bits pointer is NULL.
  * Replaces turboquant_full_attention (csrc/flash_turboquant.cu:180-211),
  * polarquant_fused_attention_cuda (patch:469-506) plus the query and output
- * rotations around them (patch:395-437). R is device fp32 [d][d], 16-byte
- * aligned. S = 0 writes zeros. */
+ * rotations around them (patch:395-437). R (and p_rot) are device fp32
+ * [d][d], 16-byte aligned. S = 0 writes zeros. */
 size_t pqkv_decode_workspace_bytes(int B, int Hq, int Hkv, int S, int d);
 
 int pqkv_decode_attn(const void *q, int q_dtype, const float *R,

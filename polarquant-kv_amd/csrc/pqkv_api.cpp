@@ -407,6 +407,7 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
   if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(PQKV_ERR_INVALID, "decode: scale must be > 0");
   if (!q || !R || !out) return fail(PQKV_ERR_INVALID, "decode: null pointer");
   if ((uintptr_t)R % 16) return fail(PQKV_ERR_INVALID, "decode: R must be 16-byte aligned");
+  if ((uintptr_t)p_rot % 16) return fail(PQKV_ERR_INVALID, "decode: p_rot must be 16-byte aligned");
   const size_t need = pqkv_decode_workspace_bytes(B, Hq, Hkv, S, d);
   if (S > 0) {
     if (!k_cache || !v_cache || !k_codebooks || !v_codebooks)

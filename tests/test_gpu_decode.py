@@ -221,3 +221,63 @@ def test_decode_full_size_config3_slices():
         ref = O.decode_attention(qn[b:b + 1, 4 * h:4 * h + 4].astype(np.float64), kb[b:b + 1, h:h + 1],
                                  vb[b:b + 1, h:h + 1], R, cb, cb)
         _check(out[b:b + 1, 4 * h:4 * h + 4], ref)
+
+
+def test_decode_workspace_any_contents_and_reuse():
+    """A workspace full of random bytes, reused across calls and across
+    shapes (different split plans), gives the same bits every time and
+    matches the oracle: nothing is read from it before being written."""
+    cases = [((2, 16, 4, 3000, 128, 4, 4), False), ((1, 8, 2, 1777, 128, 2, 2), True),
+             ((2, 16, 4, 900, 128, 4, 4), False)]
+    need = max(_lib_decode_bytes(c[0]) for c in cases)
+    ws = torch.randint(0, 256, (need,), dtype=torch.uint8, device=DEV)
+    for case, qjl in cases:
+        B, Hq, Hkv, S, d, kb, vb = case
+        print(f"workspace reuse case {case} qjl={qjl}", flush=True)
+        q, R, Rt, kc, vc, P_rot = _setup(B, Hq, Hkv, S, d, kb, vb, seed=S, qjl=qjl)
+        qt = torch.from_numpy(q).to(DEV)
+        kw = dict(jl_rot=P_rot) if qjl else {}
+        outs = [attention.decode_attention(qt, kc, vc, Rt, out_dtype=torch.float32, workspace=ws, **kw)
+                for _ in range(3)]
+        for o in outs[1:]:
+            assert torch.equal(o, outs[0])
+        if qjl:
+            ref = _oracle(q, R, kc, vc, S, P=O.jl_matrix(d, d, 43), signs=kc.qjl_signs.cpu().numpy()[:, :, :S])
+        else:
+            ref = _oracle(q, R, kc, vc, S)
+        _check(outs[0].cpu().numpy(), ref)
+
+
+def _lib_decode_bytes(case):
+    from polarquant_kv import _lib
+    B, Hq, Hkv, S, d = case[:5]
+    return _lib.lib().pqkv_decode_workspace_bytes(B, Hq, Hkv, S, d)
+
+
+def test_decode_graph_replays_match_eager():
+    """A captured decode call (query rotation, split kernel, merge) replayed
+    several times, with eager work and synchronisations in between: every
+    replay equals the eager result."""
+    B, Hq, Hkv, S, d = 2, 16, 4, 2500, 128
+    q, R, Rt, kc, vc, _ = _setup(B, Hq, Hkv, S, d, 4, 4, seed=99)
+    qt = torch.from_numpy(q).to(DEV)
+    ws = torch.zeros(_lib_decode_bytes((B, Hq, Hkv, S, d)), dtype=torch.uint8, device=DEV)
+    eager = attention.decode_attention(qt, kc, vc, Rt, out_dtype=torch.float32, workspace=ws)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):   # warm-up on the capture stream
+        attention.decode_attention(qt, kc, vc, Rt, out_dtype=torch.float32, workspace=ws)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        captured = attention.decode_attention(qt, kc, vc, Rt, out_dtype=torch.float32, workspace=ws)
+    for i in range(4):
+        captured.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager), f"replay {i}"
+        attention.decode_attention(qt, kc, vc, Rt, out_dtype=torch.float32, workspace=ws)   # eager call between
+        torch.cuda.synchronize()
+    _check(eager.cpu().numpy(), _oracle(q, R, kc, vc, S))
