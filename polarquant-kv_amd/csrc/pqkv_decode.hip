@@ -354,49 +354,72 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const float *__restri
   constexpr int NH = kMergeHeads;
   constexpr int NC = 32;           // output columns per workgroup
   constexpr int RP = D + 1;
+  constexpr int RU = NC * D / 4 / 256;   // R float4 loads per thread
+  constexpr int OU = NH * D / 256;       // (head, coordinate) sums per thread
+  constexpr int SB = 16;                 // splits whose o values are loaded at once
   __shared__ float rs[NC * RP];    // rs[jj][k] = R[k][c0 + jj]
   __shared__ float os[NH * D];
   __shared__ float wts[NH][kMaxSplits];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int head0 = blockIdx.x * NH, c0 = blockIdx.y * NC;
+  // Every independent global read goes out before the first wait: the R
+  // columns, this wave's split maxima and sums (up to 64 splits), and the
+  // first SB splits of the thread's o values.
+  float4 rv[RU];
 #pragma unroll
-  for (int u = 0; u < NC * D / 4 / 256; ++u) {
+  for (int u = 0; u < RU; ++u) {
     const int i = tid + 256 * u, k = i / (NC / 4), j4 = i % (NC / 4);
-    const float4 v = *(const float4 *)(R + (int64_t)k * D + c0 + 4 * j4);
-    rs[(4 * j4 + 0) * RP + k] = v.x;
-    rs[(4 * j4 + 1) * RP + k] = v.y;
-    rs[(4 * j4 + 2) * RP + k] = v.z;
-    rs[(4 * j4 + 3) * RP + k] = v.w;
+    rv[u] = *(const float4 *)(R + (int64_t)k * D + c0 + 4 * j4);
   }
-  {
-    const int hq = head0 + wave;
-    if (hq < BHq) {
-      const float *p = part + (int64_t)hq * splits * (D + 2);
-      float mx = -INFINITY;
-      for (int sp = lane; sp < splits; sp += 64) mx = fmaxf(mx, p[(int64_t)sp * (D + 2)]);
-      mx = wave_max(mx);
-      float L = 0.0f;
-      for (int sp = lane; sp < splits; sp += 64) {
-        const float ms = p[(int64_t)sp * (D + 2)];
-        const float e = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - mx);
-        wts[wave][sp] = e;
-        L = __builtin_fmaf(e, p[(int64_t)sp * (D + 2) + 1], L);
-      }
-      L = wave_sum(L);
-      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-      for (int sp = lane; sp < splits; sp += 64) wts[wave][sp] *= inv;
+  const int hq_w = head0 + wave;
+  const float *pw = part + (int64_t)min(hq_w, BHq - 1) * splits * (D + 2);
+  const float m0 = lane < splits ? pw[(int64_t)lane * (D + 2)] : -INFINITY;
+  const float l0 = lane < splits ? pw[(int64_t)lane * (D + 2) + 1] : 0.0f;
+  float ov[OU][SB];
+#pragma unroll
+  for (int u = 0; u < OU; ++u) {
+    const int i = tid + 256 * u, hh = i / D, c = i % D;
+    const float *p = part + (int64_t)min(head0 + hh, BHq - 1) * splits * (D + 2) + 2 + c;
+#pragma unroll
+    for (int sp = 0; sp < SB; ++sp) ov[u][sp] = sp < splits ? p[(int64_t)sp * (D + 2)] : 0.0f;
+  }
+#pragma unroll
+  for (int u = 0; u < RU; ++u) {
+    const int i = tid + 256 * u, k = i / (NC / 4), j4 = i % (NC / 4);
+    rs[(4 * j4 + 0) * RP + k] = rv[u].x;
+    rs[(4 * j4 + 1) * RP + k] = rv[u].y;
+    rs[(4 * j4 + 2) * RP + k] = rv[u].z;
+    rs[(4 * j4 + 3) * RP + k] = rv[u].w;
+  }
+  if (hq_w < BHq) {
+    float mx = m0;
+    for (int sp = lane + 64; sp < splits; sp += 64) mx = fmaxf(mx, pw[(int64_t)sp * (D + 2)]);
+    mx = wave_max(mx);
+    float L = 0.0f;
+    for (int sp = lane; sp < splits; sp += 64) {
+      const float ms = sp == lane ? m0 : pw[(int64_t)sp * (D + 2)];
+      const float ls = sp == lane ? l0 : pw[(int64_t)sp * (D + 2) + 1];
+      const float e = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - mx);
+      wts[wave][sp] = e;
+      L = __builtin_fmaf(e, ls, L);
     }
+    L = wave_sum(L);
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    for (int sp = lane; sp < splits; sp += 64) wts[wave][sp] *= inv;
   }
   __syncthreads();
 #pragma unroll
-  for (int u = 0; u < NH * D / 256; ++u) {
+  for (int u = 0; u < OU; ++u) {
     const int i = tid + 256 * u, hh = i / D, c = i % D;
     const int hq = head0 + hh;
     float o = 0.0f;
     if (hq < BHq) {
+#pragma unroll
+      for (int sp = 0; sp < SB; ++sp)
+        if (sp < splits) o = __builtin_fmaf(wts[hh][sp], ov[u][sp], o);
       const float *p = part + (int64_t)hq * splits * (D + 2) + 2 + c;
 #pragma unroll 8
-      for (int sp = 0; sp < splits; ++sp) o = __builtin_fmaf(wts[hh][sp], p[(int64_t)sp * (D + 2)], o);
+      for (int sp = SB; sp < splits; ++sp) o = __builtin_fmaf(wts[hh][sp], p[(int64_t)sp * (D + 2)], o);
     }
     os[i] = o;
   }

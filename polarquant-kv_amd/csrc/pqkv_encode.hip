@@ -161,6 +161,20 @@ __global__ void __launch_bounds__(256) rotate_kernel(const TIN *__restrict__ x, 
   __shared__ float xs[kRotVec * D];
   const int tid = threadIdx.x;
   const int c0 = blockIdx.y * kRotCols;
+  // The first group's vector loads go out before the R staging loads, so
+  // the two global round trips overlap.
+  constexpr int XU = kRotVec * D / 256;
+  const int64_t stride = (int64_t)gridDim.x * kRotVec;
+  float xv[XU];
+  auto load_x = [&](int64_t bs) {
+#pragma unroll
+    for (int u = 0; u < XU; ++u) {
+      const int i = tid + 256 * u;
+      const int64_t v = bs + i / D;
+      xv[u] = v < n ? load_as_float(x + v * D + (i % D)) : 0.0f;
+    }
+  };
+  load_x((int64_t)blockIdx.x * kRotVec);
   // rs[jj][k] = R[c0 + jj][k] (forward) or R[k][c0 + jj] (inverse)
   if (!INVERSE) {
 #pragma unroll
@@ -185,14 +199,11 @@ __global__ void __launch_bounds__(256) rotate_kernel(const TIN *__restrict__ x, 
     }
   }
   const int jj = tid % kRotCols, g = tid / kRotCols;   // g: vector of the group
-  for (int64_t base = (int64_t)blockIdx.x * kRotVec; base < n; base += (int64_t)gridDim.x * kRotVec) {
+  for (int64_t base = (int64_t)blockIdx.x * kRotVec; base < n; base += stride) {
 #pragma unroll
-    for (int u = 0; u < kRotVec * D / 256; ++u) {
-      const int i = tid + 256 * u;
-      const int64_t v = base + i / D;
-      xs[i] = v < n ? load_as_float(x + v * D + (i % D)) : 0.0f;
-    }
+    for (int u = 0; u < XU; ++u) xs[tid + 256 * u] = xv[u];
     __syncthreads();
+    if (base + stride < n) load_x(base + stride);
     float acc = 0.0f;
 #pragma unroll 16
     for (int k = 0; k < D; ++k) acc = __builtin_fmaf(xs[g * D + k], rs[jj * RP + k], acc);
