@@ -437,10 +437,10 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
   float *pq32 = (float *)((char *)part + align256((size_t)B * Hq * splits * (d + 2) * 4));
   const float kLog2e = 1.4426950408889634f;
   int tok = pqkv::prof_begin("decode_rotate", st);
-  hipError_t e = pqkv::launch_rotate(q, q_dtype, R, q32, PQKV_F32, (int64_t)B * Hq, d, 0, scale * kLog2e, st);
-  // QJL: P_rot q_rot / m once per query head (m == d), for every split
-  if (e == hipSuccess && qjl_signs) e = pqkv::launch_rotate(q32, PQKV_F32, p_rot, pq32, PQKV_F32, (int64_t)B * Hq, d, 0,
-                                                            1.0f / (float)m, st);
+  // QJL: the projections P_rot q_rot / m (m == d) come from the same launch
+  hipError_t e = qjl_signs ? pqkv::launch_rotate2(q, q_dtype, R, p_rot, q32, pq32, (int64_t)B * Hq, d, scale * kLog2e,
+                                                  1.0f / (float)m, st)
+                           : pqkv::launch_rotate(q, q_dtype, R, q32, PQKV_F32, (int64_t)B * Hq, d, 0, scale * kLog2e, st);
   pqkv::prof_end(tok, st);
   if (e != hipSuccess) return hip_status(e, "decode query rotation");
 

@@ -213,6 +213,76 @@ __global__ void __launch_bounds__(256) rotate_kernel(const TIN *__restrict__ x, 
   }
 }
 
+// Two chained forward rotations in one launch: y = (R x) sy, then
+// z = (M y) sz (decode with QJL: the rotated query and its projections
+// P_rot q_rot / m). Workgroup: kRot2Vec vectors, all D columns, both
+// matrices staged whole in LDS ([D][D + 1], padded) by one round of loads.
+// Every output is the FMA chain of rotate_kernel over k ascending, so y and
+// z are bit-identical to two rotate_kernel launches.
+constexpr int kRot2Vec = 2;
+template <int D, typename TIN>
+__global__ void __launch_bounds__(256) rotate2_kernel(const TIN *__restrict__ x, const float *__restrict__ R,
+                                                      const float *__restrict__ M, float *__restrict__ y,
+                                                      float *__restrict__ z, int64_t n, float sy, float sz) {
+  constexpr int RP = D + 1;
+  constexpr int NO = kRot2Vec * D;  // outputs per matrix
+  __shared__ float rs[D * RP], ms[D * RP];
+  __shared__ float xs[NO], ys[NO];
+  const int tid = threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * kRot2Vec;
+  for (int i = tid; i < NO; i += 256) {
+    const int64_t v = base + i / D;
+    xs[i] = v < n ? load_as_float(x + v * D + (i % D)) : 0.0f;
+  }
+#pragma unroll 4
+  for (int i = tid; i < D * D / 4; i += 256) {
+    const int j = i / (D / 4), k4 = i % (D / 4);
+    const float4 a = *(const float4 *)(R + (int64_t)j * D + 4 * k4);
+    const float4 b = *(const float4 *)(M + (int64_t)j * D + 4 * k4);
+    float *da = rs + j * RP + 4 * k4, *db = ms + j * RP + 4 * k4;
+    da[0] = a.x;
+    da[1] = a.y;
+    da[2] = a.z;
+    da[3] = a.w;
+    db[0] = b.x;
+    db[1] = b.y;
+    db[2] = b.z;
+    db[3] = b.w;
+  }
+  __syncthreads();
+  for (int i = tid; i < NO; i += 256) {
+    const int g = i / D, j = i % D;
+    float acc = 0.0f;
+#pragma unroll 16
+    for (int k = 0; k < D; ++k) acc = __builtin_fmaf(xs[g * D + k], rs[j * RP + k], acc);
+    const float yv = acc * sy;
+    ys[i] = yv;
+    if (base + g < n) y[(base + g) * D + j] = yv;
+  }
+  __syncthreads();
+  for (int i = tid; i < NO; i += 256) {
+    const int g = i / D, j = i % D;
+    float acc = 0.0f;
+#pragma unroll 16
+    for (int k = 0; k < D; ++k) acc = __builtin_fmaf(ys[g * D + k], ms[j * RP + k], acc);
+    if (base + g < n) z[(base + g) * D + j] = acc * sz;
+  }
+}
+
+hipError_t launch_rotate2(const void *x, int x_dtype, const float *R, const float *M, float *y, float *z, int64_t n,
+                          int d, float sy, float sz, hipStream_t s) {
+  const int64_t grid = (n + kRot2Vec - 1) / kRot2Vec;
+  if (grid < 1 || grid > 0x7fffffff) return hipErrorInvalidValue;
+  if (d == 128) {
+    if (x_dtype == 0) rotate2_kernel<128, float><<<(int)grid, 256, 0, s>>>((const float *)x, R, M, y, z, n, sy, sz);
+    else rotate2_kernel<128, half_t><<<(int)grid, 256, 0, s>>>((const half_t *)x, R, M, y, z, n, sy, sz);
+  } else {
+    if (x_dtype == 0) rotate2_kernel<64, float><<<(int)grid, 256, 0, s>>>((const float *)x, R, M, y, z, n, sy, sz);
+    else rotate2_kernel<64, half_t><<<(int)grid, 256, 0, s>>>((const half_t *)x, R, M, y, z, n, sy, sz);
+  }
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Exact fused encoder: the rotation above (bit-identical FMA chain) followed by
 // the per-wave quantiser, plus the optional QJL sign sketch. 256 threads, NV

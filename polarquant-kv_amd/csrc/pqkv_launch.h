@@ -72,6 +72,9 @@ void prof_end(int token, hipStream_t s);
 
 hipError_t launch_quantize_rotated(const float *x_rot, const float *codebook, int bits, uint8_t *blocks,
                                    float *radius_out, int64_t n, int d, hipStream_t s);
+// y = (R x) sy and z = (M y) sz for n vectors in one launch (fp32 outputs).
+hipError_t launch_rotate2(const void *x, int x_dtype, const float *R, const float *M, float *y, float *z, int64_t n,
+                          int d, float sy, float sz, hipStream_t s);
 hipError_t launch_rotate(const void *x, int x_dtype, const float *R, void *y, int y_dtype, int64_t n, int d,
                          int inverse, float out_scale, hipStream_t s);
 hipError_t launch_encode_exact(const EncodeArgs &a, int x_dtype, hipStream_t s);
