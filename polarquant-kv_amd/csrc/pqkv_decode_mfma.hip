@@ -176,6 +176,28 @@ __device__ __forceinline__ float row_bcast(float x, int n) {
   }
 }
 
+// DPP move of src into the banks (4-lane groups of each 16-lane row) set in
+// BANK; the other lanes keep old. Sources outside the row read 0.
+template <int CTRL, int BANK>
+__device__ __forceinline__ uint32_t dpp_into(uint32_t old, uint32_t src) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)src, CTRL, 0xF, BANK, true);
+}
+template <int CTRL, int BANK>
+__device__ __forceinline__ float dpp_intof(float old, float src) {
+  return __builtin_bit_cast(float, dpp_into<CTRL, BANK>(__builtin_bit_cast(uint32_t, old), __builtin_bit_cast(uint32_t, src)));
+}
+constexpr int kDppIdentity = 0xE4;  // quad_perm [0, 1, 2, 3]
+// Lane n of each 4-lane quad to the whole quad (DPP quad_perm [n, n, n, n]).
+__device__ __forceinline__ float quad_bcast(float x, int n) {
+  const int v = __builtin_bit_cast(int, x);
+  switch (n) {
+    case 0: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(v, 0x00, 0xF, 0xF, true));
+    case 1: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(v, 0x55, 0xF, 0xF, true));
+    case 2: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(v, 0xAA, 0xF, 0xF, true));
+    default: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(v, 0xFF, 0xF, 0xF, true));
+  }
+}
+
 constexpr int kNSub = kChunk / kSub;
 
 // One 64-token chunk of keys in operand order, straight from HBM. For
@@ -449,34 +471,74 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   };
   // Softmax bookkeeping of one chunk: logits sv (tokens >= ntok masked when
   // partial), the new running max, the rescale of the running output.
+  //
+  // With G <= 4 only lanes col < 4 of a row carry real logits (heads 0-3),
+  // so the four sub-tiles' logits are compacted into one register set: lane
+  // 4 j + h of a row holds head h of sub-tile j (three DPP row shifts into
+  // single banks per value). The maximum, the weights and their hi / lo
+  // split then run on 4 values per lane instead of 16, and each sub-tile's
+  // A operand is spread back by two bank-masked DPP moves per value. The
+  // running max and sum are kept per lane of the compact layout (head
+  // col % 4; the sum is reduced across the banks at the end).
+  constexpr bool kCompact = G <= 4;
   struct FState {
     float mnew, alpha, psum;
+    uint32_t top[kCompact ? 4 : 1], bot[kCompact ? 4 : 1];  // compact weights: (p_hi, 0), (p_lo, p_hi)
   };
-  auto fbegin = [&](float (&sv)[NSUB][4], const float4_t (&sc)[NSUB], int ntok, bool partial) {
+  auto fbegin = [&](float (&sv)[NSUB][4], const float4_t (&sc)[NSUB], int ntok, bool partial, float rvl) {
+    FState f;
+    float cmax;
+    float cv[4];
+    if constexpr (kCompact) {
 #pragma unroll
-    for (int st = 0; st < NSUB; ++st)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sv[st][i] = sc[st][i];
-    if (partial) {
+      for (int i = 0; i < 4; ++i) {
+        float c = sc[0][i];
+        c = dpp_intof<0x114, 0x2>(c, sc[1][i]);  // row_shr:4 into bank 1
+        c = dpp_intof<0x118, 0x4>(c, sc[2][i]);  // row_shr:8 into bank 2
+        c = dpp_intof<0x11C, 0x8>(c, sc[3][i]);  // row_shr:12 into bank 3
+        cv[i] = partial && kSub * (col >> 2) + 4 * grp + i >= ntok ? -INFINITY : c;
+      }
+      cmax = fmaxf(fmaxf(cv[0], cv[1]), fmaxf(cv[2], cv[3]));
+      cmax = fmaxf(cmax, __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, cmax), 0x124, 0xF, 0xF, true)));
+      cmax = fmaxf(cmax, __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, cmax), 0x128, 0xF, 0xF, true)));
+    } else {
 #pragma unroll
       for (int st = 0; st < NSUB; ++st)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (kSub * st + 4 * grp + i >= ntok) sv[st][i] = -INFINITY;
+        for (int i = 0; i < 4; ++i) sv[st][i] = sc[st][i];
+      if (partial) {
+#pragma unroll
+        for (int st = 0; st < NSUB; ++st)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (kSub * st + 4 * grp + i >= ntok) sv[st][i] = -INFINITY;
+      }
+      cmax = sv[0][0];
+#pragma unroll
+      for (int st = 0; st < NSUB; ++st)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cmax = fmaxf(cmax, sv[st][i]);
     }
-    float cmax = sv[0][0];
-#pragma unroll
-    for (int st = 0; st < NSUB; ++st)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) cmax = fmaxf(cmax, sv[st][i]);
     // token 0 of the chunk is valid, so after the row reduction every lane's
     // max is finite; the first chunk has m_run = -inf and alpha = 0.
     cmax = rows_max(cmax);
-    FState f;
     f.mnew = fmaxf(m_run, cmax);
     f.alpha = __builtin_amdgcn_exp2f(m_run - f.mnew);
     f.psum = 0.0f;
     m_run = f.mnew;
+    if constexpr (kCompact) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = __builtin_amdgcn_exp2f(cv[i] - f.mnew);
+        f.psum += p;
+        // r_v of token 16 (col / 4) + 4 grp + i: lane 4 (col / 4) + i of the quad
+        const float rv = quad_bcast(rvl, i);
+        half_t ph, pl;
+        split_hi_lo(p * rv, &ph, &pl);
+        f.top[i] = pack_h2(ph, (half_t)0.0f);
+        f.bot[i] = pack_h2(pl, ph);
+      }
+    }
     // rescale the running output: lane (col, grp) holds rows 4grp + i, i.e.
     // head 4(grp & 1) + i (hi part for grp < 2, cross part for grp >= 2);
     // alpha of head hh sits in lane hh. Skipped (wave-uniform) when no head's
@@ -498,6 +560,22 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   // col >= 8 -> (p_lo, p_hi) of head col - 8, taken from lane col - 8.
   auto fweights = [&](const float (&svk)[4], float rvl, int kb, FState &f) {
     uint32_t pa[4];
+    if constexpr (kCompact) {
+      // lanes col < 8 (banks 0, 1): top of lane 4 kb + col; lanes col >= 8
+      // (banks 2, 3): bot of lane 4 kb + col - 8
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t x;
+        switch (kb) {
+          case 0: x = dpp_into<kDppIdentity, 0x3>(0u, f.top[i]); x = dpp_into<0x118, 0xC>(x, f.bot[i]); break;
+          case 1: x = dpp_into<0x104, 0x3>(0u, f.top[i]); x = dpp_into<0x114, 0xC>(x, f.bot[i]); break;
+          case 2: x = dpp_into<0x108, 0x3>(0u, f.top[i]); x = dpp_into<kDppIdentity, 0xC>(x, f.bot[i]); break;
+          default: x = dpp_into<0x10C, 0x3>(0u, f.top[i]); x = dpp_into<0x104, 0xC>(x, f.bot[i]); break;
+        }
+        pa[i] = x;
+      }
+      return pack8u(pa[0], pa[1], pa[2], pa[3]);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float p = __builtin_amdgcn_exp2f(svk[i] - f.mnew);
@@ -530,8 +608,8 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   // Softmax update and value product of a whole chunk (the last one).
   auto finish = [&](const CV &v, const float4_t (&sc)[NSUB], int ntok, bool partial) {
     float sv[NSUB][4];
-    FState f = fbegin(sv, sc, ntok, partial);
     const float rvl = half_bits_to_float(v.r);
+    FState f = fbegin(sv, sc, ntok, partial, rvl);
     VTile vt[2];
     vread(v, 0, vt[0]);
 #pragma unroll
@@ -548,8 +626,8 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   // while they are in flight, then the two products run.
   auto step = [&](const CK &k, const CV &v, const float4_t (&sc)[NSUB], float4_t (&sn)[NSUB]) {
     float sv[NSUB][4];
-    FState f = fbegin(sv, sc, kChunk, false);
     const float rkl = half_bits_to_float(k.r), rvl = half_bits_to_float(v.r);
+    FState f = fbegin(sv, sc, kChunk, false, rvl);
 #pragma unroll
     for (int j = 0; j < NSUB; ++j) {
       KTile kt;
@@ -597,7 +675,12 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   }
 
   // ---------------- per-wave results ----------------
-  // l: sum over the four rows of lane col; m is already row-uniform.
+  // l: sum over the four rows of lane col (and, compact, over the four
+  // banks of a row); m is already row-uniform.
+  if constexpr (kCompact) {
+    l_run += __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, l_run), 0x124, 0xF, 0xF, true));
+    l_run += __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, l_run), 0x128, 0xF, 0xF, true));
+  }
   l_run = rows_sum(l_run);
   if (lane < G) {
     red_m[wave][lane] = m_run;
