@@ -44,6 +44,9 @@
 // broadcasts hand to the lanes of its score rows. LDS holds only the code
 // tables. Cross-lane steps use DPP row rotations / broadcasts and the gfx950
 // permlane16/32 swaps (VALU); ds_bpermute moves the rare rescale factors.
+// With G <= 4 a score row has only four live head lanes, so the softmax of a
+// chunk runs on the four sub-tiles' logits compacted into one register set
+// (bank-masked DPP row shifts) and is spread back per sub-tile.
 #include "pqkv_device.h"
 #include "pqkv_launch.h"
 
