@@ -42,7 +42,8 @@
 // coordinates grp*D/4 .. grp*D/4 + D/4 - 1, so they are contiguous), a value
 // lane its qs word of four tokens, and each lane one radius that DPP row
 // broadcasts hand to the lanes of its score rows. LDS holds only the code
-// tables. Cross-lane steps use DPP row rotations / broadcasts and the gfx950
+// tables, each entry stored once per lane of a half-wave (bank-sliced) so
+// that random lookups are conflict-free. Cross-lane steps use DPP row rotations / broadcasts and the gfx950
 // permlane16/32 swaps (VALU); ds_bpermute moves the rare rescale factors.
 // With G <= 4 a score row has only four live head lanes, so the softmax of a
 // chunk runs on the four sub-tiles' logits compacted into one register set
@@ -83,15 +84,66 @@ __device__ __forceinline__ void build_lut_pairs(uint2 *lut, const float *cb, int
   }
 }
 
-// QJL: 4 sign bits -> the halfs (2 bit_j - 1), j = 0..3.
-__device__ __forceinline__ void build_sign_lut(uint2 *lut, int tid) {
-  if (tid < 16) {
-    uint32_t h[4];
+// Bank-sliced tables. A lookup of random 8-byte entries by 64 lanes runs
+// into bank conflicts (~4.4 clk per wave read against ~2.7 conflict-free on
+// gfx950, measured under full load). Storing each entry 32 times, copy c at
+// uint2 index 32 e + c, gives the 32 lanes of a half-wave (copy lane & 31)
+// 32 different bank pairs. A lane's byte address for entry e is
+// e * 256 + (lane & 31) * 8, one byte permute from a code byte (slice_addr).
+constexpr int kSlices = 32;
+
+// 4-bit pairs, 8192 slots: thread t (< 256) writes slots t + 256 j, j < 32,
+// which hold entry e = (t >> 5) + 8 j: e & 15 = (t >> 5) + 8 (j & 1) and
+// e >> 4 = j >> 1 (the codebook reads of the j loop are uniform).
+__device__ __forceinline__ void build_sliced4(uint2 *tab, const float *cb, int tid) {
+  const int r = tid >> 5;
+  half_t h, l;
+  split_hi_lo(cb[r], &h, &l);
+  const uint32_t pa = pack_h2(h, l);
+  split_hi_lo(cb[r + 8], &h, &l);
+  const uint32_t pb = pack_h2(h, l);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) h[j] = ((tid >> j) & 1) ? 0x3C00u : 0xBC00u;  // +1.0 / -1.0 fp16
-    lut[tid] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+  for (int j = 0; j < 32; ++j) {
+    split_hi_lo(cb[j >> 1], &h, &l);
+    tab[tid + 256 * j] = make_uint2((j & 1) ? pb : pa, pack_h2(h, l));
   }
 }
+
+// 2-bit pairs, 512 slots: nibble e -> codes e & 3 and e >> 2.
+__device__ __forceinline__ void build_sliced2(uint2 *tab, const float *cb, int tid) {
+#pragma unroll
+  for (int i = tid; i < 16 * kSlices; i += 256) {
+    const int e = i >> 5;
+    half_t h0, l0, h1, l1;
+    split_hi_lo(cb[e & 3], &h0, &l0);
+    split_hi_lo(cb[e >> 2], &h1, &l1);
+    tab[i] = make_uint2(pack_h2(h0, l0), pack_h2(h1, l1));
+  }
+}
+
+// QJL, 512 slots: 4 sign bits e -> the halfs (2 bit_j - 1), j = 0..3.
+__device__ __forceinline__ void build_sliced_sign(uint2 *tab, int tid) {
+#pragma unroll
+  for (int i = tid; i < 16 * kSlices; i += 256) {
+    const int e = i >> 5;
+    uint32_t h[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) h[j] = ((e >> j) & 1) ? 0x3C00u : 0xBC00u;  // +1.0 / -1.0 fp16
+    tab[i] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+  }
+}
+
+// Byte address in a sliced table of the entry indexed by byte k of w:
+// (byte k) << 8 | loff, loff = (lane & 31) * 8.
+__device__ __forceinline__ uint32_t slice_addr(uint32_t w, uint32_t loff, int k) {
+  return __builtin_amdgcn_perm(w, loff, 0x0C0C0000u | ((4u + (uint32_t)k) << 8));
+}
+__device__ __forceinline__ uint2 slice_read(const uint2 *tab, uint32_t addr) {
+  return *(const uint2 *)((const char *)tab + addr);
+}
+// Nibble indices as bytes: byte k of the result is nibble 2k (lo) or 2k + 1.
+__device__ __forceinline__ uint32_t nib_lo(uint32_t w) { return w & 0x0F0F0F0Fu; }
+__device__ __forceinline__ uint32_t nib_hi(uint32_t w) { return (w >> 4) & 0x0F0F0F0Fu; }
 
 __device__ __forceinline__ half8_t pack8(uint2 a, uint2 b) {
   typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
@@ -230,26 +282,37 @@ struct ChunkV {
 
 }  // namespace
 
-template <int D, int G, int KB, int VBITS, bool QJL>
+// VSH: 4-bit keys and values with one codebook (k_cb == v_cb) read one
+// sliced table; 4-bit values with their own codebook use a plain 256-entry
+// table (two sliced 64 KB tables would not leave room for two workgroups
+// per CU).
+template <int D, int G, int KB, int VBITS, bool QJL, bool VSH>
 __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(const DecodeArgs a) {
   constexpr int VBK = vector_bytes(D, KB), VBV = vector_bytes(D, VBITS);
   constexpr int KK = D / 16;     // score MFMAs per 16-token tile
   constexpr int NB = D / 16;     // value n-tiles
   constexpr int NSUB = kNSub;
-  constexpr int NLK = KB == 4 ? 256 : 16, NLV = VBITS == 4 ? 256 : 16;
+  static_assert(!VSH || (KB == 4 && VBITS == 4), "a shared table needs 4-bit keys and values");
+  constexpr int NSK = (KB == 4 ? 256 : 16) * kSlices;                         // key table slots
+  constexpr int NSV = VSH ? 1 : VBITS == 4 ? 256 : 16 * kSlices;              // own value table
   constexpr int KQ = D / 32;     // QJL MFMAs per 16-token tile (m = d projections)
   using CK = ChunkK<D, KB, QJL>;
   using CV = ChunkV<VBITS>;
 
-  // LDS holds only the code tables and the end-of-split reduction: the
-  // operands come straight from HBM in the lane order the MFMAs want.
+  // LDS holds only the code tables and the end-of-split reduction (which
+  // reuses the tables' memory): the operands come straight from HBM in the
+  // lane order the MFMAs want.
   struct Smem {
-    uint2 lut_k[NLK], lut_v[NLV], lut_s[QJL ? 16 : 1];
+    union {
+      struct {
+        uint2 k[NSK], v[NSV], s[QJL ? 16 * kSlices : 1];
+      } t;
+      float red_o[kMWaves][G * D];
+    } u;
     float red_m[kMWaves][8], red_l[kMWaves][8];
-    float red_o[kMWaves][G * D];
   };
   __shared__ Smem sm;
-  uint2 *lut_k = sm.lut_k, *lut_v = sm.lut_v, *lut_s = sm.lut_s;
+  const uint2 *lut_k = sm.u.t.k, *lut_v = VSH ? sm.u.t.k : sm.u.t.v, *lut_s = sm.u.t.s;
   auto &red_m = sm.red_m;
   auto &red_l = sm.red_l;
 
@@ -275,9 +338,12 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   if constexpr (QJL)
     sres = stream_rsrc(a.qjl + ((int64_t)(b * a.Hkv + h) * a.S_max) * (D / 8), (uint32_t)a.S * (uint32_t)(D / 8));
 
-  build_lut_pairs<KB>(lut_k, a.k_cb + h * a.cb_head_stride, tid);
-  build_lut_pairs<VBITS>(lut_v, a.v_cb + h * a.cb_head_stride, tid);
-  if constexpr (QJL) build_sign_lut(lut_s, tid);
+  if constexpr (KB == 4) build_sliced4(sm.u.t.k, a.k_cb + h * a.cb_head_stride, tid);
+  else build_sliced2(sm.u.t.k, a.k_cb + h * a.cb_head_stride, tid);
+  if constexpr (VBITS == 2) build_sliced2(sm.u.t.v, a.v_cb + h * a.cb_head_stride, tid);
+  else if constexpr (!VSH) build_lut_pairs<4>(sm.u.t.v, a.v_cb + h * a.cb_head_stride, tid);
+  if constexpr (QJL) build_sliced_sign(sm.u.t.s, tid);
+  const uint32_t loff = (uint32_t)(lane & (kSlices - 1)) * 8u;  // this lane's table copy
 
   // q as the B operand of the score product: column col = (head col & 7,
   // part col >> 3); step kk, k = 8grp + i covers coordinate
@@ -387,21 +453,23 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
       if constexpr (KB == 4) {
         const uint32_t w = qw[kk >> 1];
         const int e = kk & 1;
-        kt.t[kk][0] = lut_k[(w >> (16 * e)) & 0xFF];
-        kt.t[kk][1] = lut_k[(w >> (16 * e + 8)) & 0xFF];
+        kt.t[kk][0] = slice_read(lut_k, slice_addr(w, loff, 2 * e));
+        kt.t[kk][1] = slice_read(lut_k, slice_addr(w, loff, 2 * e + 1));
       } else {
+        // nibbles 2e and 2e + 1 of word kk / 4
         const uint32_t w = qw[kk >> 2];
         const int e = kk & 3;
-        kt.t[kk][0] = lut_k[(w >> (8 * e)) & 0xF];
-        kt.t[kk][1] = lut_k[(w >> (8 * e + 4)) & 0xF];
+        kt.t[kk][0] = slice_read(lut_k, slice_addr(nib_lo(w), loff, e));
+        kt.t[kk][1] = slice_read(lut_k, slice_addr(nib_hi(w), loff, e));
       }
     }
     if constexpr (QJL) {
+      // sign byte kq: low nibble, high nibble
+      const uint32_t slo = nib_lo(k.sg[st]), shi = nib_hi(k.sg[st]);
 #pragma unroll
       for (int kq = 0; kq < KQ; ++kq) {
-        const uint32_t byte = (k.sg[st] >> (8 * kq)) & 0xFF;
-        kt.s[kq][0] = lut_s[byte & 15];
-        kt.s[kq][1] = lut_s[byte >> 4];
+        kt.s[kq][0] = slice_read(lut_s, slice_addr(slo, loff, kq));
+        kt.s[kq][1] = slice_read(lut_s, slice_addr(shi, loff, kq));
       }
     }
   };
@@ -463,12 +531,17 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
       // D = 64: n-tile nb is coordinate 8*(col & 7) + 2*nb + (col >> 3).
       const int par = D == 128 ? (nb & 1) : vpar;
       const int sub = D == 128 ? (nb >> 1) : nb;
-      if constexpr (VBITS == 4) {
+      if constexpr (VBITS == 4 && VSH) {
+        vt.t[nb][0] = slice_read(lut_v, slice_addr(par ? y01 : x01, loff, sub));
+        vt.t[nb][1] = slice_read(lut_v, slice_addr(par ? y23 : x23, loff, sub));
+      } else if constexpr (VBITS == 4) {
         vt.t[nb][0] = lut_v[((par ? y01 : x01) >> (8 * sub)) & 0xFF];
         vt.t[nb][1] = lut_v[((par ? y23 : x23) >> (8 * sub)) & 0xFF];
       } else {
-        vt.t[nb][0] = lut_v[((par ? y01 : x01) >> (4 * sub)) & 0xF];
-        vt.t[nb][1] = lut_v[((par ? y23 : x23) >> (4 * sub)) & 0xF];
+        // nibble sub: byte sub / 2 of the low (even) or high (odd) nibbles
+        const uint32_t w01 = par ? y01 : x01, w23 = par ? y23 : x23;
+        vt.t[nb][0] = slice_read(lut_v, slice_addr((sub & 1) ? nib_hi(w01) : nib_lo(w01), loff, sub >> 1));
+        vt.t[nb][1] = slice_read(lut_v, slice_addr((sub & 1) ? nib_hi(w23) : nib_lo(w23), loff, sub >> 1));
       }
     }
   };
@@ -690,7 +763,8 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     red_l[wave][lane] = l_run;
   }
   // O[head][coord] = D[head] + 2^-11 D[head + 8]: rows 8-15 sit 32 lanes up.
-  float *red_o = sm.red_o[wave];
+  __syncthreads();  // every wave is done with the tables that red_o overlays
+  float *red_o = sm.u.red_o[wave];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -715,7 +789,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     for (int w = 0; w < kMWaves; ++w) {
       const float sc = red_m[w][hh] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w][hh] - mx);
       L += red_l[w][hh] * sc;
-      O += sm.red_o[w][hh * D + c] * sc;
+      O += sm.u.red_o[w][hh * D + c] * sc;
     }
     float *dst = a.part + (((int64_t)(b * a.Hq + h * G + hh) * a.splits) + split) * (D + 2);
     if (c == 0) {
@@ -726,30 +800,33 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   }
 }
 
-template <int D, int KB, int VBITS, bool QJL>
+template <int D, int KB, int VBITS, bool QJL, bool VSH>
 static void launch_dm(const DecodeArgs &a, int G, hipStream_t s) {
   dim3 grid(a.splits, a.B * a.n_heads);
   switch (G) {
-    case 1: decode_mfma_kernel<D, 1, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
-    case 2: decode_mfma_kernel<D, 2, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
-    case 3: decode_mfma_kernel<D, 3, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
-    case 4: decode_mfma_kernel<D, 4, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
-    case 5: decode_mfma_kernel<D, 5, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
-    case 6: decode_mfma_kernel<D, 6, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
-    case 7: decode_mfma_kernel<D, 7, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
-    default: decode_mfma_kernel<D, 8, KB, VBITS, QJL><<<grid, 256, 0, s>>>(a); break;
+    case 1: decode_mfma_kernel<D, 1, KB, VBITS, QJL, VSH><<<grid, 256, 0, s>>>(a); break;
+    case 2: decode_mfma_kernel<D, 2, KB, VBITS, QJL, VSH><<<grid, 256, 0, s>>>(a); break;
+    case 3: decode_mfma_kernel<D, 3, KB, VBITS, QJL, VSH><<<grid, 256, 0, s>>>(a); break;
+    case 4: decode_mfma_kernel<D, 4, KB, VBITS, QJL, VSH><<<grid, 256, 0, s>>>(a); break;
+    case 5: decode_mfma_kernel<D, 5, KB, VBITS, QJL, VSH><<<grid, 256, 0, s>>>(a); break;
+    case 6: decode_mfma_kernel<D, 6, KB, VBITS, QJL, VSH><<<grid, 256, 0, s>>>(a); break;
+    case 7: decode_mfma_kernel<D, 7, KB, VBITS, QJL, VSH><<<grid, 256, 0, s>>>(a); break;
+    default: decode_mfma_kernel<D, 8, KB, VBITS, QJL, VSH><<<grid, 256, 0, s>>>(a); break;
   }
 }
 
-template <int D, int KB, int VBITS>
+template <int D, int KB, int VBITS, bool VSH = false>
 static void launch_dm_q(const DecodeArgs &a, int G, hipStream_t s) {
-  if (a.qjl != nullptr) launch_dm<D, KB, VBITS, true>(a, G, s);
-  else launch_dm<D, KB, VBITS, false>(a, G, s);
+  if (a.qjl != nullptr) launch_dm<D, KB, VBITS, true, VSH>(a, G, s);
+  else launch_dm<D, KB, VBITS, false, VSH>(a, G, s);
 }
 
 template <int D>
 static void launch_dm_w(const DecodeArgs &a, int k_bits, int v_bits, int G, hipStream_t s) {
-  if (k_bits == 4 && v_bits == 4) launch_dm_q<D, 4, 4>(a, G, s);
+  if (k_bits == 4 && v_bits == 4) {
+    if (a.k_cb == a.v_cb) launch_dm_q<D, 4, 4, true>(a, G, s);  // one codebook: one table
+    else launch_dm_q<D, 4, 4>(a, G, s);
+  }
   else if (k_bits == 4) launch_dm_q<D, 4, 2>(a, G, s);
   else if (v_bits == 4) launch_dm_q<D, 2, 4>(a, G, s);
   else launch_dm_q<D, 2, 2>(a, G, s);

@@ -78,10 +78,36 @@ def get_codebook_torch(dim: int, n_bits: int, device="cuda"):
 
 
 def padded_codebook_torch(dim: int, n_bits: int, device="cuda"):
-    """Centroids padded to 16 float32 entries (the kernels' table width)."""
+    """Centroids padded to 16 float32 entries (the kernels' table width).
+
+    One read-only tensor per (dim, n_bits, device): key and value caches of
+    the same width then pass the same codebook pointer, which lets the decode
+    kernel serve both from one LDS table. Do not modify it in place."""
+    import torch
+
+    return _padded_codebook_dev(dim, n_bits, str(torch.device(device)))
+
+
+@lru_cache(maxsize=None)
+def _padded_codebook_dev(dim: int, n_bits: int, device: str):
     import torch
 
     c, _ = build_lloyd_max_codebook(dim, n_bits)
     out = np.zeros(16, np.float32)
     out[: c.shape[0]] = c
     return torch.from_numpy(out).to(device)
+
+
+def stacked_codebooks_torch(dim: int, n_bits: tuple, device="cuda"):
+    """padded_codebook_torch for each head width, stacked [H, 16]; shared and
+    read-only in the same way."""
+    import torch
+
+    return _stacked_codebooks_dev(dim, tuple(int(b) for b in n_bits), str(torch.device(device)))
+
+
+@lru_cache(maxsize=None)
+def _stacked_codebooks_dev(dim: int, n_bits: tuple, device: str):
+    import torch
+
+    return torch.stack([_padded_codebook_dev(dim, b, device) for b in n_bits])

@@ -13,7 +13,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .lloyd_max import padded_codebook_torch
+from .lloyd_max import padded_codebook_torch, stacked_codebooks_torch
 from .types import PQCache, vector_bytes
 
 
@@ -42,7 +42,7 @@ def allocate_cache(batch: int, num_heads: int, max_seq_len: int, head_dim: int, 
         per_batch = sum(max_seq_len * vector_bytes(head_dim, b) for b in n_bits)
         blocks = torch.zeros(batch, per_batch, dtype=torch.uint8, device=device)
         if codebooks is None:
-            codebooks = torch.stack([padded_codebook_torch(head_dim, b, device) for b in n_bits])
+            codebooks = stacked_codebooks_torch(head_dim, n_bits, device)
         n_bits = tuple(int(b) for b in n_bits)
     else:
         blocks = torch.zeros(batch, num_heads, max_seq_len, vector_bytes(head_dim, n_bits),

@@ -121,6 +121,34 @@ def test_decode_valu_kernel_matches_oracle(case, monkeypatch):
     _check(out.cpu().numpy(), _oracle(q, R, kc, vc, S))
 
 
+@pytest.mark.parametrize("same_content", [True, False], ids=["copy", "scaled"])
+def test_decode_value_codebook_of_its_own(same_content):
+    """4-bit keys and values whose codebooks sit at different addresses: the
+    values read their own table (keys and values share one table only when
+    they pass the same codebook pointer). A scaled value codebook shows that
+    the values really use theirs."""
+    from polarquant_kv.lloyd_max import padded_codebook_torch
+    B, Hq, Hkv, S, d = 2, 16, 4, 600, 128
+    cbk = padded_codebook_torch(d, 4, DEV)
+    cbv = cbk.clone() if same_content else cbk * 0.9
+    rng = np.random.default_rng(5)
+    k = O.synth_kv(B, Hkv, S, d, 6, "token_ln")
+    v = O.synth_kv(B, Hkv, S, d, 7, "token_ln")
+    q = rng.standard_normal((B, Hq, d)).astype(np.float16)
+    R = O.rotation_matrix(d, 42)
+    Rt = torch.from_numpy(R.astype(np.float32)).to(DEV)
+    kc = quantizer.allocate_cache(B, Hkv, S, d, 4, DEV)
+    vc = quantizer.allocate_cache(B, Hkv, S, d, 4, DEV, codebooks=cbv)
+    assert kc.codebooks.data_ptr() != vc.codebooks.data_ptr()
+    quantizer.compress_pq(torch.from_numpy(k).to(DEV), Rt, cache=kc)
+    quantizer.compress_pq(torch.from_numpy(v).to(DEV), Rt, cache=vc)
+    out = attention.decode_attention(torch.from_numpy(q).to(DEV), kc, vc, Rt, out_dtype=torch.float32)
+    ref = O.decode_attention(q.astype(np.float64), kc.blocks.cpu().numpy()[:, :, :S], vc.blocks.cpu().numpy()[:, :, :S],
+                             R, cbk.cpu().numpy()[:16].astype(np.float64), cbv.cpu().numpy()[:16].astype(np.float64),
+                             k_bits=4, v_bits=4)
+    _check(out.cpu().numpy(), ref)
+
+
 def test_decode_outlier_channels_both_kernels(monkeypatch):
     """The metric config's data law (per-channel LogNormal std, 1 % of the
     channels x20): outputs reach ~1e2, so this is the case that needs

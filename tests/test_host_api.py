@@ -66,6 +66,21 @@ def test_cache_layout_helpers():
     assert c.head_offset(0) == 0 and c.head_offset(1) == 5 * 72 and c.head_offset(2) == 5 * 72 + 5 * 40
 
 
+def test_caches_of_one_width_share_the_codebook():
+    """Key and value caches of one width and head_dim pass the same codebook
+    pointer (decode then serves both from one table); other widths do not."""
+    from polarquant_kv import quantizer
+    a = quantizer.allocate_cache(1, 2, 8, 64, 4, "cpu")
+    b = quantizer.allocate_cache(1, 2, 8, 64, 4, "cpu")
+    assert a.codebooks is b.codebooks
+    assert quantizer.allocate_cache(1, 2, 8, 64, 2, "cpu").codebooks is not a.codebooks
+    assert quantizer.allocate_cache(1, 2, 8, 128, 4, "cpu").codebooks is not a.codebooks
+    m1 = quantizer.allocate_cache(1, 2, 8, 64, (4, 2), "cpu")
+    m2 = quantizer.allocate_cache(1, 2, 8, 64, [4, 2], "cpu")
+    assert m1.codebooks is m2.codebooks and m1.codebooks.shape == (2, 16)
+    assert torch.equal(m1.codebooks[0], a.codebooks)
+
+
 def test_gpu_entry_points_refuse_cpu_tensors():
     from polarquant_kv import attention, quantizer
     x = torch.zeros(1, 1, 4, 128)
