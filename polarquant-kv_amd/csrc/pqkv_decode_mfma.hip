@@ -193,22 +193,21 @@ __device__ __forceinline__ uint32_t bld16(__amdgpu_buffer_rsrc_t r, int off) {
   return (uint32_t)__builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
 }
 
-// N consecutive dwords at the dword-aligned byte offset `off`.
+// N consecutive dwords at byte offset `off`, which need only be 2-byte
+// aligned: buffer loads at 2 mod 4 return the bytes at that address (checked
+// on gfx950), so the qs words of a block need no realignment.
 template <int N>
 __device__ __forceinline__ void load_words(__amdgpu_buffer_rsrc_t r, int off, uint32_t (&w)[N]) {
   typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-  typedef uint32_t u32x3v __attribute__((ext_vector_type(3)));
-  if constexpr (N == 5) {
+  if constexpr (N == 4) {
     const u32x4 x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
     w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
-    w[4] = bld32(r, off + 16);
-  } else if constexpr (N == 3) {
-    const u32x3v x = __builtin_bit_cast(u32x3v, __builtin_amdgcn_raw_buffer_load_b96(r, off, 0, 0));
-    w[0] = x.x; w[1] = x.y; w[2] = x.z;
-  } else {
-    static_assert(N == 2, "operand word count");
+  } else if constexpr (N == 2) {
     const u32x2v x = __builtin_bit_cast(u32x2v, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
     w[0] = x.x; w[1] = x.y;
+  } else {
+    static_assert(N == 1, "operand word count");
+    w[0] = bld32(r, off);
   }
 }
 
@@ -257,26 +256,22 @@ constexpr int kNSub = kChunk / kSub;
 
 // One 64-token chunk of keys in operand order, straight from HBM. For
 // sub-tile st, lane (col, grp) holds the qs bytes of coordinates
-// grp*D/4 .. grp*D/4 + D/4 - 1 of token 16 st + col: kWords dwords that start
-// 2 bytes (qs start 2 mod 4) or 4 bytes (qs start dword-aligned) before them,
-// so every load stays inside its own vector and one byte permute per word
-// aligns them. r: the radius of token 16 (col / 4) + 4 grp + col % 4 (row
+// grp*D/4 .. grp*D/4 + D/4 - 1 of token 16 st + col (kWords dwords, loaded
+// at their own, possibly 2 mod 4, offset). r: the radius of token 16 (col / 4) + 4 grp + col % 4 (row
 // broadcasts hand each lane those of its score rows). sg (QJL): sign bytes
 // grp*D/32 .. of token 16 st + col.
 template <int D, int KB, bool QJL>
 struct ChunkK {
-  static constexpr int kWords = D * KB / 128 + 1;
+  static constexpr int kWords = D * KB / 128;
   uint32_t w[kNSub][kWords];
   uint32_t r;
   uint32_t sg[QJL ? kNSub : 1];
 };
 // Values: for sub-tile kb and e = 0..3, the lane's qs word of token
-// 16 kb + 4 grp + e (4-bit: the two dwords around it, aligned as for keys;
-// 2-bit: the half dword). r as for keys.
+// 16 kb + 4 grp + e (4-bit: a dword; 2-bit: a half dword). r as for keys.
 template <int VBITS>
 struct ChunkV {
-  static constexpr int kWords = VBITS == 4 ? 2 : 1;
-  uint32_t w[kNSub][4][kWords];
+  uint32_t w[kNSub][4];
   uint32_t r;
 };
 
@@ -390,12 +385,9 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   for (int nb = 0; nb < NB; ++nb) oacc[nb] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
   // Key side: the lane group's qs bytes start kphys bytes into the vector
-  // (2 mod 4 or 0 mod 4); the loaded words start 2 or 4 bytes earlier and
-  // a byte permute with ksel aligns them.
+  // (2 mod 4 or 0 mod 4).
   const int kc0 = grp * (D / 4);
   const int kphys = (kc0 / kBlock) * block_bytes(KB) + 2 + (kc0 % kBlock) * KB / 8;
-  const int koff = kphys - ((kphys & 3) ? 2 : 4);
-  const uint32_t ksel = (kphys & 3) ? 0x05040302u : 0x07060504u;
   // Value side: the lane's 8 coordinates (D = 128: 8 col .. + 7; D = 64:
   // 8 (col & 7) .. + 7 with parity col >> 3) as a qs dword (4-bit) or half
   // dword (2-bit) of each token.
@@ -403,8 +395,6 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   const int vpar = D == 128 ? 0 : (col >> 3);
   const int vob = VBITS == 4 ? (vw >> 2) * kPq4BlockBytes + 2 + 4 * (vw & 3)
                              : (vw >> 2) * kPq2BlockBytes + 2 + 2 * (vw & 3);
-  const int voff = VBITS == 4 ? vob - ((vob & 3) ? 2 : 4) : vob;
-  const uint32_t vsel = (vob & 3) ? 0x05040302u : 0x07060504u;
   // token (relative to the chunk) whose radii this lane loads
   const int rtok = kSub * (col >> 2) + 4 * grp + (col & 3);
 
@@ -412,7 +402,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   // load makes the compiler keep the register array in scratch.
   auto load_k = [&](CK &c, int t0) {
 #pragma unroll
-    for (int st = 0; st < NSUB; ++st) load_words(kres, (t0 + kSub * st + col) * VBK + koff, c.w[st]);
+    for (int st = 0; st < NSUB; ++st) load_words(kres, (t0 + kSub * st + col) * VBK + kphys, c.w[st]);
     c.r = bld16(kres, (t0 + rtok) * VBK);
     if constexpr (QJL) {
 #pragma unroll
@@ -427,9 +417,8 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     for (int kb = 0; kb < NSUB; ++kb)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int off = (t0 + kSub * kb + 4 * grp + e) * VBV + voff;
-        if constexpr (VBITS == 4) load_words(vres, off, c.w[kb][e]);
-        else c.w[kb][e][0] = bld16(vres, off);
+        const int off = (t0 + kSub * kb + 4 * grp + e) * VBV + vob;
+        c.w[kb][e] = VBITS == 4 ? bld32(vres, off) : bld16(vres, off);
       }
     c.r = bld16(vres, (t0 + rtok) * VBV);
   };
@@ -444,9 +433,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   };
   auto kread = [&](const CK &k, int st, KTile &kt) {
     // the lane group's qs words of token 16st + col
-    uint32_t qw[CK::kWords - 1];
-#pragma unroll
-    for (int i = 0; i + 1 < CK::kWords; ++i) qw[i] = __builtin_amdgcn_perm(k.w[st][i + 1], k.w[st][i], ksel);
+    const uint32_t (&qw)[CK::kWords] = k.w[st];
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       // step kk: coordinates 4kk .. 4kk + 3 of the lane group's range
@@ -507,18 +494,14 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   auto vread = [&](const CV &v, int kb, VTile &vt) {
     uint32_t x01, y01, x23, y23;
     if constexpr (VBITS == 4) {
-      uint32_t wv[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) wv[e] = __builtin_amdgcn_perm(v.w[kb][e][1], v.w[kb][e][0], vsel);
+      const uint32_t (&wv)[4] = v.w[kb];
       // byte k of x = even coordinate 2k of both tokens, of y = odd 2k + 1
       x01 = (wv[0] & 0x0F0F0F0Fu) | ((wv[1] << 4) & 0xF0F0F0F0u);
       y01 = ((wv[0] >> 4) & 0x0F0F0F0Fu) | (wv[1] & 0xF0F0F0F0u);
       x23 = (wv[2] & 0x0F0F0F0Fu) | ((wv[3] << 4) & 0xF0F0F0F0u);
       y23 = ((wv[2] >> 4) & 0x0F0F0F0Fu) | (wv[3] & 0xF0F0F0F0u);
     } else {
-      uint32_t wv[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) wv[e] = v.w[kb][e][0];
+      const uint32_t (&wv)[4] = v.w[kb];
       // nibble k of x = even coordinate 2k of both tokens, of y = odd 2k + 1
       x01 = (wv[0] & 0x3333u) | ((wv[1] << 2) & 0xCCCCu);
       y01 = ((wv[0] >> 2) & 0x3333u) | (wv[1] & 0xCCCCu);
