@@ -400,27 +400,32 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
 
   // Every load is unconditional (tokens past S read zeros); a conditional
   // load makes the compiler keep the register array in scratch.
-  auto load_k = [&](CK &c, int t0) {
-#pragma unroll
-    for (int st = 0; st < NSUB; ++st) load_words(kres, (t0 + kSub * st + col) * VBK + kphys, c.w[st]);
-    c.r = bld16(kres, (t0 + rtok) * VBK);
+  // Per sub-tile pieces, so that a step can reload each sub-tile's registers
+  // as soon as it has read them (and the radii first: they are converted at
+  // the start of a step).
+  auto load_k_sub = [&](CK &c, int t0, int st) {
+    load_words(kres, (t0 + kSub * st + col) * VBK + kphys, c.w[st]);
     if constexpr (QJL) {
-#pragma unroll
-      for (int st = 0; st < NSUB; ++st) {
-        const int so = (t0 + kSub * st + col) * (D / 8) + grp * (D / 32);
-        c.sg[st] = D == 128 ? bld32(sres, so) : bld16(sres, so);
-      }
+      const int so = (t0 + kSub * st + col) * (D / 8) + grp * (D / 32);
+      c.sg[st] = D == 128 ? bld32(sres, so) : bld16(sres, so);
     }
   };
+  auto load_v_sub = [&](CV &c, int t0, int kb) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int off = (t0 + kSub * kb + 4 * grp + e) * VBV + vob;
+      c.w[kb][e] = VBITS == 4 ? bld32(vres, off) : bld16(vres, off);
+    }
+  };
+  auto load_k = [&](CK &c, int t0) {
+    c.r = bld16(kres, (t0 + rtok) * VBK);
+#pragma unroll
+    for (int st = 0; st < NSUB; ++st) load_k_sub(c, t0, st);
+  };
   auto load_v = [&](CV &c, int t0) {
-#pragma unroll
-    for (int kb = 0; kb < NSUB; ++kb)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int off = (t0 + kSub * kb + 4 * grp + e) * VBV + vob;
-        c.w[kb][e] = VBITS == 4 ? bld32(vres, off) : bld16(vres, off);
-      }
     c.r = bld16(vres, (t0 + rtok) * VBV);
+#pragma unroll
+    for (int kb = 0; kb < NSUB; ++kb) load_v_sub(c, t0, kb);
   };
   __syncthreads();
 
@@ -683,9 +688,19 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   // finish of the chunk in v with logits sc, sub-tile by sub-tile: both
   // tiles' table reads are issued first, the softmax weights are computed
   // while they are in flight, then the two products run.
-  auto step = [&](const CK &k, const CV &v, const float4_t (&sc)[NSUB], float4_t (&sn)[NSUB]) {
+  // One iteration; k and v are reloaded in place with the chunks at tk and
+  // tv. With kPieceLoads the pieces go out as the iteration consumes them
+  // (loads complete in order, so the next iteration's first reads wait only
+  // for the first loads: config 4 28.3 -> 27.3 us); the QJL kernels with
+  // G > 4 would spill with that schedule and reload after the iteration.
+  constexpr bool kPieceLoads = !QJL || G <= 4;
+  auto step = [&](CK &k, CV &v, const float4_t (&sc)[NSUB], float4_t (&sn)[NSUB], int tk, int tv) {
     float sv[NSUB][4];
     const float rkl = half_bits_to_float(k.r), rvl = half_bits_to_float(v.r);
+    if constexpr (kPieceLoads) {
+      k.r = bld16(kres, (tk + rtok) * VBK);
+      v.r = bld16(vres, (tv + rtok) * VBV);
+    }
     FState f = fbegin(sv, sc, kChunk, false, rvl);
 #pragma unroll
     for (int j = 0; j < NSUB; ++j) {
@@ -693,6 +708,10 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
       VTile vt;
       kread(k, j, kt);
       vread(v, j, vt);
+      if constexpr (kPieceLoads) {
+        load_k_sub(k, tk, j);
+        load_v_sub(v, tv, j);
+      }
       __builtin_amdgcn_sched_barrier(0);
       const half8_t pav = fweights(sv[j], rvl, j, f);
       __builtin_amdgcn_sched_barrier(0);
@@ -700,15 +719,18 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
       vmma(pav, vt);
     }
     l_run = l_run * f.alpha + f.psum;
+    if constexpr (!kPieceLoads) {
+      load_k(k, tk);
+      load_v(v, tv);
+    }
   };
 
   // The wave's chunks start at first + i * kStep. Iteration i computes the
   // scores of chunk i + 1 and finishes chunk i (softmax + values), sub-tile
   // by sub-tile, so each one's table-read latency hides behind the other's
-  // work. A chunk's key registers are reloaded (chunk i + 2) as soon as its
-  // scores are done, its value registers (chunk i + 1) as soon as it is
-  // finished: each load has most of an iteration to land. Only the last
-  // chunk can be partial; it is finished after the loop.
+  // work. The key registers are reloaded with chunk i + 2 and the value
+  // registers with chunk i + 1. Only the last chunk can be partial; it is
+  // finished after the loop.
   constexpr int kStep = kMWaves * kChunk;
   const int first = t_begin + wave * kChunk;
   const int nch = first < t_end ? (t_end - first + kStep - 1) / kStep : 0;
@@ -723,9 +745,7 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     load_k(ck, first + min(1, nch - 1) * kStep);
     for (int i = 0; i + 1 < nch; ++i) {
       float4_t snext[NSUB];
-      step(ck, cv, sacc, snext);
-      load_k(ck, first + min(i + 2, nch - 1) * kStep);
-      load_v(cv, first + (i + 1) * kStep);
+      step(ck, cv, sacc, snext, first + min(i + 2, nch - 1) * kStep, first + (i + 1) * kStep);
 #pragma unroll
       for (int st = 0; st < NSUB; ++st) sacc[st] = snext[st];
     }
