@@ -130,6 +130,9 @@ int pqkv_encode_mfma(const void *x, int x_dtype, int64_t x_outer_stride,
  * widths each (b, h) run still holds S_max vectors of its own width, runs laid
  * out in (b, h) order. k_codebooks / v_codebooks: device [Hkv][16] fp32
  * per-head tables, or one table when the *_head_bits pointer is NULL.
+ * Passing the same pointer for k_codebooks and v_codebooks with 4-bit keys
+ * and values lets one LDS table serve both (faster); distinct pointers are
+ * always correct.
  * Replaces turboquant_full_attention (csrc/flash_turboquant.cu:180-211),
  * polarquant_fused_attention_cuda (patch:469-506) plus the query and output
  * rotations around them (patch:395-437). R (and p_rot) are device fp32
