@@ -430,6 +430,10 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   __syncthreads();
 
   // ---- building blocks of one chunk ----
+  // G <= 4 without QJL: the score products leave the MFMA raw (hi part in
+  // lanes col < 4, cross part in lanes 8..11) and fbegin combines them after
+  // compacting the four sub-tiles, on 4 values per lane instead of 16.
+  constexpr bool kRawScores = G <= 4 && !QJL;
   // Table reads of key sub-tile st: per score step kk, 4 codes x (hi, lo)
   // (two 8-byte entries); QJL adds the sign-table reads.
   struct KTile {
@@ -478,6 +482,10 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     if constexpr (QJL) {
 #pragma unroll
       for (int kq = 0; kq < KQ; ++kq) accq = mfma16(pack8(kt.s[kq][0], kt.s[kq][1]), pb[kq], accq);
+    }
+    if constexpr (kRawScores) {
+      out = acc;  // combined after the compaction (fbegin)
+      return;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -549,7 +557,8 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     float mnew, alpha, psum;
     uint32_t top[kCompact ? 4 : 1], bot[kCompact ? 4 : 1];  // compact weights: (p_hi, 0), (p_lo, p_hi)
   };
-  auto fbegin = [&](float (&sv)[NSUB][4], const float4_t (&sc)[NSUB], int ntok, bool partial, float rvl) {
+  // rks (kRawScores): this lane's loaded key radius of the chunk in sc.
+  auto fbegin = [&](float (&sv)[NSUB][4], const float4_t (&sc)[NSUB], int ntok, bool partial, float rvl, float rks) {
     FState f;
     float cmax;
     float cv[4];
@@ -560,6 +569,15 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
         c = dpp_intof<0x114, 0x2>(c, sc[1][i]);  // row_shr:4 into bank 1
         c = dpp_intof<0x118, 0x4>(c, sc[2][i]);  // row_shr:8 into bank 2
         c = dpp_intof<0x11C, 0x8>(c, sc[3][i]);  // row_shr:12 into bank 3
+        if constexpr (kRawScores) {
+          // cross parts (lanes 8 + h of sub-tile j) to lane 4 j + h
+          float x = sc[2][i];
+          x = dpp_intof<0x108, 0x1>(x, sc[0][i]);  // row_shl:8 into bank 0
+          x = dpp_intof<0x104, 0x2>(x, sc[1][i]);  // row_shl:4 into bank 1
+          x = dpp_intof<0x114, 0x8>(x, sc[3][i]);  // row_shr:4 into bank 3
+          // radius of token 16 j + 4 grp + i: lane 4 j + i of the quad
+          c = __builtin_fmaf(x, 1.0f / kLoScale, c) * quad_bcast(rks, i);
+        }
         cv[i] = partial && kSub * (col >> 2) + 4 * grp + i >= ntok ? -INFINITY : c;
       }
       cmax = fmaxf(fmaxf(cv[0], cv[1]), fmaxf(cv[2], cv[3]));
@@ -658,8 +676,9 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   };
 
   // Scores of a whole chunk (the first one): reads one sub-tile ahead.
-  auto scores = [&](const CK &k, float4_t (&sc)[NSUB]) {
+  auto scores = [&](const CK &k, float4_t (&sc)[NSUB], float &rks) {
     const float rkl = half_bits_to_float(k.r);
+    rks = rkl;
     KTile kt[2];
     kread(k, 0, kt[0]);
 #pragma unroll
@@ -670,10 +689,10 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     }
   };
   // Softmax update and value product of a whole chunk (the last one).
-  auto finish = [&](const CV &v, const float4_t (&sc)[NSUB], int ntok, bool partial) {
+  auto finish = [&](const CV &v, const float4_t (&sc)[NSUB], float rks, int ntok, bool partial) {
     float sv[NSUB][4];
     const float rvl = half_bits_to_float(v.r);
-    FState f = fbegin(sv, sc, ntok, partial, rvl);
+    FState f = fbegin(sv, sc, ntok, partial, rvl, rks);
     VTile vt[2];
     vread(v, 0, vt[0]);
 #pragma unroll
@@ -694,14 +713,16 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   // for the first loads: config 4 28.3 -> 27.3 us); the QJL kernels with
   // G > 4 would spill with that schedule and reload after the iteration.
   constexpr bool kPieceLoads = !QJL || G <= 4;
-  auto step = [&](CK &k, CV &v, const float4_t (&sc)[NSUB], float4_t (&sn)[NSUB], int tk, int tv) {
+  auto step = [&](CK &k, CV &v, const float4_t (&sc)[NSUB], float rks, float4_t (&sn)[NSUB], float &rkn, int tk,
+                  int tv) {
     float sv[NSUB][4];
     const float rkl = half_bits_to_float(k.r), rvl = half_bits_to_float(v.r);
+    rkn = rkl;
     if constexpr (kPieceLoads) {
       k.r = bld16(kres, (tk + rtok) * VBK);
       v.r = bld16(vres, (tv + rtok) * VBV);
     }
-    FState f = fbegin(sv, sc, kChunk, false, rvl);
+    FState f = fbegin(sv, sc, kChunk, false, rvl, rks);
 #pragma unroll
     for (int j = 0; j < NSUB; ++j) {
       KTile kt;
@@ -740,17 +761,20 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
     load_k(ck, first);
     load_v(cv, first);
     float4_t sacc[NSUB];
-    scores(ck, sacc);
+    float rks;
+    scores(ck, sacc, rks);
     // chunk 1 (a repeat of chunk 0 when there is none: an L2 hit)
     load_k(ck, first + min(1, nch - 1) * kStep);
     for (int i = 0; i + 1 < nch; ++i) {
       float4_t snext[NSUB];
-      step(ck, cv, sacc, snext, first + min(i + 2, nch - 1) * kStep, first + (i + 1) * kStep);
+      float rkn;
+      step(ck, cv, sacc, rks, snext, rkn, first + min(i + 2, nch - 1) * kStep, first + (i + 1) * kStep);
 #pragma unroll
       for (int st = 0; st < NSUB; ++st) sacc[st] = snext[st];
+      rks = rkn;
     }
     const int tlast = first + (nch - 1) * kStep;
-    finish(cv, sacc, min(kChunk, t_end - tlast), true);
+    finish(cv, sacc, rks, min(kChunk, t_end - tlast), true);
   }
 
   // ---------------- per-wave results ----------------
