@@ -195,18 +195,32 @@ def test_decode_mixed_widths():
     _check(out.cpu().numpy(), _oracle(q, R, kc, vc, S))
 
 
-def test_decode_qjl_correction():
-    B, Hq, Hkv, S, d = 1, 8, 2, 300, 128
-    q, R, Rt, kc, vc, P_rot = _setup(B, Hq, Hkv, S, d, 2, 2, seed=21, qjl=True)
+QJL_CASES = [
+    # B, Hq, Hkv, S, d, kbits, vbits
+    (1, 8, 2, 300, 128, 2, 2),      # config 4 shape family (G = 4)
+    (1, 16, 2, 333, 128, 4, 4),     # G = 8: whole-chunk reloads, one shared 4-bit table
+    (2, 14, 2, 257, 64, 4, 2),      # G = 7, d = 64, 4-bit K / 2-bit V
+    (1, 4, 4, 100, 128, 4, 4),      # G = 1
+]
+
+
+@pytest.mark.parametrize("case", QJL_CASES, ids=lambda c: "B{}_Hq{}_Hkv{}_S{}_d{}_k{}v{}".format(*c))
+def test_decode_qjl_correction(case):
+    B, Hq, Hkv, S, d, kb, vb = case
+    print(f"qjl case {case}", flush=True)
+    q, R, Rt, kc, vc, P_rot = _setup(B, Hq, Hkv, S, d, kb, vb, seed=21 + sum(case), qjl=True)
     out = attention.decode_attention(torch.from_numpy(q).to(DEV), kc, vc, Rt, jl_rot=P_rot,
                                      out_dtype=torch.float32)
     P = O.jl_matrix(d, d, 43)
     signs = kc.qjl_signs.cpu().numpy()[:, :, :S]
     ref = _oracle(q, R, kc, vc, S, P=P, signs=signs)
     _check(out.cpu().numpy(), ref)
-    # the correction must matter: without it the result moves
+    # the correction must matter: without it the result moves (1.2e-2 to
+    # 2.7e-2 on these cases)
     plain = _oracle(q, R, kc, vc, S)
-    assert np.abs(plain - ref).max() > 2 * MAX_ABS
+    moved = np.abs(plain - ref).max()
+    print(f"qjl correction moves the output by {moved:.3e}", flush=True)
+    assert moved > 2 * MAX_ABS
 
 
 def test_compressed_attention_gpu_api():
