@@ -423,14 +423,18 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
   // One split plan serves every launch (they share the partials layout); it
   // is sized for the largest launch: all kv heads, or with mixed widths the
   // largest group of heads sharing (k bits, v bits).
+  // Heads that are all 4/4 (one shared codebook) or 2/2 run as one launch.
+  const bool mfma = use_mfma();
   int group = Hkv;
+  bool pair = false;
   if (mixed) {
     int count[2][2] = {{0, 0}, {0, 0}};
     for (int h = 0; h < Hkv; ++h) ++count[kb[h] == 4][vb[h] == 4];
-    group = std::max(std::max(count[0][0], count[0][1]), std::max(count[1][0], count[1][1]));
+    pair = mfma && count[1][1] > 0 && count[0][0] > 0 && count[1][0] == 0 && count[0][1] == 0 &&
+           k_codebooks == v_codebooks;
+    if (!pair) group = std::max(std::max(count[0][0], count[0][1]), std::max(count[1][0], count[1][1]));
   }
   int splits = 1, tps = 0;
-  const bool mfma = use_mfma();
   decode_plan((int64_t)B * group, S, mfma ? mfma_target() : kValuTarget, &splits, &tps);
   float *q32 = (float *)workspace;
   float *part = (float *)((char *)workspace + align256((size_t)B * Hq * d * 4));
@@ -486,23 +490,42 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
     a.k_batch_stride = koff[Hkv];
     a.v_batch_stride = voff[Hkv];
     a.listed = 1;
-    for (int kbits : {4, 2})
-      for (int vbits : {4, 2}) {
-        int n = 0;
-        for (int h = 0; h < Hkv; ++h)
-          if (kb[h] == kbits && vb[h] == vbits) {
-            a.heads[n] = (int16_t)h;
-            a.k_head_off[n] = koff[h];
-            a.v_head_off[n] = voff[h];
-            ++n;
-          }
-        if (n == 0) continue;
-        a.n_heads = n;
-        tok = pqkv::prof_begin("decode_split", st);
-        e = mfma ? pqkv::launch_decode_mfma(a, kbits, vbits, st) : pqkv::launch_decode_split(a, kbits, vbits, st);
-        pqkv::prof_end(tok, st);
-        if (e != hipSuccess) return hip_status(e, "decode split launch");
+    if (pair) {
+      pqkv::DecodeArgs a2 = a;
+      int n4 = 0, n2 = 0;
+      for (int h = 0; h < Hkv; ++h) {
+        pqkv::DecodeArgs &g = kb[h] == 4 ? a : a2;
+        int &n = kb[h] == 4 ? n4 : n2;
+        g.heads[n] = (int16_t)h;
+        g.k_head_off[n] = koff[h];
+        g.v_head_off[n] = voff[h];
+        ++n;
       }
+      a.n_heads = n4;
+      a2.n_heads = n2;
+      tok = pqkv::prof_begin("decode_split", st);
+      e = pqkv::launch_decode_mfma_pair(a, a2, st);
+      pqkv::prof_end(tok, st);
+      if (e != hipSuccess) return hip_status(e, "decode split launch");
+    } else {
+      for (int kbits : {4, 2})
+        for (int vbits : {4, 2}) {
+          int n = 0;
+          for (int h = 0; h < Hkv; ++h)
+            if (kb[h] == kbits && vb[h] == vbits) {
+              a.heads[n] = (int16_t)h;
+              a.k_head_off[n] = koff[h];
+              a.v_head_off[n] = voff[h];
+              ++n;
+            }
+          if (n == 0) continue;
+          a.n_heads = n;
+          tok = pqkv::prof_begin("decode_split", st);
+          e = mfma ? pqkv::launch_decode_mfma(a, kbits, vbits, st) : pqkv::launch_decode_split(a, kbits, vbits, st);
+          pqkv::prof_end(tok, st);
+          if (e != hipSuccess) return hip_status(e, "decode split launch");
+        }
+    }
   }
   tok = pqkv::prof_begin("decode_merge", st);
   e = pqkv::launch_decode_merge(part, R, out, out_dtype, B * Hq, splits, d, st);

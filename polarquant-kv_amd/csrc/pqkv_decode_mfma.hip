@@ -281,40 +281,41 @@ struct ChunkV {
 // sliced table; 4-bit values with their own codebook use a plain 256-entry
 // table (two sliced 64 KB tables would not leave room for two workgroups
 // per CU).
+// LDS of one workgroup: only the code tables and the end-of-split reduction
+// (which reuses the tables' memory): the operands come straight from HBM in
+// the lane order the MFMAs want.
 template <int D, int G, int KB, int VBITS, bool QJL, bool VSH>
-__global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(const DecodeArgs a) {
+struct DecodeSmem {
+  static_assert(!VSH || (KB == 4 && VBITS == 4), "a shared table needs 4-bit keys and values");
+  static constexpr int NSK = (KB == 4 ? 256 : 16) * kSlices;              // key table slots
+  static constexpr int NSV = VSH ? 1 : VBITS == 4 ? 256 : 16 * kSlices;   // own value table
+  union {
+    struct {
+      uint2 k[NSK], v[NSV], s[QJL ? 16 * kSlices : 1];
+    } t;
+    float red_o[kMWaves][G * D];
+  } u;
+  float red_m[kMWaves][8], red_l[kMWaves][8];
+};
+
+// One workgroup: split `split` of the (batch, listed head) pair bh.
+template <int D, int G, int KB, int VBITS, bool QJL, bool VSH>
+__device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem<D, G, KB, VBITS, QJL, VSH> &sm,
+                                                 const int split, const int bh) {
   constexpr int VBK = vector_bytes(D, KB), VBV = vector_bytes(D, VBITS);
   constexpr int KK = D / 16;     // score MFMAs per 16-token tile
   constexpr int NB = D / 16;     // value n-tiles
   constexpr int NSUB = kNSub;
-  static_assert(!VSH || (KB == 4 && VBITS == 4), "a shared table needs 4-bit keys and values");
-  constexpr int NSK = (KB == 4 ? 256 : 16) * kSlices;                         // key table slots
-  constexpr int NSV = VSH ? 1 : VBITS == 4 ? 256 : 16 * kSlices;              // own value table
   constexpr int KQ = D / 32;     // QJL MFMAs per 16-token tile (m = d projections)
   using CK = ChunkK<D, KB, QJL>;
   using CV = ChunkV<VBITS>;
 
-  // LDS holds only the code tables and the end-of-split reduction (which
-  // reuses the tables' memory): the operands come straight from HBM in the
-  // lane order the MFMAs want.
-  struct Smem {
-    union {
-      struct {
-        uint2 k[NSK], v[NSV], s[QJL ? 16 * kSlices : 1];
-      } t;
-      float red_o[kMWaves][G * D];
-    } u;
-    float red_m[kMWaves][8], red_l[kMWaves][8];
-  };
-  __shared__ Smem sm;
   const uint2 *lut_k = sm.u.t.k, *lut_v = VSH ? sm.u.t.k : sm.u.t.v, *lut_s = sm.u.t.s;
   auto &red_m = sm.red_m;
   auto &red_l = sm.red_l;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
-  const int split = blockIdx.x;
-  const int bh = blockIdx.y;
   const int b = bh / a.n_heads, hi_ = bh - b * a.n_heads;
   const int h = a.listed ? a.heads[hi_] : hi_;
   const int t_begin = split * a.tokens_per_split;
@@ -827,6 +828,31 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(cons
   }
 }
 
+template <int D, int G, int KB, int VBITS, bool QJL, bool VSH>
+__global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(const DecodeArgs a) {
+  __shared__ DecodeSmem<D, G, KB, VBITS, QJL, VSH> sm;
+  decode_mfma_body<D, G, KB, VBITS, QJL, VSH>(a, sm, blockIdx.x, blockIdx.y);
+}
+
+// Mixed widths whose kv heads are either 4-bit keys and values (a4, one
+// shared codebook) or 2-bit keys and values (a2): both groups in one grid,
+// rows 0 .. B*a4.n_heads - 1 of blockIdx.y for the first. The two bodies
+// share one LDS allocation (a workgroup runs one of them), so two
+// workgroups still fit per CU; one launch instead of two saves a launch's
+// fill and drain.
+template <int D, int G, bool QJL>
+__global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_pair_kernel(const DecodeArgs a4,
+                                                                                 const DecodeArgs a2) {
+  using S4 = DecodeSmem<D, G, 4, 4, QJL, true>;
+  using S2 = DecodeSmem<D, G, 2, 2, QJL, false>;
+  __shared__ __attribute__((aligned(16))) uint8_t raw[sizeof(S4) > sizeof(S2) ? sizeof(S4) : sizeof(S2)];
+  const int n4 = a4.B * a4.n_heads;
+  if ((int)blockIdx.y < n4)
+    decode_mfma_body<D, G, 4, 4, QJL, true>(a4, *reinterpret_cast<S4 *>(raw), blockIdx.x, blockIdx.y);
+  else
+    decode_mfma_body<D, G, 2, 2, QJL, false>(a2, *reinterpret_cast<S2 *>(raw), blockIdx.x, blockIdx.y - n4);
+}
+
 template <int D, int KB, int VBITS, bool QJL, bool VSH>
 static void launch_dm(const DecodeArgs &a, int G, hipStream_t s) {
   dim3 grid(a.splits, a.B * a.n_heads);
@@ -857,6 +883,34 @@ static void launch_dm_w(const DecodeArgs &a, int k_bits, int v_bits, int G, hipS
   else if (k_bits == 4) launch_dm_q<D, 4, 2>(a, G, s);
   else if (v_bits == 4) launch_dm_q<D, 2, 4>(a, G, s);
   else launch_dm_q<D, 2, 2>(a, G, s);
+}
+
+template <int D, bool QJL>
+static void launch_dm_pair(const DecodeArgs &a4, const DecodeArgs &a2, int G, hipStream_t s) {
+  dim3 grid(a4.splits, a4.B * a4.n_heads + a2.B * a2.n_heads);
+  switch (G) {
+    case 1: decode_mfma_pair_kernel<D, 1, QJL><<<grid, 256, 0, s>>>(a4, a2); break;
+    case 2: decode_mfma_pair_kernel<D, 2, QJL><<<grid, 256, 0, s>>>(a4, a2); break;
+    case 3: decode_mfma_pair_kernel<D, 3, QJL><<<grid, 256, 0, s>>>(a4, a2); break;
+    case 4: decode_mfma_pair_kernel<D, 4, QJL><<<grid, 256, 0, s>>>(a4, a2); break;
+    case 5: decode_mfma_pair_kernel<D, 5, QJL><<<grid, 256, 0, s>>>(a4, a2); break;
+    case 6: decode_mfma_pair_kernel<D, 6, QJL><<<grid, 256, 0, s>>>(a4, a2); break;
+    case 7: decode_mfma_pair_kernel<D, 7, QJL><<<grid, 256, 0, s>>>(a4, a2); break;
+    default: decode_mfma_pair_kernel<D, 8, QJL><<<grid, 256, 0, s>>>(a4, a2); break;
+  }
+}
+
+hipError_t launch_decode_mfma_pair(const DecodeArgs &a4, const DecodeArgs &a2, hipStream_t s) {
+  const int G = a4.Hq / a4.Hkv;
+  const bool qjl = a4.qjl != nullptr;
+  if (a4.d == 128) {
+    if (qjl) launch_dm_pair<128, true>(a4, a2, G, s);
+    else launch_dm_pair<128, false>(a4, a2, G, s);
+  } else {
+    if (qjl) launch_dm_pair<64, true>(a4, a2, G, s);
+    else launch_dm_pair<64, false>(a4, a2, G, s);
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_decode_mfma(const DecodeArgs &a, int k_bits, int v_bits, hipStream_t s) {

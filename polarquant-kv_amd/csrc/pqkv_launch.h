@@ -93,6 +93,9 @@ hipError_t launch_decode_split(const DecodeArgs &a, int k_bits, int v_bits, hipS
 // Matrix-core variant for 2- and 4-bit keys and values, with or without QJL
 // (same workspace).
 hipError_t launch_decode_mfma(const DecodeArgs &a, int k_bits, int v_bits, hipStream_t s);
+// Mixed widths with kv heads of exactly two kinds, 4-bit K and V sharing one
+// codebook (a4) and 2-bit K and V (a2): one launch over both head lists.
+hipError_t launch_decode_mfma_pair(const DecodeArgs &a4, const DecodeArgs &a2, hipStream_t s);
 hipError_t launch_decode_merge(const float *part, const float *R, void *out, int out_dtype, int BHq, int splits,
                                int d, hipStream_t s);
 hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t s);
