@@ -76,7 +76,8 @@ def _oracle(q, R, kc, vc, S, P=None, signs=None):
             vh = vb[h] if vc.mixed else vb[:, h]
             out[:, h * g:(h + 1) * g] = O.decode_attention(
                 q[:, h * g:(h + 1) * g].astype(np.float64), kh[:, None], vh[:, None], R, cbk[h], cbv[h],
-                k_bits=kc.head_bits()[h], v_bits=vc.head_bits()[h])
+                k_bits=kc.head_bits()[h], v_bits=vc.head_bits()[h],
+                qjl_signs=None if signs is None else signs[:, h:h + 1], P=P)
         return out
     return O.decode_attention(q.astype(np.float64), kb, vb, R, cbk[0], cbv[0], k_bits=kc.head_bits()[0],
                               v_bits=vc.head_bits()[0], qjl_signs=signs, P=P)
@@ -178,21 +179,35 @@ def test_decode_empty_cache_gives_zeros():
     assert torch.count_nonzero(out).item() == 0
 
 
-def test_decode_mixed_widths():
-    B, Hq, Hkv, S, d = 2, 32, 8, 400, 128
-    widths = (4, 4, 4, 4, 2, 2, 2, 2)
+MIXED_CASES = [
+    # key widths, value widths, QJL
+    ((4, 4, 4, 4, 2, 2, 2, 2), (4, 4, 4, 4, 2, 2, 2, 2), False),   # 4/4 + 2/2: one launch
+    ((2, 4, 2, 4, 4, 2, 2, 4), (2, 4, 2, 4, 4, 2, 2, 4), True),    # the same, interleaved, QJL
+    ((4, 4, 2, 2, 4, 2, 4, 2), (2, 4, 2, 4, 4, 4, 2, 2), False),   # four groups: a launch each
+]
+
+
+@pytest.mark.parametrize("case", MIXED_CASES, ids=["pair", "pair_interleaved_qjl", "four_groups"])
+def test_decode_mixed_widths(case):
+    kw_, vw_, qjl = case
+    B, Hq, Hkv, S, d = 2, 32, 8, 1400, 128
+    print(f"mixed case {case}", flush=True)
     rng = np.random.default_rng(12)
     k = O.synth_kv(B, Hkv, S, d, 31, "channel")
     v = O.synth_kv(B, Hkv, S, d, 32, "channel")
     q = rng.standard_normal((B, Hq, d)).astype(np.float16)
     R = O.rotation_matrix(d, 42)
     Rt = torch.from_numpy(R.astype(np.float32)).to(DEV)
-    kc = quantizer.allocate_cache(B, Hkv, S, d, widths, DEV)
-    vc = quantizer.allocate_cache(B, Hkv, S, d, widths, DEV)
-    quantizer.compress_pq(torch.from_numpy(k).to(DEV), Rt, cache=kc)
+    P = O.jl_matrix(d, d, 43) if qjl else None
+    P_rot = torch.from_numpy((P @ R.T).astype(np.float32)).to(DEV) if qjl else None
+    kc = quantizer.allocate_cache(B, Hkv, S, d, kw_, DEV, jl_dim=d if qjl else 0)
+    vc = quantizer.allocate_cache(B, Hkv, S, d, vw_, DEV)
+    quantizer.compress_pq(torch.from_numpy(k).to(DEV), Rt, cache=kc, jl_rot=P_rot)
     quantizer.compress_pq(torch.from_numpy(v).to(DEV), Rt, cache=vc)
-    out = attention.decode_attention(torch.from_numpy(q).to(DEV), kc, vc, Rt, out_dtype=torch.float32)
-    _check(out.cpu().numpy(), _oracle(q, R, kc, vc, S))
+    kw = dict(jl_rot=P_rot) if qjl else {}
+    out = attention.decode_attention(torch.from_numpy(q).to(DEV), kc, vc, Rt, out_dtype=torch.float32, **kw)
+    signs = kc.qjl_signs.cpu().numpy()[:, :, :S] if qjl else None
+    _check(out.cpu().numpy(), _oracle(q, R, kc, vc, S, P=P, signs=signs))
 
 
 QJL_CASES = [
