@@ -236,6 +236,11 @@ template <int CTRL, int BANK>
 __device__ __forceinline__ uint32_t dpp_into(uint32_t old, uint32_t src) {
   return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)src, CTRL, 0xF, BANK, true);
 }
+// Every lane written (lanes without a source get 0): no old value to set up.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t src) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)src, CTRL, 0xF, 0xF, true);
+}
 template <int CTRL, int BANK>
 __device__ __forceinline__ float dpp_intof(float old, float src) {
   return __builtin_bit_cast(float, dpp_into<CTRL, BANK>(__builtin_bit_cast(uint32_t, old), __builtin_bit_cast(uint32_t, src)));
@@ -649,11 +654,12 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         uint32_t x;
+        // the top move writes every bank; banks 2, 3 are then replaced
         switch (kb) {
-          case 0: x = dpp_into<kDppIdentity, 0x3>(0u, f.top[i]); x = dpp_into<0x118, 0xC>(x, f.bot[i]); break;
-          case 1: x = dpp_into<0x104, 0x3>(0u, f.top[i]); x = dpp_into<0x114, 0xC>(x, f.bot[i]); break;
-          case 2: x = dpp_into<0x108, 0x3>(0u, f.top[i]); x = dpp_into<kDppIdentity, 0xC>(x, f.bot[i]); break;
-          default: x = dpp_into<0x10C, 0x3>(0u, f.top[i]); x = dpp_into<0x104, 0xC>(x, f.bot[i]); break;
+          case 0: x = dpp_into<0x118, 0xC>(f.top[i], f.bot[i]); break;
+          case 1: x = dpp_mov<0x104>(f.top[i]); x = dpp_into<0x114, 0xC>(x, f.bot[i]); break;
+          case 2: x = dpp_mov<0x108>(f.top[i]); x = dpp_into<kDppIdentity, 0xC>(x, f.bot[i]); break;
+          default: x = dpp_mov<0x10C>(f.top[i]); x = dpp_into<0x104, 0xC>(x, f.bot[i]); break;
         }
         pa[i] = x;
       }
