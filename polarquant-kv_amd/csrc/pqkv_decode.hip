@@ -346,19 +346,20 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
 // Workgroup (hg, cg): kMergeHeads query heads x 32 output columns. One wave
 // per head computes the split weights; every workgroup of a head group forms
 // the full normalised o_rot (cheap, L2-resident partials) and then its 32
-// outputs from the matching 32 columns of R, staged as [32][D + 1].
+// outputs from the matching 32 columns of R, staged as [32][D + 4] (16-byte
+// reads; each 16-lane phase of them covers all 64 banks).
 template <int D, typename TOUT>
 __global__ void __launch_bounds__(256) decode_merge_kernel(const float *__restrict__ part,
                                                           const float *__restrict__ R,
                                                           TOUT *__restrict__ out, int BHq, int splits) {
   constexpr int NH = kMergeHeads;
   constexpr int NC = 32;           // output columns per workgroup
-  constexpr int RP = D + 1;
+  constexpr int RP = D + 4;
   constexpr int RU = NC * D / 4 / 256;   // R float4 loads per thread
   constexpr int OU = NH * D / 256;       // (head, coordinate) sums per thread
   constexpr int SB = 16;                 // splits whose o values are loaded at once
-  __shared__ float rs[NC * RP];    // rs[jj][k] = R[k][c0 + jj]
-  __shared__ float os[NH * D];
+  __shared__ __align__(16) float rs[NC * RP];    // rs[jj][k] = R[k][c0 + jj]
+  __shared__ __align__(16) float os[NH * D];
   __shared__ float wts[NH][kMaxSplits];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int head0 = blockIdx.x * NH, c0 = blockIdx.y * NC;
@@ -426,9 +427,17 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const float *__restri
   __syncthreads();
   if (tid < NH * NC) {
     const int hh = tid / NC, jj = tid % NC;
+    const float4 *orow = (const float4 *)(os + hh * D);
+    const float4 *rr = (const float4 *)(rs + jj * RP);
     float acc = 0.0f;
-#pragma unroll 16
-    for (int k = 0; k < D; ++k) acc = __builtin_fmaf(os[hh * D + k], rs[jj * RP + k], acc);
+#pragma unroll 4
+    for (int k4 = 0; k4 < D / 4; ++k4) {
+      const float4 a4 = orow[k4], r4 = rr[k4];
+      acc = __builtin_fmaf(a4.x, r4.x, acc);
+      acc = __builtin_fmaf(a4.y, r4.y, acc);
+      acc = __builtin_fmaf(a4.z, r4.z, acc);
+      acc = __builtin_fmaf(a4.w, r4.w, acc);
+    }
     const int hq = head0 + hh;
     if (hq < BHq) out[(int64_t)hq * D + c0 + jj] = (TOUT)acc;
   }

@@ -149,16 +149,17 @@ __device__ __forceinline__ float load_as_float(const T *p) { return (float)*p; }
 // FMA chain over k ascending (the encoder's order, so both agree bit for bit).
 // Workgroup (vg, cg): 8 vectors x 32 output columns, one output per thread.
 // The 32 rows (forward) or columns (inverse) of R it needs are staged in LDS
-// as [32][D + 1] (padded: the per-lane reads r[jj][k] hit distinct banks).
+// as [32][D + 4]: the chain reads 16 bytes of x and of R per 4 steps, and
+// with the 4-float pad each 16-lane phase of those reads covers all 64 banks.
 constexpr int kRotVec = 8;   // vectors per workgroup iteration
 constexpr int kRotCols = 32; // output columns per workgroup
 
 template <int D, bool INVERSE, typename TIN, typename TOUT>
 __global__ void __launch_bounds__(256) rotate_kernel(const TIN *__restrict__ x, const float *__restrict__ R,
                                                      TOUT *__restrict__ y, int64_t n, float out_scale) {
-  constexpr int RP = D + 1;
-  __shared__ float rs[kRotCols * RP];
-  __shared__ float xs[kRotVec * D];
+  constexpr int RP = D + 4;
+  __shared__ __align__(16) float rs[kRotCols * RP];
+  __shared__ __align__(16) float xs[kRotVec * D];
   const int tid = threadIdx.x;
   const int c0 = blockIdx.y * kRotCols;
   // The first group's vector loads go out before the R staging loads, so
@@ -180,12 +181,7 @@ __global__ void __launch_bounds__(256) rotate_kernel(const TIN *__restrict__ x, 
 #pragma unroll
     for (int u = 0; u < kRotCols * D / 4 / 256; ++u) {
       const int i = tid + 256 * u, jj = i / (D / 4), k4 = i % (D / 4);
-      const float4 v = *(const float4 *)(R + (int64_t)(c0 + jj) * D + 4 * k4);
-      float *dst = rs + jj * RP + 4 * k4;
-      dst[0] = v.x;
-      dst[1] = v.y;
-      dst[2] = v.z;
-      dst[3] = v.w;
+      *(float4 *)(rs + jj * RP + 4 * k4) = *(const float4 *)(R + (int64_t)(c0 + jj) * D + 4 * k4);
     }
   } else {
 #pragma unroll
@@ -204,9 +200,17 @@ __global__ void __launch_bounds__(256) rotate_kernel(const TIN *__restrict__ x, 
     for (int u = 0; u < XU; ++u) xs[tid + 256 * u] = xv[u];
     __syncthreads();
     if (base + stride < n) load_x(base + stride);
+    const float4 *xr = (const float4 *)(xs + g * D);
+    const float4 *rr = (const float4 *)(rs + jj * RP);
     float acc = 0.0f;
-#pragma unroll 16
-    for (int k = 0; k < D; ++k) acc = __builtin_fmaf(xs[g * D + k], rs[jj * RP + k], acc);
+#pragma unroll 4
+    for (int k4 = 0; k4 < D / 4; ++k4) {
+      const float4 a4 = xr[k4], r4 = rr[k4];
+      acc = __builtin_fmaf(a4.x, r4.x, acc);
+      acc = __builtin_fmaf(a4.y, r4.y, acc);
+      acc = __builtin_fmaf(a4.z, r4.z, acc);
+      acc = __builtin_fmaf(a4.w, r4.w, acc);
+    }
     const int64_t v = base + g;
     if (v < n) y[v * D + c0 + jj] = (TOUT)(acc * out_scale);
     __syncthreads();
@@ -216,7 +220,8 @@ __global__ void __launch_bounds__(256) rotate_kernel(const TIN *__restrict__ x, 
 // Two chained forward rotations in one launch: y = (R x) sy, then
 // z = (M y) sz (decode with QJL: the rotated query and its projections
 // P_rot q_rot / m). Workgroup: kRot2Vec vectors, all D columns, both
-// matrices staged whole in LDS ([D][D + 1], padded) by one round of loads.
+// matrices staged whole in LDS ([D][D + 4], padded for 16-byte reads) by one
+// round of loads.
 // Every output is the FMA chain of rotate_kernel over k ascending, so y and
 // z are bit-identical to two rotate_kernel launches.
 constexpr int kRot2Vec = 2;
@@ -224,10 +229,12 @@ template <int D, typename TIN>
 __global__ void __launch_bounds__(256) rotate2_kernel(const TIN *__restrict__ x, const float *__restrict__ R,
                                                       const float *__restrict__ M, float *__restrict__ y,
                                                       float *__restrict__ z, int64_t n, float sy, float sz) {
-  constexpr int RP = D + 1;
+  constexpr int RP = D + 4;
   constexpr int NO = kRot2Vec * D;  // outputs per matrix
-  __shared__ float rs[D * RP], ms[D * RP];
-  __shared__ float xs[NO], ys[NO];
+  __shared__ __align__(16) float rs[D * RP];
+  __shared__ __align__(16) float ms[D * RP];
+  __shared__ __align__(16) float xs[NO];
+  __shared__ __align__(16) float ys[NO];
   const int tid = threadIdx.x;
   const int64_t base = (int64_t)blockIdx.x * kRot2Vec;
   for (int i = tid; i < NO; i += 256) {
@@ -239,22 +246,22 @@ __global__ void __launch_bounds__(256) rotate2_kernel(const TIN *__restrict__ x,
     const int j = i / (D / 4), k4 = i % (D / 4);
     const float4 a = *(const float4 *)(R + (int64_t)j * D + 4 * k4);
     const float4 b = *(const float4 *)(M + (int64_t)j * D + 4 * k4);
-    float *da = rs + j * RP + 4 * k4, *db = ms + j * RP + 4 * k4;
-    da[0] = a.x;
-    da[1] = a.y;
-    da[2] = a.z;
-    da[3] = a.w;
-    db[0] = b.x;
-    db[1] = b.y;
-    db[2] = b.z;
-    db[3] = b.w;
+    *(float4 *)(rs + j * RP + 4 * k4) = a;
+    *(float4 *)(ms + j * RP + 4 * k4) = b;
   }
   __syncthreads();
   for (int i = tid; i < NO; i += 256) {
     const int g = i / D, j = i % D;
+    const float4 *ar = (const float4 *)(xs + g * D), *mr = (const float4 *)(rs + j * RP);
     float acc = 0.0f;
-#pragma unroll 16
-    for (int k = 0; k < D; ++k) acc = __builtin_fmaf(xs[g * D + k], rs[j * RP + k], acc);
+#pragma unroll 4
+    for (int k4 = 0; k4 < D / 4; ++k4) {
+      const float4 a4 = ar[k4], m4 = mr[k4];
+      acc = __builtin_fmaf(a4.x, m4.x, acc);
+      acc = __builtin_fmaf(a4.y, m4.y, acc);
+      acc = __builtin_fmaf(a4.z, m4.z, acc);
+      acc = __builtin_fmaf(a4.w, m4.w, acc);
+    }
     const float yv = acc * sy;
     ys[i] = yv;
     if (base + g < n) y[(base + g) * D + j] = yv;
@@ -262,9 +269,16 @@ __global__ void __launch_bounds__(256) rotate2_kernel(const TIN *__restrict__ x,
   __syncthreads();
   for (int i = tid; i < NO; i += 256) {
     const int g = i / D, j = i % D;
+    const float4 *ar = (const float4 *)(ys + g * D), *mr = (const float4 *)(ms + j * RP);
     float acc = 0.0f;
-#pragma unroll 16
-    for (int k = 0; k < D; ++k) acc = __builtin_fmaf(ys[g * D + k], ms[j * RP + k], acc);
+#pragma unroll 4
+    for (int k4 = 0; k4 < D / 4; ++k4) {
+      const float4 a4 = ar[k4], m4 = mr[k4];
+      acc = __builtin_fmaf(a4.x, m4.x, acc);
+      acc = __builtin_fmaf(a4.y, m4.y, acc);
+      acc = __builtin_fmaf(a4.z, m4.z, acc);
+      acc = __builtin_fmaf(a4.w, m4.w, acc);
+    }
     if (base + g < n) z[(base + g) * D + j] = acc * sz;
   }
 }
