@@ -43,7 +43,7 @@ extern "C" {
 #define PQKV_F16  1
 #define PQKV_BF16 2
 
-#define PQKV_MAX_HEADS 256       /* kv heads per call (mixed-width tables)  */
+#define PQKV_MAX_HEADS 64        /* kv heads per call with per-head (mixed) widths */
 
 int         pqkv_version(void);
 const char *pqkv_status_string(int status);
@@ -111,12 +111,13 @@ int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride,
  * PQKV_ERR_UNSUPPORTED. The rotation runs on the matrix cores with fp32-grade
  * products but not the reference's FMA-chain rounding; the quantiser is
  * bit-exact on the rotated values it computes, which rot_out (nullable,
- * fp32 [n_outer * n_inner][d]) receives. */
+ * fp32 [n_outer * n_inner][d]) receives, together with their fp32 radii
+ * (radius_out, nullable, [n_outer * n_inner]). */
 int pqkv_encode_mfma(const void *x, int x_dtype, int64_t x_outer_stride,
                      const float *R, const float *codebook, int n_bits,
                      uint8_t *blocks, int64_t blocks_outer_stride,
                      int64_t n_outer, int64_t n_inner, int d,
-                     float *rot_out, void *stream);
+                     float *rot_out, float *radius_out, void *stream);
 
 /* ---- decode attention ----------------------------------------------------
  * One query token per sequence against a block-encoded cache:

@@ -252,13 +252,18 @@ def pack_blocks(radius: np.ndarray, idx: np.ndarray, n_bits: int = 4) -> np.ndar
     """Serialise (radius, codes) into block_pq4 (18 B / 32 coords) or
     block_pq2 (10 B / 32 coords). Layout of one block: bytes 0-1 the fp16
     radius of the whole vector (little endian, RNE from fp32), then the packed
-    codes of its 32 coordinates (README.md:73-78). Shape (..., d/32*bb)."""
+    codes of its 32 coordinates (README.md:73-78). Shape (..., d/32*bb).
+    Radii above 65504 are stored as 65504, the reference's saturating fp16
+    radius (src/polarquant_kv_cuda/compress_kernel.py:178)."""
     idx = np.asarray(idx, np.uint8)
     lead = idx.shape[:-1]
     d = idx.shape[-1]
     nb = d // BLOCK
     bb = block_bytes(n_bits)
-    r16 = np.asarray(radius, np.float32).astype(np.float16).reshape(lead + (1,))
+    r32 = np.asarray(radius, np.float32)
+    # saturated fp16, compress_kernel.py:178: clamp(-65504, 65504).half()
+    # (a radius is >= 0; NaN stays NaN)
+    r16 = np.where(r32 > np.float32(65504.0), np.float32(65504.0), r32).astype(np.float16).reshape(lead + (1,))
     rbytes = r16.view(np.uint8).reshape(lead + (2,))
     out = np.empty(lead + (nb, bb), np.uint8)
     codes = idx.reshape(lead + (nb, BLOCK))

@@ -98,14 +98,17 @@ static uint16_t f32_to_f16_rne(float f) {
 }
 
 /* Serialise to block_pq4 (n_bits 4, 18 B / 32 coords) or block_pq2
- * (n_bits 2, 10 B / 32 coords): {fp16 radius; packed codes}. */
+ * (n_bits 2, 10 B / 32 coords): {fp16 radius; packed codes}. The radius is
+ * saturated to 65504 before the fp16 rounding, as the reference's fp16
+ * radius store does (src/polarquant_kv_cuda/compress_kernel.py:178,
+ * clamp(-65504, 65504).half()); NaN stays NaN. */
 int pq_oracle_pack_blocks(const float *radius, const uint8_t *idx, int n_bits,
                           uint8_t *out, long n, int d) {
     if (d % 32 || (n_bits != 4 && n_bits != 2)) return -1;
     int bb = n_bits == 4 ? 18 : 10;
     int nb = d / 32;
     for (long v = 0; v < n; ++v) {
-        uint16_t r16 = f32_to_f16_rne(radius[v]);
+        uint16_t r16 = f32_to_f16_rne(radius[v] > 65504.0f ? 65504.0f : radius[v]);
         for (int b = 0; b < nb; ++b) {
             uint8_t *blk = out + (v * nb + b) * (long)bb;
             const uint8_t *c = idx + v * (long)d + b * 32;

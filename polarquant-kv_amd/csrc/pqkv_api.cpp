@@ -344,7 +344,7 @@ int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride, const float 
   hipError_t e;
   if (!exact && fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, n_inner, R, qjl)) {
     const int tok = pqkv::prof_begin("encode_mfma", (hipStream_t)stream);
-    e = pqkv::launch_encode_mfma(a, nullptr, device_cus(), (hipStream_t)stream);
+    e = pqkv::launch_encode_mfma(a, nullptr, nullptr, device_cus(), (hipStream_t)stream);
     pqkv::prof_end(tok, (hipStream_t)stream);
   } else {
     const int tok = pqkv::prof_begin("encode_exact", (hipStream_t)stream);
@@ -356,7 +356,7 @@ int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride, const float 
 
 int pqkv_encode_mfma(const void *x, int x_dtype, int64_t x_outer_stride, const float *R, const float *codebook,
                      int n_bits, uint8_t *blocks, int64_t blocks_outer_stride, int64_t n_outer, int64_t n_inner,
-                     int d, float *rot_out, void *stream) {
+                     int d, float *rot_out, float *radius_out, void *stream) {
   const int v = encode_validate(x, x_dtype, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride, n_outer,
                                 n_inner, d, nullptr, 0, nullptr, 0);
   if (v <= 0) return v;
@@ -365,7 +365,7 @@ int pqkv_encode_mfma(const void *x, int x_dtype, int64_t x_outer_stride, const f
   const pqkv::EncodeArgs a = encode_args(x, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride,
                                          n_outer, n_inner, d, nullptr, 0, nullptr, 0);
   const int tok = pqkv::prof_begin("encode_mfma", (hipStream_t)stream);
-  const hipError_t e = pqkv::launch_encode_mfma(a, rot_out, device_cus(), (hipStream_t)stream);
+  const hipError_t e = pqkv::launch_encode_mfma(a, rot_out, radius_out, device_cus(), (hipStream_t)stream);
   pqkv::prof_end(tok, (hipStream_t)stream);
   return hip_status(e, "encode_mfma launch");
 }

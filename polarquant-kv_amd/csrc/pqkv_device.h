@@ -29,6 +29,14 @@ __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
   return __builtin_bit_cast(uint16_t, h);
 }
 
+// The stored block radius: fp16 (RNE) of r saturated to the largest finite
+// fp16, 65504, as the reference stores fp16 radii
+// (src/polarquant_kv_cuda/compress_kernel.py:178, clamp(-65504, 65504).half()).
+// A NaN radius stays NaN.
+__device__ __forceinline__ uint16_t radius_half_bits(float r) {
+  return float_to_half_bits(r > 65504.0f ? 65504.0f : r);
+}
+
 __device__ __forceinline__ float shfl_down_f(float v, int s) { return __shfl_down(v, s, kWave); }
 __device__ __forceinline__ float shfl_xor_f(float v, int s) { return __shfl_xor(v, s, kWave); }
 

@@ -59,7 +59,7 @@ template <int D, int BITS>
 __device__ __forceinline__ void store_blocks_wave(int b0, int b1, float r, uint8_t *out_vec) {
   const int lane = threadIdx.x & (kWave - 1);
   const int cv = b0 | (b1 << 4);
-  const uint16_t r16 = float_to_half_bits(r);
+  const uint16_t r16 = radius_half_bits(r);
   if (BITS == 4) {
     // qs byte p holds coordinates 2p (low nibble) and 2p+1 (high nibble).
     const int a = (2 * lane) & 63;
@@ -436,7 +436,7 @@ __global__ void soa_to_blocks_kernel(const uint8_t *__restrict__ packed, const f
       dst[qs_offset(e, 4)] = packed[v * (d / 2) + e];
     } else {
       const int b = e - d / 2;
-      *(uint16_t *)(dst + b * kPq4BlockBytes) = float_to_half_bits(radius[v]);
+      *(uint16_t *)(dst + b * kPq4BlockBytes) = radius_half_bits(radius[v]);
     }
   }
 }

@@ -161,7 +161,8 @@ __device__ __forceinline__ float kfloat(int64_t k) {
 }  // namespace
 
 template <int D, int BITS>
-__global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeArgs a, float *rot_out) {
+__global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeArgs a, float *rot_out,
+                                                                            float *radius_out) {
   constexpr int MT = D / 16;            // output-coordinate tiles
   constexpr int KS = D / 32;            // k-steps over input coordinates
   constexpr int NL = 1 << BITS;
@@ -360,6 +361,7 @@ __global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeAr
         const float tot = w0 + w1;       // s = 1
         r = (float)__builtin_sqrt((double)tot);
       }
+      if (radius_out != nullptr && vo_bytes >= 0 && grp == 0) radius_out[(int64_t)g * kEVec + 16 * c + col] = r;
       const bool nz = r > 1e-30f;
       int code[MT][4];
       if constexpr (kTable) {
@@ -414,14 +416,14 @@ __global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeAr
                                 ((uint32_t)(code[mt][2] | (code[mt][3] << 4)) << 8);
             *(uint16_t *)(out + (mt >> 1) * kPq4BlockBytes + 2 + 8 * (mt & 1) + 2 * grp) = (uint16_t)b2;
           }
-          if (grp < D / 32) *(uint16_t *)(out + grp * kPq4BlockBytes) = float_to_half_bits(r);
+          if (grp < D / 32) *(uint16_t *)(out + grp * kPq4BlockBytes) = radius_half_bits(r);
         } else {
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             const uint32_t b1 = (uint32_t)(code[mt][0] | (code[mt][1] << 2) | (code[mt][2] << 4) | (code[mt][3] << 6));
             out[(mt >> 1) * kPq2BlockBytes + 2 + 4 * (mt & 1) + grp] = (uint8_t)b1;
           }
-          if (grp < D / 32) *(uint16_t *)(out + grp * kPq2BlockBytes) = float_to_half_bits(r);
+          if (grp < D / 32) *(uint16_t *)(out + grp * kPq2BlockBytes) = radius_half_bits(r);
         }
       }
     }
@@ -431,7 +433,7 @@ __global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeAr
   else run(TableFlag<false>{});
 }
 
-hipError_t launch_encode_mfma(const EncodeArgs &a, float *rot_out, int cus, hipStream_t s) {
+hipError_t launch_encode_mfma(const EncodeArgs &a, float *rot_out, float *radius_out, int cus, hipStream_t s) {
   const int64_t n = a.n_outer * a.n_inner;
   const int64_t groups = (n + kEVec - 1) / kEVec;
   // each workgroup builds its R operand and centroid table once, so one
@@ -439,7 +441,7 @@ hipError_t launch_encode_mfma(const EncodeArgs &a, float *rot_out, int cus, hipS
   int64_t grid = (groups + kEW - 1) / kEW;
   if (grid > 2 * (int64_t)cus) grid = 2 * (int64_t)cus;
   if (grid < 1) grid = 1;
-#define PQKV_EM(DD, BB) encode_mfma_kernel<DD, BB><<<(int)grid, kEW * 64, 0, s>>>(a, rot_out)
+#define PQKV_EM(DD, BB) encode_mfma_kernel<DD, BB><<<(int)grid, kEW * 64, 0, s>>>(a, rot_out, radius_out)
   if (a.d == 128 && a.bits == 4) PQKV_EM(128, 4);
   else if (a.d == 128 && a.bits == 2) PQKV_EM(128, 2);
   else if (a.d == 64 && a.bits == 4) PQKV_EM(64, 4);

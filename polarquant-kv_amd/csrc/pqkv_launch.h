@@ -7,11 +7,12 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "../../include/pqkv.h"
 #include "pqkv_layout.h"
 
 namespace pqkv {
 
-constexpr int kMaxListHeads = 64;  // kv heads per launch when heads are listed
+constexpr int kMaxListHeads = PQKV_MAX_HEADS;  // kv heads per launch when heads are listed
 constexpr int kMaxSplits = 1024;   // split-K partitions per (batch, kv head)
 constexpr int kMergeHeads = 4;     // query heads per merge workgroup
 constexpr int kMfmaBlocksPerCU = 2;  // decode_mfma_kernel workgroups resident per CU
@@ -78,10 +79,11 @@ hipError_t launch_rotate2(const void *x, int x_dtype, const float *R, const floa
 hipError_t launch_rotate(const void *x, int x_dtype, const float *R, void *y, int y_dtype, int64_t n, int d,
                          int inverse, float out_scale, hipStream_t s);
 hipError_t launch_encode_exact(const EncodeArgs &a, int x_dtype, hipStream_t s);
-// Matrix-core encoder for fp16 input without QJL; rot_out (nullable) receives
-// the fp32 rotated vectors the quantiser saw, [n][d].
+// Matrix-core encoder for fp16 input without QJL; rot_out and radius_out
+// (nullable) receive the fp32 rotated vectors the quantiser saw, [n][d], and
+// their fp32 radii, [n].
 // One round of workgroups (two per compute unit) loops over the vectors.
-hipError_t launch_encode_mfma(const EncodeArgs &a, float *rot_out, int cus, hipStream_t s);
+hipError_t launch_encode_mfma(const EncodeArgs &a, float *rot_out, float *radius_out, int cus, hipStream_t s);
 hipError_t launch_encode_soa(const float *x, const float *R, const float *codebook, int n_levels, float *radius,
                              uint8_t *packed, int64_t n, int d, hipStream_t s);
 hipError_t launch_soa_to_blocks(const uint8_t *packed, const float *radius, uint8_t *blocks, int64_t n, int d,

@@ -33,7 +33,7 @@ SIGNATURES = {
     "pqkv_encode": (c_int, [c_void_p, c_int, c_int64, c_void_p, c_void_p, c_int, c_void_p, c_int64,
                             c_int64, c_int64, c_int, c_void_p, c_int, c_void_p, c_int64, c_void_p]),
     "pqkv_encode_mfma": (c_int, [c_void_p, c_int, c_int64, c_void_p, c_void_p, c_int, c_void_p, c_int64,
-                                 c_int64, c_int64, c_int, c_void_p, c_void_p]),
+                                 c_int64, c_int64, c_int, c_void_p, c_void_p, c_void_p]),
     "pqkv_decode_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "pqkv_decode_attn": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                  c_int, c_int, c_int_p, c_int_p, c_void_p, c_void_p, c_int,

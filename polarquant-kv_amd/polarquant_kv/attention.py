@@ -17,7 +17,7 @@ import math
 import torch
 
 from . import _lib
-from .types import PQCache
+from .types import PQCache, vector_bytes
 
 
 def _rotated_p(jl_matrix, rotation_matrix, device):
@@ -25,21 +25,45 @@ def _rotated_p(jl_matrix, rotation_matrix, device):
     return rotated_jl_matrix(jl_matrix, rotation_matrix, device)
 
 
-def decode_attention(query: torch.Tensor, keys: PQCache, values: PQCache, rotation_matrix: torch.Tensor,
-                     scale: float | None = None, jl_rot: torch.Tensor | None = None,
-                     out_dtype: torch.dtype | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """query [B, Hq, d] (original space) -> out [B, Hq, d] (original space)."""
-    _lib.require_device(query, rotation_matrix, jl_rot)
-    B, Hq, d = query.shape
+def check_shapes(B: int, Hq: int, d: int, keys: PQCache, values: PQCache, rotation_matrix=None) -> int:
+    """Host-side agreement checks shared by decode and prefill, run before
+    any launch (the kernels trust these sizes when they address the caches).
+    Returns Hkv."""
     Hkv = keys.num_heads
-    if keys.head_dim != d or values.head_dim != d or values.num_heads != Hkv or keys.batch != B:
-        raise ValueError("query and caches disagree on shape")
+    if keys.head_dim != d or values.head_dim != d:
+        raise ValueError(f"head_dim: query {d}, keys {keys.head_dim}, values {values.head_dim}")
+    if values.num_heads != Hkv:
+        raise ValueError(f"kv heads: keys {Hkv}, values {values.num_heads}")
+    if keys.batch != B or values.batch != B:
+        raise ValueError(f"batch: query {B}, keys {keys.batch}, values {values.batch}")
     if keys.seq_len != values.seq_len:
         raise ValueError("keys and values hold different numbers of positions")
     if keys.max_seq_len != values.max_seq_len:
         raise ValueError("keys and values must share max_seq_len")
+    if not 0 <= keys.seq_len <= keys.max_seq_len:
+        raise ValueError(f"seq_len {keys.seq_len} outside 0..{keys.max_seq_len}")
     if Hq % Hkv:
         raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
+    if rotation_matrix is not None and tuple(rotation_matrix.shape) != (d, d):
+        raise ValueError(f"rotation matrix must be ({d}, {d}), got {tuple(rotation_matrix.shape)}")
+    for name, c in (("keys", keys), ("values", values)):
+        per_batch = (sum(c.max_seq_len * vector_bytes(d, b) for b in c.head_bits()))
+        if c.blocks.numel() < B * per_batch:
+            raise ValueError(f"{name}: {c.blocks.numel()} cache bytes, the shape needs {B * per_batch}")
+    if keys.qjl_signs is not None and keys.qjl_signs.numel() < B * Hkv * keys.max_seq_len * (d // 8):
+        raise ValueError("keys: QJL sign array smaller than the cache shape")
+    return Hkv
+
+
+def decode_attention(query: torch.Tensor, keys: PQCache, values: PQCache, rotation_matrix: torch.Tensor,
+                     scale: float | None = None, jl_rot: torch.Tensor | None = None,
+                     out_dtype: torch.dtype | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """query [B, Hq, d] (original space) -> out [B, Hq, d] (original space)."""
+    if query.dim() != 3:
+        raise ValueError(f"query must be [B, Hq, d], got {tuple(query.shape)}")
+    B, Hq, d = query.shape
+    Hkv = check_shapes(B, Hq, d, keys, values, rotation_matrix)
+    _lib.require_device(query, rotation_matrix, jl_rot)
     scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
     out_dtype = query.dtype if out_dtype is None else out_dtype
     q = query.contiguous()
@@ -74,9 +98,11 @@ def prefill_attention(query: torch.Tensor, keys: PQCache, values: PQCache, rotat
                       out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """query [B, Hq, Sq, d] at absolute positions q_start.. against caches that
     already hold them -> out [B, Hq, Sq, d]."""
-    _lib.require_device(query, rotation_matrix)
+    if query.dim() != 4:
+        raise ValueError(f"query must be [B, Hq, Sq, d], got {tuple(query.shape)}")
     B, Hq, Sq, d = query.shape
-    Hkv = keys.num_heads
+    Hkv = check_shapes(B, Hq, d, keys, values, rotation_matrix)
+    _lib.require_device(query, rotation_matrix)
     if keys.mixed or values.mixed:
         raise ValueError("prefill supports uniform bit widths")
     scale = 1.0 / math.sqrt(d) if scale is None else float(scale)

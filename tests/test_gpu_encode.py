@@ -167,11 +167,13 @@ def _encode_mfma(x16, R32, cb_t, bits, d, n_outer=1):
     Rt = torch.from_numpy(R32).to(DEV)
     blocks = torch.zeros(n, vb, dtype=torch.uint8, device=DEV)
     rot = torch.empty(n, d, dtype=torch.float32, device=DEV)
+    rad = torch.empty(n, dtype=torch.float32, device=DEV)
     n_inner = n // n_outer
     _lib.check(_lib.lib().pqkv_encode_mfma(xt.data_ptr(), _lib.F16, n_inner * d, Rt.data_ptr(), cb_t.data_ptr(),
                                            bits, blocks.data_ptr(), n_inner * vb, n_outer, n_inner, d,
-                                           rot.data_ptr(), _lib.stream_of(xt)))
+                                           rot.data_ptr(), rad.data_ptr(), _lib.stream_of(xt)))
     torch.cuda.synchronize()
+    _encode_mfma.radius = rad.cpu().numpy()   # fp32 radii of the last call
     return blocks.cpu().numpy(), rot.cpu().numpy()
 
 
@@ -185,6 +187,7 @@ def test_mfma_encoder_quantiser_bit_exact_on_its_rotation(d, bits, kind):
     cb = O.lloyd_max_codebook(d, bits)[0]
     r_ref, idx_ref = OC.c_quantize_rotated(rot, cb)
     assert np.array_equal(blocks, OC.c_pack_blocks(r_ref, idx_ref, bits))
+    assert np.array_equal(_encode_mfma.radius.view(np.uint32), r_ref.view(np.uint32))   # fp32 radii too
     if kind == "special":
         assert not blocks[0, :2].any() and r_ref[0] == 0.0  # zero vector: radius 0, code argmin |c|
 
@@ -225,7 +228,7 @@ def test_mfma_encoder_strided_rows(n_inner):
     Rt = torch.from_numpy(R32).to(DEV)
     blocks = torch.full((n_outer, bs, vb), 0xAB, dtype=torch.uint8, device=DEV)
     _lib.check(_lib.lib().pqkv_encode_mfma(xt.data_ptr(), _lib.F16, xs * d, Rt.data_ptr(), cb_t.data_ptr(), bits,
-                                           blocks.data_ptr(), bs * vb, n_outer, n_inner, d, None,
+                                           blocks.data_ptr(), bs * vb, n_outer, n_inner, d, None, None,
                                            _lib.stream_of(xt)))
     torch.cuda.synchronize()
     got = blocks.cpu().numpy()

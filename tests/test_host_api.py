@@ -89,8 +89,11 @@ def test_gpu_entry_points_refuse_cpu_tensors():
         quantizer.compress_pq(x, R)
     with pytest.raises(ValueError, match="no CPU fallback"):
         rotation.rotate(x, R)
+    kc = _cpu_cache(1, 1, 16, 128)
     with pytest.raises(ValueError, match="no CPU fallback"):
-        attention.decode_attention(torch.zeros(1, 2, 128), None, None, R)
+        attention.decode_attention(torch.zeros(1, 2, 128), kc, kc, R)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        attention.prefill_attention(torch.zeros(1, 2, 3, 128), kc, kc, R, q_start=0)
 
 
 def test_missing_library_fails_loudly(monkeypatch):
@@ -98,3 +101,67 @@ def test_missing_library_fails_loudly(monkeypatch):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(ImportError, match="no CPU fallback"):
         _lib.lib()
+
+
+def _cpu_cache(B, H, S_max, d, bits=4, seq_len=None):
+    from polarquant_kv.quantizer import allocate_cache
+    c = allocate_cache(B, H, S_max, d, bits, device="cpu")
+    c.seq_len = S_max if seq_len is None else seq_len
+    return c
+
+
+@pytest.mark.parametrize("which", ["values_smaller_S_max", "d_mismatch", "batch_too_big", "value_heads",
+                                   "seq_len_mismatch", "rotation_shape", "short_blocks"])
+@pytest.mark.parametrize("entry", ["decode", "prefill"])
+def test_attention_shape_mismatches_raise_before_any_launch(which, entry):
+    """Every disagreement between the query, the two caches and R raises
+    ValueError on the host (the kernels address the caches with these
+    sizes), for decode and for prefill alike."""
+    from polarquant_kv import attention
+    B, Hq, Hkv, S, d = 2, 8, 2, 64, 128
+    k, v = _cpu_cache(B, Hkv, S, d), _cpu_cache(B, Hkv, S, d)
+    R = torch.eye(d)
+    q = torch.zeros(B, Hq, d) if entry == "decode" else torch.zeros(B, Hq, 4, d)
+    if which == "values_smaller_S_max":
+        v = _cpu_cache(B, Hkv, S // 2, d, seq_len=S // 2)
+    elif which == "d_mismatch":
+        q = q[..., :64]
+    elif which == "batch_too_big":
+        q = torch.cat([q, q])
+    elif which == "value_heads":
+        v = _cpu_cache(B, 2 * Hkv, S, d)
+    elif which == "seq_len_mismatch":
+        v.seq_len = S - 1
+    elif which == "rotation_shape":
+        R = torch.eye(64)
+    elif which == "short_blocks":
+        k.blocks = k.blocks[:1]
+    with pytest.raises(ValueError) as e:
+        if entry == "decode":
+            attention.decode_attention(q, k, v, R)
+        else:
+            attention.prefill_attention(q, k, v, R, q_start=0)
+    assert "device tensors" not in str(e.value)       # the shape check, not the device check, fired
+
+
+def test_max_heads_constant_matches_the_library():
+    """include/pqkv.h's PQKV_MAX_HEADS is the library's limit for per-head
+    widths: that many kv heads pass validation, one more is refused."""
+    import re
+    from conftest import ROOT
+    import os
+    m = re.search(r"#define PQKV_MAX_HEADS\s+(\d+)", open(os.path.join(ROOT, "include", "pqkv.h")).read())
+    n = int(m.group(1))
+    L = _lib.lib()
+    FAKE = 0x1000
+
+    def call(hkv, wsb):
+        bits = _lib.int_array([4, 2] * (hkv // 2))
+        return L.pqkv_decode_attn(FAKE, 1, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 4, bits, bits, None, None, 0,
+                                  1, hkv, hkv, 16, 16, 128, 0.088, FAKE, 1, FAKE, wsb, None)
+    # a workspace one byte short: validation reaches the workspace check (the
+    # last one before any HIP call) only when the head count is accepted
+    need = L.pqkv_decode_workspace_bytes(1, n, n, 16, 128)
+    assert call(n, need - 1) == _lib.ERR_WORKSPACE
+    need2 = L.pqkv_decode_workspace_bytes(1, n + 2, n + 2, 16, 128)
+    assert call(n + 2, need2 - 1) == _lib.ERR_UNSUPPORTED

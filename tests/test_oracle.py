@@ -80,18 +80,65 @@ def test_quantize_brute_force(d, bits):
     np.testing.assert_allclose(r, np.linalg.norm(x.astype(np.float64), axis=1), rtol=1e-6)
 
 
-def test_radius_tree_order_is_the_reference_one():
-    # Values whose fp32 sum depends on association order: the 128-slot tree
-    # (pairs t, t+64 first) must be used, not a left-to-right sum.
-    x = np.zeros((1, 128), np.float32)
-    x[0, 0], x[0, 64], x[0, 1] = 1.0, 2.0 ** -12, 2.0 ** -12
-    r2_tree = O.radius_f32(x)[0] ** 2
-    seq = np.float32(0)
-    for v in (x[0] * x[0]):
-        seq = np.float32(seq + v)
-    pairs = np.float32(np.float32(x[0, 0] ** 2 + x[0, 64] ** 2) + np.float32(x[0, 1] ** 2))
-    assert np.float32(np.sqrt(pairs)) == O.radius_f32(x)[0]
-    assert r2_tree > 0 and seq > 0
+U = 2.0 ** -23          # fp32 ulp of 1.0
+
+
+def tree_probe(d):
+    """x[0] = 1 and a run of slots at 2^-12 (squares delta = 2^-24, half an
+    ulp of 1), the rest 0, so that the fp32 sum of squares depends on the
+    order. Worked by hand through the 128-slot tree of
+    csrc/flash_turboquant.cu:141-147 (slot t += slot t + s for s = 64, 32,
+    ..., 1; d = 64 pads slots 64..127 with 0):
+
+    d = 128, slots 64..127 set:
+      s=64: slot 0 = 1 + delta -> 1 (tie, even);   slots 1..63 = delta
+      s=32: slot 0 = 1 + delta -> 1;               slots 1..31 = U
+      s=16: 1 + U;  s=8: 1 + 3U;  s=4: 1 + 7U;  s=2: 1 + 15U;  s=1: 1 + 31U
+      r = RN(sqrt(1 + 31U)) = 1 + 15U   (exact sum 1 + 32U: r = 1 + 16U)
+    d = 64, slots 1..12 set:
+      s=64, 32, 16: nothing moves (the partner slots are 0)
+      s=8: slot 0 = 1 + delta -> 1;  slots 1..4 = U;  slots 5..7 = delta
+      s=4: slot 0 = 1 + U;  slots 1..3 = 1.5U
+      s=2: slot 0 = 1 + 2.5U -> 1 + 2U (tie, even);  slot 1 = 3U
+      s=1: 1 + 5U;  r = RN(sqrt(1 + 5U)) = 1 + 2U   (exact sum 1 + 6U: r = 1 + 3U)"""
+    x = np.zeros((1, d), np.float32)
+    x[0, 0] = 1.0
+    if d == 128:
+        x[0, 64:] = 2.0 ** -12
+    else:
+        x[0, 1:13] = 2.0 ** -12
+    return x
+
+
+def _other_orders(sq):
+    """fp32 sums of squares in the orders a restatement could plausibly use."""
+    out = {}
+    acc = np.float32(0)
+    for v in sq:
+        acc = np.float32(acc + v)
+    out["left_to_right"] = acc
+    acc = np.float32(0)
+    for v in sq[::-1]:
+        acc = np.float32(acc + v)
+    out["right_to_left"] = acc
+    out["numpy_pairwise"] = np.sum(sq, dtype=np.float32)
+    out["float64_rounded"] = np.float32(np.sum(sq.astype(np.float64)))
+    b = np.concatenate([sq, np.zeros(128 - sq.size, np.float32)])
+    while b.size > 1:                       # a tree over adjacent slot pairs
+        b = (b[0::2] + b[1::2]).astype(np.float32)
+    out["adjacent_pairs"] = b[0]
+    return {k: np.sqrt(np.float32(v)) for k, v in out.items()}
+
+
+@pytest.mark.parametrize("d,want_ulps", [(128, 15), (64, 2)])
+def test_radius_tree_order_is_the_reference_one(d, want_ulps):
+    x = tree_probe(d)
+    r = O.radius_f32(x)[0]
+    assert r == np.float32(1.0 + want_ulps * U)          # the hand-worked tree value
+    for name, alt in _other_orders((x[0] * x[0]).astype(np.float32)).items():
+        assert alt != r, f"the probe does not separate the tree from the {name} order"
+    r_c, _ = oracle_pkg.c_quantize_rotated(x, _codebook(d, 4))
+    assert r_c[0] == r
 
 
 def test_identity_rotation_radius_is_the_norm():
@@ -157,6 +204,19 @@ def test_crumb_order():
     packed = O.pack_codes(codes, 2)
     assert list(packed) == [1 | 2 << 2 | 3 << 4, 3 | 3 << 2 | 0 << 4 | 1 << 6]
     assert np.array_equal(O.unpack_codes(packed, 2), codes)
+
+
+def test_stored_radius_saturates_at_fp16_max():
+    # compress_kernel.py:178 stores radius.clamp(-65504, 65504).half(): a norm
+    # past the fp16 range is kept as 65504 (0x7BFF), never inf; NaN stays NaN.
+    r = np.array([65504.0, 65519.0, 65520.0, 1.1e5, np.inf, np.nan, 1.0], np.float32)
+    idx = np.zeros((r.size, 32), np.uint8)
+    for bits in (4, 2):
+        for blk in (O.pack_blocks(r, idx, bits), oracle_pkg.c_pack_blocks(r, idx, bits)):
+            r16 = blk[:, 0].astype(np.uint16) | (blk[:, 1].astype(np.uint16) << 8)
+            assert list(r16[:5]) == [0x7BFF] * 5
+            assert (r16[5] & 0x7C00) == 0x7C00 and (r16[5] & 0x3FF) != 0
+            assert r16[6] == 0x3C00
 
 
 @pytest.mark.parametrize("d,bits", [(128, 4), (64, 4), (128, 2), (64, 2)])
@@ -257,6 +317,91 @@ def test_qjl_closed_form_and_rotated_identity():
     for t in range(10):
         want = sum((1.0 if bits[t, i] else -1.0) * float(P[i] @ q) for i in range(d)) / d
         assert abs(corr[t] - want) < 1e-12
+
+
+# Code vectors whose centroids c[idx] have an fp32 tree radius of exactly 1.0
+# (found by a meet-in-the-middle search over the 4-bit Lloyd-Max codebook; the
+# property is checked below), so x_rot = 2 c[idx] encodes losslessly: r = 2,
+# dir = c[idx], residual 0.
+LOSSLESS_IDX = {
+    64: [1, 8, 3, 7, 11, 10, 11, 12, 10, 10, 1, 13, 2, 8, 8, 10, 7, 5, 4, 9, 10, 8, 8, 3, 9, 3, 6, 5, 2, 10, 13,
+         10, 10, 4, 10, 13, 10, 4, 8, 6, 6, 14, 5, 5, 10, 4, 3, 1, 3, 5, 5, 9, 8, 13, 10, 6, 8, 14, 8, 11, 13, 5,
+         11, 9],
+    128: [6, 9, 7, 5, 3, 13, 8, 9, 0, 4, 10, 5, 5, 8, 4, 5, 4, 9, 5, 12, 2, 9, 10, 2, 7, 4, 4, 12, 9, 4, 3, 10, 5,
+          9, 11, 8, 6, 3, 9, 3, 0, 7, 9, 0, 9, 10, 10, 13, 3, 4, 6, 5, 2, 8, 3, 8, 2, 11, 7, 2, 4, 3, 7, 12, 10, 8,
+          12, 4, 5, 10, 13, 6, 5, 8, 6, 8, 11, 3, 5, 8, 11, 7, 3, 7, 7, 2, 10, 0, 10, 4, 1, 11, 6, 3, 7, 5, 3, 11,
+          5, 9, 9, 6, 6, 2, 5, 6, 11, 12, 11, 5, 7, 8, 12, 6, 11, 14, 1, 8, 11, 4, 7, 4, 8, 7, 6, 8, 11, 9],
+}
+
+
+def lossless_key(d, scale=2.0):
+    return (np.float32(scale) * _codebook(d, 4)[np.array(LOSSLESS_IDX[d])]).astype(np.float32)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_lossless_key_has_zero_residual(d):
+    c = _codebook(d, 4)
+    x = lossless_key(d)[None]
+    r, idx = O.quantize_rotated(x, c)
+    assert r[0] == np.float32(2.0)
+    assert np.array_equal(idx[0], LOSSLESS_IDX[d])
+    signs, enorm = O.qjl_signs_rotated(x, r, idx, c, O.jl_matrix(d, d, 43))
+    assert enorm[0] == 0.0 and np.all(signs == 0xFF)      # P 0 = 0 >= 0: every sign 1
+
+
+def qjl_rule_cache(d=64, S=6, seed=12, key_scale=1.0):
+    """One (batch, kv-head) stream whose key 0 is the zero vector and key 1 is
+    lossless (residual 0); the rest are random. Signs as the encoder writes
+    them: P 0 = 0 >= 0 gives all ones for keys 0 and 1.
+    Returns (k_blocks, v_blocks, signs, P, R, c, x_rot)."""
+    rng = np.random.default_rng(seed)
+    c = _codebook(d, 4)
+    R = O.rotation_matrix(d, 42)
+    P = O.jl_matrix(d, d, 43)
+    xr = (key_scale * rng.standard_normal((S, d))).astype(np.float32)
+    xr[0] = 0.0
+    xr[1] = lossless_key(d)
+    r, idx = O.quantize_rotated(xr, c)
+    signs, enorm = O.qjl_signs_rotated(xr, r, idx, c, P @ R.T)
+    assert enorm[0] == 0.0 and enorm[1] == 0.0 and np.all(enorm[2:] > 0)
+    assert np.all(signs[:2] == 0xFF)
+    kb = O.pack_blocks(r, idx, 4)
+    vr = rng.standard_normal((S, d)).astype(np.float32)
+    rv, iv = O.quantize_rotated(vr, c)
+    vb = O.pack_blocks(rv, iv, 4)
+    return kb[None, None], vb[None, None], signs[None, None], P, R, c, xr
+
+
+def test_qjl_zero_key_gets_no_correction_lossless_key_does():
+    """The rule: a key whose radius is 0 (the zero key, where the CPU guard of
+    python/polarquant_kv/qjl.py:50-51 fires) adds no correction; every other
+    key adds (1/m) sum_i (2 s_i - 1) (P q)_i, as the GPU path does
+    (src/polarquant_kv_cuda/attention_kernel.py:95-107), including a lossless
+    key whose rotated-space residual is 0 and whose stored signs are all 1.
+    Scores assembled by hand here; a kernel that dropped the guard (zero key
+    corrected) or guarded on the all-ones sketch (lossless key not corrected)
+    fails."""
+    d, S, G = 64, 6, 2
+    kb, vb, signs, P, R, c, xr = qjl_rule_cache(d, S)
+    q = np.random.default_rng(3).standard_normal((1, G, d))
+    got = O.decode_attention(q, kb, vb, R, c, c, qjl_signs=signs, P=P)
+    r16, idx = O.unpack_blocks(kb[0, 0], d, 4)
+    K = r16.astype(np.float64)[:, None] * c[idx].astype(np.float64)
+    Vr = O.dequantize_rotated(vb[0, 0], d, c)
+    bits = O.bit_unpack_lsb(signs[0, 0], d).astype(np.float64) * 2 - 1
+    scale = 1 / math.sqrt(d)
+    for g in range(G):
+        qr = R @ q[0, g]
+        pq = P @ q[0, g]
+        s = np.array([qr @ K[t] + (0.0 if t == 0 else bits[t] @ pq / d) for t in range(S)]) * scale
+        assert s[0] == 0.0
+        assert abs(s[1] - scale * (qr @ K[1] + pq.sum() / d)) < 1e-12
+        w = np.exp(s - s.max())
+        w /= w.sum()
+        np.testing.assert_allclose(got[0, g], (w @ Vr) @ R, atol=1e-12)
+    # the other rules give different outputs on this cache
+    no_guard = np.array([[R @ q[0, g] @ K[t] + bits[t] @ (P @ q[0, g]) / d for t in range(S)] for g in range(G)])
+    assert abs(no_guard[0, 0]) > 1e-3
 
 
 def test_bit_pack_lsb_round_trip():
