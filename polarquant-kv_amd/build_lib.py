@@ -20,8 +20,8 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "polarquant_kv", "_lib")
 LIB = os.path.join(OUT_DIR, "libpqkv_hip.so")
 BUILD = os.path.join(HERE, "_build")
-SOURCES = ["pqkv_encode.hip", "pqkv_encode_mfma.hip", "pqkv_decode.hip", "pqkv_decode_mfma.hip", "pqkv_prefill.hip", "pqkv_api.cpp",
-           "pqkv_compat.cpp"]
+SOURCES = ["pqkv_encode.hip", "pqkv_encode_mfma.hip", "pqkv_decode.hip", "pqkv_decode_mfma.hip", "pqkv_prefill.hip",
+           "pqkv_api.cpp", "pqkv_compat.cpp"]
 
 
 def hipcc() -> str:

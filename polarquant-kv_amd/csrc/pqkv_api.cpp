@@ -376,9 +376,7 @@ size_t pqkv_decode_workspace_bytes(int B, int Hq, int Hkv, int S, int d) {
   // bound over every plan a call can make: fewest streams per launch (B),
   // largest target
   decode_plan(B, S > 0 ? S : 1, kPlanMaxTarget, &splits, &tps);
-  // rotated queries, split partials, and the QJL projections P_rot q_rot / m
-  return align256((size_t)B * Hq * d * 4) + align256((size_t)B * Hq * splits * (d + 2) * 4) +
-         align256((size_t)B * Hq * d * 4);
+  return pqkv::decode_workspace_layout(B, Hq, splits, d, nullptr, nullptr, nullptr);
 }
 
 int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *k_cache, const uint8_t *v_cache,
@@ -386,44 +384,71 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
                      const int *k_head_bits, const int *v_head_bits, const uint8_t *qjl_signs, const float *p_rot,
                      int m, int B, int Hq, int Hkv, int S, int S_max, int d, float scale, void *out, int out_dtype,
                      void *workspace, size_t workspace_bytes, void *stream) {
+  return pqkv::decode_attn_run(q, q_dtype, R, k_cache, v_cache, k_codebooks, v_codebooks, k_bits, v_bits,
+                               k_head_bits, v_head_bits, qjl_signs, p_rot, m, B, Hq, Hkv, S, S_max, d, scale, out,
+                               out_dtype, workspace, workspace_bytes, false, stream);
+}
+
+}  // extern "C"
+
+namespace pqkv {
+
+int report_hip_error(hipError_t e, const char *what) { return hip_status(e, what); }
+
+// Workspace of one decode call with `splits` partitions per stream: rotated
+// queries, split partials, and the QJL projections P_rot q_rot / m, each
+// 256-byte aligned. Returns the total; the nullable pointers receive the
+// offsets.
+size_t decode_workspace_layout(int B, int Hq, int splits, int d, size_t *q_off, size_t *part_off, size_t *pq_off) {
+  const size_t q = align256((size_t)B * Hq * d * 4);
+  const size_t part = align256((size_t)B * Hq * splits * (d + 2) * 4);
+  if (q_off) *q_off = 0;
+  if (part_off) *part_off = q;
+  if (pq_off) *pq_off = q + part;
+  return q + part + align256((size_t)B * Hq * d * 4);
+}
+
+// One decode call. With plan_sized the workspace need is this call's own
+// split plan (the allocation-free entry point, whose scratch has a fixed
+// size); otherwise it is the pqkv_decode_workspace_bytes bound the header
+// promises. No allocation of any kind happens here: per-head tables live in
+// fixed arrays (mixed widths are limited to PQKV_MAX_HEADS kv heads).
+int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k_cache, const uint8_t *v_cache,
+                    const float *k_codebooks, const float *v_codebooks, int k_bits, int v_bits,
+                    const int *k_head_bits, const int *v_head_bits, const uint8_t *qjl_signs, const float *p_rot,
+                    int m, int B, int Hq, int Hkv, int S, int S_max, int d, float scale, void *out, int out_dtype,
+                    void *workspace, size_t workspace_bytes, bool plan_sized, void *stream) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S < 0 || S_max < S)
     return fail(PQKV_ERR_INVALID, "decode: B=%d Hq=%d Hkv=%d S=%d S_max=%d", B, Hq, Hkv, S, S_max);
   if (Hq % Hkv) return fail(PQKV_ERR_INVALID, "decode: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
-  if (Hq / Hkv > 8) return fail(PQKV_ERR_UNSUPPORTED, "decode: group size %d > 8", Hq / Hkv);
   if (!supported_d(d)) return fail(PQKV_ERR_UNSUPPORTED, "decode: d=%d", d);
   if (!float_dtype(q_dtype) || !float_dtype(out_dtype)) return fail(PQKV_ERR_UNSUPPORTED, "decode: dtype");
   const bool mixed = k_head_bits != nullptr || v_head_bits != nullptr;
-  if (mixed && Hkv > pqkv::kMaxListHeads)
-    return fail(PQKV_ERR_UNSUPPORTED, "decode: mixed widths support at most %d kv heads", pqkv::kMaxListHeads);
-  std::vector<int> kb(Hkv, k_bits), vb(Hkv, v_bits);
-  for (int h = 0; h < Hkv; ++h) {
-    if (k_head_bits) kb[h] = k_head_bits[h];
-    if (v_head_bits) vb[h] = v_head_bits[h];
-    if (!supported_bits(kb[h]) || !supported_bits(vb[h]))
-      return fail(PQKV_ERR_UNSUPPORTED, "decode: head %d widths k=%d v=%d", h, kb[h], vb[h]);
-  }
+  if (mixed && Hkv > kMaxListHeads)
+    return fail(PQKV_ERR_UNSUPPORTED, "decode: mixed widths support at most %d kv heads", kMaxListHeads);
+  if (!supported_bits(k_bits) && !k_head_bits) return fail(PQKV_ERR_UNSUPPORTED, "decode: k_bits=%d", k_bits);
+  if (!supported_bits(v_bits) && !v_head_bits) return fail(PQKV_ERR_UNSUPPORTED, "decode: v_bits=%d", v_bits);
+  int kb[kMaxListHeads], vb[kMaxListHeads];
+  if (mixed)
+    for (int h = 0; h < Hkv; ++h) {
+      kb[h] = k_head_bits ? k_head_bits[h] : k_bits;
+      vb[h] = v_head_bits ? v_head_bits[h] : v_bits;
+      if (!supported_bits(kb[h]) || !supported_bits(vb[h]))
+        return fail(PQKV_ERR_UNSUPPORTED, "decode: head %d widths k=%d v=%d", h, kb[h], vb[h]);
+    }
   if ((qjl_signs == nullptr) != (p_rot == nullptr)) return fail(PQKV_ERR_INVALID, "decode: qjl and p_rot go together");
   if (qjl_signs && m != d) return fail(PQKV_ERR_UNSUPPORTED, "decode: QJL needs m == d");
   if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(PQKV_ERR_INVALID, "decode: scale must be > 0");
   if (!q || !R || !out) return fail(PQKV_ERR_INVALID, "decode: null pointer");
   if ((uintptr_t)R % 16) return fail(PQKV_ERR_INVALID, "decode: R must be 16-byte aligned");
   if ((uintptr_t)p_rot % 16) return fail(PQKV_ERR_INVALID, "decode: p_rot must be 16-byte aligned");
-  const size_t need = pqkv_decode_workspace_bytes(B, Hq, Hkv, S, d);
-  if (S > 0) {
-    if (!k_cache || !v_cache || !k_codebooks || !v_codebooks)
-      return fail(PQKV_ERR_INVALID, "decode: null cache or codebook");
-    if (!workspace || workspace_bytes < need)
-      return fail(PQKV_ERR_WORKSPACE, "decode: workspace %zu < %zu bytes", workspace_bytes, need);
-  }
-  hipStream_t st = (hipStream_t)stream;
-  if (S == 0) {
-    const size_t ob = (size_t)B * Hq * d * (out_dtype == PQKV_F32 ? 4 : 2);
-    return hip_status(pqkv::launch_fill_zero(out, ob, st), "decode zero fill");
-  }
+  if (S > 0 && (!k_cache || !v_cache || !k_codebooks || !v_codebooks))
+    return fail(PQKV_ERR_INVALID, "decode: null cache or codebook");
+
   // One split plan serves every launch (they share the partials layout); it
   // is sized for the largest launch: all kv heads, or with mixed widths the
-  // largest group of heads sharing (k bits, v bits).
-  // Heads that are all 4/4 (one shared codebook) or 2/2 run as one launch.
+  // largest group of heads sharing (k bits, v bits). Heads that are all 4/4
+  // (one shared codebook) or 2/2 run as one launch.
   const bool mfma = use_mfma();
   int group = Hkv;
   bool pair = false;
@@ -435,20 +460,36 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
     if (!pair) group = std::max(std::max(count[0][0], count[0][1]), std::max(count[1][0], count[1][1]));
   }
   int splits = 1, tps = 0;
-  decode_plan((int64_t)B * group, S, mfma ? mfma_target() : kValuTarget, &splits, &tps);
-  float *q32 = (float *)workspace;
-  float *part = (float *)((char *)workspace + align256((size_t)B * Hq * d * 4));
-  float *pq32 = (float *)((char *)part + align256((size_t)B * Hq * splits * (d + 2) * 4));
+  decode_plan((int64_t)B * group, S > 0 ? S : 1, mfma ? mfma_target() : kValuTarget, &splits, &tps);
+  size_t q_off, part_off, pq_off;
+  const size_t plan_need = decode_workspace_layout(B, Hq, splits, d, &q_off, &part_off, &pq_off);
+  if (S > 0) {
+    const size_t need = plan_sized ? plan_need : pqkv_decode_workspace_bytes(B, Hq, Hkv, S, d);
+    if (plan_sized && workspace_bytes < need)
+      return fail(PQKV_ERR_WORKSPACE,
+                  "decode_noalloc: this call needs %zu bytes of scratch, more than the %zu the library holds; "
+                  "use pqkv_decode_attn with a caller workspace", need, workspace_bytes);
+    if (!workspace || workspace_bytes < need)
+      return fail(PQKV_ERR_WORKSPACE, "decode: workspace %zu < %zu bytes", workspace_bytes, need);
+  }
+  hipStream_t st = (hipStream_t)stream;
+  if (S == 0) {
+    const size_t ob = (size_t)B * Hq * d * (out_dtype == PQKV_F32 ? 4 : 2);
+    return hip_status(launch_fill_zero(out, ob, st), "decode zero fill");
+  }
+  float *q32 = (float *)((char *)workspace + q_off);
+  float *part = (float *)((char *)workspace + part_off);
+  float *pq32 = (float *)((char *)workspace + pq_off);
   const float kLog2e = 1.4426950408889634f;
-  int tok = pqkv::prof_begin("decode_rotate", st);
+  int tok = prof_begin("decode_rotate", st);
   // QJL: the projections P_rot q_rot / m (m == d) come from the same launch
-  hipError_t e = qjl_signs ? pqkv::launch_rotate2(q, q_dtype, R, p_rot, q32, pq32, (int64_t)B * Hq, d, scale * kLog2e,
-                                                  1.0f / (float)m, st)
-                           : pqkv::launch_rotate(q, q_dtype, R, q32, PQKV_F32, (int64_t)B * Hq, d, 0, scale * kLog2e, st);
-  pqkv::prof_end(tok, st);
+  hipError_t e = qjl_signs ? launch_rotate2(q, q_dtype, R, p_rot, q32, pq32, (int64_t)B * Hq, d, scale * kLog2e,
+                                            1.0f / (float)m, st)
+                           : launch_rotate(q, q_dtype, R, q32, PQKV_F32, (int64_t)B * Hq, d, 0, scale * kLog2e, st);
+  prof_end(tok, st);
   if (e != hipSuccess) return hip_status(e, "decode query rotation");
 
-  pqkv::DecodeArgs a;
+  DecodeArgs a;
   memset(&a, 0, sizeof(a));
   a.q = q32;
   a.k_cache = k_cache;
@@ -463,11 +504,28 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
   a.B = B;
   a.Hq = Hq;
   a.Hkv = Hkv;
+  a.gq = Hq / Hkv;
   a.S = S;
   a.S_max = S_max;
   a.d = d;
   a.splits = splits;
   a.tokens_per_split = tps;
+
+  // Query heads of a kv head in launches of at most kMaxGroup (the matrix
+  // tile holds 8 heads): the group is cut into equal parts where it divides,
+  // the first ones one head larger otherwise.
+  const int n_sub = (a.gq + kMaxGroup - 1) / kMaxGroup;
+  auto for_each_subgroup = [&](auto &&launch) -> hipError_t {
+    int off = 0;
+    for (int i = 0; i < n_sub; ++i) {
+      const int g = a.gq / n_sub + (i < a.gq % n_sub ? 1 : 0);
+      hipError_t r = launch(off, g);
+      if (r != hipSuccess) return r;
+      off += g;
+    }
+    return hipSuccess;
+  };
+
   if (!mixed) {
     const int64_t kvb = pqkv_vector_bytes(d, k_bits), vvb = pqkv_vector_bytes(d, v_bits);
     a.k_head_stride = (int64_t)S_max * kvb;
@@ -476,13 +534,19 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
     a.v_batch_stride = a.v_head_stride * Hkv;
     a.n_heads = Hkv;
     a.listed = 0;
-    tok = pqkv::prof_begin("decode_split", st);
-    e = mfma ? pqkv::launch_decode_mfma(a, k_bits, v_bits, st) : pqkv::launch_decode_split(a, k_bits, v_bits, st);
-    pqkv::prof_end(tok, st);
+    e = for_each_subgroup([&](int off, int g) {
+      a.q_off = off;
+      a.g = g;
+      const int t = prof_begin("decode_split", st);
+      const hipError_t r = mfma ? launch_decode_mfma(a, k_bits, v_bits, st) : launch_decode_split(a, k_bits, v_bits, st);
+      prof_end(t, st);
+      return r;
+    });
     if (e != hipSuccess) return hip_status(e, "decode split launch");
   } else {
     // Per-(b, h) runs of S_max vectors of the head's own width, (b, h) order.
-    std::vector<int64_t> koff(Hkv + 1, 0), voff(Hkv + 1, 0);
+    int64_t koff[kMaxListHeads + 1], voff[kMaxListHeads + 1];
+    koff[0] = voff[0] = 0;
     for (int h = 0; h < Hkv; ++h) {
       koff[h + 1] = koff[h] + (int64_t)S_max * pqkv_vector_bytes(d, kb[h]);
       voff[h + 1] = voff[h] + (int64_t)S_max * pqkv_vector_bytes(d, vb[h]);
@@ -491,21 +555,26 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
     a.v_batch_stride = voff[Hkv];
     a.listed = 1;
     if (pair) {
-      pqkv::DecodeArgs a2 = a;
+      DecodeArgs a2 = a;
       int n4 = 0, n2 = 0;
       for (int h = 0; h < Hkv; ++h) {
-        pqkv::DecodeArgs &g = kb[h] == 4 ? a : a2;
+        DecodeArgs &gr = kb[h] == 4 ? a : a2;
         int &n = kb[h] == 4 ? n4 : n2;
-        g.heads[n] = (int16_t)h;
-        g.k_head_off[n] = koff[h];
-        g.v_head_off[n] = voff[h];
+        gr.heads[n] = (int16_t)h;
+        gr.k_head_off[n] = koff[h];
+        gr.v_head_off[n] = voff[h];
         ++n;
       }
       a.n_heads = n4;
       a2.n_heads = n2;
-      tok = pqkv::prof_begin("decode_split", st);
-      e = pqkv::launch_decode_mfma_pair(a, a2, st);
-      pqkv::prof_end(tok, st);
+      e = for_each_subgroup([&](int off, int g) {
+        a.q_off = a2.q_off = off;
+        a.g = a2.g = g;
+        const int t = prof_begin("decode_split", st);
+        const hipError_t r = launch_decode_mfma_pair(a, a2, st);
+        prof_end(t, st);
+        return r;
+      });
       if (e != hipSuccess) return hip_status(e, "decode split launch");
     } else {
       for (int kbits : {4, 2})
@@ -520,18 +589,28 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
             }
           if (n == 0) continue;
           a.n_heads = n;
-          tok = pqkv::prof_begin("decode_split", st);
-          e = mfma ? pqkv::launch_decode_mfma(a, kbits, vbits, st) : pqkv::launch_decode_split(a, kbits, vbits, st);
-          pqkv::prof_end(tok, st);
+          e = for_each_subgroup([&](int off, int g) {
+            a.q_off = off;
+            a.g = g;
+            const int t = prof_begin("decode_split", st);
+            const hipError_t r =
+                mfma ? launch_decode_mfma(a, kbits, vbits, st) : launch_decode_split(a, kbits, vbits, st);
+            prof_end(t, st);
+            return r;
+          });
           if (e != hipSuccess) return hip_status(e, "decode split launch");
         }
     }
   }
-  tok = pqkv::prof_begin("decode_merge", st);
-  e = pqkv::launch_decode_merge(part, R, out, out_dtype, B * Hq, splits, d, st);
-  pqkv::prof_end(tok, st);
+  tok = prof_begin("decode_merge", st);
+  e = launch_decode_merge(part, R, out, out_dtype, B * Hq, splits, d, st);
+  prof_end(tok, st);
   return hip_status(e, "decode merge launch");
 }
+
+}  // namespace pqkv
+
+extern "C" {
 
 size_t pqkv_prefill_workspace_bytes(int B, int Hq, int Hkv, int Sq, int S, int d) {
   (void)Hkv;

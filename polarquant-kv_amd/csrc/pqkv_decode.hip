@@ -111,7 +111,7 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
   build_lut<VBITS>(lut_v, a.v_cb + h * a.cb_head_stride, tid);
   for (int i = tid; i < G * D; i += 256) {
     const int hh = i / D, p = i - hh * D;
-    q_lds[hh][p] = a.q[(int64_t)(b * a.Hq + h * G + hh) * D + p];
+    q_lds[hh][p] = a.q[(int64_t)(b * a.Hq + h * a.gq + a.q_off + hh) * D + p];
   }
   __syncthreads();
   if (QJL) {
@@ -119,7 +119,7 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
     // computed once per call for every query head
     for (int i = tid; i < G * M; i += 256) {
       const int hh = i / M, r = i - hh * M;
-      pq_lds[hh][r] = a.pq[(int64_t)(b * a.Hq + h * G + hh) * M + r];
+      pq_lds[hh][r] = a.pq[(int64_t)(b * a.Hq + h * a.gq + a.q_off + hh) * M + r];
     }
     __syncthreads();
     for (int i = tid; i < (M / 4) * 16 * GP; i += 256) {
@@ -333,7 +333,7 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
       L += red_l[w][hh] * sc;
       O += red_o[(w * G + hh) * D + c] * sc;
     }
-    float *dst = a.part + (((int64_t)(b * a.Hq + h * G + hh) * a.splits) + split) * (D + 2);
+    float *dst = a.part + (((int64_t)(b * a.Hq + h * a.gq + a.q_off + hh) * a.splits) + split) * (D + 2);
     if (c == 0) {
       dst[0] = mx;
       dst[1] = L;
@@ -479,7 +479,7 @@ static void launch_dd(const DecodeArgs &a, int kb, int vb, int G, bool qjl, hipS
 }
 
 hipError_t launch_decode_split(const DecodeArgs &a, int k_bits, int v_bits, hipStream_t s) {
-  const int G = a.Hq / a.Hkv;
+  const int G = a.g;
   const bool qjl = a.qjl != nullptr;
   if (a.d == 128) launch_dd<128>(a, k_bits, v_bits, G, qjl, s);
   else launch_dd<64>(a, k_bits, v_bits, G, qjl, s);

@@ -353,7 +353,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   const int qh = col & 7;
   const bool qlo = col >= 8;
   const float qmask = qh < G ? 1.0f : 0.0f;
-  const int64_t qrow_i = (int64_t)(b * a.Hq + h * G + (qh < G ? qh : 0));
+  const int64_t qrow_i = (int64_t)(b * a.Hq + h * a.gq + a.q_off + (qh < G ? qh : 0));
   const float *qrow = a.q + qrow_i * D;
   half8_t qb[KK];
 #pragma unroll
@@ -828,7 +828,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
       L += red_l[w][hh] * sc;
       O += sm.u.red_o[w][hh * D + c] * sc;
     }
-    float *dst = a.part + (((int64_t)(b * a.Hq + h * G + hh) * a.splits) + split) * (D + 2);
+    float *dst = a.part + (((int64_t)(b * a.Hq + h * a.gq + a.q_off + hh) * a.splits) + split) * (D + 2);
     if (c == 0) {
       dst[0] = mx;
       dst[1] = L;
@@ -910,7 +910,7 @@ static void launch_dm_pair(const DecodeArgs &a4, const DecodeArgs &a2, int G, hi
 }
 
 hipError_t launch_decode_mfma_pair(const DecodeArgs &a4, const DecodeArgs &a2, hipStream_t s) {
-  const int G = a4.Hq / a4.Hkv;
+  const int G = a4.g;
   const bool qjl = a4.qjl != nullptr;
   if (a4.d == 128) {
     if (qjl) launch_dm_pair<128, true>(a4, a2, G, s);
@@ -923,7 +923,7 @@ hipError_t launch_decode_mfma_pair(const DecodeArgs &a4, const DecodeArgs &a2, h
 }
 
 hipError_t launch_decode_mfma(const DecodeArgs &a, int k_bits, int v_bits, hipStream_t s) {
-  const int G = a.Hq / a.Hkv;
+  const int G = a.g;
   if (a.d == 128) launch_dm_w<128>(a, k_bits, v_bits, G, s);
   else launch_dm_w<64>(a, k_bits, v_bits, G, s);
   return hipGetLastError();

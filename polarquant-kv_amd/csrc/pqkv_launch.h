@@ -16,6 +16,7 @@ constexpr int kMaxListHeads = PQKV_MAX_HEADS;  // kv heads per launch when heads
 constexpr int kMaxSplits = 1024;   // split-K partitions per (batch, kv head)
 constexpr int kMergeHeads = 4;     // query heads per merge workgroup
 constexpr int kMfmaBlocksPerCU = 2;  // decode_mfma_kernel workgroups resident per CU
+constexpr int kMaxGroup = 8;         // query heads per kv head in one decode launch
 
 struct EncodeArgs {
   const void *x;
@@ -47,6 +48,8 @@ struct DecodeArgs {
   const float *pq;               // [B][Hq][m] = P_rot q / m (QJL only)
   float *part;                   // [B][Hq][splits][d + 2]
   int B, Hq, Hkv, S, S_max, d;
+  int gq;                        // query heads per kv head (Hq / Hkv)
+  int q_off, g;                  // this launch: query heads q_off .. q_off + g - 1 of each kv head (g <= kMaxGroup)
   int splits, tokens_per_split;
   int n_heads;                   // heads in this launch
   int listed;                    // 1: heads / offsets below are used
@@ -65,6 +68,23 @@ struct PrefillArgs {
   int B, Hq, Hkv, G, Sq, q_start, S, S_max, d, causal;
   int qt;                        // query tokens per workgroup (rows / G)
 };
+
+// Workspace of one decode call whose plan has `splits` partitions per stream
+// (rotated queries, split partials, QJL projections); returns the total
+// bytes, the nullable pointers receive the three offsets.
+size_t decode_workspace_layout(int B, int Hq, int splits, int d, size_t *q_off, size_t *part_off, size_t *pq_off);
+// The validated decode call behind pqkv_decode_attn (plan_sized = false: the
+// workspace must hold pqkv_decode_workspace_bytes) and the allocation-free
+// entry point (plan_sized = true: the workspace must hold this call's plan).
+int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k_cache, const uint8_t *v_cache,
+                    const float *k_codebooks, const float *v_codebooks, int k_bits, int v_bits,
+                    const int *k_head_bits, const int *v_head_bits, const uint8_t *qjl_signs, const float *p_rot,
+                    int m, int B, int Hq, int Hkv, int S, int S_max, int d, float scale, void *out, int out_dtype,
+                    void *workspace, size_t workspace_bytes, bool plan_sized, void *stream);
+
+// Sets the thread's error message from a HIP error; returns PQKV_ERR_HIP
+// (PQKV_OK for hipSuccess).
+int report_hip_error(hipError_t e, const char *what);
 
 // Event brackets for the measurement hook (pqkv_profile_*): returns a token
 // for prof_end, or -1 when profiling is off.

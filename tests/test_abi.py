@@ -98,7 +98,7 @@ def _decode(**kw):
 
 def test_decode_validation():
     _status(_decode(Hq=6, Hkv=4), _lib.ERR_INVALID)            # Hq not a multiple of Hkv
-    _status(_decode(Hq=32, Hkv=2), _lib.ERR_UNSUPPORTED)       # group of 16
+    _status(_decode(Hq=32, Hkv=2, wsb=16), _lib.ERR_WORKSPACE)  # a group of 16 passes validation
     _status(_decode(d=96), _lib.ERR_UNSUPPORTED)
     _status(_decode(kb=3), _lib.ERR_UNSUPPORTED)
     _status(_decode(S=20, S_max=16), _lib.ERR_INVALID)

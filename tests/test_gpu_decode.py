@@ -95,6 +95,9 @@ CASES = [
     (2, 8, 2, 200, 128, 4, 2),      # 4-bit K, 2-bit V
     (1, 6, 2, 77, 64, 2, 4),        # 2-bit K, 4-bit V
     (1, 8, 1, 1500, 64, 2, 2),      # several splits
+    (1, 32, 2, 300, 128, 4, 4),     # G = 16: two launches of 8 query heads per kv head
+    (2, 12, 1, 200, 64, 4, 2),      # G = 12: two launches of 6
+    (1, 9, 1, 130, 128, 2, 2),      # G = 9: launches of 5 and 4
 ]
 
 
@@ -216,6 +219,7 @@ QJL_CASES = [
     (1, 16, 2, 333, 128, 4, 4),     # G = 8: whole-chunk reloads, one shared 4-bit table
     (2, 14, 2, 257, 64, 4, 2),      # G = 7, d = 64, 4-bit K / 2-bit V
     (1, 4, 4, 100, 128, 4, 4),      # G = 1
+    (1, 40, 2, 150, 128, 2, 2),     # G = 20: launches of 7, 7 and 6
 ]
 
 
