@@ -150,6 +150,26 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R,
                      void *out, int out_dtype,
                      void *workspace, size_t workspace_bytes, void *stream);
 
+/* Allocation-free variant of pqkv_decode_attn (no counterpart in the
+ * reference): for callers that cannot allocate device memory (code under
+ * stream or graph capture, serving loops that forbid it). Same arguments and
+ * results as pqkv_decode_attn without the workspace: the library keeps one
+ * PQKV_NOALLOC_SCRATCH_BYTES device array per GPU for the whole process and
+ * uses it instead. A call whose split plan needs more (rotated queries,
+ * split partials, QJL projections: about B*Hq*(2d + splits*(d+2))*4 bytes)
+ * returns PQKV_ERR_WORKSPACE. The call allocates nothing. Every call on one
+ * GPU shares that GPU's array: calls that overlap on one GPU (different
+ * streams, or threads without ordering) race. */
+#define PQKV_NOALLOC_SCRATCH_BYTES (16u << 20)
+int pqkv_decode_attn_noalloc(const void *q, int q_dtype, const float *R,
+                             const uint8_t *k_cache, const uint8_t *v_cache,
+                             const float *k_codebooks, const float *v_codebooks,
+                             int k_bits, int v_bits,
+                             const int *k_head_bits, const int *v_head_bits,
+                             const uint8_t *qjl_signs, const float *p_rot, int m,
+                             int B, int Hq, int Hkv, int S, int S_max, int d, float scale,
+                             void *out, int out_dtype, void *stream);
+
 /* ---- chunked prefill attention -------------------------------------------
  * Sq query tokens per sequence (absolute positions q_start .. q_start+Sq-1)
  * against a cache that already holds them (append-then-attend,

@@ -21,7 +21,7 @@ OUT_DIR = os.path.join(HERE, "polarquant_kv", "_lib")
 LIB = os.path.join(OUT_DIR, "libpqkv_hip.so")
 BUILD = os.path.join(HERE, "_build")
 SOURCES = ["pqkv_encode.hip", "pqkv_encode_mfma.hip", "pqkv_decode.hip", "pqkv_decode_mfma.hip", "pqkv_prefill.hip",
-           "pqkv_api.cpp", "pqkv_compat.cpp"]
+           "pqkv_api.cpp", "pqkv_compat.cpp", "pqkv_noalloc.hip"]
 
 
 def hipcc() -> str:

@@ -39,6 +39,10 @@ SIGNATURES = {
                                  c_int, c_int, c_int_p, c_int_p, c_void_p, c_void_p, c_int,
                                  c_int, c_int, c_int, c_int, c_int, c_int, c_float,
                                  c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
+    "pqkv_decode_attn_noalloc": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                         c_int, c_int, c_int_p, c_int_p, c_void_p, c_void_p, c_int,
+                                         c_int, c_int, c_int, c_int, c_int, c_int, c_float,
+                                         c_void_p, c_int, c_void_p]),
     "pqkv_prefill_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "pqkv_prefill_attn": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
