@@ -252,6 +252,28 @@ void polarquant_inverse_rotate_cuda_c(const float *input, const float *rotation,
                                       float *output, int total_q_heads, int D,
                                       void *stream);
 
+/* ---- the reference's raw-pointer Python binding -----------------------------
+ * Same names, argument order and meaning as the pybind module
+ * polarquant_turboquant (csrc/flash_turboquant.cu:180-230), which callers
+ * reach with device pointers passed as Python ints
+ * (scripts/benchmark_turboquant.py:88-114): SoA layout (packed u8 [N][D/2],
+ * coordinate 2i in the low nibble, + fp32 radius [N]), null stream,
+ * asynchronous, no status (errors print to stderr).
+ * turboquant_compress: rotate, quantise and pack N vectors of fp32 input,
+ *   bit-exact to the reference kernel's arithmetic (:111-175).
+ * turboquant_full_attention: attention of the rotated queries at q_rot over
+ *   [total_kv][S] SoA keys and values, rotated fp32 output to attn_out; q, R
+ *   and out are not read, as in the reference (:188-209); score
+ *   ([total_heads][S] fp32) is used as scratch. k_cb / v_cb: n_levels fp32
+ *   centroids each. */
+void turboquant_compress(int64_t input_ptr, int64_t R_ptr, int64_t cb_ptr,
+                         int64_t radius_ptr, int64_t packed_ptr, int N, int D, int n_levels);
+void turboquant_full_attention(int64_t q_ptr, int64_t R_ptr, int64_t pk_ptr, int64_t kr_ptr,
+                               int64_t pv_ptr, int64_t vr_ptr, int64_t k_cb_ptr, int64_t v_cb_ptr,
+                               int64_t out_ptr, int64_t q_rot_ptr, int64_t score_ptr,
+                               int64_t attn_out_ptr, int total_heads, int total_kv, int S, int D,
+                               int n_levels, float scale);
+
 #ifdef __cplusplus
 }
 #endif

@@ -388,6 +388,33 @@ def decode_attention(q: np.ndarray, k_blocks: np.ndarray, v_blocks: np.ndarray,
     return inverse_rotate(out, R)
 
 
+def decode_attention_soa(q_rot: np.ndarray, k_packed: np.ndarray, k_radius: np.ndarray,
+                         v_packed: np.ndarray, v_radius: np.ndarray, codebook: np.ndarray,
+                         n_kv_heads: int, scale: float) -> np.ndarray:
+    """The reference's fused attention on its SoA cache, in float64, with the
+    fp32 radii as given (integration/polarquant-kv.patch:320-389,
+    csrc/flash_turboquant.cu:27-105): q_rot [Hq, d] already rotated;
+    k_packed / v_packed [Hkv * S, d/2] (coordinate 2i in the low nibble),
+    k_radius / v_radius [Hkv * S] fp32; q-head h reads kv-head
+    h // (Hq / Hkv); s_t = scale * r_k,t * q_rot . c[idx_t], w = softmax(s),
+    o_rot = sum_t w_t r_v,t c[vidx_t]. Returns the rotated output [Hq, d]."""
+    q = np.asarray(q_rot, np.float64)
+    Hq, d = q.shape
+    S = k_radius.shape[0] // n_kv_heads
+    c = np.asarray(codebook, np.float32).astype(np.float64)
+    K = np.asarray(k_radius, np.float32).astype(np.float64)[:, None] * c[unpack_codes(k_packed, 4)]
+    V = np.asarray(v_radius, np.float32).astype(np.float64)[:, None] * c[unpack_codes(v_packed, 4)]
+    K = K.reshape(n_kv_heads, S, d)
+    V = V.reshape(n_kv_heads, S, d)
+    g = Hq // n_kv_heads
+    out = np.zeros((Hq, d))
+    for h in range(Hq):
+        s = K[h // g] @ q[h] * scale
+        w = np.exp(s - s.max())
+        out[h] = (w / w.sum()) @ V[h // g]
+    return out
+
+
 def prefill_attention(q: np.ndarray, k_blocks: np.ndarray, v_blocks: np.ndarray,
                       R: np.ndarray, k_cb, v_cb, q_start: int, causal: bool = True,
                       k_bits=4, v_bits=4, scale: float | None = None):

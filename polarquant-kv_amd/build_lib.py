@@ -20,8 +20,10 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "polarquant_kv", "_lib")
 LIB = os.path.join(OUT_DIR, "libpqkv_hip.so")
 BUILD = os.path.join(HERE, "_build")
-SOURCES = ["pqkv_encode.hip", "pqkv_encode_mfma.hip", "pqkv_decode.hip", "pqkv_decode_mfma.hip", "pqkv_prefill.hip",
-           "pqkv_api.cpp", "pqkv_compat.cpp", "pqkv_noalloc.hip"]
+SOURCES = ["pqkv_encode.hip", "pqkv_encode_mfma.hip", "pqkv_decode.hip", "pqkv_decode_mfma.hip",
+           "pqkv_decode_mfma_k4v4_shared.hip", "pqkv_decode_mfma_k4v4_own.hip", "pqkv_decode_mfma_k4v2.hip",
+           "pqkv_decode_mfma_k2v4.hip", "pqkv_decode_mfma_k2v2.hip", "pqkv_decode_mfma_pair.hip",
+           "pqkv_decode_mfma_soa.hip", "pqkv_prefill.hip", "pqkv_api.cpp", "pqkv_compat.cpp", "pqkv_noalloc.hip"]
 
 
 def hipcc() -> str:
@@ -36,9 +38,18 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", "--offload-arch=gfx950", "-Wall", "-Wno-
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
-def compile_one(src: str) -> str:
+def _headers_mtime() -> float:
+    hs = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    hs.append(os.path.join(HERE, "..", "include", "pqkv.h"))
+    return max(os.path.getmtime(h) for h in hs if os.path.exists(h))
+
+
+def compile_one(src: str, changed_only: bool = False) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
     path = os.path.join(CSRC, src)
+    if changed_only and os.path.exists(obj) and \
+            os.path.getmtime(obj) > max(os.path.getmtime(path), _headers_mtime()):
+        return obj
     if src.endswith(".hip"):
         cmd = [hipcc(), *COMMON, "-x", "hip", "-c", path, "-o", obj]
     else:
@@ -49,11 +60,15 @@ def compile_one(src: str) -> str:
     return obj
 
 
-def build(jobs: int = 4) -> str:
+def build(jobs: int = 8, changed_only: bool = False) -> str:
+    """Compile every unit (changed_only: only those older than their source
+    or any header) and link the library."""
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(OUT_DIR, exist_ok=True)
+    # the slowest units first, so that they overlap the rest
+    order = sorted(SOURCES, key=lambda f: -os.path.getsize(os.path.join(CSRC, f)))
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        objs = list(ex.map(compile_one, SOURCES))
+        objs = list(ex.map(lambda f: compile_one(f, changed_only), order))
     tmp = LIB + ".tmp"
     subprocess.run([hipcc(), "-shared", "-fPIC", "--offload-arch=gfx950", *objs, "-o", tmp], check=True)
     os.replace(tmp, LIB)
@@ -62,5 +77,7 @@ def build(jobs: int = 4) -> str:
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
-    ap.add_argument("--jobs", type=int, default=4)
-    print(build(ap.parse_args().jobs))
+    ap.add_argument("--jobs", type=int, default=8)
+    ap.add_argument("--changed", action="store_true", help="recompile only units older than their sources")
+    args = ap.parse_args()
+    print(build(args.jobs, args.changed))

@@ -386,7 +386,7 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
                      void *workspace, size_t workspace_bytes, void *stream) {
   return pqkv::decode_attn_run(q, q_dtype, R, k_cache, v_cache, k_codebooks, v_codebooks, k_bits, v_bits,
                                k_head_bits, v_head_bits, qjl_signs, p_rot, m, B, Hq, Hkv, S, S_max, d, scale, out,
-                               out_dtype, workspace, workspace_bytes, false, stream);
+                               out_dtype, workspace, workspace_bytes, false, nullptr, stream);
 }
 
 }  // extern "C"
@@ -417,7 +417,8 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
                     const float *k_codebooks, const float *v_codebooks, int k_bits, int v_bits,
                     const int *k_head_bits, const int *v_head_bits, const uint8_t *qjl_signs, const float *p_rot,
                     int m, int B, int Hq, int Hkv, int S, int S_max, int d, float scale, void *out, int out_dtype,
-                    void *workspace, size_t workspace_bytes, bool plan_sized, void *stream) {
+                    void *workspace, size_t workspace_bytes, bool plan_sized, const SoaCache *soa,
+                    void *stream) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S < 0 || S_max < S)
     return fail(PQKV_ERR_INVALID, "decode: B=%d Hq=%d Hkv=%d S=%d S_max=%d", B, Hq, Hkv, S, S_max);
   if (Hq % Hkv) return fail(PQKV_ERR_INVALID, "decode: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
@@ -439,8 +440,11 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
   if ((qjl_signs == nullptr) != (p_rot == nullptr)) return fail(PQKV_ERR_INVALID, "decode: qjl and p_rot go together");
   if (qjl_signs && m != d) return fail(PQKV_ERR_UNSUPPORTED, "decode: QJL needs m == d");
   if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(PQKV_ERR_INVALID, "decode: scale must be > 0");
-  if (!q || !R || !out) return fail(PQKV_ERR_INVALID, "decode: null pointer");
+  if (!q || (!R && !soa) || !out) return fail(PQKV_ERR_INVALID, "decode: null pointer");
   if ((uintptr_t)R % 16) return fail(PQKV_ERR_INVALID, "decode: R must be 16-byte aligned");
+  if (soa && (mixed || k_bits != 4 || v_bits != 4 || qjl_signs || soa->levels < 1 || soa->levels > 16 ||
+              (S > 0 && (!soa->k_rad || !soa->v_rad))))
+    return fail(PQKV_ERR_UNSUPPORTED, "decode: the SoA layout takes 4-bit codes and no QJL signs");
   if ((uintptr_t)p_rot % 16) return fail(PQKV_ERR_INVALID, "decode: p_rot must be 16-byte aligned");
   if (S > 0 && (!k_cache || !v_cache || !k_codebooks || !v_codebooks))
     return fail(PQKV_ERR_INVALID, "decode: null cache or codebook");
@@ -449,7 +453,7 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
   // is sized for the largest launch: all kv heads, or with mixed widths the
   // largest group of heads sharing (k bits, v bits). Heads that are all 4/4
   // (one shared codebook) or 2/2 run as one launch.
-  const bool mfma = use_mfma();
+  const bool mfma = use_mfma() || soa != nullptr;
   int group = Hkv;
   bool pair = false;
   if (mixed) {
@@ -465,10 +469,10 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
   const size_t plan_need = decode_workspace_layout(B, Hq, splits, d, &q_off, &part_off, &pq_off);
   if (S > 0) {
     const size_t need = plan_sized ? plan_need : pqkv_decode_workspace_bytes(B, Hq, Hkv, S, d);
-    if (plan_sized && workspace_bytes < need)
+    if (plan_sized && (!workspace || workspace_bytes < need))
       return fail(PQKV_ERR_WORKSPACE,
-                  "decode_noalloc: this call needs %zu bytes of scratch, more than the %zu the library holds; "
-                  "use pqkv_decode_attn with a caller workspace", need, workspace_bytes);
+                  "decode: this call's split plan needs %zu bytes of scratch, more than the %zu available "
+                  "(pqkv_decode_attn takes a caller workspace of any size)", need, workspace_bytes);
     if (!workspace || workspace_bytes < need)
       return fail(PQKV_ERR_WORKSPACE, "decode: workspace %zu < %zu bytes", workspace_bytes, need);
   }
@@ -497,6 +501,9 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
   a.k_cb = k_codebooks;
   a.v_cb = v_codebooks;
   a.cb_head_stride = mixed ? 16 : 0;
+  a.cb_levels = soa ? soa->levels : 16;
+  a.k_rad = soa ? soa->k_rad : nullptr;
+  a.v_rad = soa ? soa->v_rad : nullptr;
   a.qjl = qjl_signs;
   a.p_rot = p_rot;
   a.pq = qjl_signs ? pq32 : nullptr;
@@ -527,7 +534,7 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
   };
 
   if (!mixed) {
-    const int64_t kvb = pqkv_vector_bytes(d, k_bits), vvb = pqkv_vector_bytes(d, v_bits);
+    const int64_t kvb = soa ? d / 2 : pqkv_vector_bytes(d, k_bits), vvb = soa ? d / 2 : pqkv_vector_bytes(d, v_bits);
     a.k_head_stride = (int64_t)S_max * kvb;
     a.v_head_stride = (int64_t)S_max * vvb;
     a.k_batch_stride = a.k_head_stride * Hkv;
@@ -538,7 +545,9 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
       a.q_off = off;
       a.g = g;
       const int t = prof_begin("decode_split", st);
-      const hipError_t r = mfma ? launch_decode_mfma(a, k_bits, v_bits, st) : launch_decode_split(a, k_bits, v_bits, st);
+      const hipError_t r = soa    ? launch_decode_mfma_soa(a, st)
+                           : mfma ? launch_decode_mfma(a, k_bits, v_bits, st)
+                                  : launch_decode_split(a, k_bits, v_bits, st);
       prof_end(t, st);
       return r;
     });

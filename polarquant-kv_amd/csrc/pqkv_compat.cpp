@@ -3,9 +3,10 @@
 // llama.cpp binds with dlsym (patch:1508-1557). Same names, arguments, return
 // types and ownership; SoA cache layout (packed u8 [N][D/2] + fp32 radius).
 // Kernels are the library's own: the SoA encoder reproduces the reference's
-// arithmetic exactly; attention converts the SoA operands to block_pq4 and
-// runs the split-K decode kernel with an identity rotation, because these
-// entry points take an already-rotated query and return a rotated output.
+// arithmetic exactly; attention runs the split-K matrix-core decode kernel
+// reading the SoA codes and fp32 radii in place, with no rotation of the
+// query or the output (these entry points take an already-rotated query and
+// return a rotated output).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -58,6 +59,16 @@ void gram_schmidt_rotation(float *R, int D, unsigned seed) {
   }
 }
 
+// The codebooks polarquant_init uploads, for every head_dim
+// (patch:978-994, selected by n_bits at patch:600-613). They are a fixed
+// input of the ggml format, so the values are the reference's, digit for
+// digit.
+const float kGgmlCodebook4[16] = {-0.1547f, -0.1175f, -0.0928f, -0.0722f, -0.0537f, -0.0363f,
+                                  -0.0193f, -0.0024f, 0.0145f,  0.0318f,  0.0498f,  0.0692f,
+                                  0.0907f,  0.1157f,  0.1467f,  0.1947f};
+const float kGgmlCodebook3[8] = {-0.1350f, -0.0820f, -0.0440f, -0.0110f, 0.0220f, 0.0560f, 0.0950f, 0.1500f};
+const float kGgmlCodebook2[4] = {-0.1050f, -0.0280f, 0.0400f, 0.1200f};
+
 }  // namespace
 
 extern "C" {
@@ -85,11 +96,7 @@ polarquant_state *polarquant_init_c(int head_dim, int n_kv_heads, int n_q_heads,
   st->n_layers = n_layers;
   st->n_kv_max = n_kv_max;
 
-  float cb[16];
-  if (pqkv_lloyd_max_codebook(head_dim, n_bits, 300, 50000, cb, nullptr) != PQKV_OK) {
-    delete st;
-    return nullptr;
-  }
+  const float *cb = n_bits == 4 ? kGgmlCodebook4 : n_bits == 3 ? kGgmlCodebook3 : kGgmlCodebook2;
   std::vector<float> R((size_t)head_dim * head_dim);
   gram_schmidt_rotation(R.data(), head_dim, 42);
   bool ok = report(hipMalloc(&st->codebook, st->n_levels * sizeof(float)), "hipMalloc codebook") &&
@@ -181,44 +188,74 @@ void polarquant_fused_attention_cuda_c(const float *q_rotated, const uint8_t *pa
                                        float *output, int total_q_heads, int total_kv_heads, int S, int D,
                                        int n_levels, float scale, void *stream) {
   if (total_q_heads <= 0 || S <= 0 || D <= 0) return;
-  if ((D != 64 && D != 128) || total_kv_heads <= 0 || total_q_heads % total_kv_heads ||
-      total_q_heads / total_kv_heads > 8 || n_levels < 2 || n_levels > 16) {
+  if ((D != 64 && D != 128) || total_kv_heads <= 0 || total_q_heads % total_kv_heads || n_levels < 2 ||
+      n_levels > 16) {
     fprintf(stderr, "PolarQuant (HIP): attention: unsupported Hq=%d Hkv=%d D=%d n_levels=%d\n", total_q_heads,
             total_kv_heads, D, n_levels);
     return;
   }
+  // Stream-ordered scratch for the split partials, like the reference's
+  // attention dispatcher, which allocates its temporaries per call
+  // (patch:869-870); no host synchronisation.
   hipStream_t st = (hipStream_t)stream;
-  const int64_t n = (int64_t)total_kv_heads * S;
-  const int64_t vb = pqkv_vector_bytes(D, 4);
   const size_t ws = pqkv_decode_workspace_bytes(1, total_q_heads, total_kv_heads, S, D);
-  const size_t cache_bytes = (size_t)n * vb;
-  const size_t r_bytes = (size_t)D * D * sizeof(float);
-  const size_t total = 2 * ((cache_bytes + 255) & ~size_t(255)) + ((r_bytes + 255) & ~size_t(255)) + 256 + ws;
-  char *tmp = nullptr;
-  if (!report(hipMallocAsync((void **)&tmp, total, st), "hipMallocAsync")) return;
-  uint8_t *kb = (uint8_t *)tmp;
-  uint8_t *vbk = kb + ((cache_bytes + 255) & ~size_t(255));
-  float *eye = (float *)(vbk + ((cache_bytes + 255) & ~size_t(255)));
-  float *cb16 = (float *)((char *)eye + ((r_bytes + 255) & ~size_t(255)));
-  void *work = (char *)cb16 + 256;
-  std::vector<float> I((size_t)D * D, 0.0f);
-  for (int i = 0; i < D; ++i) I[(size_t)i * D + i] = 1.0f;
-  bool ok = report(hipMemcpyAsync(eye, I.data(), r_bytes, hipMemcpyHostToDevice, st), "copy identity") &&
-            report(pqkv::launch_fill_zero(cb16, 64, st), "zero codebook") &&
-            report(hipMemcpyAsync(cb16, codebook, n_levels * sizeof(float), hipMemcpyDeviceToDevice, st),
-                   "copy codebook") &&
-            report(pqkv::launch_soa_to_blocks(packed_k, k_radius, kb, n, D, st), "convert K") &&
-            report(pqkv::launch_soa_to_blocks(packed_v, v_radius, vbk, n, D, st), "convert V");
-  if (ok) {
-    const int rc = pqkv_decode_attn(q_rotated, PQKV_F32, eye, kb, vbk, cb16, cb16, 4, 4, nullptr, nullptr, nullptr,
-                                    nullptr, 0, 1, total_q_heads, total_kv_heads, S, S, D, scale, output, PQKV_F32,
-                                    work, ws, stream);
-    if (rc != PQKV_OK) fprintf(stderr, "PolarQuant (HIP): attention: %s\n", pqkv_last_error());
+  void *work = nullptr;
+  if (!report(hipMallocAsync(&work, ws, st), "hipMallocAsync")) return;
+  const pqkv::SoaCache soa{k_radius, v_radius, n_levels};
+  const int rc = pqkv::decode_attn_run(q_rotated, PQKV_F32, nullptr, packed_k, packed_v, codebook, codebook, 4, 4,
+                                       nullptr, nullptr, nullptr, nullptr, 0, 1, total_q_heads, total_kv_heads, S, S,
+                                       D, scale, output, PQKV_F32, work, ws, false, &soa, stream);
+  if (rc != PQKV_OK) fprintf(stderr, "PolarQuant (HIP): attention: %s\n", pqkv_last_error());
+  report(hipFreeAsync(work, st), "hipFreeAsync");
+}
+
+// ---- the reference's raw-pointer pybind surface (csrc/flash_turboquant.cu:180-230) ----
+
+void turboquant_compress(int64_t input_ptr, int64_t R_ptr, int64_t cb_ptr, int64_t radius_ptr, int64_t packed_ptr,
+                         int N, int D, int n_levels) {
+  polarquant_compress_cuda_c((const float *)input_ptr, (const float *)R_ptr, (const float *)cb_ptr,
+                             (float *)radius_ptr, (uint8_t *)packed_ptr, N, D, n_levels, nullptr);
+}
+
+void turboquant_full_attention(int64_t q_ptr, int64_t R_ptr, int64_t pk_ptr, int64_t kr_ptr, int64_t pv_ptr,
+                               int64_t vr_ptr, int64_t k_cb_ptr, int64_t v_cb_ptr, int64_t out_ptr,
+                               int64_t q_rot_ptr, int64_t score_ptr, int64_t attn_out_ptr, int total_heads,
+                               int total_kv, int S, int D, int n_levels, float scale) {
+  // As in the reference: the query is q_rot (rotated by the caller), the
+  // rotated output goes to attn_out; q, R and out are not read
+  // (flash_turboquant.cu:188-209). score ([total_heads][S] fp32, the
+  // reference kernel's score buffer) serves as the scratch for the split
+  // partials when this call's plan fits in it; otherwise a stream-ordered
+  // allocation is made and released on the same stream.
+  (void)q_ptr;
+  (void)R_ptr;
+  (void)out_ptr;
+  if (total_heads <= 0 || S <= 0 || D <= 0) return;
+  if ((D != 64 && D != 128) || total_kv <= 0 || total_heads % total_kv || n_levels < 2 || n_levels > 16) {
+    fprintf(stderr, "PolarQuant (HIP): turboquant_full_attention: unsupported heads=%d kv=%d D=%d n_levels=%d\n",
+            total_heads, total_kv, D, n_levels);
+    return;
   }
-  // The identity matrix is copied from pageable host memory; wait for the
-  // stream before the host vector goes away and the scratch is released.
-  report(hipStreamSynchronize(st), "stream sync");
-  report(hipFreeAsync(tmp, st), "hipFreeAsync");
+  const pqkv::SoaCache soa{(const float *)kr_ptr, (const float *)vr_ptr, n_levels};
+  void *score = (void *)score_ptr;
+  const size_t score_bytes = (size_t)total_heads * S * sizeof(float);
+  int rc = PQKV_ERR_WORKSPACE;
+  if (score && (uintptr_t)score % 16 == 0)
+    rc = pqkv::decode_attn_run((const void *)q_rot_ptr, PQKV_F32, nullptr, (const uint8_t *)pk_ptr,
+                               (const uint8_t *)pv_ptr, (const float *)k_cb_ptr, (const float *)v_cb_ptr, 4, 4,
+                               nullptr, nullptr, nullptr, nullptr, 0, 1, total_heads, total_kv, S, S, D, scale,
+                               (void *)attn_out_ptr, PQKV_F32, score, score_bytes, true, &soa, nullptr);
+  if (rc == PQKV_ERR_WORKSPACE) {
+    const size_t ws = pqkv_decode_workspace_bytes(1, total_heads, total_kv, S, D);
+    void *work = nullptr;
+    if (!report(hipMallocAsync(&work, ws, nullptr), "hipMallocAsync")) return;
+    rc = pqkv::decode_attn_run((const void *)q_rot_ptr, PQKV_F32, nullptr, (const uint8_t *)pk_ptr,
+                               (const uint8_t *)pv_ptr, (const float *)k_cb_ptr, (const float *)v_cb_ptr, 4, 4,
+                               nullptr, nullptr, nullptr, nullptr, 0, 1, total_heads, total_kv, S, S, D, scale,
+                               (void *)attn_out_ptr, PQKV_F32, work, ws, false, &soa, nullptr);
+    report(hipFreeAsync(work, nullptr), "hipFreeAsync");
+  }
+  if (rc != PQKV_OK) fprintf(stderr, "PolarQuant (HIP): turboquant_full_attention: %s\n", pqkv_last_error());
 }
 
 }  // extern "C"

@@ -348,7 +348,8 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
 // the full normalised o_rot (cheap, L2-resident partials) and then its 32
 // outputs from the matching 32 columns of R, staged as [32][D + 4] (16-byte
 // reads; each 16-lane phase of them covers all 64 banks).
-template <int D, typename TOUT>
+// ROT = false (R == nullptr): the normalised o_rot itself is the output.
+template <int D, typename TOUT, bool ROT = true>
 __global__ void __launch_bounds__(256) decode_merge_kernel(const float *__restrict__ part,
                                                           const float *__restrict__ R,
                                                           TOUT *__restrict__ out, int BHq, int splits) {
@@ -367,10 +368,12 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const float *__restri
   // columns, this wave's split maxima and sums (up to 64 splits), and the
   // first SB splits of the thread's o values.
   float4 rv[RU];
+  if constexpr (ROT) {
 #pragma unroll
-  for (int u = 0; u < RU; ++u) {
-    const int i = tid + 256 * u, k = i / (NC / 4), j4 = i % (NC / 4);
-    rv[u] = *(const float4 *)(R + (int64_t)k * D + c0 + 4 * j4);
+    for (int u = 0; u < RU; ++u) {
+      const int i = tid + 256 * u, k = i / (NC / 4), j4 = i % (NC / 4);
+      rv[u] = *(const float4 *)(R + (int64_t)k * D + c0 + 4 * j4);
+    }
   }
   const int hq_w = head0 + wave;
   const float *pw = part + (int64_t)min(hq_w, BHq - 1) * splits * (D + 2);
@@ -384,13 +387,15 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const float *__restri
 #pragma unroll
     for (int sp = 0; sp < SB; ++sp) ov[u][sp] = sp < splits ? p[(int64_t)sp * (D + 2)] : 0.0f;
   }
+  if constexpr (ROT) {
 #pragma unroll
-  for (int u = 0; u < RU; ++u) {
-    const int i = tid + 256 * u, k = i / (NC / 4), j4 = i % (NC / 4);
-    rs[(4 * j4 + 0) * RP + k] = rv[u].x;
-    rs[(4 * j4 + 1) * RP + k] = rv[u].y;
-    rs[(4 * j4 + 2) * RP + k] = rv[u].z;
-    rs[(4 * j4 + 3) * RP + k] = rv[u].w;
+    for (int u = 0; u < RU; ++u) {
+      const int i = tid + 256 * u, k = i / (NC / 4), j4 = i % (NC / 4);
+      rs[(4 * j4 + 0) * RP + k] = rv[u].x;
+      rs[(4 * j4 + 1) * RP + k] = rv[u].y;
+      rs[(4 * j4 + 2) * RP + k] = rv[u].z;
+      rs[(4 * j4 + 3) * RP + k] = rv[u].w;
+    }
   }
   if (hq_w < BHq) {
     float mx = m0;
@@ -425,7 +430,12 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const float *__restri
     os[i] = o;
   }
   __syncthreads();
-  if (tid < NH * NC) {
+  if (!ROT && tid < NH * NC) {
+    const int hh = tid / NC, jj = tid % NC;
+    const int hq = head0 + hh;
+    if (hq < BHq) out[(int64_t)hq * D + c0 + jj] = (TOUT)os[hh * D + c0 + jj];
+  }
+  if (ROT && tid < NH * NC) {
     const int hh = tid / NC, jj = tid % NC;
     const float4 *orow = (const float4 *)(os + hh * D);
     const float4 *rr = (const float4 *)(rs + jj * RP);
@@ -490,13 +500,19 @@ hipError_t launch_decode_merge(const float *part, const float *R, void *out, int
                                int d, hipStream_t s) {
   if (splits < 1 || splits > kMaxSplits) return hipErrorInvalidValue;
   const dim3 grid((BHq + kMergeHeads - 1) / kMergeHeads, d / 32);
-  if (d == 128) {
-    if (out_dtype == 0) decode_merge_kernel<128, float><<<grid, 256, 0, s>>>(part, R, (float *)out, BHq, splits);
-    else decode_merge_kernel<128, half_t><<<grid, 256, 0, s>>>(part, R, (half_t *)out, BHq, splits);
+#define PQKV_MERGE(DD, T, ROT) decode_merge_kernel<DD, T, ROT><<<grid, 256, 0, s>>>(part, R, (T *)out, BHq, splits)
+  if (R == nullptr) {
+    if (d == 128 && out_dtype == 0) PQKV_MERGE(128, float, false);
+    else if (d == 128) PQKV_MERGE(128, half_t, false);
+    else if (out_dtype == 0) PQKV_MERGE(64, float, false);
+    else PQKV_MERGE(64, half_t, false);
   } else {
-    if (out_dtype == 0) decode_merge_kernel<64, float><<<grid, 256, 0, s>>>(part, R, (float *)out, BHq, splits);
-    else decode_merge_kernel<64, half_t><<<grid, 256, 0, s>>>(part, R, (half_t *)out, BHq, splits);
+    if (d == 128 && out_dtype == 0) PQKV_MERGE(128, float, true);
+    else if (d == 128) PQKV_MERGE(128, half_t, true);
+    else if (out_dtype == 0) PQKV_MERGE(64, float, true);
+    else PQKV_MERGE(64, half_t, true);
   }
+#undef PQKV_MERGE
   return hipGetLastError();
 }
 

@@ -1,0 +1,8 @@
+// Decode kernel instantiations: 4-bit keys, 2-bit values.
+#include "pqkv_decode_mfma.h"
+
+namespace pqkv {
+
+hipError_t launch_dm_k4v2(const DecodeArgs &a, hipStream_t s) { return launch_dm_widths<4, 2>(a, s); }
+
+}  // namespace pqkv

@@ -1,0 +1,8 @@
+// Decode kernel instantiations: 4-bit keys, 4-bit values, values with a codebook of their own.
+#include "pqkv_decode_mfma.h"
+
+namespace pqkv {
+
+hipError_t launch_dm_k4v4_own(const DecodeArgs &a, hipStream_t s) { return launch_dm_widths<4, 4, false>(a, s); }
+
+}  // namespace pqkv

@@ -217,6 +217,15 @@ __global__ void __launch_bounds__(256) rotate_kernel(const TIN *__restrict__ x, 
   }
 }
 
+// The identity rotation: y = x * out_scale (what rotate_kernel gives for
+// R = I, whose FMA chain adds exact zeros to x_j * 1).
+template <typename TIN, typename TOUT>
+__global__ void __launch_bounds__(256) scale_kernel(const TIN *__restrict__ x, TOUT *__restrict__ y, int64_t n,
+                                                    float out_scale) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    y[i] = (TOUT)(load_as_float(x + i) * out_scale);
+}
+
 // Two chained forward rotations in one launch: y = (R x) sy, then
 // z = (M y) sz (decode with QJL: the rotated query and its projections
 // P_rot q_rot / m). Workgroup: kRot2Vec vectors, all D columns, both
@@ -493,6 +502,15 @@ static void rotate_dispatch(const void *x, int xt, const float *R, void *y, int 
 
 hipError_t launch_rotate(const void *x, int x_dtype, const float *R, void *y, int y_dtype, int64_t n, int d,
                          int inverse, float out_scale, hipStream_t s) {
+  if (R == nullptr) {
+    const int64_t m = n * d;
+    const int grid = grid_for(m, 256, 4096);
+    if (x_dtype == 0 && y_dtype == 0) scale_kernel<<<grid, 256, 0, s>>>((const float *)x, (float *)y, m, out_scale);
+    else if (x_dtype == 0) scale_kernel<<<grid, 256, 0, s>>>((const float *)x, (half_t *)y, m, out_scale);
+    else if (y_dtype == 0) scale_kernel<<<grid, 256, 0, s>>>((const half_t *)x, (float *)y, m, out_scale);
+    else scale_kernel<<<grid, 256, 0, s>>>((const half_t *)x, (half_t *)y, m, out_scale);
+    return hipGetLastError();
+  }
   if (d == 128) {
     if (inverse) rotate_dispatch<128, true>(x, x_dtype, R, y, y_dtype, n, out_scale, s);
     else rotate_dispatch<128, false>(x, x_dtype, R, y, y_dtype, n, out_scale, s);

@@ -43,6 +43,8 @@ struct DecodeArgs {
   int64_t k_head_stride, v_head_stride;     // bytes between heads (uniform mode)
   const float *k_cb, *v_cb;      // codebook(s)
   int cb_head_stride;            // 0: one table; 16: per-head tables
+  int cb_levels;                 // entries of each table (16, or fewer in the SoA layout)
+  const float *k_rad, *v_rad;    // SoA layout only: fp32 radii, [B][Hkv][S_max]
   const uint8_t *qjl;            // [B][Hkv][S_max][m/8] or null
   const float *p_rot;            // [m][d] (QJL only)
   const float *pq;               // [B][Hq][m] = P_rot q / m (QJL only)
@@ -73,14 +75,24 @@ struct PrefillArgs {
 // (rotated queries, split partials, QJL projections); returns the total
 // bytes, the nullable pointers receive the three offsets.
 size_t decode_workspace_layout(int B, int Hq, int splits, int d, size_t *q_off, size_t *part_off, size_t *pq_off);
+// A 4-bit cache in the reference kernels' SoA layout: k_cache / v_cache hold
+// the packed codes [B][Hkv][S_max][d/2], these the fp32 radii
+// [B][Hkv][S_max]; the codebook has `levels` (<= 16) entries.
+struct SoaCache {
+  const float *k_rad, *v_rad;
+  int levels;
+};
 // The validated decode call behind pqkv_decode_attn (plan_sized = false: the
 // workspace must hold pqkv_decode_workspace_bytes) and the allocation-free
 // entry point (plan_sized = true: the workspace must hold this call's plan).
+// soa (nullable): the caches are SoA; R may then be nullptr, meaning queries
+// that are already rotated and a rotated output.
 int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k_cache, const uint8_t *v_cache,
                     const float *k_codebooks, const float *v_codebooks, int k_bits, int v_bits,
                     const int *k_head_bits, const int *v_head_bits, const uint8_t *qjl_signs, const float *p_rot,
                     int m, int B, int Hq, int Hkv, int S, int S_max, int d, float scale, void *out, int out_dtype,
-                    void *workspace, size_t workspace_bytes, bool plan_sized, void *stream);
+                    void *workspace, size_t workspace_bytes, bool plan_sized, const SoaCache *soa,
+                    void *stream);
 
 // Sets the thread's error message from a HIP error; returns PQKV_ERR_HIP
 // (PQKV_OK for hipSuccess).
@@ -96,6 +108,7 @@ hipError_t launch_quantize_rotated(const float *x_rot, const float *codebook, in
 // y = (R x) sy and z = (M y) sz for n vectors in one launch (fp32 outputs).
 hipError_t launch_rotate2(const void *x, int x_dtype, const float *R, const float *M, float *y, float *z, int64_t n,
                           int d, float sy, float sz, hipStream_t s);
+// R == nullptr: y = x * out_scale (an identity rotation, exactly).
 hipError_t launch_rotate(const void *x, int x_dtype, const float *R, void *y, int y_dtype, int64_t n, int d,
                          int inverse, float out_scale, hipStream_t s);
 hipError_t launch_encode_exact(const EncodeArgs &a, int x_dtype, hipStream_t s);
@@ -118,6 +131,11 @@ hipError_t launch_decode_mfma(const DecodeArgs &a, int k_bits, int v_bits, hipSt
 // Mixed widths with kv heads of exactly two kinds, 4-bit K and V sharing one
 // codebook (a4) and 2-bit K and V (a2): one launch over both head lists.
 hipError_t launch_decode_mfma_pair(const DecodeArgs &a4, const DecodeArgs &a2, hipStream_t s);
+// 4-bit keys and values in the SoA layout (packed codes [stream][S_max][d/2]
+// in k_cache / v_cache, fp32 radii in k_rad / v_rad), codebooks of cb_levels
+// entries (one shared table when k_cb == v_cb), no QJL.
+hipError_t launch_decode_mfma_soa(const DecodeArgs &a, hipStream_t s);
+// R == nullptr: the normalised rotated output, not rotated back.
 hipError_t launch_decode_merge(const float *part, const float *R, void *out, int out_dtype, int BHq, int splits,
                                int d, hipStream_t s);
 hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t s);

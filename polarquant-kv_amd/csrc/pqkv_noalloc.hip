@@ -65,5 +65,5 @@ extern "C" int pqkv_decode_attn_noalloc(const void *q, int q_dtype, const float 
   if (ws == nullptr) return pqkv::report_hip_error(e, "decode_noalloc: scratch address");
   return pqkv::decode_attn_run(q, q_dtype, R, k_cache, v_cache, k_codebooks, v_codebooks, k_bits, v_bits,
                                k_head_bits, v_head_bits, qjl_signs, p_rot, m, B, Hq, Hkv, S, S_max, d, scale, out,
-                               out_dtype, ws, (size_t)PQKV_NOALLOC_SCRATCH_BYTES, true, stream);
+                               out_dtype, ws, (size_t)PQKV_NOALLOC_SCRATCH_BYTES, true, nullptr, stream);
 }

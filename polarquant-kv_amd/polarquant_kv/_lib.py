@@ -61,6 +61,8 @@ SIGNATURES = {
                                                  c_void_p, c_int, c_int, c_int, c_int, c_int, c_float,
                                                  c_void_p]),
     "polarquant_inverse_rotate_cuda_c": (None, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "turboquant_compress": (None, [c_int64] * 5 + [c_int] * 3),
+    "turboquant_full_attention": (None, [c_int64] * 12 + [c_int] * 5 + [c_float]),
 }
 
 _lib = None

@@ -54,31 +54,57 @@ def test_rotate_query_and_inverse_bit_exact():
     assert np.array_equal(z.cpu().numpy().view(np.uint32), OC.c_rotate_fma(yr, R, inverse=True).view(np.uint32))
 
 
-def test_fused_attention_soa_matches_oracle():
-    Hq, Hkv, S, d = 8, 2, 300, 128
-    rng = np.random.default_rng(4)
-    cb = O.lloyd_max_codebook(d, 4)[0]
-    k = rng.standard_normal((Hkv * S, d)).astype(np.float32)
-    v = rng.standard_normal((Hkv * S, d)).astype(np.float32)
+FUSED_CASES = [
+    # Hq, Hkv, S, d, n_levels, data
+    (8, 2, 300, 128, 16, "channel"),     # outlier channels: radii spread over decades
+    (32, 8, 1500, 128, 16, "channel"),   # 8B shape, several splits
+    (14, 2, 512, 64, 16, "normal"),      # config-1 shape
+    (32, 2, 200, 128, 8, "normal"),      # G = 16, the 3-bit ggml codebook
+    (4, 1, 77, 128, 16, "huge"),         # radii past the fp16 range stay exact
+]
+
+
+@pytest.mark.parametrize("case", FUSED_CASES, ids=lambda c: "Hq{}_Hkv{}_S{}_d{}_L{}_{}".format(*c))
+def test_fused_attention_soa_matches_oracle(case):
+    """polarquant_fused_attention_cuda_c attends with the caller's fp32 radii
+    (no fp16 rounding): checked against the SoA oracle fed the same
+    unrounded radii, on data whose radii fp16 would change."""
+    Hq, Hkv, S, d, n_levels, kind = case
+    print(f"compat fused attention {case}", flush=True)
+    rng = np.random.default_rng(Hq + S)
+    bits = {16: 4, 8: 3}[n_levels]
+    import json
+    from conftest import GOLDEN
+    cb = np.asarray(json.load(open(f"{GOLDEN}/ggml_codebooks.json"))["codebooks"][str(bits)], np.float32)
+    if kind == "huge":
+        k = (rng.standard_normal((Hkv * S, d)) * 8e3).astype(np.float32)
+        v = (rng.standard_normal((Hkv * S, d)) * 8e3).astype(np.float32)
+        q_scale = 1e-4
+    else:
+        src = O.synth_kv(1, Hkv, 2 * S, d, Hq + S, "channel" if kind == "channel" else "normal").astype(np.float32)
+        k = src[0, :, :S].reshape(-1, d)
+        v = src[0, :, S:].reshape(-1, d)
+        q_scale = 1.0
     kr, ki = OC.c_quantize_rotated(k, cb)
     vr, vi = OC.c_quantize_rotated(v, cb)
-    pk = (ki[:, 0::2] | (ki[:, 1::2] << 4)).astype(np.uint8)
-    pv = (vi[:, 0::2] | (vi[:, 1::2] << 4)).astype(np.uint8)
-    q_rot = rng.standard_normal((Hq, d)).astype(np.float32)
-    t = {n: torch.from_numpy(a).to(DEV) for n, a in dict(q=q_rot, pk=pk, kr=kr, pv=pv, vr=vr, cb=cb).items()}
-    out = torch.empty(Hq, d, device=DEV)
+    assert (kr.astype(np.float16).astype(np.float32) != kr).any()   # fp16 would round these radii
+    if kind == "huge":
+        assert kr.max() > 65504
+    pk, pv = O.pack_codes(ki, 4), O.pack_codes(vi, 4)
+    q_rot = (q_scale * rng.standard_normal((Hq, d))).astype(np.float32)
+    t = {n: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+         for n, a in dict(q=q_rot, pk=pk, kr=kr, pv=pv, vr=vr, cb=cb).items()}
+    out = torch.full((Hq, d), float("nan"), device=DEV)
     scale = 1 / math.sqrt(d)
     _lib.lib().polarquant_fused_attention_cuda_c(t["q"].data_ptr(), t["pk"].data_ptr(), t["kr"].data_ptr(),
                                                  t["pv"].data_ptr(), t["vr"].data_ptr(), t["cb"].data_ptr(),
-                                                 out.data_ptr(), Hq, Hkv, S, d, 16, ctypes.c_float(scale),
+                                                 out.data_ptr(), Hq, Hkv, S, d, n_levels, ctypes.c_float(scale),
                                                  _stream())
     torch.cuda.synchronize()
-    # oracle in the rotated space: identity rotation, fp16-rounded radii as stored in block_pq4
-    kb = O.pack_blocks(kr, ki, 4).reshape(1, Hkv, S, -1)
-    vb = O.pack_blocks(vr, vi, 4).reshape(1, Hkv, S, -1)
-    ref = O.decode_attention(q_rot[None].astype(np.float64), kb, vb, np.eye(d), cb, cb)[0]
-    got = out.cpu().numpy()
-    assert np.abs(got - ref).max() <= 2e-3
+    ref = O.decode_attention_soa(q_rot, pk, kr, pv, vr, cb, Hkv, scale)
+    got = out.cpu().numpy().astype(np.float64)
+    tol = 2e-3 * max(1.0, np.abs(ref).max() / 100)        # relative beyond |o| = 100
+    assert np.abs(got - ref).max() <= tol, np.abs(got - ref).max()
     assert (got * ref).sum() / np.linalg.norm(got) / np.linalg.norm(ref) >= 0.9999
 
 
@@ -98,14 +124,111 @@ def test_init_and_free():
 
     s = ctypes.cast(st, ctypes.POINTER(State)).contents
     assert (s.enabled, s.n_bits, s.n_levels, s.head_dim, s.n_layers) == (1, 4, 16, 128, 2)
-    cb = np.zeros(16, np.float32)
     R = np.zeros((128, 128), np.float32)
     torch.cuda.synchronize()
     import ctypes as C
     hip = C.CDLL("libamdhip64.so")
-    hip.hipMemcpy(C.c_void_p(cb.ctypes.data), C.c_void_p(s.codebook), C.c_size_t(64), 2)
     hip.hipMemcpy(C.c_void_p(R.ctypes.data), C.c_void_p(s.rotation), C.c_size_t(R.nbytes), 2)
-    assert np.array_equal(cb, O.lloyd_max_codebook(128, 4)[0])
     np.testing.assert_allclose(R @ R.T, np.eye(128), atol=1e-4)
     assert s.layers[1].v_radius
     L.polarquant_free_c(st)
+
+    # the codebook is the reference's table for the width (patch:600-613,
+    # 978-994); an unsupported width falls back to 4 bits
+    import json
+    from conftest import GOLDEN
+    books = json.load(open(f"{GOLDEN}/ggml_codebooks.json"))["codebooks"]
+    for n_bits, want_bits in ((4, 4), (3, 3), (2, 2), (5, 4)):
+        st = L.polarquant_init_c(64 if n_bits == 3 else 128, 2, 4, 1, 64, n_bits)
+        s = ctypes.cast(st, ctypes.POINTER(State)).contents
+        assert (s.n_bits, s.n_levels) == (want_bits, 1 << want_bits)
+        cb = np.zeros(s.n_levels, np.float32)
+        hip.hipMemcpy(C.c_void_p(cb.ctypes.data), C.c_void_p(s.codebook), C.c_size_t(cb.nbytes), 2)
+        assert np.array_equal(cb, np.asarray(books[str(want_bits)], np.float32))
+        L.polarquant_free_c(st)
+
+
+# ---- the raw-pointer binding (polarquant_turboquant, flash_turboquant.cu:180-230) ----
+
+@pytest.mark.parametrize("d", [128, 64])
+def test_turboquant_compress_bit_exact(d):
+    import polarquant_turboquant as tq
+    print(f"turboquant_compress d={d}", flush=True)
+    N = 1000
+    rng = np.random.default_rng(d)
+    x = (rng.standard_normal((N, d)) * rng.lognormal(0, 1, (N, 1))).astype(np.float32)
+    cb = O.lloyd_max_codebook(d, 4)[0]
+    R = O.rotation_matrix(d, 42).astype(np.float32)
+    xt, Rt, cbt = (torch.from_numpy(a).to(DEV) for a in (x, R, cb))
+    r = torch.zeros(N, device=DEV)
+    p = torch.zeros(N, d // 2, dtype=torch.uint8, device=DEV)
+    tq.turboquant_compress(xt.data_ptr(), Rt.data_ptr(), cbt.data_ptr(), r.data_ptr(), p.data_ptr(), N, d, 16)
+    torch.cuda.synchronize()
+    r_ref, idx = OC.c_quantize_rotated(OC.c_rotate_fma(x, R), cb)
+    assert np.array_equal(r.cpu().numpy().view(np.uint32), r_ref.view(np.uint32))
+    assert np.array_equal(p.cpu().numpy(), O.pack_codes(idx, 4))
+
+
+TQ_CASES = [
+    # Hq, Hkv, S, d, value codebook
+    (32, 32, 1024, 128, "same"),      # the reference benchmark's MHA layout (Hq == Hkv)
+    (32, 8, 300, 128, "copy"),        # GQA; equal values in a separate tensor
+    (14, 2, 40, 64, "scaled"),        # S so small the score buffer cannot hold the plan
+]
+
+
+@pytest.mark.parametrize("case", TQ_CASES, ids=lambda c: "Hq{}_Hkv{}_S{}_d{}_{}".format(*c))
+def test_turboquant_full_attention(case):
+    """The benchmark's flow (scripts/benchmark_turboquant.py:78-114): fp32
+    K/V compressed with turboquant_compress, q_rot = q R^T, attention into
+    attn_out (rotated), compared with the SoA oracle on the same bytes, then
+    rotated back and compared with attention on the original K/V."""
+    import polarquant_turboquant as tq
+    Hq, Hkv, S, d, vcb_kind = case
+    print(f"turboquant_full_attention {case}", flush=True)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(S + Hq)
+    K = torch.randn(Hkv, S, d, generator=g, device=DEV)
+    V = torch.randn(Hkv, S, d, generator=g, device=DEV)
+    Q = torch.randn(Hq, d, generator=g, device=DEV)
+    R64 = O.rotation_matrix(d, 42)
+    R = torch.from_numpy(R64.astype(np.float32)).to(DEV)
+    cb = O.lloyd_max_codebook(d, 4)[0]
+    k_cb = torch.from_numpy(cb).to(DEV)
+    v_cb_np = {"same": cb, "copy": cb.copy(), "scaled": (cb * np.float32(1.25)).astype(np.float32)}[vcb_kind]
+    v_cb = k_cb if vcb_kind == "same" else torch.from_numpy(v_cb_np).to(DEV)
+    N = Hkv * S
+    kr = torch.zeros(N, device=DEV)
+    pk = torch.zeros(N, d // 2, dtype=torch.uint8, device=DEV)
+    vr = torch.zeros(N, device=DEV)
+    pv = torch.zeros(N, d // 2, dtype=torch.uint8, device=DEV)
+    tq.turboquant_compress(K.reshape(-1, d).data_ptr(), R.data_ptr(), k_cb.data_ptr(), kr.data_ptr(), pk.data_ptr(),
+                           N, d, 16)
+    tq.turboquant_compress(V.reshape(-1, d).data_ptr(), R.data_ptr(), v_cb.data_ptr(), vr.data_ptr(), pv.data_ptr(),
+                           N, d, 16)
+    q_rot = (Q @ R.T).contiguous()
+    out = torch.full((Hq, d), float("nan"), device=DEV)
+    score = torch.full((Hq, S), float("nan"), device=DEV)
+    scale = 1 / math.sqrt(d)
+    tq.turboquant_full_attention(q_rot.data_ptr(), R.data_ptr(), pk.data_ptr(), kr.data_ptr(), pv.data_ptr(),
+                                 vr.data_ptr(), k_cb.data_ptr(), v_cb.data_ptr(), out.data_ptr(), q_rot.data_ptr(),
+                                 score.data_ptr(), out.data_ptr(), Hq, Hkv, S, d, 16, scale)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().astype(np.float64)
+    c = {n: t.cpu().numpy() for n, t in dict(q=q_rot, pk=pk, kr=kr, pv=pv, vr=vr).items()}
+    # the oracle with separate key and value codebooks: values through their own table
+    ref_k = O.decode_attention_soa(c["q"], c["pk"], c["kr"], c["pv"], c["vr"], cb, Hkv, scale)
+    if vcb_kind == "scaled":
+        ref = O.decode_attention_soa(c["q"], c["pk"], c["kr"], c["pv"], c["vr"] * np.float32(1.25), cb, Hkv, scale)
+        assert np.abs(ref - ref_k).max() > 0.05          # the value codebook matters
+    else:
+        ref = ref_k
+    assert np.abs(got - ref).max() <= 2e-3
+    # rotated back, against attention on the uncompressed K/V (the benchmark's check)
+    o = got @ R64
+    G = Hq // Hkv
+    Kn, Vn, Qn = (t.cpu().numpy().astype(np.float64) for t in (K, V, Q))
+    full = np.stack([O.sdpa(Qn[h][None], Kn[h // G], Vn[h // G])[0] for h in range(Hq)])
+    if vcb_kind != "scaled":
+        cos = (o * full).sum() / np.linalg.norm(o) / np.linalg.norm(full)
+        assert cos > 0.98, cos

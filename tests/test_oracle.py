@@ -410,3 +410,39 @@ def test_bit_pack_lsb_round_trip():
     assert p.shape == (3, 2)
     assert np.array_equal(O.bit_unpack_lsb(p, 13), s)
     assert O.bit_pack_lsb(np.array([True] + [False] * 7))[0] == 1     # bit 0 is the first sign
+
+
+def test_soa_attention_equals_block_attention_on_fp16_exact_radii():
+    """decode_attention_soa (fp32 radii as given) against the pinned block
+    decode with an identity rotation: radii that fp16 holds exactly give the
+    same scores, so the two agree to rounding; radii that fp16 rounds give a
+    measurable difference (the reason the SoA path keeps fp32 radii)."""
+    rng = np.random.default_rng(21)
+    Hq, Hkv, S, d = 6, 2, 50, 64
+    c = _codebook(d, 4)
+    idx_k = rng.integers(0, 16, (Hkv * S, d)).astype(np.uint8)
+    idx_v = rng.integers(0, 16, (Hkv * S, d)).astype(np.uint8)
+    rk = rng.lognormal(2, 1, Hkv * S).astype(np.float16).astype(np.float32)     # fp16-exact
+    rv = rng.lognormal(2, 1, Hkv * S).astype(np.float16).astype(np.float32)
+    q = rng.standard_normal((Hq, d))
+    pk, pv = O.pack_codes(idx_k, 4), O.pack_codes(idx_v, 4)
+    got = O.decode_attention_soa(q, pk, rk, pv, rv, c, Hkv, 1 / math.sqrt(d))
+    kb = O.pack_blocks(rk, idx_k, 4).reshape(1, Hkv, S, -1)
+    vb = O.pack_blocks(rv, idx_v, 4).reshape(1, Hkv, S, -1)
+    want = O.decode_attention(q[None], kb, vb, np.eye(d), c, c)[0]
+    np.testing.assert_allclose(got, want, atol=1e-10)
+    rk2 = rk * np.float32(1 + 2 ** -13)                       # not fp16 numbers any more
+    moved = O.decode_attention_soa(q, pk, rk2, pv, rv * np.float32(1 + 2 ** -13), c, Hkv, 1 / math.sqrt(d))
+    assert np.abs(moved - want).max() > 1e-6
+
+
+def test_ggml_codebook_fixture():
+    import json
+    import os
+    from conftest import GOLDEN
+    books = json.load(open(os.path.join(GOLDEN, "ggml_codebooks.json")))["codebooks"]
+    for bits, vals in books.items():
+        assert len(vals) == 1 << int(bits) and np.all(np.diff(vals) > 0)
+    # the reference's 4-bit table is not the Lloyd-Max table (asymmetric,
+    # narrower): ggml callers get codes of their own codebook
+    assert not np.allclose(books["4"], _codebook(128, 4), atol=1e-3)
