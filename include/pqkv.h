@@ -175,17 +175,33 @@ int pqkv_decode_attn_noalloc(const void *q, int q_dtype, const float *R,
  * against a cache that already holds them (append-then-attend,
  * src/polarquant_kv_cuda/inference/attention.py:59-61). With causal = 1
  * query i attends to cache positions <= q_start + i; with causal = 0 to all
- * S positions. q / out [B][Hq][Sq][d]. Uniform widths only. */
+ * S positions. q / out [B][Hq][Sq][d]. Widths, per-head tables and the QJL
+ * correction (applied to every query token, as the reference's
+ * attention_kernel.py:95-107 does) take the same arguments as
+ * pqkv_decode_attn. */
 size_t pqkv_prefill_workspace_bytes(int B, int Hq, int Hkv, int Sq, int S, int d);
 
 int pqkv_prefill_attn(const void *q, int q_dtype, const float *R,
                       const uint8_t *k_cache, const uint8_t *v_cache,
-                      const float *k_codebook, const float *v_codebook,
+                      const float *k_codebooks, const float *v_codebooks,
                       int k_bits, int v_bits,
+                      const int *k_head_bits, const int *v_head_bits,
+                      const uint8_t *qjl_signs, const float *p_rot, int m,
                       int B, int Hq, int Hkv, int Sq, int q_start, int S, int S_max,
                       int d, float scale, int causal,
                       void *out, int out_dtype,
                       void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- dequantise -----------------------------------------------------------
+ * out = (r16 c[code]) R for n block-encoded vectors: the stored radius times
+ * the centroids, rotated back to the original space, each output one fp32
+ * FMA chain over k ascending (as pqkv_rotate with inverse = 1). fp16 output
+ * saturates at +-65504. Replaces the decompression of decompress_gpu
+ * (src/polarquant_kv_cuda/decompress_kernel.py:10-55) for the codebook
+ * format. blocks [n][vector bytes], codebook [16] fp32 (zero-padded),
+ * R [d][d] fp32 16-byte aligned, out [n][d] fp32/fp16. */
+int pqkv_dequantize(const uint8_t *blocks, const float *codebook, int n_bits, const float *R,
+                    void *out, int out_dtype, int64_t n, int d, void *stream);
 
 /* ---- layout converters ---------------------------------------------------
  * SoA (the reference kernels' format: packed u8 [n][d/2] + fp32 radius [n],

@@ -417,13 +417,15 @@ def decode_attention_soa(q_rot: np.ndarray, k_packed: np.ndarray, k_radius: np.n
 
 def prefill_attention(q: np.ndarray, k_blocks: np.ndarray, v_blocks: np.ndarray,
                       R: np.ndarray, k_cb, v_cb, q_start: int, causal: bool = True,
-                      k_bits=4, v_bits=4, scale: float | None = None):
+                      k_bits=4, v_bits=4, scale: float | None = None, qjl_signs=None, P=None):
     """Chunked prefill against an encoded cache that already holds the chunk.
 
     q [B, Hq, Sq, d]; the cache [B, Hkv, S_total, bytes] holds positions
     0 .. q_start+Sq-1 (append-then-attend, inference/attention.py:59-61).
     Query i of the chunk (absolute position q_start+i) attends to positions
-    <= q_start+i when causal, to all S_total positions otherwise.
+    <= q_start+i when causal, to all S_total positions otherwise. The QJL
+    correction (qjl_signs [B, Hkv, S_total, m/8], P) applies to every query
+    token, as attention_kernel.py:95-107 does for Sq > 1.
     Computed as one decode_attention per query row.
     """
     q = np.asarray(q, np.float64)
@@ -434,7 +436,8 @@ def prefill_attention(q: np.ndarray, k_blocks: np.ndarray, v_blocks: np.ndarray,
         L = q_start + i + 1 if causal else S_total
         out[:, :, i] = decode_attention(q[:, :, i], k_blocks[:, :, :L], v_blocks[:, :, :L],
                                         R, k_cb, v_cb, k_bits=k_bits, v_bits=v_bits,
-                                        scale=scale)
+                                        scale=scale,
+                                        qjl_signs=None if qjl_signs is None else qjl_signs[:, :, :L], P=P)
     return out
 
 

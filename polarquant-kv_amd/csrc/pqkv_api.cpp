@@ -625,45 +625,70 @@ size_t pqkv_prefill_workspace_bytes(int B, int Hq, int Hkv, int Sq, int S, int d
   (void)Hkv;
   (void)S;
   if (B <= 0 || Hq <= 0 || Sq <= 0 || d <= 0) return 0;
-  // rotated queries and rotated outputs, fp32 [B][Hq][Sq][d] each
-  return 2 * align256((size_t)B * Hq * Sq * d * 4);
+  // rotated queries, rotated outputs and (QJL) the projections P_rot q_rot / m,
+  // fp32 [B][Hq][Sq][d] each
+  return 3 * align256((size_t)B * Hq * Sq * d * 4);
 }
 
 int pqkv_prefill_attn(const void *q, int q_dtype, const float *R, const uint8_t *k_cache, const uint8_t *v_cache,
-                      const float *k_codebook, const float *v_codebook, int k_bits, int v_bits, int B, int Hq,
-                      int Hkv, int Sq, int q_start, int S, int S_max, int d, float scale, int causal, void *out,
-                      int out_dtype, void *workspace, size_t workspace_bytes, void *stream) {
+                      const float *k_codebooks, const float *v_codebooks, int k_bits, int v_bits,
+                      const int *k_head_bits, const int *v_head_bits, const uint8_t *qjl_signs, const float *p_rot,
+                      int m, int B, int Hq, int Hkv, int Sq, int q_start, int S, int S_max, int d, float scale,
+                      int causal, void *out, int out_dtype, void *workspace, size_t workspace_bytes, void *stream) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || S < 0 || S_max < S || q_start < 0)
     return fail(PQKV_ERR_INVALID, "prefill: B=%d Hq=%d Hkv=%d Sq=%d S=%d S_max=%d q_start=%d", B, Hq, Hkv, Sq, S,
                 S_max, q_start);
   if (Hq % Hkv) return fail(PQKV_ERR_INVALID, "prefill: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
-  if (Hq / Hkv > pqkv::prefill_rows_per_block())
+  const bool qjl = qjl_signs != nullptr;
+  if (Hq / Hkv > pqkv::prefill_rows_per_block(qjl))
     return fail(PQKV_ERR_UNSUPPORTED, "prefill: group size %d", Hq / Hkv);
   if (causal && (int64_t)q_start + Sq > S)
     return fail(PQKV_ERR_INVALID, "prefill: causal queries at %d..%d are not all in the cache (S=%d)", q_start,
                 q_start + Sq - 1, S);
   if (!supported_d(d)) return fail(PQKV_ERR_UNSUPPORTED, "prefill: d=%d", d);
-  if (k_bits != 4 || v_bits != 4) return fail(PQKV_ERR_UNSUPPORTED, "prefill: widths k=%d v=%d (4-bit only)", k_bits, v_bits);
+  const bool mixed = k_head_bits != nullptr || v_head_bits != nullptr;
+  if (mixed && Hkv > pqkv::kMaxListHeads)
+    return fail(PQKV_ERR_UNSUPPORTED, "prefill: mixed widths support at most %d kv heads", pqkv::kMaxListHeads);
+  if (!supported_bits(k_bits) && !k_head_bits) return fail(PQKV_ERR_UNSUPPORTED, "prefill: k_bits=%d", k_bits);
+  if (!supported_bits(v_bits) && !v_head_bits) return fail(PQKV_ERR_UNSUPPORTED, "prefill: v_bits=%d", v_bits);
+  int kb[pqkv::kMaxListHeads], vb[pqkv::kMaxListHeads];
+  if (mixed)
+    for (int h = 0; h < Hkv; ++h) {
+      kb[h] = k_head_bits ? k_head_bits[h] : k_bits;
+      vb[h] = v_head_bits ? v_head_bits[h] : v_bits;
+      if (!supported_bits(kb[h]) || !supported_bits(vb[h]))
+        return fail(PQKV_ERR_UNSUPPORTED, "prefill: head %d widths k=%d v=%d", h, kb[h], vb[h]);
+    }
+  if ((qjl_signs == nullptr) != (p_rot == nullptr)) return fail(PQKV_ERR_INVALID, "prefill: qjl and p_rot go together");
+  if (qjl && m != d) return fail(PQKV_ERR_UNSUPPORTED, "prefill: QJL needs m == d");
   if (!float_dtype(q_dtype) || !float_dtype(out_dtype)) return fail(PQKV_ERR_UNSUPPORTED, "prefill: dtype");
   if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(PQKV_ERR_INVALID, "prefill: scale must be > 0");
   if (Sq == 0) return PQKV_OK;
   if (!q || !R || !out) return fail(PQKV_ERR_INVALID, "prefill: null pointer");
   if ((uintptr_t)R % 16) return fail(PQKV_ERR_INVALID, "prefill: R must be 16-byte aligned");
+  if ((uintptr_t)p_rot % 16) return fail(PQKV_ERR_INVALID, "prefill: p_rot must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   if (S == 0) {
     const size_t ob = (size_t)B * Hq * Sq * d * (out_dtype == PQKV_F32 ? 4 : 2);
     return hip_status(pqkv::launch_fill_zero(out, ob, st), "prefill zero fill");
   }
-  if (!k_cache || !v_cache || !k_codebook || !v_codebook) return fail(PQKV_ERR_INVALID, "prefill: null cache or codebook");
+  if (!k_cache || !v_cache || !k_codebooks || !v_codebooks)
+    return fail(PQKV_ERR_INVALID, "prefill: null cache or codebook");
   const size_t need = pqkv_prefill_workspace_bytes(B, Hq, Hkv, Sq, S, d);
   if (!workspace || workspace_bytes < need)
     return fail(PQKV_ERR_WORKSPACE, "prefill: workspace %zu < %zu bytes", workspace_bytes, need);
   const int64_t nvec = (int64_t)B * Hq * Sq;
+  const size_t arr = align256((size_t)nvec * d * 4);
   float *q32 = (float *)workspace;
-  float *o32 = (float *)((char *)workspace + align256((size_t)nvec * d * 4));
+  float *o32 = (float *)((char *)workspace + arr);
+  float *pq32 = (float *)((char *)workspace + 2 * arr);
   const float kLog2e = 1.4426950408889634f;
   int tok = pqkv::prof_begin("prefill_rotate", st);
-  hipError_t e = pqkv::launch_rotate(q, q_dtype, R, q32, PQKV_F32, nvec, d, 0, scale * kLog2e, st);
+  // the kernel's queries carry kPrefillPlaneScale; the projections do not
+  const float qs = scale * kLog2e * pqkv::kPrefillPlaneScale;
+  hipError_t e = qjl ? pqkv::launch_rotate2(q, q_dtype, R, p_rot, q32, pq32, nvec, d, qs,
+                                            1.0f / ((float)m * pqkv::kPrefillPlaneScale), st)
+                     : pqkv::launch_rotate(q, q_dtype, R, q32, PQKV_F32, nvec, d, 0, qs, st);
   pqkv::prof_end(tok, st);
   if (e != hipSuccess) return hip_status(e, "prefill query rotation");
   pqkv::PrefillArgs a;
@@ -671,10 +696,11 @@ int pqkv_prefill_attn(const void *q, int q_dtype, const float *R, const uint8_t 
   a.q = q32;
   a.k_cache = k_cache;
   a.v_cache = v_cache;
-  a.head_stride = (int64_t)S_max * pqkv_vector_bytes(d, 4);
-  a.batch_stride = a.head_stride * Hkv;
-  a.k_cb = k_codebook;
-  a.v_cb = v_codebook;
+  a.k_cb = k_codebooks;
+  a.v_cb = v_codebooks;
+  a.cb_head_stride = mixed ? 16 : 0;
+  a.qjl = qjl_signs;
+  a.pq = qjl ? pq32 : nullptr;
   a.o = o32;
   a.B = B;
   a.Hq = Hq;
@@ -686,15 +712,65 @@ int pqkv_prefill_attn(const void *q, int q_dtype, const float *R, const uint8_t 
   a.S_max = S_max;
   a.d = d;
   a.causal = causal ? 1 : 0;
-  a.qt = pqkv::prefill_rows_per_block() / a.G;
-  tok = pqkv::prof_begin("prefill_attn", st);
-  e = pqkv::launch_prefill(a, st);
-  pqkv::prof_end(tok, st);
-  if (e != hipSuccess) return hip_status(e, "prefill launch");
+  a.qt = pqkv::prefill_rows_per_block(qjl) / a.G;
+  if (!mixed) {
+    a.k_head_stride = (int64_t)S_max * pqkv_vector_bytes(d, k_bits);
+    a.v_head_stride = (int64_t)S_max * pqkv_vector_bytes(d, v_bits);
+    a.k_batch_stride = a.k_head_stride * Hkv;
+    a.v_batch_stride = a.v_head_stride * Hkv;
+    a.n_heads = Hkv;
+    tok = pqkv::prof_begin("prefill_attn", st);
+    e = pqkv::launch_prefill(a, k_bits, v_bits, st);
+    pqkv::prof_end(tok, st);
+    if (e != hipSuccess) return hip_status(e, "prefill launch");
+  } else {
+    // per-(b, h) runs of S_max vectors of the head's own width, (b, h) order;
+    // one launch per (key bits, value bits) group of heads
+    int64_t koff[pqkv::kMaxListHeads + 1], voff[pqkv::kMaxListHeads + 1];
+    koff[0] = voff[0] = 0;
+    for (int h = 0; h < Hkv; ++h) {
+      koff[h + 1] = koff[h] + (int64_t)S_max * pqkv_vector_bytes(d, kb[h]);
+      voff[h + 1] = voff[h] + (int64_t)S_max * pqkv_vector_bytes(d, vb[h]);
+    }
+    a.k_batch_stride = koff[Hkv];
+    a.v_batch_stride = voff[Hkv];
+    a.listed = 1;
+    for (int kbits : {4, 2})
+      for (int vbits : {4, 2}) {
+        int n = 0;
+        for (int h = 0; h < Hkv; ++h)
+          if (kb[h] == kbits && vb[h] == vbits) {
+            a.heads[n] = (int16_t)h;
+            a.k_head_off[n] = koff[h];
+            a.v_head_off[n] = voff[h];
+            ++n;
+          }
+        if (n == 0) continue;
+        a.n_heads = n;
+        tok = pqkv::prof_begin("prefill_attn", st);
+        e = pqkv::launch_prefill(a, kbits, vbits, st);
+        pqkv::prof_end(tok, st);
+        if (e != hipSuccess) return hip_status(e, "prefill launch");
+      }
+  }
   tok = pqkv::prof_begin("prefill_out_rotate", st);
   e = pqkv::launch_rotate(o32, PQKV_F32, R, out, out_dtype, nvec, d, 1, 1.0f, st);
   pqkv::prof_end(tok, st);
   return hip_status(e, "prefill output rotation");
+}
+
+int pqkv_dequantize(const uint8_t *blocks, const float *codebook, int n_bits, const float *R, void *out,
+                    int out_dtype, int64_t n, int d, void *stream) {
+  if (n < 0) return fail(PQKV_ERR_INVALID, "dequantize: n < 0");
+  if (!supported_d(d) || !supported_bits(n_bits)) return fail(PQKV_ERR_UNSUPPORTED, "dequantize: d=%d bits=%d", d, n_bits);
+  if (!float_dtype(out_dtype)) return fail(PQKV_ERR_UNSUPPORTED, "dequantize: dtype %d", out_dtype);
+  if (n == 0) return PQKV_OK;
+  if (!blocks || !codebook || !R || !out) return fail(PQKV_ERR_INVALID, "dequantize: null pointer");
+  if ((uintptr_t)R % 16) return fail(PQKV_ERR_INVALID, "dequantize: R must be 16-byte aligned");
+  const int tok = pqkv::prof_begin("dequantize", (hipStream_t)stream);
+  const hipError_t e = pqkv::launch_dequantize(blocks, codebook, n_bits, R, out, out_dtype, n, d, (hipStream_t)stream);
+  pqkv::prof_end(tok, (hipStream_t)stream);
+  return hip_status(e, "dequantize launch");
 }
 
 int pqkv_soa_to_blocks(const uint8_t *packed, const float *radius, uint8_t *blocks, int64_t n, int d,

@@ -154,8 +154,33 @@ __device__ __forceinline__ float load_as_float(const T *p) { return (float)*p; }
 constexpr int kRotVec = 8;   // vectors per workgroup iteration
 constexpr int kRotCols = 32; // output columns per workgroup
 
-template <int D, bool INVERSE, typename TIN, typename TOUT>
-__global__ void __launch_bounds__(256) rotate_kernel(const TIN *__restrict__ x, const float *__restrict__ R,
+// The vectors come from a source functor: element j of vector v.
+template <typename TIN, int D>
+struct PlainSource {
+  const TIN *x;
+  __device__ __forceinline__ float operator()(int64_t v, int j) const { return load_as_float(x + v * D + j); }
+};
+// Block-encoded vectors (block_pq4 / block_pq2): r16 * c[code], the rotated
+// reconstruction the attention kernels use.
+template <int D, int BITS>
+struct BlockSource {
+  const uint8_t *blocks;
+  const float *cb;
+  __device__ __forceinline__ float operator()(int64_t v, int j) const {
+    constexpr int VB = vector_bytes(D, BITS);
+    const uint8_t *vec = blocks + v * VB;
+    const float r = half_bits_to_float(*(const uint16_t *)vec);
+    const int per = 8 / BITS;                              // codes per byte
+    const uint8_t byte = vec[qs_offset(j / per, BITS)];
+    const int code = (byte >> (BITS * (j % per))) & ((1 << BITS) - 1);
+    return r * cb[code];
+  }
+};
+
+// SAT16: fp16 output saturates at +-65504 like the reference's decompress
+// (decompress_kernel.py:52-55, clamp(-65504, 65504).half()).
+template <int D, bool INVERSE, typename SRC, typename TOUT, bool SAT16 = false>
+__global__ void __launch_bounds__(256) rotate_kernel(const SRC src, const float *__restrict__ R,
                                                      TOUT *__restrict__ y, int64_t n, float out_scale) {
   constexpr int RP = D + 4;
   __shared__ __align__(16) float rs[kRotCols * RP];
@@ -172,7 +197,7 @@ __global__ void __launch_bounds__(256) rotate_kernel(const TIN *__restrict__ x, 
     for (int u = 0; u < XU; ++u) {
       const int i = tid + 256 * u;
       const int64_t v = bs + i / D;
-      xv[u] = v < n ? load_as_float(x + v * D + (i % D)) : 0.0f;
+      xv[u] = v < n ? src(v, i % D) : 0.0f;
     }
   };
   load_x((int64_t)blockIdx.x * kRotVec);
@@ -212,7 +237,11 @@ __global__ void __launch_bounds__(256) rotate_kernel(const TIN *__restrict__ x, 
       acc = __builtin_fmaf(a4.w, r4.w, acc);
     }
     const int64_t v = base + g;
-    if (v < n) y[v * D + c0 + jj] = (TOUT)(acc * out_scale);
+    if (v < n) {
+      float o = acc * out_scale;
+      if (SAT16) o = o > 65504.0f ? 65504.0f : (o < -65504.0f ? -65504.0f : o);
+      y[v * D + c0 + jj] = (TOUT)o;
+    }
     __syncthreads();
   }
 }
@@ -490,14 +519,34 @@ template <int D, bool INV>
 static void rotate_dispatch(const void *x, int xt, const float *R, void *y, int yt, int64_t n, float sc,
                             hipStream_t s) {
   const dim3 grid(grid_for(n, kRotVec, 2048), D / kRotCols);
+  using F = PlainSource<float, D>;
+  using H = PlainSource<half_t, D>;
   if (xt == 0 && yt == 0)
-    rotate_kernel<D, INV, float, float><<<grid, 256, 0, s>>>((const float *)x, R, (float *)y, n, sc);
+    rotate_kernel<D, INV, F, float><<<grid, 256, 0, s>>>(F{(const float *)x}, R, (float *)y, n, sc);
   else if (xt == 0 && yt == 1)
-    rotate_kernel<D, INV, float, half_t><<<grid, 256, 0, s>>>((const float *)x, R, (half_t *)y, n, sc);
+    rotate_kernel<D, INV, F, half_t><<<grid, 256, 0, s>>>(F{(const float *)x}, R, (half_t *)y, n, sc);
   else if (xt == 1 && yt == 0)
-    rotate_kernel<D, INV, half_t, float><<<grid, 256, 0, s>>>((const half_t *)x, R, (float *)y, n, sc);
+    rotate_kernel<D, INV, H, float><<<grid, 256, 0, s>>>(H{(const half_t *)x}, R, (float *)y, n, sc);
   else
-    rotate_kernel<D, INV, half_t, half_t><<<grid, 256, 0, s>>>((const half_t *)x, R, (half_t *)y, n, sc);
+    rotate_kernel<D, INV, H, half_t><<<grid, 256, 0, s>>>(H{(const half_t *)x}, R, (half_t *)y, n, sc);
+}
+
+template <int D, int BITS>
+static void dequant_dispatch(const uint8_t *blocks, const float *cb, const float *R, void *y, int yt, int64_t n,
+                             hipStream_t s) {
+  const dim3 grid(grid_for(n, kRotVec, 4096), D / kRotCols);
+  using S = BlockSource<D, BITS>;
+  if (yt == 0) rotate_kernel<D, true, S, float><<<grid, 256, 0, s>>>(S{blocks, cb}, R, (float *)y, n, 1.0f);
+  else rotate_kernel<D, true, S, half_t, true><<<grid, 256, 0, s>>>(S{blocks, cb}, R, (half_t *)y, n, 1.0f);
+}
+
+hipError_t launch_dequantize(const uint8_t *blocks, const float *codebook, int bits, const float *R, void *y,
+                             int y_dtype, int64_t n, int d, hipStream_t s) {
+  if (d == 128 && bits == 4) dequant_dispatch<128, 4>(blocks, codebook, R, y, y_dtype, n, s);
+  else if (d == 128) dequant_dispatch<128, 2>(blocks, codebook, R, y, y_dtype, n, s);
+  else if (bits == 4) dequant_dispatch<64, 4>(blocks, codebook, R, y, y_dtype, n, s);
+  else dequant_dispatch<64, 2>(blocks, codebook, R, y, y_dtype, n, s);
+  return hipGetLastError();
 }
 
 hipError_t launch_rotate(const void *x, int x_dtype, const float *R, void *y, int y_dtype, int64_t n, int d,

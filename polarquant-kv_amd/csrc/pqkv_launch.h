@@ -17,6 +17,9 @@ constexpr int kMaxSplits = 1024;   // split-K partitions per (batch, kv head)
 constexpr int kMergeHeads = 4;     // query heads per merge workgroup
 constexpr int kMfmaBlocksPerCU = 2;  // decode_mfma_kernel workgroups resident per CU
 constexpr int kMaxGroup = 8;         // query heads per kv head in one decode launch
+// The prefill kernel's rotated queries and codebook planes carry this factor
+// (fp16 hi / lo parts stay normal numbers); it divides out exactly.
+constexpr float kPrefillPlaneScale = 64.0f;
 
 struct EncodeArgs {
   const void *x;
@@ -59,16 +62,25 @@ struct DecodeArgs {
   int64_t k_head_off[kMaxListHeads], v_head_off[kMaxListHeads];
 };
 
-// One launch of the chunked-prefill kernel: workgroups of 256 query rows
-// (qt tokens x G heads) of one (batch, kv-head); 4-bit K and V.
+// One launch of the chunked-prefill kernel: workgroups of prefill_rows(qjl)
+// query rows (qt tokens x G heads) of one (batch, kv-head) with the same key
+// and value widths; with listed = 1 the kv heads and their byte offsets
+// come from the tables below (mixed widths), as in DecodeArgs.
 struct PrefillArgs {
-  const float *q;                // [B][Hq][Sq][d] fp32, rotated, times scale*log2(e)
+  const float *q;                // [B][Hq][Sq][d] fp32, rotated, times scale*log2(e)*kPrefillPlaneScale
   const uint8_t *k_cache, *v_cache;
-  int64_t batch_stride, head_stride;        // bytes (both caches: block_pq4, S_max vectors)
-  const float *k_cb, *v_cb;      // [16]
+  int64_t k_batch_stride, v_batch_stride;   // bytes between batches
+  int64_t k_head_stride, v_head_stride;     // bytes between heads (listed = 0)
+  const float *k_cb, *v_cb;      // [16], or per-head [Hkv][16] with cb_head_stride 16
+  int cb_head_stride;
+  const uint8_t *qjl;            // [B][Hkv][S_max][d/8] or null
+  const float *pq;               // [B][Hq][Sq][d] = P_rot q_rot / m (QJL only)
   float *o;                      // [B][Hq][Sq][d] fp32, rotated, normalised
   int B, Hq, Hkv, G, Sq, q_start, S, S_max, d, causal;
   int qt;                        // query tokens per workgroup (rows / G)
+  int n_heads, listed;
+  int16_t heads[kMaxListHeads];
+  int64_t k_head_off[kMaxListHeads], v_head_off[kMaxListHeads];
 };
 
 // Workspace of one decode call whose plan has `splits` partitions per stream
@@ -111,6 +123,10 @@ hipError_t launch_rotate2(const void *x, int x_dtype, const float *R, const floa
 // R == nullptr: y = x * out_scale (an identity rotation, exactly).
 hipError_t launch_rotate(const void *x, int x_dtype, const float *R, void *y, int y_dtype, int64_t n, int d,
                          int inverse, float out_scale, hipStream_t s);
+// y = (r16 c[code]) R for n block-encoded vectors (inverse rotation, one
+// FMA chain per output as in launch_rotate); fp16 output saturates.
+hipError_t launch_dequantize(const uint8_t *blocks, const float *codebook, int bits, const float *R, void *y,
+                             int y_dtype, int64_t n, int d, hipStream_t s);
 hipError_t launch_encode_exact(const EncodeArgs &a, int x_dtype, hipStream_t s);
 // Matrix-core encoder for fp16 input without QJL; rot_out and radius_out
 // (nullable) receive the fp32 rotated vectors the quantiser saw, [n][d], and
@@ -139,7 +155,9 @@ hipError_t launch_decode_mfma_soa(const DecodeArgs &a, hipStream_t s);
 hipError_t launch_decode_merge(const float *part, const float *R, void *out, int out_dtype, int BHq, int splits,
                                int d, hipStream_t s);
 hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t s);
-hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s);
-int prefill_rows_per_block();
+hipError_t launch_prefill(const PrefillArgs &a, int k_bits, int v_bits, hipStream_t s);
+// Query rows per prefill workgroup (the QJL kernel holds 16 rows per wave
+// instead of 32, to make room for the projection operands).
+int prefill_rows_per_block(bool qjl);
 
 }  // namespace pqkv

@@ -45,8 +45,10 @@ SIGNATURES = {
                                          c_void_p, c_int, c_void_p]),
     "pqkv_prefill_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "pqkv_prefill_attn": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-                                  c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                  c_int, c_int, c_int_p, c_int_p, c_void_p, c_void_p, c_int,
+                                  c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                                   c_int, c_float, c_int, c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
+    "pqkv_dequantize": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_int64, c_int, c_void_p]),
     "pqkv_soa_to_blocks": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p]),
     "pqkv_blocks_to_soa": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p]),
     "pqkv_profile_enable": (c_int, [c_int]),

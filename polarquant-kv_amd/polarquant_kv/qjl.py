@@ -52,3 +52,56 @@ def bit_unpack(packed, m: int):
     w = torch.tensor([1, 2, 4, 8, 16, 32, 64, 128], dtype=torch.uint8, device=packed.device)
     bits = (packed.unsqueeze(-1) & w) > 0
     return bits.reshape(*packed.shape[:-1], -1)[..., :m]
+
+
+def compute_signatures(residual, jl_matrix):
+    """Signs of P e for one residual e [d] (python/polarquant_kv/qjl.py:25-35),
+    in float64 on the host like the reference's CPU API: QJLSignatures with
+    signs = (P e >= 0) and the residual norm."""
+    from .types import QJLSignatures
+    P = np.asarray(jl_matrix, np.float64)
+    e = np.asarray(residual, np.float64)
+    return QJLSignatures(signs=(P @ e) >= 0, jl_dim=P.shape[0], residual_norm=float(np.linalg.norm(e)))
+
+
+def compute_correction(query, signatures, jl_matrix) -> float:
+    """(1/m) sum_i (2 s_i - 1) (P q)_i, 0 for a zero residual
+    (python/polarquant_kv/qjl.py:38-57). Host float64, as the reference."""
+    if signatures.residual_norm < 1e-30:
+        return 0.0
+    P = np.asarray(jl_matrix, np.float64)
+    sv = 2.0 * np.asarray(signatures.signs, np.float64) - 1.0
+    return float(np.dot(sv, P @ np.asarray(query, np.float64)) / signatures.jl_dim)
+
+
+def compute_signatures_gpu(residual, jl_matrix):
+    """Device version (src/polarquant_kv_cuda/qjl_kernel.py:6-37): residual
+    [..., d] fp32 on the GPU, jl_matrix [m, d] with m == d -> (packed signs
+    [..., m/8] uint8 LSB-first, residual norms [...] fp16). The projections
+    run on the HIP rotate kernel (P e as one FMA chain per row)."""
+    import torch
+
+    from .rotation import rotate
+    P = jl_matrix if isinstance(jl_matrix, torch.Tensor) else torch.from_numpy(np.asarray(jl_matrix, np.float32))
+    P = P.to(device=residual.device, dtype=torch.float32)
+    if P.shape[0] != P.shape[1] or P.shape[1] != residual.shape[-1]:
+        raise ValueError("the device sketch takes a square JL matrix (m == d)")
+    e = residual.to(torch.float32).contiguous()
+    proj = rotate(e, P)                          # e P^T = (P e) per vector
+    return bit_pack(proj >= 0), torch.linalg.vector_norm(e, dim=-1).half()
+
+
+def compute_correction_gpu(query, packed_signs, residual_norms, jl_matrix):
+    """Device version of the correction (src/polarquant_kv_cuda/qjl_kernel.py:40-70):
+    query [..., d] against packed signs [..., m/8] of the same leading shape
+    -> [...] = (1/m) sum_i (2 s_i - 1) (P q)_i. residual_norms is accepted for
+    the reference's signature and, as there, not used."""
+    import torch
+
+    from .rotation import rotate
+    P = jl_matrix if isinstance(jl_matrix, torch.Tensor) else torch.from_numpy(np.asarray(jl_matrix, np.float32))
+    P = P.to(device=query.device, dtype=torch.float32)
+    m = P.shape[0]
+    s = bit_unpack(packed_signs, m).to(torch.float32) * 2.0 - 1.0
+    qp = rotate(query.to(torch.float32).contiguous(), P)
+    return (s * qp).sum(-1) / m

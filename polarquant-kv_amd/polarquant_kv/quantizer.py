@@ -1,11 +1,13 @@
-"""PQ4 / PQ2 encoder entry points (device tensors only).
+"""PQ4 / PQ2 encoder and decoder entry points (device tensors only).
 
 compress_pq is the codebook counterpart of the reference's compress_gpu
 (src/polarquant_kv_cuda/compress_kernel.py:100-189) and of
 turboquant_compress (csrc/flash_turboquant.cu:213-225): rotate, polar split,
 nearest Lloyd-Max centroid per coordinate, pack into blocks, plus the optional
-QJL key sketch. quantize_rotated is the bit-exact surface on fp32 rotated
-input. Both call libpqkv_hip.so; there is no CPU path.
+QJL key sketch. compress_gpu / decompress_gpu keep the reference's names and
+arguments for that format; dequantize is the general decoder. quantize_rotated
+is the bit-exact surface on fp32 rotated input. All call libpqkv_hip.so;
+there is no CPU path.
 """
 
 from __future__ import annotations
@@ -114,3 +116,87 @@ def compress_pq(kv: torch.Tensor, rotation_matrix: torch.Tensor, n_bits=4, cache
                                        _lib.ptr(P), d if P is not None else 0, qjl_ptr, qjl_stride, stream))
     cache.seq_len = max(cache.seq_len, start + T)
     return cache
+
+
+def _validate_params(n_bits: int, group_size: int, d: int) -> None:
+    """The reference's argument checks (python/polarquant_kv/quantizer.py:15-22,
+    src/polarquant_kv_cuda/compress_kernel.py:13-20), same messages' meaning."""
+    if not (2 <= n_bits <= 8):
+        raise ValueError(f"n_bits must be in [2, 8], got {n_bits}")
+    if group_size <= 0:
+        raise ValueError(f"group_size must be positive, got {group_size}")
+    if group_size > d:
+        raise ValueError(f"group_size ({group_size}) cannot exceed the vector dimension d ({d})")
+
+
+def compress_gpu(kv: torch.Tensor, rotation_matrix: torch.Tensor, n_bits: int = 4, group_size: int = 32,
+                 jl_matrix=None) -> PQCache:
+    """The reference's compress_gpu entry point
+    (src/polarquant_kv_cuda/compress_kernel.py:100-189) for the codebook
+    (PQ4 / PQ2) format: kv [B, H, S, d] -> a PQCache of exactly S positions.
+    The codebook format's block is 32 coordinates; group_size is checked like
+    the reference's and otherwise has no effect. jl_matrix (P, [d, d]) adds
+    the QJL signs of each vector's residual (compress_kernel.py:166-175).
+    Empty input gives an empty cache with the input's shape."""
+    if kv.dim() != 4:
+        raise ValueError("kv must be [batch, heads, seq, head_dim]")
+    B, H, S, d = kv.shape
+    _validate_params(n_bits, group_size, max(d, 1))
+    if n_bits not in (2, 4):
+        raise ValueError(f"the codebook format stores 2- or 4-bit codes, got n_bits={n_bits}")
+    jl_rot = None
+    if jl_matrix is not None:
+        from .qjl import rotated_jl_matrix
+        jl_rot = rotated_jl_matrix(jl_matrix, rotation_matrix, kv.device)
+    if kv.numel() == 0:
+        return allocate_cache(B, H, S, d, n_bits, kv.device, jl_dim=d if jl_rot is not None else 0)
+    return compress_pq(kv, rotation_matrix, n_bits, jl_rot=jl_rot)
+
+
+def dequantize(cache: PQCache, rotation_matrix: torch.Tensor | None, out_dtype=torch.float16,
+               positions: int | None = None) -> torch.Tensor:
+    """Reconstruction r16 c[code] of the first `positions` (default seq_len)
+    positions of every (batch, head), rotated back with R (pqkv_dequantize):
+    [B, H, positions, d] of out_dtype. rotation_matrix None leaves the
+    rotated-space reconstruction (R = I, exact)."""
+    S = cache.seq_len if positions is None else int(positions)
+    B, H, d = cache.batch, cache.num_heads, cache.head_dim
+    dev = cache.blocks.device
+    R = (torch.eye(d, device=dev) if rotation_matrix is None else rotation_matrix).to(torch.float32).contiguous()
+    _lib.require_device(cache.blocks, R)
+    out = torch.empty(B, H, S, d, dtype=out_dtype, device=dev)
+    if S == 0:
+        return out
+    lib = _lib.lib()
+    stream = _lib.stream_of(out)
+    for b in range(B):
+        for h, bits in enumerate(cache.head_bits()):
+            vb = vector_bytes(d, bits)
+            if cache.mixed:
+                src = cache.blocks[b].data_ptr() + cache.head_offset(h)
+                cb = cache.codebooks[h] if cache.codebooks.dim() == 2 else cache.codebooks
+            else:
+                if h > 0:
+                    continue
+                # uniform widths: every head of the batch row in one call when
+                # the rows are contiguous (S == max_seq_len), else per head
+                cb = cache.codebooks
+                if S == cache.max_seq_len:
+                    _lib.check(lib.pqkv_dequantize(cache.blocks[b].data_ptr(), cb.data_ptr(), bits, R.data_ptr(),
+                                                   out[b].data_ptr(), _lib.dtype_code(out_dtype), H * S, d, stream))
+                    continue
+                for hh in range(H):
+                    _lib.check(lib.pqkv_dequantize(cache.blocks[b, hh].data_ptr(), cb.data_ptr(), bits,
+                                                   R.data_ptr(), out[b, hh].data_ptr(), _lib.dtype_code(out_dtype),
+                                                   S, d, stream))
+                continue
+            _lib.check(lib.pqkv_dequantize(src, cb.data_ptr(), bits, R.data_ptr(), out[b, h].data_ptr(),
+                                           _lib.dtype_code(out_dtype), S, d, stream))
+    return out
+
+
+def decompress_gpu(cache: PQCache, rotation_matrix: torch.Tensor) -> torch.Tensor:
+    """The reference's decompress_gpu (src/polarquant_kv_cuda/decompress_kernel.py:10-55)
+    for the codebook format: fp16 [B, H, seq_len, d] in the original space,
+    saturated at +-65504; an empty cache gives an empty tensor."""
+    return dequantize(cache, rotation_matrix, torch.float16)

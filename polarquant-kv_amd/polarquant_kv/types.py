@@ -70,3 +70,13 @@ class PQCache:
         if self.qjl_signs is not None:
             n += self.qjl_signs.numel()
         return n
+
+
+@dataclass
+class QJLSignatures:
+    """Sign sketch of one residual (python/polarquant_kv/types.py:19-25):
+    signs [jl_dim] bool, the sketch size, and the residual's norm, which the
+    correction uses only to return 0 for a zero residual."""
+    signs: "object"
+    jl_dim: int
+    residual_norm: float = 0.0

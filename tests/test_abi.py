@@ -114,12 +114,14 @@ def test_decode_validation():
 
 
 def _prefill(**kw):
-    a = dict(q=FAKE, qt=1, R=FAKE, k=FAKE, v=FAKE, kcb=FAKE, vcb=FAKE, kb=4, vb=4, B=1, Hq=8, Hkv=2, Sq=16,
-             q0=48, S=64, S_max=64, d=128, scale=0.088, causal=1, out=FAKE, ot=1, ws=FAKE, wsb=1 << 24)
+    a = dict(q=FAKE, qt=1, R=FAKE, k=FAKE, v=FAKE, kcb=FAKE, vcb=FAKE, kb=4, vb=4, khb=None, vhb=None, qjl=None,
+             p=None, m=0, B=1, Hq=8, Hkv=2, Sq=16, q0=48, S=64, S_max=64, d=128, scale=0.088, causal=1, out=FAKE,
+             ot=1, ws=FAKE, wsb=1 << 24)
     a.update(kw)
     return _lib.lib().pqkv_prefill_attn(a["q"], a["qt"], a["R"], a["k"], a["v"], a["kcb"], a["vcb"], a["kb"],
-                                        a["vb"], a["B"], a["Hq"], a["Hkv"], a["Sq"], a["q0"], a["S"], a["S_max"],
-                                        a["d"], a["scale"], a["causal"], a["out"], a["ot"], a["ws"], a["wsb"], None)
+                                        a["vb"], a["khb"], a["vhb"], a["qjl"], a["p"], a["m"], a["B"], a["Hq"],
+                                        a["Hkv"], a["Sq"], a["q0"], a["S"], a["S_max"], a["d"], a["scale"],
+                                        a["causal"], a["out"], a["ot"], a["ws"], a["wsb"], None)
 
 
 def test_prefill_validation():
@@ -128,12 +130,16 @@ def test_prefill_validation():
     _status(_prefill(q0=-1), _lib.ERR_INVALID)
     _status(_prefill(S=80), _lib.ERR_INVALID)                  # S > S_max
     _status(_prefill(d=96), _lib.ERR_UNSUPPORTED)
-    _status(_prefill(kb=2), _lib.ERR_UNSUPPORTED)              # 4-bit caches only
+    _status(_prefill(kb=3), _lib.ERR_UNSUPPORTED)              # 2- and 4-bit codes
+    _status(_prefill(qjl=FAKE), _lib.ERR_INVALID)              # signs without projection
+    _status(_prefill(qjl=FAKE, p=FAKE, m=64), _lib.ERR_UNSUPPORTED)
+    _status(_prefill(khb=_lib.int_array([4, 3])), _lib.ERR_UNSUPPORTED)
+    _status(_prefill(kb=2, vb=2, khb=_lib.int_array([4, 2]), wsb=16), _lib.ERR_WORKSPACE)
     _status(_prefill(scale=-1.0), _lib.ERR_INVALID)
     _status(_prefill(R=FAKE + 4), _lib.ERR_INVALID)            # R alignment
     _status(_prefill(wsb=1024), _lib.ERR_WORKSPACE)
     need = _lib.lib().pqkv_prefill_workspace_bytes(1, 64, 8, 2048, 133120, 128)
-    assert need == 2 * 64 * 2048 * 128 * 4
+    assert need == 3 * 64 * 2048 * 128 * 4
     assert _prefill(Sq=0) == 0                                 # nothing to do
 
 

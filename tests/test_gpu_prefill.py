@@ -127,3 +127,139 @@ def test_prefill_config5_rows_at_full_size():
         L = S_cache + i + 1
         ref = O.decode_attention(qn[:, :, i], kb[:, :, :L], vb[:, :, :L], R, cb, cb)
         _check(out[:, 8 * h:8 * h + 8, i].cpu().numpy(), ref)
+
+
+# ---- widths, per-head width maps and the QJL correction ----
+
+def _case_w(B, Hq, Hkv, Sq, q_start, S, d, kbits, vbits, seed, kind="normal", qjl=False):
+    k = O.synth_kv(B, Hkv, S, d, seed + 1, kind)
+    v = O.synth_kv(B, Hkv, S, d, seed + 2, kind)
+    q = np.random.default_rng(seed).standard_normal((B, Hq, Sq, d)).astype(np.float16)
+    R = O.rotation_matrix(d, 42)
+    Rt = torch.from_numpy(R.astype(np.float32)).to(DEV)
+    P = O.jl_matrix(d, d, 43) if qjl else None
+    P_rot = torch.from_numpy((P @ R.T).astype(np.float32)).to(DEV) if qjl else None
+    kc = quantizer.allocate_cache(B, Hkv, S, d, kbits, DEV, jl_dim=d if qjl else 0)
+    vc = quantizer.allocate_cache(B, Hkv, S, d, vbits, DEV)
+    quantizer.compress_pq(torch.from_numpy(k).to(DEV), Rt, cache=kc, jl_rot=P_rot)
+    quantizer.compress_pq(torch.from_numpy(v).to(DEV), Rt, cache=vc)
+    return q, R, Rt, kc, vc, P, P_rot
+
+
+def _host_blocks(cache, S):
+    b = cache.blocks.cpu().numpy()
+    if not cache.mixed:
+        return b[:, :, :S]
+    return [b[:, cache.head_offset(h):cache.head_offset(h) + S * O.vector_bytes(cache.head_dim, bits)]
+            .reshape(b.shape[0], S, -1) for h, bits in enumerate(cache.head_bits())]
+
+
+def _oracle_w(q, R, kc, vc, S, q_start, causal, P=None):
+    d = kc.head_dim
+    signs = kc.qjl_signs.cpu().numpy()[:, :, :S] if P is not None else None
+    kb, vb = _host_blocks(kc, S), _host_blocks(vc, S)
+    cbk = [O.lloyd_max_codebook(d, b)[0] for b in kc.head_bits()]
+    cbv = [O.lloyd_max_codebook(d, b)[0] for b in vc.head_bits()]
+    B, Hq = q.shape[:2]
+    Hkv = kc.num_heads
+    g = Hq // Hkv
+    out = np.zeros(q.shape)
+    for h in range(Hkv):
+        kh = kb[h] if kc.mixed else kb[:, h]
+        vh = vb[h] if vc.mixed else vb[:, h]
+        out[:, h * g:(h + 1) * g] = O.prefill_attention(
+            q[:, h * g:(h + 1) * g].astype(np.float64), kh[:, None], vh[:, None], R, cbk[h], cbv[h],
+            q_start=q_start, causal=causal, k_bits=kc.head_bits()[h], v_bits=vc.head_bits()[h],
+            qjl_signs=None if signs is None else signs[:, h:h + 1], P=P)
+    return out
+
+
+WIDTH_CASES = [
+    # B, Hq, Hkv, Sq, q_start, S, d, key bits, value bits, causal, qjl
+    (1, 8, 2, 40, 100, 140, 128, 2, 2, True, False),
+    (1, 16, 2, 70, 0, 200, 128, 4, 2, False, False),
+    (2, 6, 3, 33, 67, 100, 64, 2, 4, True, False),
+    (1, 8, 2, 48, 80, 128, 128, 4, 4, True, True),       # QJL, 4-bit
+    (1, 32, 4, 20, 180, 200, 128, 2, 2, True, True),     # QJL, 2-bit, G = 8 (16 tokens per workgroup)
+    (1, 4, 4, 130, 0, 300, 64, 4, 2, False, True),       # QJL, G = 1, d = 64, non-causal
+    (1, 8, 2, 16, 48, 64, 128, (4, 2), (2, 4), True, False),               # per-head widths
+    (2, 16, 4, 24, 40, 64, 128, (4, 4, 2, 2), (4, 2, 4, 2), True, True),   # four groups, QJL
+]
+
+
+@pytest.mark.parametrize("case", WIDTH_CASES, ids=lambda c: "B{}_Hq{}_Hkv{}_Sq{}_q{}_S{}_d{}_k{}_v{}_{}_{}".format(
+    *c[:7], "".join(map(str, np.atleast_1d(c[7]))), "".join(map(str, np.atleast_1d(c[8]))),
+    "c" if c[9] else "nc", "qjl" if c[10] else "plain"))
+def test_prefill_widths_and_qjl(case):
+    B, Hq, Hkv, Sq, q0, S, d, kb, vb, causal, qjl = case
+    print(f"prefill widths/qjl case {case}", flush=True)
+    q, R, Rt, kc, vc, P, P_rot = _case_w(B, Hq, Hkv, Sq, q0, S, d, kb, vb, seed=Sq + S, kind="channel", qjl=qjl)
+    out = attention.prefill_attention(torch.from_numpy(q).to(DEV), kc, vc, Rt, q_start=q0, causal=causal,
+                                      out_dtype=torch.float32, jl_rot=P_rot)
+    ref = _oracle_w(q, R, kc, vc, S, q0, causal, P=P)
+    _check(out.cpu().numpy(), ref)
+    if qjl:
+        moved = np.abs(_oracle_w(q, R, kc, vc, S, q0, causal) - ref).max()
+        print(f"qjl correction moves the output by {moved:.3e}", flush=True)
+        assert moved > 2 * MAX_ABS
+
+
+def test_compressed_attention_gpu_multi_token_with_qjl():
+    """The reference applies the QJL term for every query token
+    (attention_kernel.py:95-107); compressed_attention_gpu now does too."""
+    B, Hq, Hkv, Sq, S, d = 1, 8, 2, 12, 90, 128
+    q, R, Rt, kc, vc, P, P_rot = _case_w(B, Hq, Hkv, Sq, S - Sq, S, d, 4, 4, seed=7, qjl=True)
+    out = attention.compressed_attention_gpu(torch.from_numpy(q).to(DEV), kc, vc, Rt, jl_matrix=P, causal=True)
+    _check(out.float().cpu().numpy(), _oracle_w(q, R, kc, vc, S, S - Sq, True, P=P))
+
+
+def test_array_api_compressed_and_standard_attention():
+    """polarquant_kv.attention.compressed_attention / standard_attention on
+    numpy arrays (the reference's CPU API names), 2-D and 3-D GQA shapes, with
+    and without QJL; checked against the oracle on the bytes the GPU encoder
+    wrote and, loosely, against uncompressed attention."""
+    rng = np.random.default_rng(0)
+    d, S = 64, 200
+    R = O.rotation_matrix(d, 42)
+    P = O.jl_matrix(d, d, 43)
+    k2 = rng.standard_normal((S, d)).astype(np.float32)
+    v2 = rng.standard_normal((S, d)).astype(np.float32)
+    q2 = rng.standard_normal((5, d)).astype(np.float32)
+    std = attention.standard_attention(q2, k2, v2)
+    np.testing.assert_allclose(std, O.sdpa(q2, k2, v2), atol=1e-5)
+    for jl in (None, P):
+        res = attention.compressed_attention(q2, k2, v2, R, jl_matrix=jl, return_scores=True)
+        out, scores = res["output"], res["scores"]
+        assert out.dtype == np.float32 and out.shape == (5, d) and scores.shape == (5, S)
+        # the oracle on the same encoded bytes
+        Rt = torch.from_numpy(R.astype(np.float32)).to(DEV)
+        P_rot = None if jl is None else torch.from_numpy((jl @ R.T).astype(np.float32)).to(DEV)
+        kc = quantizer.compress_pq(torch.from_numpy(k2)[None, None].to(DEV), Rt, 4, jl_rot=P_rot)
+        vc = quantizer.compress_pq(torch.from_numpy(v2)[None, None].to(DEV), Rt, 4)
+        cb = O.lloyd_max_codebook(d, 4)[0]
+        signs = None if jl is None else kc.qjl_signs.cpu().numpy()
+        ref = O.prefill_attention(q2[None, None].astype(np.float64), kc.blocks.cpu().numpy(),
+                                  vc.blocks.cpu().numpy(), R, cb, cb, q_start=0, causal=False,
+                                  qjl_signs=signs, P=jl)[0, 0]
+        _check(out, ref)
+        # scores: softmax of them with the dequantised values gives the output
+        w = np.exp(scores - scores.max(-1, keepdims=True))
+        w /= w.sum(-1, keepdims=True)
+        V = O.inverse_rotate(O.dequantize_rotated(vc.blocks.cpu().numpy()[0, 0], d, cb), R)
+        np.testing.assert_allclose(w @ V, ref, atol=2e-4)
+        cos = (out * std).sum() / np.linalg.norm(out) / np.linalg.norm(std)
+        assert cos > 0.95
+    # 3-D GQA, one query token per head (decode path) and several (prefill path)
+    k3 = rng.standard_normal((2, S, d)).astype(np.float32)
+    v3 = rng.standard_normal((2, S, d)).astype(np.float32)
+    for sq in (1, 7):
+        q3 = rng.standard_normal((8, sq, d)).astype(np.float32)
+        out3 = attention.compressed_attention(q3, k3, v3, R, jl_matrix=P, num_kv_heads=2)
+        std3 = attention.standard_attention(q3, k3, v3, num_kv_heads=2)
+        assert out3.shape == (8, sq, d)
+        cos = (out3 * std3).sum() / np.linalg.norm(out3) / np.linalg.norm(std3)
+        assert cos > 0.95
+    with pytest.raises(ValueError):
+        attention.compressed_attention(q2, k2, v2, R, n_bits=9)
+    empty = attention.compressed_attention(q2, k2[:0], v2[:0], R)
+    assert empty.shape == (5, d) and not empty.any()

@@ -165,3 +165,23 @@ def test_max_heads_constant_matches_the_library():
     assert call(n, need - 1) == _lib.ERR_WORKSPACE
     need2 = L.pqkv_decode_workspace_bytes(1, n + 2, n + 2, 16, 128)
     assert call(n + 2, need2 - 1) == _lib.ERR_UNSUPPORTED
+
+
+def test_host_qjl_signatures_and_correction():
+    """compute_signatures / compute_correction (python/polarquant_kv/qjl.py:25-57):
+    signs = (P e >= 0); correction (1/m) sum (2 s - 1)(P q), 0 for a zero
+    residual (tests/test_qjl.py:142-154 asserts that case)."""
+    d = 64
+    P = qjl.generate_jl_matrix(d, d, seed=43)
+    rng = np.random.default_rng(2)
+    e = rng.standard_normal(d)
+    sig = qjl.compute_signatures(e, P)
+    assert sig.jl_dim == d and sig.signs.dtype == bool and sig.signs.shape == (d,)
+    assert np.array_equal(sig.signs, P @ e >= 0)
+    assert abs(sig.residual_norm - np.linalg.norm(e)) < 1e-12
+    q = rng.standard_normal(d)
+    want = sum((1.0 if s else -1.0) * float(P[i] @ q) for i, s in enumerate(sig.signs)) / d
+    assert abs(qjl.compute_correction(q, sig, P) - want) < 1e-12
+    zero = qjl.compute_signatures(np.zeros(d, np.float32), P)
+    assert zero.signs.all() and zero.residual_norm == 0.0
+    assert qjl.compute_correction(np.ones(d), zero, P) == 0.0
