@@ -2,27 +2,40 @@
 """PQ4 decode-attention throughput on one MI355X (plus encode tokens/s).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                    [--workload config3|config1|config2|config4|config5]
 
-Workload (the 32K-context metric config): one
-Llama-3-8B-shaped attention layer, B=8, 32 query / 8 kv heads, d=128, 32768
-cached tokens. K and V are synthetic fp16 with per-(head, channel) std drawn
-from LogNormal(0, 1) and 1 % of the channels scaled x20, seeded. The whole
-cache (K and V) is PQ4-encoded on the GPU, then a "step" is one decode
+Default workload (the 32K-context metric config):
+one Llama-3-8B-shaped attention layer, B=8, 32 query / 8 kv heads, d=128,
+32768 cached tokens. K and V are synthetic fp16 with per-(head, channel) std
+drawn from LogNormal(0, 1) and 1 % of the channels scaled x20, seeded. The
+whole cache (K and V) is PQ4-encoded on the GPU, then a "step" is one decode
 attention call for the batch (query rotation, split-K attention over the
 compressed cache, merge + inverse rotation). Inputs are resident in HBM before
-the timed region.
+the timed region. R and P come from the package's own generators
+(polarquant_kv.rotation / qjl).
 
 value = algorithmic bytes per step (compressed K+V read once, query read,
-output written) / step time. roofline: the split-K decode kernel's algorithmic
-bytes per launch over its mean duration, timed with hipEvents that the library
-records on the launch stream in a second loop of `--steps` calls (the timed
-loop runs without them); roofline.traffic is the HBM bytes per launch of
-that kernel from the committed rocprofv3 counter summary
+output written) / step time, K eager steps bracketed by events.
+
+roofline: the split-K decode kernel's algorithmic bytes per launch (302 120 960
+at config 3) over its mean duration. Two durations are reported:
+  kernel_ms          the rocprofv3 kernel-trace mean of the committed summary
+                     (profiles/decode_mfma_config3_kernel_stats.md, the same
+                     command on the same build) -- achieved / frac use it;
+  kernel_ms_events   the library's hipEvents around each launch, live in this
+                     run (they also count the launch's dispatch latency).
+roofline.traffic: HBM bytes per launch from the committed counter summary
 (profiles/decode_mfma_config3_hbm_traffic.md: FETCH_SIZE and WRITE_SIZE, each
-scaled by the same counter's reading on a plain 1 GiB device copy, which
-`--calibrate` adds after the timed region). cpu_baseline: the CPU oracle
-(float64 numpy decode, one thread) over whole (batch, kv-head) streams of the
-same cache for about 8 s, and the C oracle's encoder for about 4 s.
+scaled by the counter's reading on a plain 1 GiB copy, which --calibrate adds
+after the timed region).
+stream_read: a plain 16-byte-load read of the same 302 MB
+(pqkv_profile_stream_read), the most a read-only kernel draws on this box;
+pct_of_stream_read = decode kernel rate / that.
+
+cpu_baseline: the CPU oracle (float64 numpy, BLAS on all the process's
+affinity cores) decoding whole (batch, kv-head) streams of the same cache,
+median of >= 5 runs of a bounded sample; the C oracle's encoder (one thread)
+likewise. The CPU model and thread counts are reported.
 """
 
 from __future__ import annotations
@@ -30,6 +43,8 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
+import statistics
 import sys
 import time
 
@@ -39,9 +54,14 @@ for _p in (os.path.join(ROOT, "polarquant-kv_amd"), ROOT):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_mfma_config3_hbm_traffic.md")
+MFMA_F16_PEAK_TFLOPS = 2500.0
+PROFILES = os.path.join(ROOT, "profiles")
+TRAFFIC_FILE = os.path.join(PROFILES, "decode_mfma_config3_hbm_traffic.md")
+KSTATS_FILE = os.path.join(PROFILES, "decode_mfma_config3_kernel_stats.md")
 METRIC = "PQ4 decode-attn GB/s & % HBM peak; encode tokens/s; at 1 MI355X, 32K ctx"
 
+
+# ---------------------------------------------------------------- inputs
 
 def synth_channel_kv(torch, B, H, S, d, seed, dev):
     """fp16 [B, H, S, d]: N(0,1) times a per-(head, channel) LogNormal(0,1)
@@ -57,40 +77,94 @@ def synth_channel_kv(torch, B, H, S, d, seed, dev):
     return (x * std).clamp_(-65504, 65504).to(torch.float16)
 
 
-def cpu_baseline(kc, vc, q, R, d, budget_s=8.0):
-    """Time the CPU oracle's decode (float64 numpy, one thread) over whole
-    (batch, kv-head) streams of the same cache until `budget_s` has elapsed.
-    Returns (GB/s of compressed cache + query/output bytes, streams, seconds)."""
+def synth_token_lognormal_kv(torch, B, H, S, d, seed, dev):
+    """fp16 [B, H, S, d]: N(0,1) with each token's vector scaled by
+    LogNormal(0, 0.5)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    x = torch.randn(B, H, S, d, generator=g, device=dev)
+    return (x * torch.exp(0.5 * torch.randn(B, H, S, 1, generator=g, device=dev))).to(torch.float16)
+
+
+def rotation(torch, d, dev):
+    from polarquant_kv.rotation import generate_rotation_matrix
+    return generate_rotation_matrix(d, seed=42, device=dev)
+
+
+# ---------------------------------------------------------------- CPU baseline
+
+def cpu_info():
+    """(threads the process may use, CPU model string, BLAS thread count)."""
+    n = len(os.sched_getaffinity(0))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return n, model
+
+
+def timed_median(fn, runs=5):
+    """1 warm-up, then the median wall time of `runs` calls (perf_counter)."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def cpu_decode_baseline(kc, vc, q, R, d, streams, runs=5, qjl=None, P=None):
+    """The oracle's float64 decode of `streams` whole (batch, kv-head)
+    streams of the cache (with their query heads), BLAS on every affinity
+    core; median of `runs`. Returns (GB/s of cache + query/output bytes,
+    seconds per run, cores, model, BLAS threads)."""
     import numpy as np
-    from threadpoolctl import threadpool_limits
+    import torch
+    from threadpoolctl import threadpool_info, threadpool_limits
 
     from oracle import oracle as O
 
+    n, model = cpu_info()
+    torch.set_num_threads(n)
     B, Hkv = kc.batch, kc.num_heads
     G = q.shape[1] // Hkv
-    kb_all = kc.blocks.cpu().numpy()
-    vb_all = vc.blocks.cpu().numpy()
+    kb_all, vb_all = kc.blocks.cpu().numpy(), vc.blocks.cpu().numpy()
+    sg_all = None if qjl is None else kc.qjl_signs.cpu().numpy()
     q_all = q.float().cpu().numpy().astype(np.float64)
-    cb = O.lloyd_max_codebook(d, 4)[0]
+    kbits, vbits = kc.head_bits(), vc.head_bits()
     Rn = R.cpu().numpy().astype(np.float64)
-    done_bytes, streams, elapsed = 0, 0, 0.0
-    with threadpool_limits(limits=1):
-        O.decode_attention(q_all[:1, :G], kb_all[:1, :1, :256], vb_all[:1, :1, :256], Rn, cb, cb)  # warm-up
-        while elapsed < budget_s and streams < B * Hkv * 8:
-            b, h = divmod(streams % (B * Hkv), Hkv)
+    picks = [divmod(i % (B * Hkv), Hkv) for i in range(streams)]
+    nbytes = 0
+
+    def run():
+        nonlocal nbytes
+        nbytes = 0
+        for b, h in picks:
+            cbk = O.lloyd_max_codebook(d, kbits[h])[0]
+            cbv = O.lloyd_max_codebook(d, vbits[h])[0]
             kb, vb = kb_all[b:b + 1, h:h + 1], vb_all[b:b + 1, h:h + 1]
             qs = q_all[b:b + 1, G * h:G * (h + 1)]
-            t0 = time.perf_counter()
-            O.decode_attention(qs, kb, vb, Rn, cb, cb)
-            elapsed += time.perf_counter() - t0
-            done_bytes += kb.nbytes + vb.nbytes + qs.size * 2 * 2
-            streams += 1
-    return done_bytes / elapsed / 1e9, streams, elapsed
+            sg = None if sg_all is None else sg_all[b:b + 1, h:h + 1]
+            O.decode_attention(qs, kb, vb, Rn, cbk, cbv, k_bits=kbits[h], v_bits=vbits[h], qjl_signs=sg, P=P)
+            nbytes += kb.nbytes + vb.nbytes + qs.size * 2 * 2 + (0 if sg is None else sg.nbytes)
+
+    with threadpool_limits(limits=n):
+        # numpy's BLAS (the one the oracle's products run on)
+        blas = next((p.get("num_threads") for p in threadpool_info()
+                     if p.get("user_api") == "blas" and "numpy" in p.get("filepath", "")), None)
+        t = timed_median(run, runs)
+    return nbytes / t / 1e9, t, n, model, blas
 
 
-def cpu_encode_baseline(d, budget_s=4.0, n=4096):
-    """C oracle (single thread): FMA-chain rotation + quantiser + packing of
-    n-vector batches until `budget_s` has elapsed. Returns vectors/s."""
+def cpu_encode_baseline(d, n=4096, runs=5):
+    """The C oracle (one thread: FMA-chain rotation + quantiser + packing) on
+    n random vectors; median of `runs`. Returns vectors/s."""
     import numpy as np
 
     import oracle as OC
@@ -99,37 +173,128 @@ def cpu_encode_baseline(d, budget_s=4.0, n=4096):
     x = np.random.default_rng(0).standard_normal((n, d)).astype(np.float32)
     R = O.rotation_matrix(d, 42).astype(np.float32)
     cb = O.lloyd_max_codebook(d, 4)[0]
-    OC.c_rotate_fma(x[:64], R)
-    vectors, elapsed = 0, 0.0
-    while elapsed < budget_s:
-        t0 = time.perf_counter()
+
+    def run():
         y = OC.c_rotate_fma(x, R)
         r, idx = OC.c_quantize_rotated(y, cb)
         OC.c_pack_blocks(r, idx, 4)
-        elapsed += time.perf_counter() - t0
-        vectors += n
-    return vectors / elapsed
+
+    return n / timed_median(run, runs)
 
 
-def decode_kernel_name(d: int) -> str:
-    """The split kernel pqkv_decode_attn launches for a uniform PQ4 cache."""
-    if os.environ.get("PQKV_DECODE_KERNEL", "") == "valu":
-        return f"decode_split_kernel<{d},4,4,4>"
-    return f"decode_mfma_kernel<{d},4,4,4>"
+# ---------------------------------------------------------------- GPU timing helpers
+
+def _events(torch):
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def timed_eager(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0, t1 = _events(torch)
+    t0.record()
+    for _ in range(steps):
+        out = fn()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps, out
+
+
+def timed_graph(torch, fn, steps, warmup, per_graph=10):
+    """Steps captured `per_graph` at a time into one hipGraph, replayed until
+    `steps` steps have run; ms per step (launch overheads amortised)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(max(1, warmup)):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(per_graph):
+            out = fn()
+    reps = max(1, steps // per_graph)
+    g.replay()
+    torch.cuda.synchronize()
+    t0, t1 = _events(torch)
+    t0.record()
+    for _ in range(reps):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / (reps * per_graph), out
+
+
+def kernel_means(torch, _lib, fn, steps, names):
+    """Per-step time of each named kernel family from the library's
+    hipEvents on the launch stream (all launches of a step summed)."""
+    _lib.profile_enable(True)
+    _lib.profile_collect("")
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    res = {}
+    for n in names:
+        ms, _ = _lib.profile_collect(n)
+        res[n] = ms / steps
+    _lib.profile_enable(False)
+    return res
+
+
+def stream_read_gbps(torch, _lib, tensors, reps=20):
+    """Rate of a plain streaming read of the tensors' bytes, one read kernel
+    per tensor back to back (best of a few grid sizes), GB/s."""
+    sizes = [t.numel() * t.element_size() // 16 * 16 for t in tensors]
+    sink = torch.zeros(8192, dtype=torch.int32, device=tensors[0].device)
+    st = torch.cuda.current_stream().cuda_stream
+    best = 0.0
+
+    def read_all(blocks):
+        for t, nb in zip(tensors, sizes):
+            _lib.check(_lib.lib().pqkv_profile_stream_read(t.data_ptr(), nb, sink.data_ptr(), blocks, st))
+
+    for blocks in (1024, 2048, 4096, 8192):
+        for _ in range(3):
+            read_all(blocks)
+        t0, t1 = _events(torch)
+        t0.record()
+        for _ in range(reps):
+            read_all(blocks)
+        t1.record()
+        torch.cuda.synchronize()
+        best = max(best, sum(sizes) / (t0.elapsed_time(t1) / reps / 1e3) / 1e9)
+    return best
+
+
+def _summary_fields(path):
+    """`- key = value` lines of a committed profile summary."""
+    try:
+        with open(path) as f:
+            lines = f.read().splitlines()
+    except OSError:
+        return {}
+    out = {}
+    for line in lines:
+        m = re.match(r"^- (\w[\w ]*?) = `?([^`]+)`?\s*$", line)
+        if m:
+            out[m.group(1).strip()] = m.group(2).strip()
+    return out
 
 
 def committed_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed counter summary, or
-    None when the summary is absent or covers another kernel."""
-    try:
-        with open(TRAFFIC_FILE) as f:
-            fields = dict(line.split("=", 1) for line in f.read().splitlines() if line.startswith("- ") and "=" in line)
-    except OSError:
+    f = _summary_fields(TRAFFIC_FILE)
+    if f.get("kernel") != kernel or "traffic_bytes_per_launch" not in f:
         return None
-    fields = {k[2:].strip(): v.strip().strip("`") for k, v in fields.items()}
-    if fields.get("kernel") != kernel:
+    return int(float(f["traffic_bytes_per_launch"]))
+
+
+def committed_kernel_us(kernel: str):
+    f = _summary_fields(KSTATS_FILE)
+    if f.get("kernel") != kernel or "avg_us" not in f:
         return None
-    return int(float(fields["traffic_bytes_per_launch"]))
+    return float(f["avg_us"])
 
 
 def calibrate(torch, dev):
@@ -144,15 +309,23 @@ def calibrate(torch, dev):
     del x, y
 
 
+def _cpu_obj(gbps, unit, cores, model, blas, sample):
+    return {"value": round(gbps, 5), "unit": unit, "cores": cores, "kind": "port", "cpu_model": model,
+            "blas_threads": blas, "sample": sample}
+
+
+# ---------------------------------------------------------------- workloads
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--workload", choices=("config3", "config4", "config5"), default="config3",
-                    help="config3 (default): the metric line; config4 / config5: the low-bit + QJL decode and "
-                         "the chunked-prefill configurations, for their own measurement lines")
+    ap.add_argument("--workload", choices=("config3", "config1", "config2", "config4", "config5"), default="config3",
+                    help="config3 (default): the metric line; the others: BASELINE.json's remaining "
+                         "configurations, each its own line")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-runs", type=int, default=5)
     ap.add_argument("--encode-iters", type=int, default=3)
     ap.add_argument("--calibrate", action="store_true",
                     help="after the timed region, run a plain 1 GiB device copy (counter calibration)")
@@ -161,12 +334,8 @@ def main() -> int:
         print(f"bench.py measures one GPU only (the path shards by (batch, kv-head) with no exchange); "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
-
-    if args.workload == "config4":
-        return run_config4(args)
-    if args.workload == "config5":
-        return run_config5(args)
-    return run_config3(args)
+    return {"config3": run_config3, "config1": run_config1, "config2": run_config2, "config4": run_config4,
+            "config5": run_config5}[args.workload](args)
 
 
 def run_config3(args) -> int:
@@ -176,8 +345,7 @@ def run_config3(args) -> int:
 
     dev = "cuda:0"
     B, Hq, Hkv, S, d = 8, 32, 8, 32768, 128
-    from oracle import oracle as O
-    R = torch.from_numpy(O.rotation_matrix(d, 42).astype("float32")).to(dev)
+    R = rotation(torch, d, dev)
     K = synth_channel_kv(torch, B, Hkv, S, d, 1234, dev)
     V = synth_channel_kv(torch, B, Hkv, S, d, 5678, dev)
     kc = quantizer.allocate_cache(B, Hkv, S, d, 4, dev)
@@ -189,7 +357,7 @@ def run_config3(args) -> int:
     quantizer.compress_pq(V, R, cache=vc, start=0)
     torch.cuda.synchronize()
     _lib.profile_collect("encode")
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0, e1 = _events(torch)
     e0.record()
     for _ in range(args.encode_iters):
         quantizer.compress_pq(K, R, cache=kc, start=0)
@@ -198,60 +366,49 @@ def run_config3(args) -> int:
     torch.cuda.synchronize()
     enc_ms = e0.elapsed_time(e1) / args.encode_iters
     enc_kernel_ms, enc_launches = _lib.profile_collect("encode")
+    _lib.profile_enable(False)
     enc_tokens_s = B * S / (enc_ms / 1e3)
     enc_bytes = 2 * (K.numel() * 2 + kc.blocks.numel())
+    enc_kernel_each = enc_kernel_ms / max(enc_launches, 1)
     del K, V
 
     # ---- decode ----
-    # Timed region: library event hooks off (each hook pair costs ~6 us of
-    # stream time). A second loop of the same length then records the hooks'
-    # hipEvents on the launch stream for the per-kernel means.
-    _lib.profile_enable(False)
     q = torch.randn(B, Hq, d, device=dev, dtype=torch.float16)
     ws = torch.empty(_lib.lib().pqkv_decode_workspace_bytes(B, Hq, Hkv, S, d), dtype=torch.uint8, device=dev)
-    for _ in range(args.warmup):
-        attention.decode_attention(q, kc, vc, R, workspace=ws)
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record()
-    for _ in range(args.steps):
-        out = attention.decode_attention(q, kc, vc, R, workspace=ws)
-    t1.record()
-    torch.cuda.synchronize()
-    step_ms = t0.elapsed_time(t1) / args.steps
-    _lib.profile_enable(True)
-    _lib.profile_collect("")
-    for _ in range(args.steps):
-        attention.decode_attention(q, kc, vc, R, workspace=ws)
-    torch.cuda.synchronize()
-    split_ms, split_n = _lib.profile_collect("decode_split")
-    merge_ms, merge_n = _lib.profile_collect("decode_merge")
-    rot_ms, rot_n = _lib.profile_collect("decode_rotate")
-    _lib.profile_enable(False)
+
+    def step():
+        return attention.decode_attention(q, kc, vc, R, workspace=ws)
+
+    step_ms, out = timed_eager(torch, step, args.steps, args.warmup)
+    graph_ms, _ = timed_graph(torch, step, args.steps, 2)
+    km = kernel_means(torch, _lib, step, args.steps, ("decode_split", "decode_merge", "decode_rotate"))
     assert torch.isfinite(out.float()).all()
 
     cache_bytes = kc.blocks.numel() + vc.blocks.numel()            # 301 989 888
     qo_bytes = B * Hq * d * 2 * 2                                  # fp16 query in, fp16 output out
     step_bytes = cache_bytes + qo_bytes
     value = step_bytes / (step_ms / 1e3) / 1e9
-    kern_ms = split_ms / max(split_n, 1)
     kern_bytes = cache_bytes + B * Hq * d * 4                      # compressed K+V + fp32 rotated query
+    kernel = "decode_mfma_kernel<128,4,4,4>"
+    ev_ms = km["decode_split"]
+    rp_us = committed_kernel_us(kernel)
+    kern_ms = rp_us / 1e3 if rp_us is not None else ev_ms
     achieved = kern_bytes / (kern_ms / 1e3) / 1e9
+    sr = stream_read_gbps(torch, _lib, (kc.blocks, vc.blocks))
 
     if args.calibrate:
         calibrate(torch, dev)
 
-    kernel = decode_kernel_name(d)
-    traffic = committed_traffic(kernel)
     cpu = None
     if not args.no_cpu:
-        gbs, streams, t = cpu_baseline(kc, vc, q, R, d)
-        enc_vs = cpu_encode_baseline(d)
-        cpu = {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"oracle float64 numpy decode, one thread, of {streams} whole (batch, kv-head) streams "
-                         f"of the same cache (S=32768, {Hq // Hkv} query heads each; 64 streams = one step) "
-                         f"in {t:.1f} s; encode: C oracle FMA rotation + quantiser + packing, one thread, "
-                         f"{enc_vs:.0f} vectors/s = {enc_vs / (2 * Hkv):.0f} tokens/s (K+V of {Hkv} kv heads)"}
+        gbs, t, n, model, blas = cpu_decode_baseline(kc, vc, q, R, d, streams=B * Hkv, runs=args.cpu_runs)
+        enc_vs = cpu_encode_baseline(d, runs=args.cpu_runs)
+        cpu = _cpu_obj(gbs, "GB/s", n, model, blas,
+                       f"oracle float64 numpy decode of one whole step (all 64 (batch, kv-head) streams of the "
+                       f"cache, S=32768, {Hq // Hkv} query heads each), BLAS on {n} threads, "
+                       f"median of {args.cpu_runs} runs of {t:.2f} s; encode: C oracle FMA rotation + quantiser "
+                       f"+ packing, one thread, median of {args.cpu_runs}: {enc_vs:.0f} vectors/s = "
+                       f"{enc_vs / (2 * Hkv):.0f} tokens/s (K+V of {Hkv} kv heads)")
 
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -261,59 +418,75 @@ def run_config3(args) -> int:
                                "(block_pq4 72 B/vector), per-channel LogNormal(0,1) std + 1% x20 outliers",
                    "global_batch": B, "seq_len": S, "parallelism": "single GPU"},
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "graph_ms_per_step": round(graph_ms, 5),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic(kernel),
                      "kernel": kernel, "kernel_ms": round(kern_ms, 5),
-                     "bytes_per_launch": kern_bytes},
-        "stages_ms": {"query_rotate": round(rot_ms / max(rot_n, 1), 5), "split": round(kern_ms, 5),
-                      "merge": round(merge_ms / max(merge_n, 1), 5)},
+                     "kernel_ms_source": "rocprofv3 kernel trace (profiles/decode_mfma_config3_kernel_stats.md)"
+                     if rp_us is not None else "library hipEvents (no committed trace for this kernel)",
+                     "kernel_ms_events": round(ev_ms, 5),
+                     "achieved_events": round(kern_bytes / (ev_ms / 1e3) / 1e9, 2),
+                     "bytes_per_launch": kern_bytes,
+                     "stream_read_GBps": round(sr, 1), "pct_of_stream_read": round(100 * achieved / sr, 2)},
+        "stages_ms": {"query_rotate": round(km["decode_rotate"], 5), "split": round(ev_ms, 5),
+                      "merge": round(km["decode_merge"], 5)},
         "encode": {"tokens_per_s": round(enc_tokens_s), "ms": round(enc_ms, 4),
-                   "kernel_ms": round(enc_kernel_ms / max(enc_launches, 1), 4), "GB_per_s": round(
-                       enc_bytes / (enc_ms / 1e3) / 1e9, 2), "vectors": 2 * B * Hkv * S,
+                   "kernel_ms": round(enc_kernel_each, 4), "GB_per_s": round(enc_bytes / (enc_ms / 1e3) / 1e9, 2),
+                   "vectors": 2 * B * Hkv * S,
                    "kernel": "encode_mfma_kernel (matrix-core rotation, bit-exact quantiser)",
-                   "roofline": {"bound": "hbm", "bytes": enc_bytes, "achieved_GBps": round(
-                       enc_bytes / (enc_kernel_ms / max(enc_launches, 1) * 2 / 1e3) / 1e9, 2),
-                       "frac": round(enc_bytes / (enc_kernel_ms / max(enc_launches, 1) * 2 / 1e3) / 1e9
-                                     / HBM_PEAK_GBS, 4)}},
+                   "roofline": {"bound": "hbm", "bytes": enc_bytes,
+                                "achieved_GBps": round(enc_bytes / (enc_kernel_each * 2 / 1e3) / 1e9, 2),
+                                "frac": round(enc_bytes / (enc_kernel_each * 2 / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
     return 0
 
 
-def _timed(torch, fn, steps, warmup):
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record()
-    for _ in range(steps):
-        out = fn()
-    t1.record()
-    torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / steps, out
+def _decode_line(args, name, metric_workload, B, Hq, Hkv, S, d, kc, vc, q, R, jl_rot, kernel, extra=None):
+    """Eager and hipGraph-batched timing of one decode configuration."""
+    import torch
+
+    from polarquant_kv import _lib, attention
+
+    ws = torch.empty(_lib.lib().pqkv_decode_workspace_bytes(B, Hq, Hkv, S, d), dtype=torch.uint8, device=q.device)
+
+    def step():
+        return attention.decode_attention(q, kc, vc, R, jl_rot=jl_rot, workspace=ws)
+
+    eager_ms, out = timed_eager(torch, step, args.steps, args.warmup)
+    assert torch.isfinite(out.float()).all()
+    graph_ms, _ = timed_graph(torch, step, max(args.steps, 100), 2)
+    km = kernel_means(torch, _lib, step, args.steps, ("decode_split", "decode_merge", "decode_rotate"))
+    cache_bytes = kc.blocks.numel() + vc.blocks.numel() + (0 if kc.qjl_signs is None or jl_rot is None
+                                                          else kc.qjl_signs.numel())
+    step_bytes = cache_bytes + B * Hq * d * 2 * 2
+    kern_bytes = cache_bytes + B * Hq * d * 4
+    line = {
+        "metric": name, "value": round(step_bytes / (graph_ms / 1e3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(graph_ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u2/u4 codes; f16 hi/lo MFMA, f32 accumulate",
+        "data": "synthetic",
+        "config": {"workload": metric_workload, "global_batch": B, "seq_len": S, "parallelism": "single GPU"},
+        "timing": "hipGraph replays of 10 captured steps (the configuration is launch-bound); eager step "
+                  "in eager_ms_per_step",
+        "eager_ms_per_step": round(eager_ms, 5), "bytes_per_step": step_bytes,
+        "roofline": {"bound": "hbm", "achieved": round(kern_bytes / (km["decode_split"] / 1e3) / 1e9, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(kern_bytes / (km["decode_split"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": kernel, "kernel_ms_events": round(km["decode_split"], 5)},
+        "stages_ms_events": {k: round(v, 5) for k, v in km.items()},
+    }
+    if extra:
+        line.update(extra)
+    return line
 
 
-def _kernel_means(torch, _lib, fn, steps, names):
-    """Kernel time per step (all launches of a kernel in one step summed),
-    from the library's hipEvents on the launch stream."""
-    _lib.profile_enable(True)
-    _lib.profile_collect("")
-    for _ in range(steps):
-        fn()
-    torch.cuda.synchronize()
-    res = {}
-    for n in names:
-        ms, _ = _lib.profile_collect(n)
-        res[n] = ms / steps
-    _lib.profile_enable(False)
-    return res
-
-
-def run_config4(args) -> int:
-    """Low-bit decode: B=4, 32 q / 8 kv heads, d=128, S=16384, keys with the
-    QJL sign sketch (m = d, P seed 43); (i) 2-bit K and V, (ii) kv heads 0-3
-    at 4 bits and 4-7 at 2 bits. value = variant (i)'s algorithmic GB/s."""
+def run_config1(args) -> int:
+    """BASELINE configs[0], the reference's CPU-runnable case: one
+    Qwen2.5-0.5B layer, B=1, 14 q / 2 kv heads, d=64, S=512, Q/K/V fp16
+    N(0,1) from PCG64(42); a step is the PQ4 encode of K and V plus one
+    decode step (hipGraph-batched, the configuration is launch-bound)."""
     import numpy as np
     import torch
 
@@ -321,51 +494,142 @@ def run_config4(args) -> int:
     from polarquant_kv import _lib, attention, quantizer
 
     dev = "cuda:0"
+    B, Hq, Hkv, S, d = 1, 14, 2, 512, 64
+    rng = np.random.Generator(np.random.PCG64(42))
+    k = rng.standard_normal((B, Hkv, S, d)).astype(np.float16)
+    v = rng.standard_normal((B, Hkv, S, d)).astype(np.float16)
+    qn = rng.standard_normal((B, Hq, d)).astype(np.float16)
+    R = rotation(torch, d, dev)
+    K, V, q = (torch.from_numpy(a).to(dev) for a in (k, v, qn))
+    kc = quantizer.allocate_cache(B, Hkv, S, d, 4, dev)
+    vc = quantizer.allocate_cache(B, Hkv, S, d, 4, dev)
+    ws = torch.empty(_lib.lib().pqkv_decode_workspace_bytes(B, Hq, Hkv, S, d), dtype=torch.uint8, device=dev)
+
+    def step():
+        quantizer.compress_pq(K, R, cache=kc, start=0)
+        quantizer.compress_pq(V, R, cache=vc, start=0)
+        return attention.decode_attention(q, kc, vc, R, workspace=ws)
+
+    eager_ms, _ = timed_eager(torch, step, args.steps, args.warmup)
+    graph_ms, out = timed_graph(torch, step, max(args.steps, 100), 2)
+    assert torch.isfinite(out.float()).all()
+    cpu = None
+    if not args.no_cpu:
+        import oracle as OC
+        from threadpoolctl import threadpool_limits
+        n, model = cpu_info()
+        torch.set_num_threads(n)
+        Rn = O.rotation_matrix(d, 42)
+        cb = O.lloyd_max_codebook(d, 4)[0]
+        R32 = Rn.astype(np.float32)
+
+        def cpu_step():
+            blocks = []
+            for x in (k, v):
+                y = OC.c_rotate_fma(x.reshape(-1, d).astype(np.float32), R32)
+                r, idx = OC.c_quantize_rotated(y, cb)
+                blocks.append(OC.c_pack_blocks(r, idx, 4).reshape(B, Hkv, S, -1))
+            return O.decode_attention(qn.astype(np.float64), blocks[0], blocks[1], Rn, cb, cb)
+
+        with threadpool_limits(limits=n):
+            t = timed_median(cpu_step, args.cpu_runs)
+        cpu = _cpu_obj(1e3 * t, "ms per step", n, model, n,
+                       f"the whole step (C oracle encode of K and V, one thread, + oracle float64 decode, BLAS on "
+                       f"{n} threads), median of {args.cpu_runs} runs")
+    line = {
+        "metric": "config1 step latency (PQ4 encode K+V + decode) at 1 MI355X", "value": round(1e3 * graph_ms, 2),
+        "unit": "us per step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(graph_ms, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u4 codes; f16 hi/lo MFMA, f32 accumulate", "data": "synthetic",
+        "config": {"workload": "config1: Qwen2.5-0.5B layer, B=1 Hq=14 Hkv=2 d=64 S=512, Q/K/V fp16 N(0,1) "
+                               "PCG64(42); PQ4 encode of K and V then one decode step",
+                   "global_batch": B, "seq_len": S, "parallelism": "single GPU"},
+        "timing": "hipGraph replays of 10 captured steps; eager in eager_ms_per_step",
+        "eager_ms_per_step": round(eager_ms, 5),
+        "roofline": {"bound": "latency", "achieved": None, "peak": None, "unit": None, "frac": None, "traffic": None,
+                     "note": "77 KB of decode traffic and 336 KB of encode traffic: launch latency, not HBM, "
+                             "bounds this configuration"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+def run_config2(args) -> int:
+    """Qwen shape, B=16, 14 q / 2 kv heads, d=64,
+    S=4096, K/V N(0,1) times a per-token LogNormal(0, 0.5), PQ4 K+V, one
+    query token per sequence."""
+    import torch
+
+    from polarquant_kv import quantizer
+
+    dev = "cuda:0"
+    B, Hq, Hkv, S, d = 16, 14, 2, 4096, 64
+    R = rotation(torch, d, dev)
+    kc = quantizer.compress_pq(synth_token_lognormal_kv(torch, B, Hkv, S, d, 21, dev), R, 4)
+    vc = quantizer.compress_pq(synth_token_lognormal_kv(torch, B, Hkv, S, d, 22, dev), R, 4)
+    q = torch.randn(B, Hq, d, device=dev, dtype=torch.float16)
+    line = _decode_line(args, METRIC.replace("32K ctx", "config 2"),
+                        "config2: Qwen2.5-0.5B shape decode, B=16 Hq=14 Hkv=2 d=64 S=4096, PQ4 K+V, per-token "
+                        "LogNormal(0,0.5) norms", B, Hq, Hkv, S, d, kc, vc, q, R, None, "decode_mfma_kernel<64,7,4,4>")
+    cpu = None
+    if not args.no_cpu:
+        gbs, t, n, model, blas = cpu_decode_baseline(kc, vc, q, R, d, streams=B * Hkv, runs=args.cpu_runs)
+        cpu = _cpu_obj(gbs, "GB/s", n, model, blas,
+                       f"oracle float64 numpy decode of the whole step (32 streams), BLAS on {n} threads, median "
+                       f"of {args.cpu_runs} runs of {t:.2f} s")
+    line["cpu_baseline"] = cpu
+    print(json.dumps(line))
+    return 0
+
+
+def run_config4(args) -> int:
+    """Low-bit decode: B=4, 32 q / 8 kv heads, d=128, S=16384, keys with the
+    QJL sign sketch (m = d, P seed 43); (i) 2-bit K and V, (ii) kv heads 0-3
+    at 4 bits and 4-7 at 2 bits. value = variant (i)'s algorithmic GB/s per
+    hipGraph-replayed step."""
+    import torch
+
+    from polarquant_kv import quantizer
+    from polarquant_kv.qjl import generate_jl_matrix, rotated_jl_matrix
+
+    dev = "cuda:0"
     B, Hq, Hkv, S, d = 4, 32, 8, 16384, 128
-    R64 = O.rotation_matrix(d, 42)
-    R = torch.from_numpy(R64.astype("float32")).to(dev)
-    P_rot = torch.from_numpy((O.jl_matrix(d, d, 43) @ R64.T).astype("float32")).to(dev)
+    R = rotation(torch, d, dev)
+    P = generate_jl_matrix(d, d, seed=43)
+    P_rot = rotated_jl_matrix(P, R.cpu().numpy(), dev)
     K = synth_channel_kv(torch, B, Hkv, S, d, 4321, dev)
     V = synth_channel_kv(torch, B, Hkv, S, d, 8765, dev)
     q = torch.randn(B, Hq, d, device=dev, dtype=torch.float16)
-    variants = {"2bit": 2, "mixed": (4, 4, 4, 4, 2, 2, 2, 2)}
     res = {}
-    for name, bits in variants.items():
+    cpu = None
+    for name, bits in (("2bit", 2), ("mixed", (4, 4, 4, 4, 2, 2, 2, 2))):
         kc = quantizer.allocate_cache(B, Hkv, S, d, bits, dev, jl_dim=d)
         vc = quantizer.allocate_cache(B, Hkv, S, d, bits, dev)
         quantizer.compress_pq(K, R, cache=kc, jl_rot=P_rot)
         quantizer.compress_pq(V, R, cache=vc)
-        ws = torch.empty(_lib.lib().pqkv_decode_workspace_bytes(B, Hq, Hkv, S, d), dtype=torch.uint8, device=dev)
-
-        def step():
-            return attention.decode_attention(q, kc, vc, R, jl_rot=P_rot, workspace=ws)
-
-        _lib.profile_enable(False)
-        step_ms, out = _timed(torch, step, args.steps, args.warmup)
-        assert torch.isfinite(out.float()).all()
-        km = _kernel_means(torch, _lib, step, args.steps, ("decode_split", "decode_merge", "decode_rotate"))
-        cache_bytes = kc.blocks.numel() + vc.blocks.numel() + kc.qjl_signs.numel()
-        step_bytes = cache_bytes + B * Hq * d * 2 * 2
-        kern_bytes = cache_bytes + B * Hq * d * 4 + d * d * 4
-        res[name] = {"ms_per_step": round(step_ms, 5), "GB_per_s": round(step_bytes / (step_ms / 1e3) / 1e9, 2),
-                     "bytes_per_step": step_bytes, "split_ms": round(km["decode_split"], 5),
-                     "split_GB_per_s": round(kern_bytes / (km["decode_split"] / 1e3) / 1e9, 2),
-                     "merge_ms": round(km["decode_merge"], 5), "rotate_ms": round(km["decode_rotate"], 5)}
+        res[name] = _decode_line(args, "", "", B, Hq, Hkv, S, d, kc, vc, q, R, P_rot,
+                                 "decode_mfma_kernel<128,4,2,2,qjl>")
+        if name == "2bit" and not args.no_cpu:
+            gbs, t, n, model, blas = cpu_decode_baseline(kc, vc, q, R, d, streams=2, runs=args.cpu_runs, qjl=True,
+                                                         P=P)
+            cpu = _cpu_obj(gbs, "GB/s", n, model, blas,
+                           f"oracle float64 numpy decode with the QJL term, 2 whole (batch, kv-head) streams of the "
+                           f"2-bit cache (32 streams = one step), BLAS on {n} threads, median of {args.cpu_runs} "
+                           f"runs of {t:.2f} s")
         del kc, vc
     v = res["2bit"]
-    line = {
-        "metric": "decode-attn GB/s at 1 MI355X (low-bit + QJL)", "value": v["GB_per_s"], "unit": "GB/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": v["ms_per_step"],
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "u2/u4 codes + 1-bit QJL signs; f16 hi/lo MFMA, f32 accumulate", "data": "synthetic",
+    line = dict(v)
+    line.update({
+        "metric": "decode-attn GB/s at 1 MI355X (low-bit + QJL)",
         "config": {"workload": "config4: Llama-3-8B layer decode, B=4 Hq=32 Hkv=8 d=128 S=16384, QJL keys m=128 "
                                "(P seed 43); variants 2bit (block_pq2 K+V) and mixed (kv heads 0-3 PQ4, 4-7 PQ2)",
                    "global_batch": B, "seq_len": S, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": v["split_GB_per_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(v["split_GB_per_s"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode_mfma_kernel<128,4,2,2,qjl>", "kernel_ms": v["split_ms"]},
-        "variants": res, "cpu_baseline": None,
-    }
+        "variants": {k: {kk: vv for kk, vv in r.items() if kk in ("value", "ms_per_step", "eager_ms_per_step",
+                                                                 "bytes_per_step", "roofline", "stages_ms_events")}
+                     for k, r in res.items()},
+        "cpu_baseline": cpu,
+    })
     print(json.dumps(line))
     return 0
 
@@ -375,16 +639,16 @@ def run_config5(args) -> int:
     tokens + a 2048-token fp16 chunk, causal. A step encodes the chunk's K
     and V into the cache and runs prefill attention for the chunk. value =
     algorithmic TFLOP/s of the attention (64 (2048 131072 + 2048 2049 / 2) 4 128)."""
+    import numpy as np
     import torch
 
-    from oracle import oracle as O
-    from polarquant_kv import _lib, attention, quantizer
+    from polarquant_kv import attention, quantizer, _lib
 
     dev = "cuda:0"
     B, Hq, Hkv, d = 1, 64, 8, 128
     S_cache, Sq = 131072, 2048
     S = S_cache + Sq
-    R = torch.from_numpy(O.rotation_matrix(d, 42).astype("float32")).to(dev)
+    R = rotation(torch, d, dev)
     g = torch.Generator(device=dev)
     g.manual_seed(5)
     kc = quantizer.allocate_cache(B, Hkv, S, d, 4, dev)
@@ -401,13 +665,31 @@ def run_config5(args) -> int:
         return attention.prefill_attention(q, kc, vc, R, q_start=S_cache, causal=True)
 
     steps = max(1, min(args.steps, 20))
-    _lib.profile_enable(False)
-    step_ms, out = _timed(torch, step, steps, max(1, min(args.warmup, 3)))
+    step_ms, out = timed_eager(torch, step, steps, max(1, min(args.warmup, 3)))
     assert torch.isfinite(out.float()).all()
-    km = _kernel_means(torch, _lib, step, steps, ("prefill_attn", "prefill_rotate", "prefill_out_rotate", "encode"))
+    km = kernel_means(torch, _lib, step, steps, ("prefill_attn", "prefill_rotate", "prefill_out_rotate", "encode"))
     flops = 64 * (Sq * S_cache + Sq * (Sq + 1) / 2) * 4 * d
     tflops = flops / (step_ms / 1e3) / 1e12
     kern_tflops = flops / (km["prefill_attn"] / 1e3) / 1e12
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        from threadpoolctl import threadpool_limits
+        n, model = cpu_info()
+        kb = kc.blocks[:, :1].cpu().numpy()
+        vb = vc.blocks[:, :1].cpu().numpy()
+        qs = q[:, :8, -2:].float().cpu().numpy().astype(np.float64)   # kv head 0, the last 2 chunk tokens
+        Rn = R.cpu().numpy().astype(np.float64)
+        cb = O.lloyd_max_codebook(d, 4)[0]
+        with threadpool_limits(limits=n):
+            t = timed_median(lambda: O.prefill_attention(qs, kb, vb, Rn, cb, cb, q_start=S - 2, causal=True),
+                             max(3, min(args.cpu_runs, 5)))
+        rows = 2 * 8
+        row_flops = flops / (Sq * Hq)
+        cpu = _cpu_obj(rows * row_flops / t / 1e12, "TFLOP/s", n, model, n,
+                       f"extrapolated: oracle float64 prefill of 2 query tokens x 8 heads of kv head 0 over the "
+                       f"full 133120-token cache, BLAS on {n} threads, median of runs of {t:.2f} s, scaled by "
+                       f"the algorithmic FLOPs per query row")
     line = {
         "metric": "chunked-prefill attention TFLOP/s at 1 MI355X", "value": round(tflops, 2), "unit": "TFLOP/s",
         "n_gpus": 1, "steps": steps, "warmup": max(1, min(args.warmup, 3)), "ms_per_step": round(step_ms, 4),
@@ -417,12 +699,13 @@ def run_config5(args) -> int:
                                "tokens + 2048-token fp16 chunk (encoded into the cache each step), causal; "
                                "K/V/Q N(0,1)",
                    "global_batch": B, "seq_len": S, "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
-                     "frac": round(kern_tflops / 2500.0, 4), "traffic": None, "kernel": "prefill_mfma_kernel<128>",
-                     "kernel_ms": round(km["prefill_attn"], 4), "flops_per_launch": flops,
+        "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(kern_tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "prefill_mfma_kernel<128,4,4,false>", "kernel_ms_events": round(km["prefill_attn"], 4),
+                     "flops_per_launch": flops,
                      "note": "fp32-grade products cost 3 fp16 MFMAs each: this arithmetic tops out at 1/3"},
         "stages_ms": {k: round(v, 4) for k, v in km.items()},
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line))
     return 0

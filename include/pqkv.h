@@ -220,6 +220,12 @@ int pqkv_blocks_to_soa(const uint8_t *blocks, uint8_t *packed, float *radius,
  * bench.py; off by default, and costs nothing when off. */
 int pqkv_profile_enable(int on);
 int pqkv_profile_collect(const char *name, double *total_ms, int64_t *launches);
+/* A plain streaming read of `bytes` (a multiple of 16) at p with 16-byte
+ * loads by `blocks` workgroups (the data is XOR-folded; sink, of `blocks`
+ * words, is written only on a fold that never occurs in practice): the
+ * most a read-only kernel draws from HBM on the device, which bench.py
+ * reports beside the decode kernel's rate. */
+int pqkv_profile_stream_read(const void *p, size_t bytes, uint32_t *sink, int blocks, void *stream);
 
 /* ---- reference-compatible entry points -------------------------------------
  * Same names, arguments and return types as the extern "C" exports of the

@@ -152,6 +152,11 @@ int pqkv_profile_collect(const char *name, double *total_ms, int64_t *launches) 
   return PQKV_OK;
 }
 
+int pqkv_profile_stream_read(const void *p, size_t bytes, uint32_t *sink, int blocks, void *stream) {
+  if (!p || !sink || bytes % 16 || blocks <= 0) return fail(PQKV_ERR_INVALID, "stream_read: bad arguments");
+  return hip_status(pqkv::launch_stream_read(p, bytes, sink, blocks, (hipStream_t)stream), "stream_read launch");
+}
+
 int pqkv_version(void) { return 1; }
 
 const char *pqkv_status_string(int status) {

@@ -453,6 +453,28 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const float *__restri
   }
 }
 
+// Streaming-read probe for the measurement hook: every byte of [p, p + n16
+// * 16) read once with 16-byte loads in a grid-stride loop, XOR-folded per
+// thread; a store that depends on the fold keeps the loads alive.
+__global__ void __launch_bounds__(256) stream_read_kernel(const u32x4 *__restrict__ p, int64_t n16,
+                                                          uint32_t *__restrict__ sink) {
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const u32x4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
+    acc ^= a ^ b ^ c ^ d;
+  }
+  for (; i < n16; i += stride) acc ^= p[i];
+  const uint32_t f = acc.x ^ acc.y ^ acc.z ^ acc.w;
+  if (f == 0x9E3779B9u) sink[blockIdx.x] = f;
+}
+
+hipError_t launch_stream_read(const void *p, size_t bytes, uint32_t *sink, int blocks, hipStream_t s) {
+  stream_read_kernel<<<blocks, 256, 0, s>>>((const u32x4 *)p, (int64_t)(bytes / 16), sink);
+  return hipGetLastError();
+}
+
 __global__ void fill_zero_kernel(uint32_t *p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
     p[i] = 0u;

@@ -155,6 +155,8 @@ hipError_t launch_decode_mfma_soa(const DecodeArgs &a, hipStream_t s);
 hipError_t launch_decode_merge(const float *part, const float *R, void *out, int out_dtype, int BHq, int splits,
                                int d, hipStream_t s);
 hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t s);
+// Measurement: read `bytes` (a multiple of 16) from p once, XOR into sink[block].
+hipError_t launch_stream_read(const void *p, size_t bytes, uint32_t *sink, int blocks, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs &a, int k_bits, int v_bits, hipStream_t s);
 // Query rows per prefill workgroup (the QJL kernel holds 16 rows per wave
 // instead of 32, to make room for the projection operands).

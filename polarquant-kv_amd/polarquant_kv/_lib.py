@@ -52,6 +52,7 @@ SIGNATURES = {
     "pqkv_soa_to_blocks": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p]),
     "pqkv_blocks_to_soa": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p]),
     "pqkv_profile_enable": (c_int, [c_int]),
+    "pqkv_profile_stream_read": (c_int, [c_void_p, c_size_t, c_void_p, c_int, c_void_p]),
     "pqkv_profile_collect": (c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                      ctypes.POINTER(ctypes.c_int64)]),
     "polarquant_init_c": (c_void_p, [c_int, c_int, c_int, c_int, c_int, c_int]),
