@@ -7,8 +7,11 @@ python/polarquant_kv and src/polarquant_kv_cuda) for the codebook
   rotation   generate_rotation_matrix, rotate, inverse_rotate
   lloyd_max  build_lloyd_max_codebook, quantize_with_codebook, ...
   qjl        generate_jl_matrix, bit_pack, bit_unpack
-  quantizer  compress_pq, quantize_rotated, allocate_cache      (HIP)
-  attention  compressed_attention_gpu, decode_attention, ...     (HIP)
+  quantizer  compress_pq, compress_gpu, decompress_gpu, ...    (HIP)
+  attention  compressed_attention_gpu, compressed_attention, ... (HIP)
+  turboquant turboquant_compress, turboquant_full_attention      (HIP, raw pointers)
+  inference  PolarQuantConfig, KVCacheManager, CompressedMultiHeadAttention
+  hf_integration CompressedDynamicCache, patch_model
 
 GPU work goes through libpqkv_hip.so (include/pqkv.h) via ctypes.
 """
@@ -22,7 +25,7 @@ __all__ = ["lloyd_max", "qjl", "rotation", "types", "PQCache", "block_bytes", "v
 def __getattr__(name):
     # GPU modules load libpqkv_hip.so lazily so the host-side API imports
     # on machines without a GPU.
-    if name in ("attention", "quantizer", "turboquant"):
+    if name in ("attention", "quantizer", "turboquant", "inference", "hf_integration"):
         import importlib
         return importlib.import_module(f".{name}", __name__)
     raise AttributeError(name)

@@ -185,3 +185,15 @@ def test_host_qjl_signatures_and_correction():
     zero = qjl.compute_signatures(np.zeros(d, np.float32), P)
     assert zero.signs.all() and zero.residual_norm == 0.0
     assert qjl.compute_correction(np.ones(d), zero, P) == 0.0
+
+
+def test_inference_config_validation():
+    from polarquant_kv.inference import KVCacheManager, PolarQuantConfig
+    with pytest.raises(ValueError):
+        KVCacheManager(PolarQuantConfig(n_bits=3), 16, 1, 2, 64, device="cpu")
+    with pytest.raises(ValueError):
+        KVCacheManager(PolarQuantConfig(enable_qjl=True, jl_dim=32), 16, 1, 2, 64, device="cpu")
+    m = KVCacheManager(PolarQuantConfig(), 16, 1, 2, 64, device="cpu")
+    assert m.seq_len == 0 and m.memory_bytes == 0 and m.compression_ratio == 0.0
+    with pytest.raises(ValueError):
+        m.append(torch.zeros(1, 3, 4, 64), torch.zeros(1, 3, 4, 64))   # wrong head count
