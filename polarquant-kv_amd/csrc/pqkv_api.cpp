@@ -306,13 +306,13 @@ int encode_validate(const void *x, int x_dtype, int64_t x_outer_stride, const fl
 }
 
 // The matrix-core encoder takes fp16 input without QJL whose rows and R allow
-// 16-byte loads.
+// 16-byte loads, and blocks that allow dword stores.
 bool fast_encode_ok(const void *x, int x_dtype, int64_t x_outer_stride, int64_t n_outer, int64_t n_inner,
-                    const float *R, const uint8_t *qjl) {
+                    const float *R, const uint8_t *qjl, const uint8_t *blocks, int64_t blocks_outer_stride) {
   if (x_dtype != PQKV_F16 || qjl != nullptr) return false;
-  if ((uintptr_t)x % 16 || (uintptr_t)R % 16) return false;
+  if ((uintptr_t)x % 16 || (uintptr_t)R % 16 || (uintptr_t)blocks % 4) return false;
   if (n_outer * n_inner > ((int64_t)1 << 32) - 64) return false;  // 32-bit vector indices
-  return n_outer <= 1 || x_outer_stride % 8 == 0;
+  return n_outer <= 1 || (x_outer_stride % 8 == 0 && blocks_outer_stride % 4 == 0);
 }
 
 // Rows that follow each other with no gap in x, the blocks and the signs are
@@ -347,7 +347,7 @@ int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride, const float 
   const char *env = getenv("PQKV_ENCODE_KERNEL");
   const bool exact = env && strcmp(env, "exact") == 0;
   hipError_t e;
-  if (!exact && fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, n_inner, R, qjl)) {
+  if (!exact && fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, n_inner, R, qjl, blocks, blocks_outer_stride)) {
     const int tok = pqkv::prof_begin("encode_mfma", (hipStream_t)stream);
     e = pqkv::launch_encode_mfma(a, nullptr, nullptr, device_cus(), (hipStream_t)stream);
     pqkv::prof_end(tok, (hipStream_t)stream);
@@ -365,8 +365,9 @@ int pqkv_encode_mfma(const void *x, int x_dtype, int64_t x_outer_stride, const f
   const int v = encode_validate(x, x_dtype, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride, n_outer,
                                 n_inner, d, nullptr, 0, nullptr, 0);
   if (v <= 0) return v;
-  if (!fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, n_inner, R, nullptr))
-    return fail(PQKV_ERR_UNSUPPORTED, "encode_mfma: needs fp16 x, 16-byte aligned x rows and R, < 2^32 vectors");
+  if (!fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, n_inner, R, nullptr, blocks, blocks_outer_stride))
+    return fail(PQKV_ERR_UNSUPPORTED,
+                "encode_mfma: needs fp16 x, 16-byte aligned x rows and R, 4-byte aligned blocks, < 2^32 vectors");
   const pqkv::EncodeArgs a = encode_args(x, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride,
                                          n_outer, n_inner, d, nullptr, 0, nullptr, 0);
   const int tok = pqkv::prof_begin("encode_mfma", (hipStream_t)stream);

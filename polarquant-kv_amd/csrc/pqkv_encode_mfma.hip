@@ -1,41 +1,51 @@
 // Fast fused encoder on the matrix cores (gfx950) for fp16 input vectors:
 // rotate, radius, direction, nearest centroid, block_pq4 / block_pq2 packing.
 //
-// Rotation: Y^T = R . X^T with v_mfma_f32_16x16x32_f16. A = R (16 output
-// coordinates x 32 input coordinates, from LDS), B = X^T (the fp16 input, 16
-// vectors per tile, straight from HBM). fp16 input is exact, so only R is
-// split (R = R_hi + R_lo, R_lo = fp16(R - R_hi), subnormals kept by the MFMA):
-// two MFMAs per tile product give fp32-grade rotated values (not the FMA-chain
-// rounding of the exact encoder; the quantiser below is bit-exact on the
-// values this rotation produces).
+// Work split. A workgroup of four waves takes 64 vectors per step. The
+// step's input (64 x d fp16) arrives in LDS by direct global->LDS copies
+// issued one step ahead, and every wave reads all of it as the B operand of
+// v_mfma_f32_16x16x32_f16 (B = X^T, 16 vectors per tile). Wave w computes a
+// quarter of the output coordinates, j = 16 k + 4 w + i (i = 0..3,
+// k = 0..d/16-1), so its A operand (those d/4 rows of R, split as
+// R = R_hi + R_lo in fp16, the fp16 input being exact) stays in registers for
+// the whole launch: two MFMAs per tile product give fp32-grade rotated values
+// (not the FMA-chain rounding of the exact encoder; the quantiser below is
+// bit-exact on the values this rotation produces).
 //
-// The result lands with lane (col, grp) holding output coordinates
-// 16 mt + 4 grp + i of vector col, which maps the reference's 128-slot tree of
-// squares (slot t += slot t + s for s = 64 .. 1) onto the lanes exactly: s = 64,
-// 32, 16 are in-lane (mt + 4, + 2, + 1), s = 8 and 4 are the permlane32 / 16
-// swaps (lanes + 32, + 16; both sides add the same pair, and IEEE addition
-// commutes), s = 2, 1 are in-lane (i + 2, i + 1).
+// Radius: the reference's tree of squares (slot t += slot t + s for
+// s = 64 .. 1, csrc/flash_turboquant.cu:141-147) with the coordinate split
+// above: the steps s >= 16 pair coordinates of one wave (k bit 2 in-lane,
+// k bits 1 and 0 across the permlane32 / permlane16 swaps; IEEE addition
+// commutes, so both lanes of a swap hold the same sum), which leaves wave w
+// with slots 4 w + i. Those 16 partial sums per vector go through LDS, and
+// lane L of every wave finishes the steps s = 8 .. 1 of vector L.
 //
 // Nearest centroid: the reference scans |dir - c_i| and keeps the first
 // minimum. For a sorted codebook that index is a step function of dir, so it
 // equals the number of switch points theta_i <= dir, where theta_i is the
 // smallest fp32 value the scan maps to i + 1. Each workgroup finds the
 // switch points by bisection over fp32 values with the scan itself, then
-// builds a table over 1024 direction cells holding (index at the cell start,
+// builds a table over 1027 direction cells holding (index at the cell start,
 // the switch point inside the cell): one LDS read and one compare per
-// coordinate. A codebook that is not strictly increasing, with two switch
-// points in one cell, or with a switch point below 2^-60 in magnitude, falls
-// back to the scan.
+// coordinate. The cell of dir is round(512 dir) + 513, read from the low bits
+// of fma(dir, 512, 1.5 * 2^23) (monotone in dir; the table is built with the
+// same function). A codebook that is not strictly increasing, with a switch
+// point outside (-1, 1), two switch points in one cell or one below 2^-60 in
+// magnitude falls back to the scan.
 //
 // Direction on the table path: dir = q0 + e * inv with inv = RN(1 / r) (one
 // correctly rounded division per vector), q0 = RN(y * inv) and the residual
 // e = fma(-r, q0, y). By Markstein's theorem this is RN(y / r), the
 // reference's division, whenever e is exact, which holds when
-// exp(r) + exp(q0) - 46 >= -149. The fast form is taken per 16-vector tile
-// when every radius is finite and >= 2^-40 (or zero-like, dir = 0): then every
-// direction within a factor of two of a switch point (>= 2^-60) is exact, and a
-// direction off by an ulp elsewhere crosses no switch point, so the index is
-// the reference's. Tiles with other radii divide per coordinate.
+// exp(r) + exp(q0) - 46 >= -149. The fast form is taken per 64-vector step
+// when every radius is finite and >= 2^-40 (or zero-like, dir = 0): then
+// every direction within a factor of two of a switch point (>= 2^-60) is
+// exact, and a direction off by an ulp elsewhere crosses no switch point, so
+// the index is the reference's. Steps with other radii divide per coordinate.
+//
+// Output: each wave writes its codes (and wave w the radius of block w) into
+// an LDS copy of the step's blocks; the next step stores it with dword
+// writes, so the stores' completion is waited for one step later.
 #include "pqkv_device.h"
 #include "pqkv_launch.h"
 
@@ -43,41 +53,44 @@ namespace pqkv {
 
 namespace {
 
+#ifndef PQKV_ENC_TILES
+#define PQKV_ENC_TILES 2
+#endif
+#ifndef PQKV_ENC_BLOCKS
+#define PQKV_ENC_BLOCKS 3
+#endif
 constexpr int kEW = 4;              // waves per workgroup
+constexpr int kET = PQKV_ENC_TILES; // 16-vector tiles per workgroup step
+constexpr int kEG = 16 * kET;       // vectors per workgroup step
+constexpr int kEBlocksPerCU = PQKV_ENC_BLOCKS;  // resident workgroups per compute unit
 constexpr int kECells = 1024;       // direction cells over [-1, 1], 1/512 wide
-constexpr int kECellSlots = kECells + 3;  // cell u covers [u - 513, u - 512) / 512
-constexpr int kESeg = 64 * 8;       // one operand segment: 64 lanes x 8 bytes
-constexpr int kEVec = 64;           // vectors per wave iteration (4 tiles of 16)
-
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
-typedef __attribute__((address_space(3))) const u32x2 lds_cu32x2;
-
-__device__ __forceinline__ void lds_put8(uint8_t *p, uint32_t a, uint32_t b) { *(lds_u32x2 *)p = (u32x2){a, b}; }
-__device__ __forceinline__ u32x2 lds_get8(const uint8_t *p) { return *(lds_cu32x2 *)p; }
-
-__device__ __forceinline__ half8_t pack8u(u32x2 a, u32x2 b) {
-  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-  u32x4v v = {a.x, a.y, b.x, b.y};
-  return __builtin_bit_cast(half8_t, v);
-}
+constexpr int kECellSlots = kECells + 3;
+constexpr int kECellOff = 513;      // cell of dir = round(512 dir) + 513
+constexpr float kEMagic = 12582912.0f;  // 1.5 * 2^23: ulp 1, so fma(d, 512, kEMagic) holds round(512 d) in its low bits
+constexpr float kEClamp = 1.001f;   // |dir| of the table path stays below; beyond, no switch point lies
+constexpr int kEPart = 20;          // floats per vector in the partial-sum exchange (16 used; 80-byte rows
+                                    // put the 16-byte reads of lanes 0..15 in distinct banks)
 
 __device__ __forceinline__ float4_t mfma16(half8_t a, half8_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ uint32_t pack_h2(half_t a, half_t b) {
-  half2_t v = {a, b};
-  return __builtin_bit_cast(uint32_t, v);
+
+// Two tree steps at once: after v_permlane32_swap of a and b, lane L < 32
+// holds a[L] + a[L + 32] and lane L >= 32 holds b[L - 32] + b[L].
+__device__ __forceinline__ float swap32_pair_add(float a, float b) {
+  auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), false, false);
+  return __builtin_bit_cast(float, (uint32_t)s[0]) + __builtin_bit_cast(float, (uint32_t)s[1]);
+}
+// After v_permlane16_swap of a and b (rows of 16 lanes): row 0 holds
+// a[r0] + a[r1], row 1 b[r0] + b[r1], row 2 a[r2] + a[r3], row 3 b[r2] + b[r3].
+__device__ __forceinline__ float swap16_pair_add(float a, float b) {
+  auto s = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), false, false);
+  return __builtin_bit_cast(float, (uint32_t)s[0]) + __builtin_bit_cast(float, (uint32_t)s[1]);
 }
 
-__device__ __forceinline__ float swap32_add(float x) {
-  auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x), false, false);
-  return __builtin_bit_cast(float, (uint32_t)s[0]) + __builtin_bit_cast(float, (uint32_t)s[1]);
-}
-__device__ __forceinline__ float swap16_add(float x) {
-  auto s = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x), false, false);
-  return __builtin_bit_cast(float, (uint32_t)s[0]) + __builtin_bit_cast(float, (uint32_t)s[1]);
+__device__ __forceinline__ float bperm_f(int src_lane, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane * 4, __builtin_bit_cast(int, v)));
 }
 
 // The reference quantiser: first i minimising |d - c_i| (strict '<').
@@ -115,14 +128,13 @@ __device__ __forceinline__ int scan_index_rolled(float d, const float *cb, int n
   return b;
 }
 
-// Direction cell, monotone in d (the table is built with the same function;
-// a rounded fma of a monotone exact function is monotone). For |d| <= 1 + 2^-9
-// the clamp never acts: dir_cell_unclamped is the same function there.
-__device__ __forceinline__ int dir_cell_unclamped(float d) {
-  return (int)__builtin_fmaf(d, (float)(kECells / 2), (float)(kECells / 2 + 1));
+// Direction cell, monotone in d: round(512 d) + 513, for |d| <= kEClamp in
+// 0 .. kECellSlots - 1.
+__device__ __forceinline__ uint32_t cell_bits(float d) {
+  return __builtin_bit_cast(uint32_t, __builtin_fmaf(d, 512.0f, kEMagic));
 }
 __device__ __forceinline__ int dir_cell(float d) {
-  return min(max(dir_cell_unclamped(d), 0), kECellSlots - 1);
+  return (int)(cell_bits(d) - __builtin_bit_cast(uint32_t, kEMagic)) + kECellOff;
 }
 
 // Unsigned division by a divisor fixed per launch (Granlund and Montgomery,
@@ -158,43 +170,74 @@ __device__ __forceinline__ float kfloat(int64_t k) {
   return k >= 0 ? __builtin_bit_cast(float, (int32_t)k) : __builtin_bit_cast(float, (int32_t)(0x80000000u | (uint32_t)(-k)));
 }
 
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+// Stores into the stage copy of a step's blocks. Written as instructions the
+// compiler's wait tracking does not see: it would otherwise wait for the
+// next step's copies into xs (still in flight, never overlapping the stage
+// copy) before each LDS store. The workgroup barrier that follows the stores
+// waits for them (lgkmcnt 0); as volatile asm they stay in order with it.
+__device__ __forceinline__ void stage_st16(lds_u8 *p, uint32_t v) {
+  asm volatile("ds_write_b16 %0, %1" ::"v"((uint32_t)(uintptr_t)p), "v"(v));
+}
+__device__ __forceinline__ void stage_st8(lds_u8 *p, uint32_t v) {
+  asm volatile("ds_write_b8 %0, %1" ::"v"((uint32_t)(uintptr_t)p), "v"(v));
+}
+typedef __attribute__((address_space(3))) half8_t lds_half8;
+typedef __attribute__((address_space(3))) float4_t lds_float4;
+
 }  // namespace
 
 template <int D, int BITS>
-__global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeArgs a, float *rot_out,
-                                                                            float *radius_out) {
-  constexpr int MT = D / 16;            // output-coordinate tiles
-  constexpr int KS = D / 32;            // k-steps over input coordinates
+__global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(const EncodeArgs a, float *rot_out,
+                                                                                float *radius_out) {
+  constexpr int KS = D / 32;             // k-steps over input coordinates
+  constexpr int MTW = D / 64;            // 16-row output tiles per wave
   constexpr int NL = 1 << BITS;
+  constexpr int BB = block_bytes(BITS);
   constexpr int VB = vector_bytes(D, BITS);
-  constexpr int SEGS = MT * KS * 2 * 2; // (mt, ks, plane, half)
-  __shared__ __attribute__((aligned(16))) uint8_t rl[SEGS * kESeg];
-  __shared__ uint2 cells[kECellSlots];  // (index at the cell start, switch point bits or +inf)
+  constexpr int XB = 2 * D;              // input bytes per vector
+  constexpr int CH = XB / 16;            // 16-byte chunks per vector
+  constexpr int VPI = 1024 / XB;         // vectors per wave copy instruction (64 lanes x 16 bytes)
+  constexpr int NCOPY = kEG / VPI;       // copy instructions per step
+  constexpr int DW = VB / 4;             // output dwords per vector
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kEG * XB];
+  __shared__ __attribute__((aligned(16))) float part[kEG * kEPart];
+  __shared__ __attribute__((aligned(16))) uint8_t stage[kEG * VB];
+  __shared__ uint2 cells[kECellSlots];   // (index at the cell start, switch point bits or +inf)
   __shared__ float cb[16], thr[16];
   __shared__ int ucell[16];
   __shared__ int table_ok;
+  typedef __attribute__((address_space(3))) uint32_t lds_u32;
+  lds_u8 *const stg = (lds_u8 *)stage;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
+  // chunk swizzle of a vector's 16-byte pieces in LDS: the B-operand reads of
+  // lanes 0..15 (16 vectors, one chunk each) land in distinct banks
+  auto swz = [](int vl) { return D == 128 ? (vl & 15) : ((vl >> 1) & 7); };
 
-  // ---- R as the A operand: seg(mt, ks, plane, h), lane 16 grp + col holds
-  // R[16 mt + col][32 ks + 8 grp + 4 h .. + 3] ----
-  for (int it = tid; it < D * D / 4; it += kEW * 64) {
-    const int j = it / (D / 4), q = it % (D / 4);
-    const float4 r4 = *(const float4 *)(a.R + (int64_t)j * D + 4 * q);
-    const float rv[4] = {r4.x, r4.y, r4.z, r4.w};
-    half_t hi[4], lo[4];
+  // ---- A operand, in registers for the launch: row p of tile mt is output
+  // coordinate j = 16 (4 mt + p / 4) + 4 wave + p % 4; lane (p, grp) holds
+  // R[j][32 ks + 8 grp .. + 7] ----
+  half8_t ah[MTW][KS], al[MTW][KS];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      hi[u] = (half_t)rv[u];
-      lo[u] = (half_t)(rv[u] - (float)hi[u]);
+  for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int j = 16 * (4 * mt + (col >> 2)) + 4 * wave + (col & 3);
+      const float4 *rr = (const float4 *)(a.R + (int64_t)j * D + 32 * ks + 8 * grp);
+      const float4 r0 = rr[0], r1 = rr[1];
+      const float rv[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const half_t h = (half_t)rv[e];
+        ah[mt][ks][e] = h;
+        al[mt][ks][e] = (half_t)(rv[e] - (float)h);
+      }
     }
-    const int mt = j >> 4, c = j & 15, ks = q >> 3, g = (q >> 1) & 3, h = q & 1;
-    const int seg = ((mt * KS + ks) * 2 + 0) * 2 + h;
-    uint8_t *p = rl + seg * kESeg + (16 * g + c) * 8;
-    lds_put8(p, pack_h2(hi[0], hi[1]), pack_h2(hi[2], hi[3]));
-    lds_put8(p + 2 * kESeg, pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));  // plane 1 is two segments on
-  }
+
   if (tid < 16) cb[tid] = tid < NL ? a.codebook[tid] : 0.0f;
   if (tid == 0) table_ok = 1;
   __syncthreads();
@@ -228,206 +271,251 @@ __global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeAr
       if (!ok || hi - lo != 1) {
         table_ok = 0;
       } else {
-        thr[i] = kfloat(hi);
-        ucell[i] = dir_cell(kfloat(hi));
-        if (!(fabsf(thr[i]) >= 0x1p-60f)) table_ok = 0;
+        const float t = kfloat(hi);
+        thr[i] = t;
+        if (!(fabsf(t) >= 0x1p-60f) || !(fabsf(t) < 1.0f)) table_ok = 0;
+        else ucell[i] = dir_cell(t);
       }
     }
   }
   __syncthreads();
-  for (int u = tid; u < kECellSlots; u += kEW * 64) {
-    int base = 0, inside = -1, count = 0;
-    for (int i = 0; i < NL - 1; ++i) {
-      if (ucell[i] < u) ++base;
-      else if (ucell[i] == u) {
-        inside = i;
-        ++count;
+  if (table_ok != 0) {
+    for (int u = tid; u < kECellSlots; u += kEW * 64) {
+      int base = 0, inside = -1, count = 0;
+      for (int i = 0; i < NL - 1; ++i) {
+        if (ucell[i] < u) ++base;
+        else if (ucell[i] == u) {
+          inside = i;
+          ++count;
+        }
       }
+      if (count > 1) table_ok = 0;
+      cells[u] = make_uint2((uint32_t)base, inside >= 0 ? __builtin_bit_cast(uint32_t, thr[inside]) : 0x7F800000u);
     }
-    if (count > 1) table_ok = 0;
-    cells[u] = make_uint2((uint32_t)base, inside >= 0 ? __builtin_bit_cast(uint32_t, thr[inside]) : 0x7F800000u);
   }
   __syncthreads();
 
   const half_t *x = (const half_t *)a.x;
   // vector v = n_inner * vo + vi; the host keeps n below 2^32
   const uint32_t n = (uint32_t)(a.n_outer * a.n_inner);
-  const int64_t groups = ((int64_t)n + kEVec - 1) / kEVec;
+  const int64_t groups = ((int64_t)n + kEG - 1) / kEG;
   const FastDiv by_inner((uint32_t)a.n_inner);
   const bool rows = a.n_outer > 1;
   auto split = [&](uint32_t v, uint32_t &vo, uint32_t &vi) {
     vo = rows ? by_inner.div(v) : 0u;
     vi = v - vo * (uint32_t)a.n_inner;
   };
-  // The table test is uniform per workgroup: one copy of the loop per path,
-  // so no branch sits between the per-coordinate table reads.
-  // B operand: lane (col, grp), tile c holds vector 64 g + 16 c + col, input
-  // coordinates 32 ks + 8 grp .. + 7 (zeros past the end).
-  auto load_x = [&](int64_t g, half8_t (&xb)[4][KS]) {
+  // Step g's input into xs[b]: copy instruction q covers vectors q VPI ..,
+  // lane L piece L % CH of vector q VPI + L / CH, which holds chunk
+  // (L % CH) ^ swz(vector). Lanes past the end copy nothing.
+  auto issue = [&](int64_t g, int b) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint32_t v = (uint32_t)g * kEVec + 16 * c + col;
-      uint32_t vo, vi;
-      split(v, vo, vi);
-      const half_t *xv = x + (int64_t)vo * a.x_outer_stride + (int64_t)vi * D;
+    for (int q = wave; q < NCOPY; q += kEW) {
+      const int vl = q * VPI + lane / CH;
+      const uint32_t v = (uint32_t)g * kEG + vl;
+      if (v < n) {
+        const half_t *row = x + (int64_t)v * D;
+        if (rows) {
+          uint32_t vo, vi;
+          split(v, vo, vi);
+          row = x + (int64_t)vo * a.x_outer_stride + (int64_t)vi * D;
+        }
+        __builtin_amdgcn_global_load_lds((const void *)(row + 8 * ((lane % CH) ^ swz(vl))), (lds_void *)(xs[b] + 1024 * q),
+                                         16, 0, 0);
+      }
+    }
+  };
+  // Step g's blocks from the LDS copy to memory: one run of 16-byte pieces
+  // when the blocks are one aligned run, else dword by dword.
+  const bool run16 = !rows && ((uintptr_t)a.blocks & 15) == 0;
+  auto flush = [&](int64_t g) {
+    if (run16) {
+      const uint32_t v0 = (uint32_t)g * kEG;
+      const int nbytes = (int)min(n - v0, (uint32_t)kEG) * VB;
+      uint8_t *base = a.blocks + (int64_t)v0 * VB;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
+      for (int it = 0; it < (kEG * VB / 16 + kEW * 64 - 1) / (kEW * 64); ++it) {
+        const int p = tid + kEW * 64 * it;
+        if (16 * p + 16 <= nbytes) {
+          *(u32x4 *)(base + 16 * p) = *(const __attribute__((address_space(3))) u32x4 *)(stg + 16 * p);
+        } else if (16 * p < nbytes) {
+          for (int c = 0; c < 4 && 16 * p + 4 * c < nbytes; ++c)
+            *(uint32_t *)(base + 16 * p + 4 * c) = *(const lds_u32 *)(stg + 16 * p + 4 * c);
+        }
+      }
+      return;
+    }
+#pragma unroll
+    for (int it = 0; it < (kEG * DW + kEW * 64 - 1) / (kEW * 64); ++it) {
+      const int q = tid + kEW * 64 * it;
+      if (q < kEG * DW) {
+        const int vl = q / DW, c = q - vl * DW;
+        const uint32_t v = (uint32_t)g * kEG + vl;
         if (v < n) {
-          xb[c][ks] = *(const half8_t *)(xv + 32 * ks + 8 * grp);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) xb[c][ks][e] = (half_t)0.0f;
+          uint32_t vo, vi;
+          split(v, vo, vi);
+          const uint32_t w = *(const lds_u32 *)(stg + vl * VB + 4 * c);
+          *(uint32_t *)(a.blocks + (int64_t)vo * a.blocks_outer_stride + (int64_t)vi * VB + 4 * c) = w;
         }
       }
     }
   };
-  const int64_t g_step = (int64_t)gridDim.x * kEW;
-  auto run = [&](auto flag) {
-  constexpr bool kTable = decltype(flag)::on;
-  half8_t xb[4][KS];
-  int64_t g = (int64_t)blockIdx.x * kEW + wave;
-  if (g < groups) load_x(g, xb);
-  for (; g < groups; g += g_step) {
-    float4_t acc[4][MT];
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) acc[c][mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const uint8_t *s0 = rl + ((mt * KS + ks) * 2 * 2) * kESeg + lane * 8;
-        const half8_t ah = pack8u(lds_get8(s0), lds_get8(s0 + kESeg));
-        const half8_t al = pack8u(lds_get8(s0 + 2 * kESeg), lds_get8(s0 + 3 * kESeg));
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          acc[c][mt] = mfma16(ah, xb[c][ks], acc[c][mt]);
-          acc[c][mt] = mfma16(al, xb[c][ks], acc[c][mt]);
-        }
-      }
-    // The next group's input streams in while this one is quantised.
-    if (g + g_step < groups) load_x(g + g_step, xb);
+  // Workgroup barrier for LDS hand-offs: unlike __syncthreads it does not
+  // wait for this wave's copies and stores still in flight.
+  auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
-    // ---- per vector: radius tree, direction, index, packing ----
+  const int64_t g_step = gridDim.x;
+  auto run = [&](auto flag) {
+    constexpr bool kTable = decltype(flag)::on;
+    int64_t g = blockIdx.x, g_prev = -1;
+    if (g < groups) issue(g, 0);
+    for (int b = 0; g < groups; g += g_step, b ^= 1) {
+      // this wave's copies of step g and its stores of the step before landed
+      // (the builtin, which the compiler's wait tracking sees: vmcnt 0)
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      barrier();  // step g in xs[b]; xs[b ^ 1] and the stage copy free
+      if (g_prev >= 0) flush(g_prev);
+
+      // ---- rotation: acc[t][mt] = rows of tile mt for vectors 16 t + col ----
+      float4_t acc[kET][MTW];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float y[MT][4];
+      for (int t = 0; t < kET; ++t)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MTW; ++mt) acc[t][mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) y[mt][i] = acc[c][mt][i];
-      int64_t vo_bytes;
-      {
-        const uint32_t v = (uint32_t)g * kEVec + 16 * c + col;
-        uint32_t vo, vi;
-        split(v, vo, vi);
-        vo_bytes = v < n ? (int64_t)vo * a.blocks_outer_stride + (int64_t)vi * VB : -1;
-      }
-      if (rot_out != nullptr && vo_bytes >= 0) {
-        const int64_t v = (int64_t)g * kEVec + 16 * c + col;
+      for (int t = 0; t < kET; ++t)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+        for (int ks = 0; ks < KS; ++ks) {
+          const int vl = 16 * t + col;
+          const half8_t xb = *(const lds_half8 *)(xs[b] + vl * XB + 16 * ((4 * ks + grp) ^ swz(vl)));
 #pragma unroll
-          for (int i = 0; i < 4; ++i) rot_out[v * D + 16 * mt + 4 * grp + i] = y[mt][i];
-      }
-      float r;
-      {
-#pragma clang fp contract(off)
-        float t[MT][4];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) t[mt][i] = y[mt][i] * y[mt][i];
-        // slots 16 mt + 4 grp + i; the s = 64 step exists for D = 128 only
-        float v0[4], v1[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float s0 = t[0][i], s1 = t[1][i], s2 = t[2][i], s3 = t[3][i];
-          if (D == 128) {
-            s0 = s0 + t[4][i];
-            s1 = s1 + t[5][i];
-            s2 = s2 + t[6][i];
-            s3 = s3 + t[7][i];
+          for (int mt = 0; mt < MTW; ++mt) {
+            acc[t][mt] = mfma16(ah[mt][ks], xb, acc[t][mt]);
+            acc[t][mt] = mfma16(al[mt][ks], xb, acc[t][mt]);
           }
-          s0 = s0 + s2;                 // s = 32
-          s1 = s1 + s3;
-          v0[i] = s0 + s1;              // s = 16
-          v0[i] = swap32_add(v0[i]);    // s = 8: slots t, t + 8 (lanes +32)
-          v1[i] = swap16_add(v0[i]);    // s = 4: slots t, t + 4 (lanes +16)
         }
-        const float w0 = v1[0] + v1[2];  // s = 2
-        const float w1 = v1[1] + v1[3];
-        const float tot = w0 + w1;       // s = 1
-        r = (float)__builtin_sqrt((double)tot);
-      }
-      if (radius_out != nullptr && vo_bytes >= 0 && grp == 0) radius_out[(int64_t)g * kEVec + 16 * c + col] = r;
-      const bool nz = r > 1e-30f;
-      int code[MT][4];
-      if constexpr (kTable) {
-        // Fast form for the tile when every radius is zero-like (dir = 0,
-        // reached through inv = 0 on finite y) or finite and >= 2^-40
-        // (Markstein quotient exact, |dir| <= 1 + 11 ulp so the cell needs no
-        // clamp). A NaN radius (dir = 0 by the reference, but y * 0 is NaN)
-        // takes the per-coordinate form.
-        const bool fast = r <= 1e-30f || (r >= 0x1p-40f && r < __builtin_inff());
-        if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
-          const float inv = nz ? __fdiv_rn(1.0f, r) : 0.0f;
+      // The next step's copies go out after this step's reads of xs: issued
+      // earlier, they would make the compiler wait for them before the reads
+      // (it cannot tell xs[b] from xs[b ^ 1]).
+      if (g + g_step < groups) issue(g + g_step, b ^ 1);
+
+      // ---- radius tree, steps s >= 16 in the wave; slots 4 wave + i out.
+      // The swaps pair lanes grp, grp ^ 2 (s = 32) and grp, grp ^ 1 (s = 16)
+      // for two slots at a time, leaving slot i = 2 (grp & 1) + grp / 2 in
+      // lane (col, grp). ----
+      const int my_slot = 2 * (grp & 1) + (grp >> 1);
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              float d;
-              {
+      for (int t = 0; t < kET; ++t) {
+        float z;
+        {
 #pragma clang fp contract(off)
-                const float q0 = y[mt][i] * inv;
-                const float e = __builtin_fmaf(-r, q0, y[mt][i]);
-                d = __builtin_fmaf(e, inv, q0);
-              }
-              const uint2 ce = cells[dir_cell_unclamped(d)];
-              code[mt][i] = (int)ce.x + (d >= __builtin_bit_cast(float, ce.y) ? 1 : 0);
-            }
-        } else {
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              float d = nz ? __fdiv_rn(y[mt][i], r) : 0.0f;
-              d = d == d ? d : -2.0f;  // NaN: index 0, as the scan gives
-              const uint2 ce = cells[dir_cell(d)];
-              code[mt][i] = (int)ce.x + (d >= __builtin_bit_cast(float, ce.y) ? 1 : 0);
-            }
-        }
-      } else {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+          float s[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float d = nz ? __fdiv_rn(y[mt][i], r) : 0.0f;
-            code[mt][i] = scan_index_rolled(d, cb, NL);
+            s[i] = acc[t][0][i] * acc[t][0][i];
+            if constexpr (MTW == 2) s[i] = s[i] + acc[t][1][i] * acc[t][1][i];  // s = 64
           }
+          const float s01 = swap32_pair_add(s[0], s[1]);  // s = 32: slot 0 (lanes < 32), slot 1
+          const float s23 = swap32_pair_add(s[2], s[3]);  // slot 2, slot 3
+          z = swap16_pair_add(s01, s23);                  // s = 16
+        }
+        part[(16 * t + col) * kEPart + 4 * wave + my_slot] = z;
       }
-      if (vo_bytes >= 0) {
-        uint8_t *out = a.blocks + vo_bytes;
-        if (BITS == 4) {
+      barrier();
+      // ---- lane L: steps s = 8 .. 1 of vector L (lanes L mod kEG), its
+      // radius and 1 / r ----
+      const int lv = lane % kEG;
+      const uint32_t vme = (uint32_t)g * kEG + lv;
+      float r, inv;
+      bool fast;
+      {
+#pragma clang fp contract(off)
+        const float4_t p0 = *(const lds_float4 *)(part + lv * kEPart);
+        const float4_t p1 = *(const lds_float4 *)(part + lv * kEPart + 4);
+        const float4_t p2 = *(const lds_float4 *)(part + lv * kEPart + 8);
+        const float4_t p3 = *(const lds_float4 *)(part + lv * kEPart + 12);
+        // slots 0..15 = p0 p1 p2 p3; s = 8: t += t + 8
+        const float q0 = p0[0] + p2[0], q1 = p0[1] + p2[1], q2 = p0[2] + p2[2], q3 = p0[3] + p2[3];
+        const float q4 = p1[0] + p3[0], q5 = p1[1] + p3[1], q6 = p1[2] + p3[2], q7 = p1[3] + p3[3];
+        const float u0 = q0 + q4, u1 = q1 + q5, u2 = q2 + q6, u3 = q3 + q7;  // s = 4
+        const float w0 = u0 + u2, w1 = u1 + u3;                             // s = 2
+        const float tot = w0 + w1;                                          // s = 1
+        r = (float)__builtin_sqrt((double)tot);
+        const bool nz = r > 1e-30f;
+        inv = nz ? __fdiv_rn(1.0f, r) : 0.0f;
+        // zero-like (dir = 0, reached through inv = 0 on finite y) or finite
+        // and >= 2^-40 (Markstein quotient exact, |dir| <= 1 + 11 ulp)
+        fast = r <= 1e-30f || (r >= 0x1p-40f && r < __builtin_inff());
+      }
+      if (vme < n && lane < kEG) {
+        if (wave < D / 32) stage_st16(stg + lv * VB + wave * BB, radius_half_bits(r));
+        if (radius_out != nullptr && wave == 0) radius_out[vme] = r;
+      }
+      // the table's fast form for the step when every radius allows it
+      const bool step_fast = __builtin_amdgcn_ballot_w64(!fast && vme < n) == 0;
+
+      // ---- per tile: directions, indices, packing into the stage copy ----
+      auto quantise = [&](auto fast_flag) {
+      constexpr bool kFast = decltype(fast_flag)::on;
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const uint32_t b2 = (uint32_t)(code[mt][0] | (code[mt][1] << 4)) |
-                                ((uint32_t)(code[mt][2] | (code[mt][3] << 4)) << 8);
-            *(uint16_t *)(out + (mt >> 1) * kPq4BlockBytes + 2 + 8 * (mt & 1) + 2 * grp) = (uint16_t)b2;
-          }
-          if (grp < D / 32) *(uint16_t *)(out + grp * kPq4BlockBytes) = radius_half_bits(r);
-        } else {
+      for (int t = 0; t < kET; ++t) {
+        const int vl = 16 * t + col;
+        const float rt = bperm_f(vl, r), it = bperm_f(vl, inv);
+        const bool nzt = rt > 1e-30f;
+        int code[MTW][4];
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const uint32_t b1 = (uint32_t)(code[mt][0] | (code[mt][1] << 2) | (code[mt][2] << 4) | (code[mt][3] << 6));
-            out[(mt >> 1) * kPq2BlockBytes + 2 + 4 * (mt & 1) + grp] = (uint8_t)b1;
+        for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float y = acc[t][mt][i];
+            if constexpr (kTable) {
+              float d;
+              if constexpr (kFast) {
+#pragma clang fp contract(off)
+                const float q0 = y * it;
+                const float e = __builtin_fmaf(-rt, q0, y);
+                d = __builtin_fmaf(e, it, q0);
+              } else {
+                d = nzt ? __fdiv_rn(y, rt) : 0.0f;
+                d = d == d ? d : -2.0f;  // NaN: index 0, as the scan gives
+                d = __builtin_fminf(__builtin_fmaxf(d, -kEClamp), kEClamp);
+              }
+              const uint2 ce = cells[dir_cell(d)];
+              code[mt][i] = (int)ce.x + (d >= __builtin_bit_cast(float, ce.y) ? 1 : 0);
+            } else {
+              const float d = nzt ? __fdiv_rn(y, rt) : 0.0f;
+              code[mt][i] = scan_index_rolled(d, cb, NL);
+            }
           }
-          if (grp < D / 32) *(uint16_t *)(out + grp * kPq2BlockBytes) = radius_half_bits(r);
+        const uint32_t vg = (uint32_t)g * kEG + vl;
+        if (rot_out != nullptr && vg < n) {
+#pragma unroll
+          for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              rot_out[(int64_t)vg * D + 16 * (4 * mt + grp) + 4 * wave + i] = acc[t][mt][i];
+        }
+        // coordinate j = 16 k + 4 wave + i, k = 4 mt + grp: block k / 2,
+        // qs byte 8 (k & 1) + 2 wave + i / 2 (4-bit) or 4 (k & 1) + wave (2-bit)
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt) {
+          lds_u8 *dst = stg + vl * VB + (2 * mt + (grp >> 1)) * BB + 2;
+          if constexpr (BITS == 4) {
+            const uint32_t h = (uint32_t)(code[mt][0] | (code[mt][1] << 4) | (code[mt][2] << 8) | (code[mt][3] << 12));
+            stage_st16(dst + 8 * (grp & 1) + 2 * wave, h);
+          } else {
+            const uint32_t h = (uint32_t)(code[mt][0] | (code[mt][1] << 2) | (code[mt][2] << 4) | (code[mt][3] << 6));
+            stage_st8(dst + 4 * (grp & 1) + wave, h);
+          }
         }
       }
+      };
+      if (!kTable || step_fast) quantise(TableFlag<true>{});
+      else quantise(TableFlag<false>{});
+      g_prev = g;
     }
-  }
+    barrier();  // the last step's stage copy complete
+    if (g_prev >= 0) flush(g_prev);
   };
   if (table_ok != 0) run(TableFlag<true>{});
   else run(TableFlag<false>{});
@@ -435,11 +523,11 @@ __global__ void __launch_bounds__(kEW * 64, 2) encode_mfma_kernel(const EncodeAr
 
 hipError_t launch_encode_mfma(const EncodeArgs &a, float *rot_out, float *radius_out, int cus, hipStream_t s) {
   const int64_t n = a.n_outer * a.n_inner;
-  const int64_t groups = (n + kEVec - 1) / kEVec;
-  // each workgroup builds its R operand and centroid table once, so one
-  // resident round (the launch bounds give two per CU) loops over the groups
-  int64_t grid = (groups + kEW - 1) / kEW;
-  if (grid > 2 * (int64_t)cus) grid = 2 * (int64_t)cus;
+  const int64_t groups = (n + kEG - 1) / kEG;
+  // each workgroup keeps its share of R in registers and builds its centroid
+  // table once, so one resident round of workgroups loops over the steps
+  int64_t grid = groups;
+  if (grid > kEBlocksPerCU * (int64_t)cus) grid = kEBlocksPerCU * (int64_t)cus;
   if (grid < 1) grid = 1;
 #define PQKV_EM(DD, BB) encode_mfma_kernel<DD, BB><<<(int)grid, kEW * 64, 0, s>>>(a, rot_out, radius_out)
   if (a.d == 128 && a.bits == 4) PQKV_EM(128, 4);
