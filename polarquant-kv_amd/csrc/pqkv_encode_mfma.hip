@@ -44,8 +44,13 @@
 // the index is the reference's. Steps with other radii divide per coordinate.
 //
 // Output: each wave writes its codes (and wave w the radius of block w) into
-// an LDS copy of the step's blocks; the next step stores it with dword
-// writes, so the stores' completion is waited for one step later.
+// an LDS copy of the step's blocks, stored to memory one step later with
+// 16-byte writes (dword writes for strided rows).
+//
+// Schedule: a software pipeline with one workgroup barrier per step. While
+// a wave's matrix-core products rotate step k, its vector ALUs quantise step
+// k - 1 (rotation held in registers); step k + 1's input is in flight and
+// step k - 2's blocks are being written.
 #include "pqkv_device.h"
 #include "pqkv_launch.h"
 
@@ -54,10 +59,13 @@ namespace pqkv {
 namespace {
 
 #ifndef PQKV_ENC_TILES
-#define PQKV_ENC_TILES 2
+#define PQKV_ENC_TILES 4
+#endif
+#ifndef PQKV_ENC_VALU_PER_MFMA
+#define PQKV_ENC_VALU_PER_MFMA 2
 #endif
 #ifndef PQKV_ENC_BLOCKS
-#define PQKV_ENC_BLOCKS 3
+#define PQKV_ENC_BLOCKS 2
 #endif
 constexpr int kEW = 4;              // waves per workgroup
 constexpr int kET = PQKV_ENC_TILES; // 16-vector tiles per workgroup step
@@ -173,11 +181,16 @@ __device__ __forceinline__ float kfloat(int64_t k) {
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
-// Stores into the stage copy of a step's blocks. Written as instructions the
-// compiler's wait tracking does not see: it would otherwise wait for the
-// next step's copies into xs (still in flight, never overlapping the stage
-// copy) before each LDS store. The workgroup barrier that follows the stores
-// waits for them (lgkmcnt 0); as volatile asm they stay in order with it.
+// LDS stores issued while the next step's copies into xs are in flight (the
+// stage copy of a step's blocks, the radius partial sums). Written as
+// instructions the compiler's wait tracking does not see: it would otherwise
+// wait for those copies (which never overlap these buffers) and for the
+// block stores before each LDS store. The workgroup barrier that follows the
+// stores waits for them (lgkmcnt 0); as volatile asm they stay in order with
+// it.
+__device__ __forceinline__ void lds_st32(__attribute__((address_space(3))) float *p, float v) {
+  asm volatile("ds_write_b32 %0, %1" ::"v"((uint32_t)(uintptr_t)p), "v"(v));
+}
 __device__ __forceinline__ void stage_st16(lds_u8 *p, uint32_t v) {
   asm volatile("ds_write_b16 %0, %1" ::"v"((uint32_t)(uintptr_t)p), "v"(v));
 }
@@ -203,16 +216,16 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   constexpr int NCOPY = kEG / VPI;       // copy instructions per step
   constexpr int DW = VB / 4;             // output dwords per vector
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][kEG * XB];
-  __shared__ __attribute__((aligned(16))) float part[kEG * kEPart];
-  __shared__ __attribute__((aligned(16))) uint8_t stage[kEG * VB];
+  __shared__ __attribute__((aligned(16))) float part[2][kEG * kEPart];
+  __shared__ __attribute__((aligned(16))) uint8_t stage[2][kEG * VB];
   __shared__ uint2 cells[kECellSlots];   // (index at the cell start, switch point bits or +inf)
   __shared__ float cb[16], thr[16];
   __shared__ int ucell[16];
   __shared__ int table_ok;
   typedef __attribute__((address_space(3))) uint32_t lds_u32;
-  lds_u8 *const stg = (lds_u8 *)stage;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
   // chunk swizzle of a vector's 16-byte pieces in LDS: the B-operand reads of
   // lanes 0..15 (16 vectors, one chunk each) land in distinct banks
@@ -296,39 +309,37 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   __syncthreads();
 
   const half_t *x = (const half_t *)a.x;
-  // vector v = n_inner * vo + vi; the host keeps n below 2^32
+  // vector v = n_inner * vo + vi; the host keeps n below 2^32 (a single row
+  // has n_inner = n, so vo = 0 there)
   const uint32_t n = (uint32_t)(a.n_outer * a.n_inner);
   const int64_t groups = ((int64_t)n + kEG - 1) / kEG;
   const FastDiv by_inner((uint32_t)a.n_inner);
-  const bool rows = a.n_outer > 1;
   auto split = [&](uint32_t v, uint32_t &vo, uint32_t &vi) {
-    vo = rows ? by_inner.div(v) : 0u;
+    vo = by_inner.div(v);
     vi = v - vo * (uint32_t)a.n_inner;
   };
   // Step g's input into xs[b]: copy instruction q covers vectors q VPI ..,
   // lane L piece L % CH of vector q VPI + L / CH, which holds chunk
-  // (L % CH) ^ swz(vector). Lanes past the end copy nothing.
+  // (L % CH) ^ swz(vector). Lanes past the end copy the last vector again
+  // (into slots no step reads), so the copies need no branch.
+  static_assert(NCOPY % kEW == 0, "copy instructions split evenly over the waves");
   auto issue = [&](int64_t g, int b) {
 #pragma unroll
-    for (int q = wave; q < NCOPY; q += kEW) {
+    for (int j = 0; j < NCOPY / kEW; ++j) {
+      const int q = wave + kEW * j;
       const int vl = q * VPI + lane / CH;
-      const uint32_t v = (uint32_t)g * kEG + vl;
-      if (v < n) {
-        const half_t *row = x + (int64_t)v * D;
-        if (rows) {
-          uint32_t vo, vi;
-          split(v, vo, vi);
-          row = x + (int64_t)vo * a.x_outer_stride + (int64_t)vi * D;
-        }
-        __builtin_amdgcn_global_load_lds((const void *)(row + 8 * ((lane % CH) ^ swz(vl))), (lds_void *)(xs[b] + 1024 * q),
-                                         16, 0, 0);
-      }
+      uint32_t vo, vi;
+      split(min((uint32_t)g * kEG + vl, n - 1), vo, vi);
+      const half_t *row = x + (int64_t)vo * a.x_outer_stride + (int64_t)vi * D;
+      __builtin_amdgcn_global_load_lds((const void *)(row + 8 * ((lane % CH) ^ swz(vl))), (lds_void *)(xs[b] + 1024 * q),
+                                       16, 0, 0);
     }
   };
-  // Step g's blocks from the LDS copy to memory: one run of 16-byte pieces
-  // when the blocks are one aligned run, else dword by dword.
-  const bool run16 = !rows && ((uintptr_t)a.blocks & 15) == 0;
-  auto flush = [&](int64_t g) {
+  // Step g's blocks from stage[sb] to memory: one run of 16-byte pieces when
+  // the blocks are one aligned run, else dword by dword.
+  const bool run16 = a.n_outer <= 1 && ((uintptr_t)a.blocks & 15) == 0;
+  auto flush = [&](int64_t g, int sb) {
+    const lds_u8 *stg = (const lds_u8 *)stage[sb];
     if (run16) {
       const uint32_t v0 = (uint32_t)g * kEG;
       const int nbytes = (int)min(n - v0, (uint32_t)kEG) * VB;
@@ -363,159 +374,218 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   // Workgroup barrier for LDS hand-offs: unlike __syncthreads it does not
   // wait for this wave's copies and stores still in flight.
   auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+  // Wait for this wave's copies and stores (the builtin, which the
+  // compiler's wait tracking sees: vmcnt 0).
+  auto wait_mem = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };
 
-  const int64_t g_step = gridDim.x;
-  auto run = [&](auto flag) {
-    constexpr bool kTable = decltype(flag)::on;
-    int64_t g = blockIdx.x, g_prev = -1;
-    if (g < groups) issue(g, 0);
-    for (int b = 0; g < groups; g += g_step, b ^= 1) {
-      // this wave's copies of step g and its stores of the step before landed
-      // (the builtin, which the compiler's wait tracking sees: vmcnt 0)
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-      barrier();  // step g in xs[b]; xs[b ^ 1] and the stage copy free
-      if (g_prev >= 0) flush(g_prev);
-
-      // ---- rotation: acc[t][mt] = rows of tile mt for vectors 16 t + col ----
-      float4_t acc[kET][MTW];
+  typedef float4_t Tile[kET][MTW];
+  // ---- rotation of the step in xs[b]: y[t][mt] = rows of tile mt for
+  // vectors 16 t + col ----
+  auto rotate = [&](int b, Tile &y) {
 #pragma unroll
-      for (int t = 0; t < kET; ++t)
+    for (int t = 0; t < kET; ++t)
 #pragma unroll
-        for (int mt = 0; mt < MTW; ++mt) acc[t][mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+      for (int mt = 0; mt < MTW; ++mt) y[t][mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int t = 0; t < kET; ++t)
+    for (int t = 0; t < kET; ++t)
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const int vl = 16 * t + col;
-          const half8_t xb = *(const lds_half8 *)(xs[b] + vl * XB + 16 * ((4 * ks + grp) ^ swz(vl)));
+      for (int ks = 0; ks < KS; ++ks) {
+        const int vl = 16 * t + col;
+        const half8_t xb = *(const lds_half8 *)(xs[b] + vl * XB + 16 * ((4 * ks + grp) ^ swz(vl)));
 #pragma unroll
-          for (int mt = 0; mt < MTW; ++mt) {
-            acc[t][mt] = mfma16(ah[mt][ks], xb, acc[t][mt]);
-            acc[t][mt] = mfma16(al[mt][ks], xb, acc[t][mt]);
-          }
+        for (int mt = 0; mt < MTW; ++mt) {
+          y[t][mt] = mfma16(ah[mt][ks], xb, y[t][mt]);
+          y[t][mt] = mfma16(al[mt][ks], xb, y[t][mt]);
         }
-      // The next step's copies go out after this step's reads of xs: issued
-      // earlier, they would make the compiler wait for them before the reads
-      // (it cannot tell xs[b] from xs[b ^ 1]).
-      if (g + g_step < groups) issue(g + g_step, b ^ 1);
-
-      // ---- radius tree, steps s >= 16 in the wave; slots 4 wave + i out.
-      // The swaps pair lanes grp, grp ^ 2 (s = 32) and grp, grp ^ 1 (s = 16)
-      // for two slots at a time, leaving slot i = 2 (grp & 1) + grp / 2 in
-      // lane (col, grp). ----
-      const int my_slot = 2 * (grp & 1) + (grp >> 1);
-#pragma unroll
-      for (int t = 0; t < kET; ++t) {
-        float z;
-        {
-#pragma clang fp contract(off)
-          float s[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            s[i] = acc[t][0][i] * acc[t][0][i];
-            if constexpr (MTW == 2) s[i] = s[i] + acc[t][1][i] * acc[t][1][i];  // s = 64
-          }
-          const float s01 = swap32_pair_add(s[0], s[1]);  // s = 32: slot 0 (lanes < 32), slot 1
-          const float s23 = swap32_pair_add(s[2], s[3]);  // slot 2, slot 3
-          z = swap16_pair_add(s01, s23);                  // s = 16
-        }
-        part[(16 * t + col) * kEPart + 4 * wave + my_slot] = z;
       }
-      barrier();
-      // ---- lane L: steps s = 8 .. 1 of vector L (lanes L mod kEG), its
-      // radius and 1 / r ----
-      const int lv = lane % kEG;
-      const uint32_t vme = (uint32_t)g * kEG + lv;
-      float r, inv;
-      bool fast;
+  };
+  // ---- radius tree, steps s >= 16 in the wave, into part[pb]: slots
+  // 4 wave + i. The swaps pair lanes grp, grp ^ 2 (s = 32) and grp, grp ^ 1
+  // (s = 16) for two slots at a time, leaving slot i = 2 (grp & 1) + grp / 2
+  // in lane (col, grp). ----
+  const int my_slot = 2 * (grp & 1) + (grp >> 1);
+  auto tree = [&](const Tile &y, int pb) {
+#pragma unroll
+    for (int t = 0; t < kET; ++t) {
+      float z;
       {
 #pragma clang fp contract(off)
-        const float4_t p0 = *(const lds_float4 *)(part + lv * kEPart);
-        const float4_t p1 = *(const lds_float4 *)(part + lv * kEPart + 4);
-        const float4_t p2 = *(const lds_float4 *)(part + lv * kEPart + 8);
-        const float4_t p3 = *(const lds_float4 *)(part + lv * kEPart + 12);
-        // slots 0..15 = p0 p1 p2 p3; s = 8: t += t + 8
-        const float q0 = p0[0] + p2[0], q1 = p0[1] + p2[1], q2 = p0[2] + p2[2], q3 = p0[3] + p2[3];
-        const float q4 = p1[0] + p3[0], q5 = p1[1] + p3[1], q6 = p1[2] + p3[2], q7 = p1[3] + p3[3];
-        const float u0 = q0 + q4, u1 = q1 + q5, u2 = q2 + q6, u3 = q3 + q7;  // s = 4
-        const float w0 = u0 + u2, w1 = u1 + u3;                             // s = 2
-        const float tot = w0 + w1;                                          // s = 1
-        r = (float)__builtin_sqrt((double)tot);
-        const bool nz = r > 1e-30f;
-        inv = nz ? __fdiv_rn(1.0f, r) : 0.0f;
-        // zero-like (dir = 0, reached through inv = 0 on finite y) or finite
-        // and >= 2^-40 (Markstein quotient exact, |dir| <= 1 + 11 ulp)
-        fast = r <= 1e-30f || (r >= 0x1p-40f && r < __builtin_inff());
-      }
-      if (vme < n && lane < kEG) {
-        if (wave < D / 32) stage_st16(stg + lv * VB + wave * BB, radius_half_bits(r));
-        if (radius_out != nullptr && wave == 0) radius_out[vme] = r;
-      }
-      // the table's fast form for the step when every radius allows it
-      const bool step_fast = __builtin_amdgcn_ballot_w64(!fast && vme < n) == 0;
-
-      // ---- per tile: directions, indices, packing into the stage copy ----
-      auto quantise = [&](auto fast_flag) {
-      constexpr bool kFast = decltype(fast_flag)::on;
+        float s[4];
 #pragma unroll
-      for (int t = 0; t < kET; ++t) {
-        const int vl = 16 * t + col;
-        const float rt = bperm_f(vl, r), it = bperm_f(vl, inv);
-        const bool nzt = rt > 1e-30f;
-        int code[MTW][4];
+        for (int i = 0; i < 4; ++i) {
+          s[i] = y[t][0][i] * y[t][0][i];
+          if constexpr (MTW == 2) s[i] = s[i] + y[t][1][i] * y[t][1][i];  // s = 64
+        }
+        const float s01 = swap32_pair_add(s[0], s[1]);  // s = 32: slot 0 (lanes < 32), slot 1
+        const float s23 = swap32_pair_add(s[2], s[3]);  // slot 2, slot 3
+        z = swap16_pair_add(s01, s23);                  // s = 16
+      }
+      lds_st32((__attribute__((address_space(3))) float *)part[pb] + (16 * t + col) * kEPart + 4 * wave + my_slot, z);
+    }
+  };
+  // ---- lane L: steps s = 8 .. 1 of vector L (lanes L mod kEG) of step g
+  // from part[pb], its radius (into stage[sb]) and 1 / r; whether the whole
+  // step takes the table's fast form ----
+  auto finish = [&](int64_t g, int pb, int sb, float &r, float &inv) -> bool {
+    const int lv = lane % kEG;
+    const uint32_t vme = (uint32_t)g * kEG + lv;
+    bool fast;
+    {
+#pragma clang fp contract(off)
+      const float *pp = part[pb] + lv * kEPart;
+      const float4_t p0 = *(const lds_float4 *)(pp), p1 = *(const lds_float4 *)(pp + 4);
+      const float4_t p2 = *(const lds_float4 *)(pp + 8), p3 = *(const lds_float4 *)(pp + 12);
+      // slots 0..15 = p0 p1 p2 p3; s = 8: t += t + 8
+      const float q0 = p0[0] + p2[0], q1 = p0[1] + p2[1], q2 = p0[2] + p2[2], q3 = p0[3] + p2[3];
+      const float q4 = p1[0] + p3[0], q5 = p1[1] + p3[1], q6 = p1[2] + p3[2], q7 = p1[3] + p3[3];
+      const float u0 = q0 + q4, u1 = q1 + q5, u2 = q2 + q6, u3 = q3 + q7;  // s = 4
+      const float w0 = u0 + u2, w1 = u1 + u3;                             // s = 2
+      const float tot = w0 + w1;                                          // s = 1
+      r = (float)__builtin_sqrt((double)tot);
+      const bool nz = r > 1e-30f;
+      inv = nz ? __fdiv_rn(1.0f, r) : 0.0f;
+      // zero-like (dir = 0, reached through inv = 0 on finite y) or finite
+      // and >= 2^-40 (Markstein quotient exact, |dir| <= 1 + 11 ulp)
+      fast = r <= 1e-30f || (r >= 0x1p-40f && r < __builtin_inff());
+    }
+    if (vme < n && lane < kEG) {
+      if (wave < D / 32) stage_st16((lds_u8 *)stage[sb] + lv * VB + wave * BB, radius_half_bits(r));
+      if (radius_out != nullptr && wave == 0) radius_out[vme] = r;
+    }
+    return __builtin_amdgcn_ballot_w64(!fast && vme < n) == 0;
+  };
+  // ---- directions, indices, packing of step g (rotation y, radii r / inv
+  // held by lane 16 t + col) into stage[sb] ----
+  auto quantise = [&](auto table_flag, auto fast_flag, const Tile &y, int sb, float r, float inv) {
+    constexpr bool kTable = decltype(table_flag)::on;
+    constexpr bool kFast = decltype(fast_flag)::on;
+#pragma unroll
+    for (int t = 0; t < kET; ++t) {
+      const int vl = 16 * t + col;
+      const float rt = bperm_f(vl, r), it = bperm_f(vl, inv);
+      const bool nzt = rt > 1e-30f;
+      int code[MTW][4];
+#pragma unroll
+      for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float yv = y[t][mt][i];
+          if constexpr (kTable) {
+            float d;
+            if constexpr (kFast) {
+#pragma clang fp contract(off)
+              const float q0 = yv * it;
+              const float e = __builtin_fmaf(-rt, q0, yv);
+              d = __builtin_fmaf(e, it, q0);
+            } else {
+              d = nzt ? __fdiv_rn(yv, rt) : 0.0f;
+              d = d == d ? d : -2.0f;  // NaN: index 0, as the scan gives
+              d = __builtin_fminf(__builtin_fmaxf(d, -kEClamp), kEClamp);
+            }
+            const uint2 ce = cells[dir_cell(d)];
+            code[mt][i] = (int)ce.x + (d >= __builtin_bit_cast(float, ce.y) ? 1 : 0);
+          } else {
+            const float d = nzt ? __fdiv_rn(yv, rt) : 0.0f;
+            code[mt][i] = scan_index_rolled(d, cb, NL);
+          }
+        }
+      // coordinate j = 16 k + 4 wave + i, k = 4 mt + grp: block k / 2,
+      // qs byte 8 (k & 1) + 2 wave + i / 2 (4-bit) or 4 (k & 1) + wave (2-bit)
+#pragma unroll
+      for (int mt = 0; mt < MTW; ++mt) {
+        lds_u8 *dst = (lds_u8 *)stage[sb] + vl * VB + (2 * mt + (grp >> 1)) * BB + 2;
+        if constexpr (BITS == 4) {
+          const uint32_t h = (uint32_t)(code[mt][0] | (code[mt][1] << 4) | (code[mt][2] << 8) | (code[mt][3] << 12));
+          stage_st16(dst + 8 * (grp & 1) + 2 * wave, h);
+        } else {
+          const uint32_t h = (uint32_t)(code[mt][0] | (code[mt][1] << 2) | (code[mt][2] << 4) | (code[mt][3] << 6));
+          stage_st8(dst + 4 * (grp & 1) + wave, h);
+        }
+      }
+    }
+  };
+  auto store_rot = [&](const Tile &y, int64_t g) {
+    if (rot_out == nullptr) return;
+#pragma unroll
+    for (int t = 0; t < kET; ++t) {
+      const uint32_t vg = (uint32_t)g * kEG + 16 * t + col;
+      if (vg < n) {
 #pragma unroll
         for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float y = acc[t][mt][i];
-            if constexpr (kTable) {
-              float d;
-              if constexpr (kFast) {
-#pragma clang fp contract(off)
-                const float q0 = y * it;
-                const float e = __builtin_fmaf(-rt, q0, y);
-                d = __builtin_fmaf(e, it, q0);
-              } else {
-                d = nzt ? __fdiv_rn(y, rt) : 0.0f;
-                d = d == d ? d : -2.0f;  // NaN: index 0, as the scan gives
-                d = __builtin_fminf(__builtin_fmaxf(d, -kEClamp), kEClamp);
-              }
-              const uint2 ce = cells[dir_cell(d)];
-              code[mt][i] = (int)ce.x + (d >= __builtin_bit_cast(float, ce.y) ? 1 : 0);
-            } else {
-              const float d = nzt ? __fdiv_rn(y, rt) : 0.0f;
-              code[mt][i] = scan_index_rolled(d, cb, NL);
-            }
-          }
-        const uint32_t vg = (uint32_t)g * kEG + vl;
-        if (rot_out != nullptr && vg < n) {
-#pragma unroll
-          for (int mt = 0; mt < MTW; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              rot_out[(int64_t)vg * D + 16 * (4 * mt + grp) + 4 * wave + i] = acc[t][mt][i];
-        }
-        // coordinate j = 16 k + 4 wave + i, k = 4 mt + grp: block k / 2,
-        // qs byte 8 (k & 1) + 2 wave + i / 2 (4-bit) or 4 (k & 1) + wave (2-bit)
-#pragma unroll
-        for (int mt = 0; mt < MTW; ++mt) {
-          lds_u8 *dst = stg + vl * VB + (2 * mt + (grp >> 1)) * BB + 2;
-          if constexpr (BITS == 4) {
-            const uint32_t h = (uint32_t)(code[mt][0] | (code[mt][1] << 4) | (code[mt][2] << 8) | (code[mt][3] << 12));
-            stage_st16(dst + 8 * (grp & 1) + 2 * wave, h);
-          } else {
-            const uint32_t h = (uint32_t)(code[mt][0] | (code[mt][1] << 2) | (code[mt][2] << 4) | (code[mt][3] << 6));
-            stage_st8(dst + 4 * (grp & 1) + wave, h);
-          }
-        }
+          for (int i = 0; i < 4; ++i) rot_out[(int64_t)vg * D + 16 * (4 * mt + grp) + 4 * wave + i] = y[t][mt][i];
       }
-      };
-      if (!kTable || step_fast) quantise(TableFlag<true>{});
-      else quantise(TableFlag<false>{});
-      g_prev = g;
     }
-    barrier();  // the last step's stage copy complete
-    if (g_prev >= 0) flush(g_prev);
+  };
+
+  // Software pipeline over the workgroup's steps g0, g0 + G, ...: iteration k
+  // rotates step g_k (input in xs[k & 1], tree partials into part[k & 1]),
+  // copies step g_{k+1} into xs[(k + 1) & 1], quantises step g_{k-1} (rotation
+  // kept in registers, partials from part[(k - 1) & 1]) into stage[k & 1] and
+  // stores step g_{k-2} from stage[(k - 2) & 1]: one workgroup barrier per
+  // step, and each wave's matrix-core products of one step run beside its
+  // quantiser arithmetic of the step before.
+  const int64_t g_step = gridDim.x;
+  auto run = [&](auto table_flag) {
+    constexpr bool kTable = decltype(table_flag)::on;
+    int64_t g = blockIdx.x;
+    Tile acc, accp;
+    issue(g, 0);
+    wait_mem();
+    barrier();
+    rotate(0, acc);
+    if (g + g_step < groups) issue(g + g_step, 1);
+    tree(acc, 0);
+    store_rot(acc, g);
+    int64_t gp = g, gpp = -1;
+    int k = 1;
+    for (g += g_step; g < groups; g += g_step, ++k) {
+      const int b = k & 1;
+#pragma unroll
+      for (int t = 0; t < kET; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt) accp[t][mt] = acc[t][mt];
+      wait_mem();
+      barrier();  // xs[b], part[b ^ 1] and stage[b ^ 1] complete; xs[b ^ 1], part[b], stage[b] free
+      if (gpp >= 0) flush(gpp, b ^ 1);
+      float r, inv;
+      const bool step_fast = finish(gp, b ^ 1, b, r, inv);
+      // the step whose input goes into xs[b ^ 1]: the next one, or this one
+      // again at the end (a copy nothing reads), so the body has no branch
+      const int64_t g_next = g + g_step < groups ? g + g_step : g;
+      auto body = [&](auto fast_flag) {
+        rotate(b, acc);
+        // the next step's copies go out after this step's reads of xs:
+        // issued earlier, the compiler would wait for them before the reads
+        // (it cannot tell xs[b] from xs[b ^ 1])
+        issue(g_next, b ^ 1);
+        quantise(table_flag, fast_flag, accp, b, r, inv);
+        tree(acc, b);
+        // interleave the rotation's matrix-core products with the previous
+        // step's quantiser arithmetic: one product, then two vector ops
+#pragma unroll
+        for (int i = 0; i < kET * KS * MTW * 2; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, PQKV_ENC_VALU_PER_MFMA, 0);
+        }
+      };
+      if (!kTable || step_fast) body(TableFlag<true>{});
+      else body(TableFlag<false>{});
+      store_rot(acc, g);
+      gpp = gp;
+      gp = g;
+    }
+    // the last step: quantise, then store it and the one before
+    const int b = k & 1;
+    wait_mem();
+    barrier();
+    if (gpp >= 0) flush(gpp, b ^ 1);
+    float r, inv;
+    const bool step_fast = finish(gp, b ^ 1, b, r, inv);
+    if (!kTable || step_fast) quantise(table_flag, TableFlag<true>{}, acc, b, r, inv);
+    else quantise(table_flag, TableFlag<false>{}, acc, b, r, inv);
+    barrier();
+    flush(gp, b);
   };
   if (table_ok != 0) run(TableFlag<true>{});
   else run(TableFlag<false>{});
