@@ -305,14 +305,17 @@ int encode_validate(const void *x, int x_dtype, int64_t x_outer_stride, const fl
   return 1;  // valid, work to do
 }
 
-// The matrix-core encoder takes fp16 input without QJL whose rows and R allow
-// 16-byte loads, and blocks that allow dword stores.
+// The matrix-core encoder takes fp16 input whose rows and R (and P_rot) allow
+// 16-byte loads, and blocks (and signs) that allow dword stores.
 bool fast_encode_ok(const void *x, int x_dtype, int64_t x_outer_stride, int64_t n_outer, int64_t n_inner,
-                    const float *R, const uint8_t *qjl, const uint8_t *blocks, int64_t blocks_outer_stride) {
-  if (x_dtype != PQKV_F16 || qjl != nullptr) return false;
+                    const float *R, const float *p_rot, const uint8_t *qjl, int64_t qjl_outer_stride,
+                    const uint8_t *blocks, int64_t blocks_outer_stride) {
+  if (x_dtype != PQKV_F16) return false;
   if ((uintptr_t)x % 16 || (uintptr_t)R % 16 || (uintptr_t)blocks % 4) return false;
+  if (qjl != nullptr && ((uintptr_t)p_rot % 16 || (uintptr_t)qjl % 4)) return false;
   if (n_outer * n_inner > ((int64_t)1 << 32) - 64) return false;  // 32-bit vector indices
-  return n_outer <= 1 || (x_outer_stride % 8 == 0 && blocks_outer_stride % 4 == 0);
+  return n_outer <= 1 || (x_outer_stride % 8 == 0 && blocks_outer_stride % 4 == 0 &&
+                          (qjl == nullptr || qjl_outer_stride % 4 == 0));
 }
 
 // Rows that follow each other with no gap in x, the blocks and the signs are
@@ -347,7 +350,8 @@ int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride, const float 
   const char *env = getenv("PQKV_ENCODE_KERNEL");
   const bool exact = env && strcmp(env, "exact") == 0;
   hipError_t e;
-  if (!exact && fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, n_inner, R, qjl, blocks, blocks_outer_stride)) {
+  if (!exact && fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, n_inner, R, p_rot, qjl, qjl_outer_stride, blocks,
+                                 blocks_outer_stride)) {
     const int tok = pqkv::prof_begin("encode_mfma", (hipStream_t)stream);
     e = pqkv::launch_encode_mfma(a, nullptr, nullptr, device_cus(), (hipStream_t)stream);
     pqkv::prof_end(tok, (hipStream_t)stream);
@@ -365,7 +369,8 @@ int pqkv_encode_mfma(const void *x, int x_dtype, int64_t x_outer_stride, const f
   const int v = encode_validate(x, x_dtype, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride, n_outer,
                                 n_inner, d, nullptr, 0, nullptr, 0);
   if (v <= 0) return v;
-  if (!fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, n_inner, R, nullptr, blocks, blocks_outer_stride))
+  if (!fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, n_inner, R, nullptr, nullptr, 0, blocks,
+                      blocks_outer_stride))
     return fail(PQKV_ERR_UNSUPPORTED,
                 "encode_mfma: needs fp16 x, 16-byte aligned x rows and R, 4-byte aligned blocks, < 2^32 vectors");
   const pqkv::EncodeArgs a = encode_args(x, x_outer_stride, R, codebook, n_bits, blocks, blocks_outer_stride,

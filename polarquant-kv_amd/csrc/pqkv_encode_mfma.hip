@@ -47,6 +47,15 @@
 // an LDS copy of the step's blocks, stored to memory one step later with
 // 16-byte writes (dword writes for strided rows).
 //
+// QJL keys (m = d projections): the quantiser also writes the residual
+// e = y - r c[code] (fp32 r) times 1 / r into LDS as fp16 hi / lo planes, and
+// one step later wave w computes projections (d / 4) w .. of P_rot e on the
+// matrix cores (P_rot = P R^T split hi / lo in registers like R; three
+// products per tile product, ~2^-21 relative) and packs sign bit m =
+// (P_rot e)[m] >= 0, LSB first. Scaling e by 1 / r keeps the fp16 planes in
+// range and leaves every sign as it is. Steps are 32 vectors there (register
+// and LDS room for P).
+//
 // Schedule: a software pipeline with one workgroup barrier per step. While
 // a wave's matrix-core products rotate step k, its vector ALUs quantise step
 // k - 1 (rotation held in registers); step k + 1's input is in flight and
@@ -191,6 +200,13 @@ typedef __attribute__((address_space(3))) uint8_t lds_u8;
 __device__ __forceinline__ void lds_st32(__attribute__((address_space(3))) float *p, float v) {
   asm volatile("ds_write_b32 %0, %1" ::"v"((uint32_t)(uintptr_t)p), "v"(v));
 }
+__device__ __forceinline__ void lds_st64(__attribute__((address_space(3))) half_t *p, uint64_t v) {
+  asm volatile("ds_write_b64 %0, %1" ::"v"((uint32_t)(uintptr_t)p), "v"(v));
+}
+__device__ __forceinline__ uint32_t pack_h2(half_t a, half_t b) {
+  half2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, v);
+}
 __device__ __forceinline__ void stage_st16(lds_u8 *p, uint32_t v) {
   asm volatile("ds_write_b16 %0, %1" ::"v"((uint32_t)(uintptr_t)p), "v"(v));
 }
@@ -202,9 +218,11 @@ typedef __attribute__((address_space(3))) float4_t lds_float4;
 
 }  // namespace
 
-template <int D, int BITS>
+template <int D, int BITS, bool QJL>
 __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(const EncodeArgs a, float *rot_out,
                                                                                 float *radius_out) {
+  constexpr int ET = QJL ? 2 : kET;      // 16-vector tiles per step (QJL: register and LDS room for P)
+  constexpr int EG = 16 * ET;            // vectors per step
   constexpr int KS = D / 32;             // k-steps over input coordinates
   constexpr int MTW = D / 64;            // 16-row output tiles per wave
   constexpr int NL = 1 << BITS;
@@ -213,11 +231,17 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   constexpr int XB = 2 * D;              // input bytes per vector
   constexpr int CH = XB / 16;            // 16-byte chunks per vector
   constexpr int VPI = 1024 / XB;         // vectors per wave copy instruction (64 lanes x 16 bytes)
-  constexpr int NCOPY = kEG / VPI;       // copy instructions per step
+  constexpr int NCOPY = EG / VPI;       // copy instructions per step
   constexpr int DW = VB / 4;             // output dwords per vector
-  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kEG * XB];
-  __shared__ __attribute__((aligned(16))) float part[2][kEG * kEPart];
-  __shared__ __attribute__((aligned(16))) uint8_t stage[2][kEG * VB];
+  constexpr int SB = D / 8;              // sign bytes per vector (m = d projections)
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][EG * XB];
+  __shared__ __attribute__((aligned(16))) float part[2][EG * kEPart];
+  __shared__ __attribute__((aligned(16))) uint8_t stage[2][EG * VB];
+  // QJL: the step's rotated residuals scaled by 1 / r, as the B operand of the
+  // sign product (fp16 hi / lo planes, chunk-swizzled like xs), and the
+  // step's sign bytes
+  __shared__ __attribute__((aligned(16))) half_t ebuf[2][QJL ? 2 * EG * D : 8];
+  __shared__ __attribute__((aligned(16))) uint8_t sstage[2][QJL ? EG * SB : 16];
   __shared__ uint2 cells[kECellSlots];   // (index at the cell start, switch point bits or +inf)
   __shared__ float cb[16], thr[16];
   __shared__ int ucell[16];
@@ -250,6 +274,26 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
         al[mt][ks][e] = (half_t)(rv[e] - (float)h);
       }
     }
+  // QJL: P_rot = P R^T as the A operand of the sign product, the same way:
+  // row p of tile mt is projection (d / 4) wave + 16 mt + p
+  half8_t ph[QJL ? MTW : 1][KS], pl[QJL ? MTW : 1][KS];
+  if constexpr (QJL) {
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int mrow = (D / 4) * wave + 16 * mt + col;
+        const float4 *pr = (const float4 *)(a.p_rot + (int64_t)mrow * D + 32 * ks + 8 * grp);
+        const float4 r0 = pr[0], r1 = pr[1];
+        const float rv[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const half_t h = (half_t)rv[e];
+          ph[mt][ks][e] = h;
+          pl[mt][ks][e] = (half_t)(rv[e] - (float)h);
+        }
+      }
+  }
 
   if (tid < 16) cb[tid] = tid < NL ? a.codebook[tid] : 0.0f;
   if (tid == 0) table_ok = 1;
@@ -312,7 +356,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   // vector v = n_inner * vo + vi; the host keeps n below 2^32 (a single row
   // has n_inner = n, so vo = 0 there)
   const uint32_t n = (uint32_t)(a.n_outer * a.n_inner);
-  const int64_t groups = ((int64_t)n + kEG - 1) / kEG;
+  const int64_t groups = ((int64_t)n + EG - 1) / EG;
   const FastDiv by_inner((uint32_t)a.n_inner);
   auto split = [&](uint32_t v, uint32_t &vo, uint32_t &vi) {
     vo = by_inner.div(v);
@@ -329,7 +373,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
       const int q = wave + kEW * j;
       const int vl = q * VPI + lane / CH;
       uint32_t vo, vi;
-      split(min((uint32_t)g * kEG + vl, n - 1), vo, vi);
+      split(min((uint32_t)g * EG + vl, n - 1), vo, vi);
       const half_t *row = x + (int64_t)vo * a.x_outer_stride + (int64_t)vi * D;
       __builtin_amdgcn_global_load_lds((const void *)(row + 8 * ((lane % CH) ^ swz(vl))), (lds_void *)(xs[b] + 1024 * q),
                                        16, 0, 0);
@@ -341,11 +385,11 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   auto flush = [&](int64_t g, int sb) {
     const lds_u8 *stg = (const lds_u8 *)stage[sb];
     if (run16) {
-      const uint32_t v0 = (uint32_t)g * kEG;
-      const int nbytes = (int)min(n - v0, (uint32_t)kEG) * VB;
+      const uint32_t v0 = (uint32_t)g * EG;
+      const int nbytes = (int)min(n - v0, (uint32_t)EG) * VB;
       uint8_t *base = a.blocks + (int64_t)v0 * VB;
 #pragma unroll
-      for (int it = 0; it < (kEG * VB / 16 + kEW * 64 - 1) / (kEW * 64); ++it) {
+      for (int it = 0; it < (EG * VB / 16 + kEW * 64 - 1) / (kEW * 64); ++it) {
         const int p = tid + kEW * 64 * it;
         if (16 * p + 16 <= nbytes) {
           *(u32x4 *)(base + 16 * p) = *(const __attribute__((address_space(3))) u32x4 *)(stg + 16 * p);
@@ -357,11 +401,11 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
       return;
     }
 #pragma unroll
-    for (int it = 0; it < (kEG * DW + kEW * 64 - 1) / (kEW * 64); ++it) {
+    for (int it = 0; it < (EG * DW + kEW * 64 - 1) / (kEW * 64); ++it) {
       const int q = tid + kEW * 64 * it;
-      if (q < kEG * DW) {
+      if (q < EG * DW) {
         const int vl = q / DW, c = q - vl * DW;
-        const uint32_t v = (uint32_t)g * kEG + vl;
+        const uint32_t v = (uint32_t)g * EG + vl;
         if (v < n) {
           uint32_t vo, vi;
           split(v, vo, vi);
@@ -378,16 +422,16 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   // compiler's wait tracking sees: vmcnt 0).
   auto wait_mem = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };
 
-  typedef float4_t Tile[kET][MTW];
+  typedef float4_t Tile[ET][MTW];
   // ---- rotation of the step in xs[b]: y[t][mt] = rows of tile mt for
   // vectors 16 t + col ----
   auto rotate = [&](int b, Tile &y) {
 #pragma unroll
-    for (int t = 0; t < kET; ++t)
+    for (int t = 0; t < ET; ++t)
 #pragma unroll
       for (int mt = 0; mt < MTW; ++mt) y[t][mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < kET; ++t)
+    for (int t = 0; t < ET; ++t)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int vl = 16 * t + col;
@@ -406,7 +450,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   const int my_slot = 2 * (grp & 1) + (grp >> 1);
   auto tree = [&](const Tile &y, int pb) {
 #pragma unroll
-    for (int t = 0; t < kET; ++t) {
+    for (int t = 0; t < ET; ++t) {
       float z;
       {
 #pragma clang fp contract(off)
@@ -423,12 +467,12 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
       lds_st32((__attribute__((address_space(3))) float *)part[pb] + (16 * t + col) * kEPart + 4 * wave + my_slot, z);
     }
   };
-  // ---- lane L: steps s = 8 .. 1 of vector L (lanes L mod kEG) of step g
+  // ---- lane L: steps s = 8 .. 1 of vector L (lanes L mod EG) of step g
   // from part[pb], its radius (into stage[sb]) and 1 / r; whether the whole
   // step takes the table's fast form ----
   auto finish = [&](int64_t g, int pb, int sb, float &r, float &inv) -> bool {
-    const int lv = lane % kEG;
-    const uint32_t vme = (uint32_t)g * kEG + lv;
+    const int lv = lane % EG;
+    const uint32_t vme = (uint32_t)g * EG + lv;
     bool fast;
     {
 #pragma clang fp contract(off)
@@ -448,7 +492,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
       // and >= 2^-40 (Markstein quotient exact, |dir| <= 1 + 11 ulp)
       fast = r <= 1e-30f || (r >= 0x1p-40f && r < __builtin_inff());
     }
-    if (vme < n && lane < kEG) {
+    if (vme < n && lane < EG) {
       if (wave < D / 32) stage_st16((lds_u8 *)stage[sb] + lv * VB + wave * BB, radius_half_bits(r));
       if (radius_out != nullptr && wave == 0) radius_out[vme] = r;
     }
@@ -460,7 +504,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
     constexpr bool kTable = decltype(table_flag)::on;
     constexpr bool kFast = decltype(fast_flag)::on;
 #pragma unroll
-    for (int t = 0; t < kET; ++t) {
+    for (int t = 0; t < ET; ++t) {
       const int vl = 16 * t + col;
       const float rt = bperm_f(vl, r), it = bperm_f(vl, inv);
       const bool nzt = rt > 1e-30f;
@@ -489,6 +533,27 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
             code[mt][i] = scan_index_rolled(d, cb, NL);
           }
         }
+      if constexpr (QJL) {
+        // residual e = y - r c[code] (fp32 r), times 1 / r (the signs do not
+        // change; fp16 planes cannot hold e itself), into ebuf[sb]: four
+        // coordinates 16 (4 mt + grp) + 4 wave .. + 3 per (lane, mt)
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt) {
+          half_t hv[4], lv[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float e = __builtin_fmaf(-rt, cb[code[mt][i]], y[t][mt][i]) * it;
+            hv[i] = (half_t)e;
+            lv[i] = (half_t)(e - (float)hv[i]);
+          }
+          const int j0 = 16 * (4 * mt + grp) + 4 * wave;
+          const int off = vl * D + 8 * ((j0 >> 3) ^ swz(vl)) + (j0 & 7);
+          const uint64_t hq = (uint64_t)pack_h2(hv[0], hv[1]) | ((uint64_t)pack_h2(hv[2], hv[3]) << 32);
+          const uint64_t lq = (uint64_t)pack_h2(lv[0], lv[1]) | ((uint64_t)pack_h2(lv[2], lv[3]) << 32);
+          lds_st64((__attribute__((address_space(3))) half_t *)ebuf[sb] + off, hq);
+          lds_st64((__attribute__((address_space(3))) half_t *)ebuf[sb] + EG * D + off, lq);
+        }
+      }
       // coordinate j = 16 k + 4 wave + i, k = 4 mt + grp: block k / 2,
       // qs byte 8 (k & 1) + 2 wave + i / 2 (4-bit) or 4 (k & 1) + wave (2-bit)
 #pragma unroll
@@ -507,14 +572,118 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   auto store_rot = [&](const Tile &y, int64_t g) {
     if (rot_out == nullptr) return;
 #pragma unroll
-    for (int t = 0; t < kET; ++t) {
-      const uint32_t vg = (uint32_t)g * kEG + 16 * t + col;
+    for (int t = 0; t < ET; ++t) {
+      const uint32_t vg = (uint32_t)g * EG + 16 * t + col;
       if (vg < n) {
 #pragma unroll
         for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) rot_out[(int64_t)vg * D + 16 * (4 * mt + grp) + 4 * wave + i] = y[t][mt][i];
       }
+    }
+  };
+
+  const int64_t g_step = gridDim.x;  // a workgroup's steps are blockIdx.x + k gridDim.x
+
+  // ---- QJL sign product of the step whose residuals are in ebuf[eb]: wave
+  // w takes projections (d / 4) w .. + d / 4 - 1 (three products per tile,
+  // P_hi e_hi + P_hi e_lo + P_lo e_hi); bit m of a vector's signs is
+  // (P_rot e)[m] >= 0, LSB first, into sstage[sb] ----
+  auto sign_product = [&](int eb, int sb) {
+#pragma unroll
+    for (int t = 0; t < ET; ++t) {
+      const int vl = 16 * t + col;
+      float4_t sacc[MTW];
+#pragma unroll
+      for (int mt = 0; mt < MTW; ++mt) sacc[mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int off = vl * D + 8 * ((4 * ks + grp) ^ swz(vl));
+        const half8_t eh = *(const lds_half8 *)(ebuf[eb] + off);
+        const half8_t el = *(const lds_half8 *)(ebuf[eb] + EG * D + off);
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt) {
+          sacc[mt] = mfma16(ph[mt][ks], eh, sacc[mt]);
+          sacc[mt] = mfma16(ph[mt][ks], el, sacc[mt]);
+          sacc[mt] = mfma16(pl[mt][ks], eh, sacc[mt]);
+        }
+      }
+      // lane (col, grp) holds projections (d / 4) w + 16 mt + 4 grp + i:
+      // bits 4 (grp & 1) + i of sign byte (d / 32) w + 2 mt + grp / 2
+#pragma unroll
+      for (int mt = 0; mt < MTW; ++mt) {
+        const uint32_t nib = (sacc[mt][0] >= 0.0f ? 1u : 0u) | (sacc[mt][1] >= 0.0f ? 2u : 0u) |
+                             (sacc[mt][2] >= 0.0f ? 4u : 0u) | (sacc[mt][3] >= 0.0f ? 8u : 0u);
+        const uint32_t other = (uint32_t)__shfl_xor((int)nib, 16, 64);
+        if ((grp & 1) == 0)
+          stage_st8((lds_u8 *)sstage[sb] + vl * SB + (D / 32) * wave + 2 * mt + (grp >> 1), nib | (other << 4));
+      }
+    }
+  };
+  const bool run16q = a.n_outer <= 1 && ((uintptr_t)a.qjl & 15) == 0;
+  auto flush_signs = [&](int64_t g, int sb) {
+    const lds_u8 *stg = (const lds_u8 *)sstage[sb];
+    if (run16q) {
+      const uint32_t v0 = (uint32_t)g * EG;
+      const int nbytes = (int)min(n - v0, (uint32_t)EG) * SB;
+      uint8_t *base = a.qjl + (int64_t)v0 * SB;
+      const int p = tid;
+      if (16 * p + 16 <= nbytes) {
+        *(u32x4 *)(base + 16 * p) = *(const __attribute__((address_space(3))) u32x4 *)(stg + 16 * p);
+      } else if (16 * p < nbytes) {
+        for (int c = 0; c < 4 && 16 * p + 4 * c < nbytes; ++c)
+          *(uint32_t *)(base + 16 * p + 4 * c) = *(const lds_u32 *)(stg + 16 * p + 4 * c);
+      }
+      return;
+    }
+    const int q = tid;  // dword q of the step's signs
+    if (q < EG * SB / 4) {
+      const int vl = q / (SB / 4), c = q - vl * (SB / 4);
+      const uint32_t v = (uint32_t)g * EG + vl;
+      if (v < n) {
+        uint32_t vo, vi;
+        split(v, vo, vi);
+        *(uint32_t *)(a.qjl + (int64_t)vo * a.qjl_outer_stride + (int64_t)vi * SB + 4 * c) =
+            *(const lds_u32 *)(stg + vl * SB + 4 * c);
+      }
+    }
+  };
+  static_assert(!QJL || EG * SB <= 16 * kEW * 64, "one 16-byte piece of signs per thread");
+
+  // QJL keys: the same pipeline one stage deeper. Iteration k rotates step
+  // g_k, quantises g_{k-1} (codes, and its residuals into ebuf[k & 1]), runs
+  // the sign product of g_{k-2} from ebuf[(k - 1) & 1] into sstage[k & 1],
+  // stores the blocks of g_{k-2} and the signs of g_{k-3}.
+  auto run_qjl = [&](auto table_flag) {
+    constexpr bool kTable = decltype(table_flag)::on;
+    const int64_t g0 = blockIdx.x;
+    const int64_t steps = (groups - g0 + g_step - 1) / g_step;  // this workgroup's steps
+    Tile acc, accp;
+    issue(g0, 0);
+    for (int64_t k = 0; k < steps + 3; ++k) {
+      const int b = (int)(k & 1);
+      const int64_t gk = g0 + k * g_step;
+#pragma unroll
+      for (int t = 0; t < ET; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt) accp[t][mt] = acc[t][mt];
+      wait_mem();
+      barrier();
+      if (k >= 2 && k - 2 < steps) flush(gk - 2 * g_step, b ^ 1);
+      if (k >= 3 && k - 3 < steps) flush_signs(gk - 3 * g_step, b ^ 1);
+      float r = 0.f, inv = 0.f;
+      bool step_fast = true;
+      if (k >= 1 && k - 1 < steps) step_fast = finish(gk - g_step, b ^ 1, b, r, inv);
+      if (k >= 2 && k - 2 < steps) sign_product(b ^ 1, b);
+      if (k < steps) {
+        rotate(b, acc);
+        issue(k + 1 < steps ? gk + g_step : gk, b ^ 1);
+      }
+      if (k >= 1 && k - 1 < steps) {
+        if (!kTable || step_fast) quantise(table_flag, TableFlag<true>{}, accp, b, r, inv);
+        else quantise(table_flag, TableFlag<false>{}, accp, b, r, inv);
+      }
+      if (k < steps) tree(acc, b);
     }
   };
 
@@ -525,7 +694,6 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   // stores step g_{k-2} from stage[(k - 2) & 1]: one workgroup barrier per
   // step, and each wave's matrix-core products of one step run beside its
   // quantiser arithmetic of the step before.
-  const int64_t g_step = gridDim.x;
   auto run = [&](auto table_flag) {
     constexpr bool kTable = decltype(table_flag)::on;
     int64_t g = blockIdx.x;
@@ -542,7 +710,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
     for (g += g_step; g < groups; g += g_step, ++k) {
       const int b = k & 1;
 #pragma unroll
-      for (int t = 0; t < kET; ++t)
+      for (int t = 0; t < ET; ++t)
 #pragma unroll
         for (int mt = 0; mt < MTW; ++mt) accp[t][mt] = acc[t][mt];
       wait_mem();
@@ -564,7 +732,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
         // interleave the rotation's matrix-core products with the previous
         // step's quantiser arithmetic: one product, then two vector ops
 #pragma unroll
-        for (int i = 0; i < kET * KS * MTW * 2; ++i) {
+        for (int i = 0; i < ET * KS * MTW * 2; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x002, PQKV_ENC_VALU_PER_MFMA, 0);
         }
@@ -587,23 +755,34 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
     barrier();
     flush(gp, b);
   };
-  if (table_ok != 0) run(TableFlag<true>{});
-  else run(TableFlag<false>{});
+  if constexpr (QJL) {
+    if (table_ok != 0) run_qjl(TableFlag<true>{});
+    else run_qjl(TableFlag<false>{});
+  } else {
+    if (table_ok != 0) run(TableFlag<true>{});
+    else run(TableFlag<false>{});
+  }
 }
 
 hipError_t launch_encode_mfma(const EncodeArgs &a, float *rot_out, float *radius_out, int cus, hipStream_t s) {
+  const bool qjl = a.qjl != nullptr;
   const int64_t n = a.n_outer * a.n_inner;
-  const int64_t groups = (n + kEG - 1) / kEG;
+  const int eg = qjl ? 32 : kEG;
+  const int64_t groups = (n + eg - 1) / eg;
   // each workgroup keeps its share of R in registers and builds its centroid
   // table once, so one resident round of workgroups loops over the steps
   int64_t grid = groups;
   if (grid > kEBlocksPerCU * (int64_t)cus) grid = kEBlocksPerCU * (int64_t)cus;
   if (grid < 1) grid = 1;
-#define PQKV_EM(DD, BB) encode_mfma_kernel<DD, BB><<<(int)grid, kEW * 64, 0, s>>>(a, rot_out, radius_out)
-  if (a.d == 128 && a.bits == 4) PQKV_EM(128, 4);
-  else if (a.d == 128 && a.bits == 2) PQKV_EM(128, 2);
-  else if (a.d == 64 && a.bits == 4) PQKV_EM(64, 4);
-  else PQKV_EM(64, 2);
+#define PQKV_EM(DD, BB, QQ) encode_mfma_kernel<DD, BB, QQ><<<(int)grid, kEW * 64, 0, s>>>(a, rot_out, radius_out)
+#define PQKV_EMQ(DD, BB) \
+  if (qjl) PQKV_EM(DD, BB, true); \
+  else PQKV_EM(DD, BB, false)
+  if (a.d == 128 && a.bits == 4) PQKV_EMQ(128, 4);
+  else if (a.d == 128 && a.bits == 2) PQKV_EMQ(128, 2);
+  else if (a.d == 64 && a.bits == 4) PQKV_EMQ(64, 4);
+  else PQKV_EMQ(64, 2);
+#undef PQKV_EMQ
 #undef PQKV_EM
   return hipGetLastError();
 }

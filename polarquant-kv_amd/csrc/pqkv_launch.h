@@ -128,7 +128,8 @@ hipError_t launch_rotate(const void *x, int x_dtype, const float *R, void *y, in
 hipError_t launch_dequantize(const uint8_t *blocks, const float *codebook, int bits, const float *R, void *y,
                              int y_dtype, int64_t n, int d, hipStream_t s);
 hipError_t launch_encode_exact(const EncodeArgs &a, int x_dtype, hipStream_t s);
-// Matrix-core encoder for fp16 input without QJL; rot_out and radius_out
+// Matrix-core encoder for fp16 input (with the QJL signs when a.qjl is set;
+// rot_out and radius_out are for keys without them); rot_out and radius_out
 // (nullable) receive the fp32 rotated vectors the quantiser saw, [n][d], and
 // their fp32 radii, [n].
 // One round of workgroups (two per compute unit) loops over the vectors.

@@ -1,15 +1,16 @@
 """GPU parity of the encoders against the CPU oracle (bit-exact).
 
 Two encoders sit behind pqkv_encode:
-  * the exact encoder (PQKV_ENCODE_KERNEL=exact, and always for fp32 input or
-    QJL): its rotation is the reference's fp32 FMA chain, so the whole encode
-    is compared bit for bit with oracle.c_rotate_fma -> c_quantize_rotated ->
-    c_pack_blocks on the same inputs;
-  * the matrix-core encoder (fp16 input without QJL, the default there): its
+  * the exact encoder (PQKV_ENCODE_KERNEL=exact, and always for fp32
+    input): its rotation is the reference's fp32 FMA chain, so the whole
+    encode is compared bit for bit with oracle.c_rotate_fma ->
+    c_quantize_rotated -> c_pack_blocks on the same inputs;
+  * the matrix-core encoder (fp16 input, with or without QJL): its
     rotation has fp32-grade products with another rounding, so its quantiser
     is compared bit for bit with the oracle on the rotated values it returns
     (pqkv_encode_mfma's rot_out), and its rotation is checked against the FMA
-    chain within fp32 rounding."""
+    chain within fp32 rounding. Its QJL signs are checked against the
+    oracle's projection of the residual of that rotation, up to ties."""
 
 import numpy as np
 import pytest
@@ -113,7 +114,9 @@ def test_encode_mixed_widths_bit_exact(monkeypatch):
         assert np.array_equal(seg, want), f"head {h}"
 
 
-def test_encode_qjl_signs():
+def test_encode_qjl_signs(monkeypatch):
+    """The exact encoder's QJL signs (fp32 FMA-chain rotation)."""
+    monkeypatch.setenv("PQKV_ENCODE_KERNEL", "exact")
     B, H, T, d = 1, 2, 200, 128
     rng = np.random.default_rng(8)
     x = rng.standard_normal((B, H, T, d)).astype(np.float16)
@@ -287,3 +290,41 @@ def test_compress_pq_fp16_takes_the_mfma_encoder(monkeypatch):
     quantizer.compress_pq(torch.from_numpy(x).to(DEV), Rt, cache=cache, start=0)
     want_exact, *_ = _oracle_encode(x.astype(np.float32), R32, 4)
     assert np.array_equal(cache.blocks.cpu().numpy()[:, :, :T].reshape(-1, 72), want_exact)
+
+
+@pytest.mark.parametrize("d,bits", [(128, 4), (64, 4), (128, 2)])
+@pytest.mark.parametrize("layout", ["strided", "contiguous"])
+def test_mfma_encoder_qjl_signs(d, bits, layout):
+    """QJL keys on the matrix-core encoder: the blocks are the non-QJL
+    encoder's bit for bit (same rotation, same quantiser), and sign m of a
+    vector is (P_rot e)[m] >= 0 for e = y - r c[code] of that rotation (y, r
+    from pqkv_encode_mfma's rot_out / radius_out), up to projections within
+    fp32 summation error of zero."""
+    print(f"encode_mfma qjl d={d} bits={bits} {layout}", flush=True)
+    B, H, T = 2, 3, 333
+    S_max = T if layout == "contiguous" else T + 11
+    x = _fp16_inputs(B * H * T, d, 100 + d + bits, "special").reshape(B, H, T, d)
+    R32 = O.rotation_matrix(d, 42).astype(np.float32)
+    P_rot = (O.jl_matrix(d, d, 43) @ R32.astype(np.float64).T).astype(np.float32)
+    cache = quantizer.allocate_cache(B, H, S_max, d, bits, DEV, jl_dim=d)
+    quantizer.compress_pq(torch.from_numpy(x).to(DEV), torch.from_numpy(R32).to(DEV), cache=cache,
+                          jl_rot=torch.from_numpy(P_rot).to(DEV))
+    torch.cuda.synchronize()
+    vb = O.vector_bytes(d, bits)
+    got_blocks = cache.blocks.cpu().numpy()[:, :, :T].reshape(-1, vb)
+    want_blocks, rot = _encode_mfma(x.reshape(-1, d), R32, padded_codebook_torch(d, bits, DEV), bits, d)
+    assert np.array_equal(got_blocks, want_blocks)
+    cb = O.lloyd_max_codebook(d, bits)[0]
+    r, idx = OC.c_quantize_rotated(rot, cb)
+    assert np.array_equal(_encode_mfma.radius.view(np.uint32), r.view(np.uint32))
+    e = rot.astype(np.float64) - r[:, None].astype(np.float64) * cb[idx].astype(np.float64)
+    proj = e @ P_rot.astype(np.float64).T
+    want = proj >= 0
+    got = O.bit_unpack_lsb(cache.qjl_signs.cpu().numpy()[:, :, :T].reshape(-1, d // 8), d)
+    tol = 1e-5 * np.linalg.norm(e, axis=1, keepdims=True) * np.linalg.norm(P_rot, axis=1)[None]
+    bad = (got != want) & (np.abs(proj) > tol)
+    assert not bad.any(), int(bad.sum())
+    assert (got != want).mean() < 1e-3
+    assert got[0].all()                                       # zero vector: e = 0, every projection >= 0
+    if S_max > T:
+        assert not cache.qjl_signs[:, :, T:].any().item()     # padding positions untouched
