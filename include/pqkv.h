@@ -104,9 +104,10 @@ int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride,
                 void *stream);
 
 /* Matrix-core encoder (no counterpart in the reference: a second, faster
- * implementation of pqkv_encode for fp16 input without QJL, which
- * pqkv_encode uses whenever its conditions hold unless the environment sets
- * PQKV_ENCODE_KERNEL=exact). x must be 16-byte aligned with a row stride that
+ * implementation of pqkv_encode for fp16 input, which pqkv_encode uses with
+ * or without QJL signs whenever its conditions hold unless the environment
+ * sets PQKV_ENCODE_KERNEL=exact; this entry point takes keys without QJL and
+ * exposes the rotation). x must be 16-byte aligned with a row stride that
  * is a multiple of 8 elements, R 16-byte aligned; otherwise
  * PQKV_ERR_UNSUPPORTED. The rotation runs on the matrix cores with fp32-grade
  * products but not the reference's FMA-chain rounding; the quantiser is
@@ -169,6 +170,29 @@ int pqkv_decode_attn_noalloc(const void *q, int q_dtype, const float *R,
                              const uint8_t *qjl_signs, const float *p_rot, int m,
                              int B, int Hq, int Hkv, int S, int S_max, int d, float scale,
                              void *out, int out_dtype, void *stream);
+
+/* Decode attention over a cache split into segments of different widths
+ * (per-token mixed precision, e.g. sink and recent-window tokens at 4 bits,
+ * the rest at 2 bits; src/polarquant_kv_cuda/token_importance.py:17-40 of the
+ * reference computes such widths but attends on no such cache). Segment i
+ * holds caches k_caches[i] / v_caches[i] ([B][Hkv][S_max[i]] vectors of
+ * k_bits[i] / v_bits[i], first S[i] valid) with device codebooks
+ * k_codebooks[i] / v_codebooks[i]. The softmax runs over the tokens of all
+ * segments together (token order does not matter to decode attention): every
+ * segment's split-K partials land in one workspace and one merge combines
+ * them. Otherwise as pqkv_decode_attn with uniform widths and no QJL.
+ * At most PQKV_MAX_SEGMENTS segments; the pointer and size arrays are host
+ * memory. */
+#define PQKV_MAX_SEGMENTS 8
+size_t pqkv_decode_segments_workspace_bytes(int B, int Hq, int Hkv, int n_seg, const int *S, int d);
+
+int pqkv_decode_attn_segments(const void *q, int q_dtype, const float *R, int n_seg,
+                              const uint8_t *const *k_caches, const uint8_t *const *v_caches,
+                              const float *const *k_codebooks, const float *const *v_codebooks,
+                              const int *k_bits, const int *v_bits, const int *S, const int *S_max,
+                              int B, int Hq, int Hkv, int d, float scale,
+                              void *out, int out_dtype,
+                              void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---- chunked prefill attention -------------------------------------------
  * Sq query tokens per sequence (absolute positions q_start .. q_start+Sq-1)

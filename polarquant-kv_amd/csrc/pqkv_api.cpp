@@ -400,6 +400,25 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
                                out_dtype, workspace, workspace_bytes, false, nullptr, stream);
 }
 
+
+size_t pqkv_decode_segments_workspace_bytes(int B, int Hq, int Hkv, int n_seg, const int *S, int d) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || d <= 0 || n_seg < 1 || n_seg > PQKV_MAX_SEGMENTS || !S) return 0;
+  for (int i = 0; i < n_seg; ++i)
+    if (S[i] < 0) return 0;
+  int splits[PQKV_MAX_SEGMENTS], tps[PQKV_MAX_SEGMENTS];
+  // bound over the plans a call can make (largest target)
+  const int total = pqkv::segment_plans(B, Hkv, n_seg, S, kPlanMaxTarget, splits, tps);
+  return pqkv::decode_workspace_layout(B, Hq, total > 0 ? total : 1, d, nullptr, nullptr, nullptr);
+}
+
+int pqkv_decode_attn_segments(const void *q, int q_dtype, const float *R, int n_seg, const uint8_t *const *k_caches,
+                              const uint8_t *const *v_caches, const float *const *k_codebooks,
+                              const float *const *v_codebooks, const int *k_bits, const int *v_bits, const int *S,
+                              const int *S_max, int B, int Hq, int Hkv, int d, float scale, void *out, int out_dtype,
+                              void *workspace, size_t workspace_bytes, void *stream) {
+  return pqkv::decode_segments_run(q, q_dtype, R, n_seg, k_caches, v_caches, k_codebooks, v_codebooks, k_bits, v_bits,
+                                   S, S_max, B, Hq, Hkv, d, scale, out, out_dtype, workspace, workspace_bytes, stream);
+}
 }  // extern "C"
 
 namespace pqkv {
@@ -528,6 +547,8 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
   a.d = d;
   a.splits = splits;
   a.tokens_per_split = tps;
+  a.split_base = 0;
+  a.split_stride = splits;
 
   // Query heads of a kv head in launches of at most kMaxGroup (the matrix
   // tile holds 8 heads): the group is cut into equal parts where it divides,
@@ -626,6 +647,121 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
   e = launch_decode_merge(part, R, out, out_dtype, B * Hq, splits, d, st);
   prof_end(tok, st);
   return hip_status(e, "decode merge launch");
+}
+
+// Split plans of the segments of a segmented decode call (B * Hkv streams
+// of S[i] tokens each); returns the total, the partials per query head that
+// the plans share.
+int segment_plans(int B, int Hkv, int n_seg, const int *S, int target, int *splits, int *tps) {
+  int total = 0;
+  for (int i = 0; i < n_seg; ++i) {
+    splits[i] = 0;
+    tps[i] = 0;
+    if (S[i] > 0) {
+      decode_plan((int64_t)B * Hkv, S[i], target, &splits[i], &tps[i]);
+      total += splits[i];
+    }
+  }
+  return total;
+}
+
+// Decode attention over segments of one logical cache: one query rotation,
+// each segment's split launches writing partials split_base .. of one
+// layout, one merge over all of them.
+int decode_segments_run(const void *q, int q_dtype, const float *R, int n_seg, const uint8_t *const *k_caches,
+                        const uint8_t *const *v_caches, const float *const *k_codebooks,
+                        const float *const *v_codebooks, const int *k_bits, const int *v_bits, const int *S,
+                        const int *S_max, int B, int Hq, int Hkv, int d, float scale, void *out, int out_dtype,
+                        void *workspace, size_t workspace_bytes, void *stream) {
+  if (n_seg < 1 || n_seg > PQKV_MAX_SEGMENTS)
+    return fail(PQKV_ERR_UNSUPPORTED, "decode segments: %d segments (1..%d)", n_seg, PQKV_MAX_SEGMENTS);
+  if (!k_caches || !v_caches || !k_codebooks || !v_codebooks || !k_bits || !v_bits || !S || !S_max)
+    return fail(PQKV_ERR_INVALID, "decode segments: null segment array");
+  if (B <= 0 || Hq <= 0 || Hkv <= 0) return fail(PQKV_ERR_INVALID, "decode segments: B=%d Hq=%d Hkv=%d", B, Hq, Hkv);
+  if (Hq % Hkv) return fail(PQKV_ERR_INVALID, "decode segments: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
+  if (!supported_d(d)) return fail(PQKV_ERR_UNSUPPORTED, "decode segments: d=%d", d);
+  if (!float_dtype(q_dtype) || !float_dtype(out_dtype)) return fail(PQKV_ERR_UNSUPPORTED, "decode segments: dtype");
+  if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(PQKV_ERR_INVALID, "decode segments: scale must be > 0");
+  if (!q || !R || !out) return fail(PQKV_ERR_INVALID, "decode segments: null pointer");
+  if ((uintptr_t)R % 16) return fail(PQKV_ERR_INVALID, "decode segments: R must be 16-byte aligned");
+  for (int i = 0; i < n_seg; ++i) {
+    if (S[i] < 0 || S_max[i] < S[i])
+      return fail(PQKV_ERR_INVALID, "decode segments: segment %d S=%d S_max=%d", i, S[i], S_max[i]);
+    if (!supported_bits(k_bits[i]) || !supported_bits(v_bits[i]))
+      return fail(PQKV_ERR_UNSUPPORTED, "decode segments: segment %d widths k=%d v=%d", i, k_bits[i], v_bits[i]);
+    if (S[i] > 0 && (!k_caches[i] || !v_caches[i] || !k_codebooks[i] || !v_codebooks[i]))
+      return fail(PQKV_ERR_INVALID, "decode segments: segment %d null cache or codebook", i);
+  }
+  const bool mfma = use_mfma();
+  int splits[PQKV_MAX_SEGMENTS], tps[PQKV_MAX_SEGMENTS];
+  const int total = segment_plans(B, Hkv, n_seg, S, mfma ? mfma_target() : kValuTarget, splits, tps);
+  hipStream_t st = (hipStream_t)stream;
+  if (total == 0) {
+    const size_t ob = (size_t)B * Hq * d * (out_dtype == PQKV_F32 ? 4 : 2);
+    return hip_status(launch_fill_zero(out, ob, st), "decode segments zero fill");
+  }
+  if (total > kMaxSplits)
+    return fail(PQKV_ERR_UNSUPPORTED, "decode segments: %d split partials per query head (at most %d)", total,
+                kMaxSplits);
+  size_t q_off, part_off;
+  decode_workspace_layout(B, Hq, total, d, &q_off, &part_off, nullptr);
+  const size_t need = pqkv_decode_segments_workspace_bytes(B, Hq, Hkv, n_seg, S, d);
+  if (!workspace || workspace_bytes < need)
+    return fail(PQKV_ERR_WORKSPACE, "decode segments: workspace %zu < %zu bytes", workspace_bytes, need);
+  float *q32 = (float *)((char *)workspace + q_off);
+  float *part = (float *)((char *)workspace + part_off);
+  const float kLog2e = 1.4426950408889634f;
+  int tok = prof_begin("decode_rotate", st);
+  hipError_t e = launch_rotate(q, q_dtype, R, q32, PQKV_F32, (int64_t)B * Hq, d, 0, scale * kLog2e, st);
+  prof_end(tok, st);
+  if (e != hipSuccess) return hip_status(e, "decode segments query rotation");
+  int base = 0;
+  for (int i = 0; i < n_seg; ++i) {
+    if (S[i] == 0) continue;
+    DecodeArgs a;
+    memset(&a, 0, sizeof(a));
+    a.q = q32;
+    a.k_cache = k_caches[i];
+    a.v_cache = v_caches[i];
+    a.k_cb = k_codebooks[i];
+    a.v_cb = v_codebooks[i];
+    a.cb_levels = 16;
+    a.part = part;
+    a.B = B;
+    a.Hq = Hq;
+    a.Hkv = Hkv;
+    a.gq = Hq / Hkv;
+    a.S = S[i];
+    a.S_max = S_max[i];
+    a.d = d;
+    a.splits = splits[i];
+    a.tokens_per_split = tps[i];
+    a.split_base = base;
+    a.split_stride = total;
+    a.k_head_stride = (int64_t)S_max[i] * pqkv_vector_bytes(d, k_bits[i]);
+    a.v_head_stride = (int64_t)S_max[i] * pqkv_vector_bytes(d, v_bits[i]);
+    a.k_batch_stride = a.k_head_stride * Hkv;
+    a.v_batch_stride = a.v_head_stride * Hkv;
+    a.n_heads = Hkv;
+    // query heads of a kv head in launches of at most kMaxGroup, as in
+    // decode_attn_run
+    const int n_sub = (a.gq + kMaxGroup - 1) / kMaxGroup;
+    int off = 0;
+    for (int j = 0; j < n_sub; ++j) {
+      a.q_off = off;
+      a.g = a.gq / n_sub + (j < a.gq % n_sub ? 1 : 0);
+      const int t = prof_begin("decode_split", st);
+      e = mfma ? launch_decode_mfma(a, k_bits[i], v_bits[i], st) : launch_decode_split(a, k_bits[i], v_bits[i], st);
+      prof_end(t, st);
+      if (e != hipSuccess) return hip_status(e, "decode segments split launch");
+      off += a.g;
+    }
+    base += splits[i];
+  }
+  tok = prof_begin("decode_merge", st);
+  e = launch_decode_merge(part, R, out, out_dtype, B * Hq, total, d, st);
+  prof_end(tok, st);
+  return hip_status(e, "decode segments merge launch");
 }
 
 }  // namespace pqkv

@@ -333,7 +333,8 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
       L += red_l[w][hh] * sc;
       O += red_o[(w * G + hh) * D + c] * sc;
     }
-    float *dst = a.part + (((int64_t)(b * a.Hq + h * a.gq + a.q_off + hh) * a.splits) + split) * (D + 2);
+    float *dst =
+        a.part + (((int64_t)(b * a.Hq + h * a.gq + a.q_off + hh) * a.split_stride) + a.split_base + split) * (D + 2);
     if (c == 0) {
       dst[0] = mx;
       dst[1] = L;

@@ -876,7 +876,8 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
       L += red_l[w][hh] * sc;
       O += sm.u.red_o[w][hh * D + c] * sc;
     }
-    float *dst = a.part + (((int64_t)(b * a.Hq + h * a.gq + a.q_off + hh) * a.splits) + split) * (D + 2);
+    float *dst =
+        a.part + (((int64_t)(b * a.Hq + h * a.gq + a.q_off + hh) * a.split_stride) + a.split_base + split) * (D + 2);
     if (c == 0) {
       dst[0] = mx;
       dst[1] = L;

@@ -51,11 +51,12 @@ struct DecodeArgs {
   const uint8_t *qjl;            // [B][Hkv][S_max][m/8] or null
   const float *p_rot;            // [m][d] (QJL only)
   const float *pq;               // [B][Hq][m] = P_rot q / m (QJL only)
-  float *part;                   // [B][Hq][splits][d + 2]
+  float *part;                   // [B][Hq][split_stride][d + 2]
   int B, Hq, Hkv, S, S_max, d;
   int gq;                        // query heads per kv head (Hq / Hkv)
   int q_off, g;                  // this launch: query heads q_off .. q_off + g - 1 of each kv head (g <= kMaxGroup)
   int splits, tokens_per_split;
+  int split_base, split_stride;  // this launch's splits are partials split_base .. of split_stride per query head
   int n_heads;                   // heads in this launch
   int listed;                    // 1: heads / offsets below are used
   int16_t heads[kMaxListHeads];
@@ -105,6 +106,15 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
                     int m, int B, int Hq, int Hkv, int S, int S_max, int d, float scale, void *out, int out_dtype,
                     void *workspace, size_t workspace_bytes, bool plan_sized, const SoaCache *soa,
                     void *stream);
+// The validated call behind pqkv_decode_attn_segments, and the split plans
+// it makes (one per segment, sharing one partials layout; returns their
+// total).
+int segment_plans(int B, int Hkv, int n_seg, const int *S, int target, int *splits, int *tps);
+int decode_segments_run(const void *q, int q_dtype, const float *R, int n_seg, const uint8_t *const *k_caches,
+                        const uint8_t *const *v_caches, const float *const *k_codebooks,
+                        const float *const *v_codebooks, const int *k_bits, const int *v_bits, const int *S,
+                        const int *S_max, int B, int Hq, int Hkv, int d, float scale, void *out, int out_dtype,
+                        void *workspace, size_t workspace_bytes, void *stream);
 
 // Sets the thread's error message from a HIP error; returns PQKV_ERR_HIP
 // (PQKV_OK for hipSuccess).

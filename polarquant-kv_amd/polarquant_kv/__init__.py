@@ -12,6 +12,8 @@ python/polarquant_kv and src/polarquant_kv_cuda) for the codebook
   turboquant turboquant_compress, turboquant_full_attention      (HIP, raw pointers)
   inference  PolarQuantConfig, KVCacheManager, CompressedMultiHeadAttention
   hf_integration CompressedDynamicCache, patch_model
+  policies   compute_token_bitwidths, compute_layer_bitwidths, TokenMixedCache,
+             differential_encode, ...                            (HIP for the cache)
 
 GPU work goes through libpqkv_hip.so (include/pqkv.h) via ctypes.
 """
@@ -25,7 +27,7 @@ __all__ = ["lloyd_max", "qjl", "rotation", "types", "PQCache", "block_bytes", "v
 def __getattr__(name):
     # GPU modules load libpqkv_hip.so lazily so the host-side API imports
     # on machines without a GPU.
-    if name in ("attention", "quantizer", "turboquant", "inference", "hf_integration"):
+    if name in ("attention", "quantizer", "turboquant", "inference", "hf_integration", "policies"):
         import importlib
         return importlib.import_module(f".{name}", __name__)
     raise AttributeError(name)

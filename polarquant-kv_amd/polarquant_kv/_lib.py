@@ -43,6 +43,13 @@ SIGNATURES = {
                                          c_int, c_int, c_int_p, c_int_p, c_void_p, c_void_p, c_int,
                                          c_int, c_int, c_int, c_int, c_int, c_int, c_float,
                                          c_void_p, c_int, c_void_p]),
+    "pqkv_decode_segments_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int_p, c_int]),
+    "pqkv_decode_attn_segments": (c_int, [c_void_p, c_int, c_void_p, c_int,
+                                          ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p),
+                                          ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p),
+                                          c_int_p, c_int_p, c_int_p, c_int_p,
+                                          c_int, c_int, c_int, c_int, c_float,
+                                          c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
     "pqkv_prefill_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "pqkv_prefill_attn": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_int, c_int, c_int_p, c_int_p, c_void_p, c_void_p, c_int,
@@ -123,6 +130,11 @@ def require_device(*tensors) -> None:
     for t in tensors:
         if t is not None and not t.is_cuda:
             raise ValueError("GPU entry points take device tensors (the hot path has no CPU fallback)")
+
+
+def ptr_array(tensors):
+    """Host array of the tensors' device pointers (for the segment arrays)."""
+    return (c_void_p * len(tensors))(*[t.data_ptr() for t in tensors])
 
 
 def int_array(values):

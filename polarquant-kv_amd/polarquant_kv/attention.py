@@ -90,6 +90,48 @@ def decode_attention(query: torch.Tensor, keys: PQCache, values: PQCache, rotati
     return out
 
 
+def decode_attention_segments(query: torch.Tensor, segments: list, rotation_matrix: torch.Tensor,
+                              scale: float | None = None, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """query [B, Hq, d] against the tokens of several (keys, values) cache
+    pairs at once (one softmax over all of them; each pair of uniform widths,
+    no QJL) -> out [B, Hq, d]. Segments with no valid tokens are skipped."""
+    if query.dim() != 3:
+        raise ValueError(f"query must be [B, Hq, d], got {tuple(query.shape)}")
+    if not segments:
+        raise ValueError("at least one segment is required")
+    B, Hq, d = query.shape
+    Hkv = None
+    for kc, vc in segments:
+        if kc.mixed or vc.mixed:
+            raise ValueError("segments take caches of one width each")
+        h = check_shapes(B, Hq, d, kc, vc, rotation_matrix)
+        if Hkv is not None and h != Hkv:
+            raise ValueError("every segment must have the same kv heads")
+        Hkv = h
+    _lib.require_device(query, rotation_matrix)
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    out_dtype = query.dtype if out_dtype is None else out_dtype
+    q = query.contiguous()
+    R = rotation_matrix.to(torch.float32).contiguous()
+    out = torch.empty(B, Hq, d, dtype=out_dtype, device=q.device)
+    lib = _lib.lib()
+    n = len(segments)
+    S = _lib.int_array([kc.seq_len for kc, _ in segments])
+    S_max = _lib.int_array([kc.max_seq_len for kc, _ in segments])
+    need = lib.pqkv_decode_segments_workspace_bytes(B, Hq, Hkv, n, S, d)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    kcb = [kc.codebooks.to(torch.float32).contiguous() for kc, _ in segments]
+    vcb = [vc.codebooks.to(torch.float32).contiguous() for _, vc in segments]
+    _lib.check(lib.pqkv_decode_attn_segments(
+        q.data_ptr(), _lib.dtype_code(q.dtype), R.data_ptr(), n,
+        _lib.ptr_array([kc.blocks for kc, _ in segments]), _lib.ptr_array([vc.blocks for _, vc in segments]),
+        _lib.ptr_array(kcb), _lib.ptr_array(vcb),
+        _lib.int_array([kc.n_bits for kc, _ in segments]), _lib.int_array([vc.n_bits for _, vc in segments]),
+        S, S_max, B, Hq, Hkv, d, scale, out.data_ptr(), _lib.dtype_code(out_dtype), ws.data_ptr(), ws.numel(),
+        _lib.stream_of(q)))
+    return out
+
+
 def prefill_attention(query: torch.Tensor, keys: PQCache, values: PQCache, rotation_matrix: torch.Tensor,
                       q_start: int, causal: bool = True, scale: float | None = None,
                       out_dtype: torch.dtype | None = None, jl_rot: torch.Tensor | None = None) -> torch.Tensor:
