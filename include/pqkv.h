@@ -194,6 +194,25 @@ int pqkv_decode_attn_segments(const void *q, int q_dtype, const float *R, int n_
                               void *out, int out_dtype,
                               void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- group (min / scale) format ------------------------------------------
+ * The reference's CPU quantizer format (python/polarquant_kv/quantizer.py:
+ * 25-158, behind polarquant_kv.quantizer.compress / decompress /
+ * compress_batch / decompress_batch) on the GPU: rotate with an fp64 R
+ * (device [d][d] float64, the reference's rotation matrix), fp32 radius and
+ * direction, then per group of group_size coordinates (the last group
+ * zero-padded) min, scale = (max - min) / (2^n_bits - 1) (1 for a flat
+ * group) and codes rint((u - min) / scale) clipped to [0, 2^n_bits - 1]
+ * (0 for a flat group), one uint8 per coordinate. x [n][d] fp32 / fp16;
+ * radius [n] fp32; codes [n][ng * group_size] uint8; mins, scales [n][ng]
+ * fp32 with ng = ceil(d / group_size). 1 <= d <= 256, 2 <= n_bits <= 8,
+ * 1 <= group_size <= d. decompress writes out [n][d] fp32 (zeros where the
+ * radius is below 1e-30). Replaces compress / decompress
+ * (python/polarquant_kv/quantizer.py:88-158). */
+int pqkv_group_compress(const void *x, int x_dtype, const double *R, int64_t n, int d, int n_bits, int group_size,
+                        float *radius, uint8_t *codes, float *mins, float *scales, void *stream);
+int pqkv_group_decompress(const float *radius, const uint8_t *codes, const float *mins, const float *scales,
+                          const double *R, int64_t n, int d, int group_size, float *out, void *stream);
+
 /* ---- chunked prefill attention -------------------------------------------
  * Sq query tokens per sequence (absolute positions q_start .. q_start+Sq-1)
  * against a cache that already holds them (append-then-attend,

@@ -28,6 +28,9 @@ Parity pins (what checks each function besides itself), see tests/test_oracle.py
   prefill_attention    decode_attention row by row (causal rule), SDPA
   qjl_*                closed form of qjl.py:38-57, bit-pack round trip,
                        rotated-space identity P e = (P R^T)(R e)
+  group_*              hand-worked codes (round half to even, flat groups,
+                       padding), zero vector, the reference tests' cosine
+                       thresholds per width (tests/test_quantizer.py:66-82)
 """
 
 from __future__ import annotations
@@ -456,6 +459,57 @@ def sdpa(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float | None = None
 # ---------------------------------------------------------------------------
 # Synthetic inputs of the benchmark configurations
 # ---------------------------------------------------------------------------
+
+# ---------------------------------------------------------------------------
+# Group (min / scale) format of the reference's CPU quantizer
+# ---------------------------------------------------------------------------
+
+def group_quantize_direction(u: np.ndarray, n_bits: int, group_size: int):
+    """Per-group min / scale codes of a direction u [d] (float32)
+    (python/polarquant_kv/quantizer.py:25-66): zero-pad to whole groups;
+    scale = (max - min) / levels, 1 for a flat group; codes
+    clip(round_half_even((u - min) / scale), 0, levels), 0 in a flat group."""
+    d = u.shape[-1]
+    ng = math.ceil(d / group_size)
+    u = np.concatenate([u.astype(np.float32), np.zeros(ng * group_size - d, np.float32)])
+    groups = u.reshape(ng, group_size)
+    lo = groups.min(axis=1).astype(np.float32)
+    hi = groups.max(axis=1).astype(np.float32)
+    levels = (1 << n_bits) - 1
+    scales = np.where(hi - lo > 0, (hi - lo) / np.float32(levels), np.float32(1.0)).astype(np.float32)
+    codes = np.zeros((ng, group_size), np.uint8)
+    for g in range(ng):
+        if scales[g] > 0 and hi[g] - lo[g] > 0:
+            codes[g] = np.clip(np.round((groups[g] - lo[g]) / scales[g]), 0, levels).astype(np.uint8)
+    return codes.reshape(-1), lo, scales
+
+
+def group_compress(v: np.ndarray, R: np.ndarray, n_bits: int, group_size: int):
+    """One vector -> (radius f32, codes, mins, scales)
+    (python/polarquant_kv/quantizer.py:88-134; rotation.py:48 rotates in
+    fp64 and casts back to fp32)."""
+    v32 = np.asarray(v).astype(np.float32)
+    y = (v32.astype(np.float64) @ R.T).astype(np.float32)
+    r = np.float32(np.linalg.norm(y))
+    d = y.shape[-1]
+    ng = math.ceil(d / group_size)
+    if r < 1e-30:
+        return np.float32(0.0), np.zeros(ng * group_size, np.uint8), np.zeros(ng, np.float32), np.ones(ng, np.float32)
+    codes, lo, sc = group_quantize_direction((y / r).astype(np.float32), n_bits, group_size)
+    return r, codes, lo, sc
+
+
+def group_decompress(r, codes, lo, sc, R: np.ndarray, d: int, group_size: int) -> np.ndarray:
+    """(python/polarquant_kv/quantizer.py:69-85,137-158): u = code * scale +
+    min in fp32, the first d values times r, rotated back in fp64."""
+    if r < 1e-30:
+        return np.zeros(d, np.float32)
+    ng = len(lo)
+    g = codes[:ng * group_size].reshape(ng, group_size).astype(np.float32)
+    g = g * sc.astype(np.float32)[:, None] + lo.astype(np.float32)[:, None]
+    y = g.reshape(-1)[:d] * np.float32(r)
+    return (y.astype(np.float64) @ R).astype(np.float32)
+
 
 def synth_kv(B: int, H: int, S: int, d: int, seed: int, kind: str = "normal") -> np.ndarray:
     """fp16 K or V [B, H, S, d].

@@ -401,6 +401,35 @@ int pqkv_decode_attn(const void *q, int q_dtype, const float *R, const uint8_t *
 }
 
 
+int pqkv_group_compress(const void *x, int x_dtype, const double *R, int64_t n, int d, int n_bits, int group_size,
+                        float *radius, uint8_t *codes, float *mins, float *scales, void *stream) {
+  if (n < 0) return fail(PQKV_ERR_INVALID, "group_compress: n < 0");
+  if (d < 1 || d > 256) return fail(PQKV_ERR_UNSUPPORTED, "group_compress: d=%d (1..256)", d);
+  if (n_bits < 2 || n_bits > 8) return fail(PQKV_ERR_INVALID, "group_compress: n_bits=%d (2..8)", n_bits);
+  if (group_size < 1 || group_size > d)
+    return fail(PQKV_ERR_INVALID, "group_compress: group_size=%d (1..d=%d)", group_size, d);
+  if (x_dtype != PQKV_F32 && x_dtype != PQKV_F16) return fail(PQKV_ERR_UNSUPPORTED, "group_compress: x dtype");
+  if (n == 0) return PQKV_OK;
+  if (!x || !R || !radius || !codes || !mins || !scales) return fail(PQKV_ERR_INVALID, "group_compress: null pointer");
+  return hip_status(pqkv::launch_group_compress(x, x_dtype, R, n, d, n_bits, group_size, radius, codes, mins, scales,
+                                                (hipStream_t)stream),
+                    "group_compress launch");
+}
+
+int pqkv_group_decompress(const float *radius, const uint8_t *codes, const float *mins, const float *scales,
+                          const double *R, int64_t n, int d, int group_size, float *out, void *stream) {
+  if (n < 0) return fail(PQKV_ERR_INVALID, "group_decompress: n < 0");
+  if (d < 1 || d > 256) return fail(PQKV_ERR_UNSUPPORTED, "group_decompress: d=%d (1..256)", d);
+  if (group_size < 1 || group_size > d)
+    return fail(PQKV_ERR_INVALID, "group_decompress: group_size=%d (1..d=%d)", group_size, d);
+  if (n == 0) return PQKV_OK;
+  if (!radius || !codes || !mins || !scales || !R || !out)
+    return fail(PQKV_ERR_INVALID, "group_decompress: null pointer");
+  return hip_status(pqkv::launch_group_decompress(radius, codes, mins, scales, R, n, d, group_size, out,
+                                                  (hipStream_t)stream),
+                    "group_decompress launch");
+}
+
 size_t pqkv_decode_segments_workspace_bytes(int B, int Hq, int Hkv, int n_seg, const int *S, int d) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || d <= 0 || n_seg < 1 || n_seg > PQKV_MAX_SEGMENTS || !S) return 0;
   for (int i = 0; i < n_seg; ++i)

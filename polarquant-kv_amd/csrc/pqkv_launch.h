@@ -166,6 +166,13 @@ hipError_t launch_decode_mfma_soa(const DecodeArgs &a, hipStream_t s);
 hipError_t launch_decode_merge(const float *part, const float *R, void *out, int out_dtype, int BHq, int splits,
                                int d, hipStream_t s);
 hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t s);
+
+// Group (min / scale) format of the reference's CPU quantizer: d <= 256,
+// 1 <= gs <= d; codes [n][ceil(d/gs) gs], mins / scales [n][ceil(d/gs)].
+hipError_t launch_group_compress(const void *x, int x_dtype, const double *R, int64_t n, int d, int bits, int gs,
+                                 float *radius, uint8_t *codes, float *mins, float *scales, hipStream_t s);
+hipError_t launch_group_decompress(const float *radius, const uint8_t *codes, const float *mins, const float *scales,
+                                   const double *R, int64_t n, int d, int gs, float *out, hipStream_t s);
 // Measurement: read `bytes` (a multiple of 16) from p once, XOR into sink[block].
 hipError_t launch_stream_read(const void *p, size_t bytes, uint32_t *sink, int blocks, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs &a, int k_bits, int v_bits, hipStream_t s);

@@ -50,6 +50,10 @@ SIGNATURES = {
                                           c_int_p, c_int_p, c_int_p, c_int_p,
                                           c_int, c_int, c_int, c_int, c_float,
                                           c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
+    "pqkv_group_compress": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int, c_int, c_int,
+                                    c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "pqkv_group_decompress": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int,
+                                      c_void_p, c_void_p]),
     "pqkv_prefill_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "pqkv_prefill_attn": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_int, c_int, c_int_p, c_int_p, c_void_p, c_void_p, c_int,

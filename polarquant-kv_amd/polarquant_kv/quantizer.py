@@ -6,8 +6,10 @@ turboquant_compress (csrc/flash_turboquant.cu:213-225): rotate, polar split,
 nearest Lloyd-Max centroid per coordinate, pack into blocks, plus the optional
 QJL key sketch. compress_gpu / decompress_gpu keep the reference's names and
 arguments for that format; dequantize is the general decoder. quantize_rotated
-is the bit-exact surface on fp32 rotated input. All call libpqkv_hip.so;
-there is no CPU path.
+is the bit-exact surface on fp32 rotated input. compress / decompress /
+compress_batch / decompress_batch are the reference's CPU quantizer API over
+its group (min / scale) format, computed on the GPU. All call
+libpqkv_hip.so; there is no CPU path.
 """
 
 from __future__ import annotations
@@ -200,3 +202,152 @@ def decompress_gpu(cache: PQCache, rotation_matrix: torch.Tensor) -> torch.Tenso
     for the codebook format: fp16 [B, H, seq_len, d] in the original space,
     saturated at +-65504; an empty cache gives an empty tensor."""
     return dequantize(cache, rotation_matrix, torch.float16)
+
+
+# ---------------------------------------------------------------- group format
+#
+# The reference's CPU quantizer API (python/polarquant_kv/quantizer.py:88-222:
+# compress, decompress, compress_batch, decompress_batch) over the group
+# (min / scale) format, computed by pqkv_group_compress / pqkv_group_decompress
+# on the GPU. Host numpy in, host numpy out, as there; the arithmetic runs on
+# the device only.
+
+def _group_device() -> torch.device:
+    if not torch.cuda.is_available():
+        raise RuntimeError("the group quantizer runs on the GPU (no CPU fallback) and no device is available")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _rotation64(rotation_matrix, device) -> torch.Tensor:
+    if torch.is_tensor(rotation_matrix):
+        return rotation_matrix.to(device=device, dtype=torch.float64).contiguous()
+    import numpy as np
+    return torch.from_numpy(np.ascontiguousarray(rotation_matrix, dtype=np.float64)).to(device)
+
+
+def group_compress_arrays(x, rotation_matrix, n_bits: int = 4, group_size: int = 32):
+    """x [N, d] (host or device; fp16 input stays fp16, anything else is
+    taken as fp32) -> (radius [N] f32, codes [N, d_pad] u8, mins [N, ng] f32,
+    scales [N, ng] f32) as host numpy arrays."""
+    import numpy as np
+    dev = _group_device()
+    if torch.is_tensor(x):
+        xt = x.to(dev)
+        if xt.dtype != torch.float16:
+            xt = xt.to(torch.float32)
+    else:
+        arr = np.asarray(x)
+        xt = torch.from_numpy(np.ascontiguousarray(arr if arr.dtype == np.float16 else arr.astype(np.float32))).to(dev)
+    if xt.dim() != 2:
+        raise ValueError("x must be [N, d]")
+    xt = xt.contiguous()
+    n, d = xt.shape
+    _validate_params(n_bits, group_size, d)
+    if d > 256:
+        raise ValueError(f"the GPU group quantizer takes d <= 256, got {d}")
+    ng = -(-d // group_size)
+    R = _rotation64(rotation_matrix, dev)
+    if R.shape != (d, d):
+        raise ValueError(f"rotation_matrix must be [{d}, {d}], got {tuple(R.shape)}")
+    radius = torch.empty(n, dtype=torch.float32, device=dev)
+    codes = torch.empty(n, ng * group_size, dtype=torch.uint8, device=dev)
+    mins = torch.empty(n, ng, dtype=torch.float32, device=dev)
+    scales = torch.empty(n, ng, dtype=torch.float32, device=dev)
+    _lib.check(_lib.lib().pqkv_group_compress(xt.data_ptr(), _lib.dtype_code(xt.dtype), R.data_ptr(), n, d, n_bits,
+                                              group_size, radius.data_ptr(), codes.data_ptr(), mins.data_ptr(),
+                                              scales.data_ptr(), _lib.stream_of(xt)))
+    return radius.cpu().numpy(), codes.cpu().numpy(), mins.cpu().numpy(), scales.cpu().numpy()
+
+
+def group_decompress_arrays(radius, codes, mins, scales, rotation_matrix, d: int, group_size: int):
+    """Inverse of group_compress_arrays: host arrays -> [N, d] float32 numpy."""
+    import numpy as np
+    dev = _group_device()
+    r = torch.from_numpy(np.ascontiguousarray(radius, dtype=np.float32).reshape(-1)).to(dev)
+    n = r.numel()
+    c = torch.from_numpy(np.ascontiguousarray(codes, dtype=np.uint8).reshape(n, -1)).to(dev)
+    lo = torch.from_numpy(np.ascontiguousarray(mins, dtype=np.float32).reshape(n, -1)).to(dev)
+    sc = torch.from_numpy(np.ascontiguousarray(scales, dtype=np.float32).reshape(n, -1)).to(dev)
+    ng = -(-d // group_size)
+    if c.shape[1] != ng * group_size or lo.shape[1] != ng or sc.shape[1] != ng:
+        raise ValueError("codes / mins / scales do not match d and group_size")
+    R = _rotation64(rotation_matrix, dev)
+    out = torch.empty(n, d, dtype=torch.float32, device=dev)
+    _lib.check(_lib.lib().pqkv_group_decompress(r.data_ptr(), c.data_ptr(), lo.data_ptr(), sc.data_ptr(), R.data_ptr(),
+                                                n, d, group_size, out.data_ptr(), _lib.stream_of(out)))
+    return out.cpu().numpy()
+
+
+def compress(v, rotation_matrix, n_bits: int = 4, group_size: int = 32):
+    """One vector v [d] -> CompressedKV (python/polarquant_kv/quantizer.py:88-134):
+    rotate, radius, direction, per-group min / scale codes."""
+    import numpy as np
+    from .types import CompressedKV
+    arr = np.asarray(v)
+    if arr.ndim != 1:
+        raise ValueError(f"compress takes one vector [d], got shape {arr.shape} (compress_batch takes batches)")
+    _validate_params(n_bits, group_size, arr.shape[-1])
+    r, c, lo, sc = group_compress_arrays(arr[None], rotation_matrix, n_bits, group_size)
+    return CompressedKV(radius=np.float32(r[0]), quantized_direction=c[0], group_mins=lo[0], group_scales=sc[0],
+                        n_bits=n_bits, group_size=group_size, original_dim=arr.shape[-1])
+
+
+def decompress(compressed, rotation_matrix):
+    """CompressedKV -> the vector [original_dim] float32
+    (python/polarquant_kv/quantizer.py:137-158)."""
+    out = group_decompress_arrays([compressed.radius], compressed.quantized_direction[None],
+                                  compressed.group_mins[None], compressed.group_scales[None], rotation_matrix,
+                                  compressed.original_dim, compressed.group_size)
+    return out[0]
+
+
+def compress_batch(kv, rotation_matrix, n_bits: int = 4, group_size: int = 32):
+    """kv [batch, num_heads, seq_len, head_dim] -> nested lists [b][h][s] of
+    CompressedKV, all vectors in one GPU call; an empty kv gives
+    {"empty": True, "shape": kv.shape} (python/polarquant_kv/quantizer.py:161-193)."""
+    import logging
+    import numpy as np
+    from .types import CompressedKV
+    from .utils import check_memory_warning, estimate_memory_bytes
+    arr = np.asarray(kv)
+    if arr.size == 0:
+        return {"empty": True, "shape": arr.shape}
+    B, H, S, d = arr.shape
+    est = estimate_memory_bytes(B, H, S, d, n_bits, group_size, jl_dim=0)
+    if check_memory_warning(est):
+        logging.getLogger(__name__).warning("estimated memory %.2f GB exceeds 80%% of the available memory",
+                                            est / 1e9)
+    r, c, lo, sc = group_compress_arrays(arr.reshape(-1, d), rotation_matrix, n_bits, group_size)
+    out, i = [], 0
+    for _b in range(B):
+        heads = []
+        for _h in range(H):
+            seq = []
+            for _s in range(S):
+                seq.append(CompressedKV(radius=np.float32(r[i]), quantized_direction=c[i], group_mins=lo[i],
+                                        group_scales=sc[i], n_bits=n_bits, group_size=group_size, original_dim=d))
+                i += 1
+            heads.append(seq)
+        out.append(heads)
+    return out
+
+
+def decompress_batch(compressed_list, rotation_matrix):
+    """Nested lists from compress_batch -> [batch, num_heads, seq_len, head_dim]
+    float32 (python/polarquant_kv/quantizer.py:196-222)."""
+    import numpy as np
+    if isinstance(compressed_list, dict) and compressed_list.get("empty"):
+        return np.empty(compressed_list["shape"], dtype=np.float32)
+    if not compressed_list:
+        return np.empty((0,), dtype=np.float32)
+    B, H = len(compressed_list), len(compressed_list[0])
+    S = len(compressed_list[0][0]) if H else 0
+    if S == 0:
+        return np.zeros((B, H, 0, 0), dtype=np.float32)
+    flat = [c for heads in compressed_list for seq in heads for c in seq]
+    d, gs = flat[0].original_dim, flat[0].group_size
+    out = group_decompress_arrays(np.array([c.radius for c in flat], np.float32),
+                                  np.stack([c.quantized_direction for c in flat]),
+                                  np.stack([c.group_mins for c in flat]), np.stack([c.group_scales for c in flat]),
+                                  rotation_matrix, d, gs)
+    return out.reshape(B, H, S, d)

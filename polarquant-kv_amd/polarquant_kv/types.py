@@ -80,3 +80,17 @@ class QJLSignatures:
     signs: "object"
     jl_dim: int
     residual_norm: float = 0.0
+
+
+@dataclass
+class CompressedKV:
+    """One vector in the group (min / scale) format
+    (python/polarquant_kv/types.py:7-16 of the reference): fp32 radius,
+    uint8 codes of the padded direction, fp32 per-group minimum and scale."""
+    radius: "object"                  # np.float32
+    quantized_direction: "object"     # np.uint8 [ceil(d / group_size) * group_size]
+    group_mins: "object"              # np.float32 [ceil(d / group_size)]
+    group_scales: "object"            # np.float32 [ceil(d / group_size)]
+    n_bits: int
+    group_size: int
+    original_dim: int
