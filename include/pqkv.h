@@ -91,9 +91,10 @@ int pqkv_quantize_rotated(const float *x_rot, const float *codebook, int n_bits,
  * m = d): signs at qjl + o * qjl_outer_stride + i * (m/8), bit i of the
  * sketch = (p_rot[i] . (x_rot - r c[idx]) >= 0), LSB first
  * (src/polarquant_kv_cuda/compress_kernel.py:166-175, qjl_kernel.py:6-37).
- * fp16 input without QJL (x rows and R 16-byte aligned) runs on the
- * matrix-core encoder of pqkv_encode_mfma; PQKV_ENCODE_KERNEL=exact in the
- * environment forces the FMA-chain rotation of pqkv_rotate everywhere.
+ * fp16 input (x rows and R 16-byte aligned, blocks 4-byte aligned; with QJL
+ * also p_rot 16-byte and the signs 4-byte aligned) runs on the matrix-core
+ * encoder of pqkv_encode_mfma, signs included; PQKV_ENCODE_KERNEL=exact in
+ * the environment forces the FMA-chain rotation of pqkv_rotate everywhere.
  * Replaces turboquant_compress (csrc/flash_turboquant.cu:213-225) and
  * polarquant_compress_cuda (patch:443-467). */
 int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride,
