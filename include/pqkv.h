@@ -9,8 +9,9 @@
  * status (PQKV_OK = 0, negative on error); pqkv_last_error() gives the
  * message of the last failure on the calling thread. No function keeps state
  * between calls or allocates device memory, except the reference-compatible
- * polarquant_* entry points at the end, which mirror the reference's own
- * ownership rules.
+ * polarquant_* entry points, which mirror the reference's own ownership
+ * rules, pqkv_decode_attn_noalloc's scratch array and the host copy of the
+ * ggml type's default rotation.
  *
  * Storage format (README.md:73-78 of the reference, "block_pq4"):
  *   one head vector of d coordinates = d/32 blocks; block = {fp16 radius;
@@ -339,6 +340,71 @@ void turboquant_full_attention(int64_t q_ptr, int64_t R_ptr, int64_t pk_ptr, int
                                int64_t out_ptr, int64_t q_rot_ptr, int64_t score_ptr,
                                int64_t attn_out_ptr, int total_heads, int total_kv, int S, int D,
                                int n_levels, float scale);
+
+/* ---- GGML_TYPE_PQ4: a ggml type and its HIP backend ops -------------------
+ * No counterpart exists in the reference: its llama.cpp integration keeps the
+ * cache as Q4_0 and never calls its kernels from the graph
+ * (integration/polarquant-kv.patch:1130-1137,1303-1362,1385-1404). These are
+ * the pieces a ggml type and backend would register for a cache in the block
+ * format: blocks of PQKV_GGML_QK_PQ4 elements, PQKV_GGML_PQ4_TYPE_SIZE bytes
+ * ({fp16 radius; uint8 qs[16]}, README.md:73-78); a row is whole heads of
+ * head_dim (64 or 128) elements; a head is rotated by R (q_rot = R x), its
+ * fp32 radius (the 128-slot tree, csrc/flash_turboquant.cu:141-148) stored
+ * as fp16 saturated at 65504 in each of its blocks, and each direction
+ * coordinate stored as the first nearest of 16 codebook entries; its value
+ * is (r16 c[code]) R. */
+#define PQKV_GGML_QK_PQ4 32
+#define PQKV_GGML_PQ4_TYPE_SIZE 18
+
+/* CPU type traits with an explicit head_dim, R ([head_dim][head_dim] fp32)
+ * and codebook (16 fp32), host memory; k elements per call (whole heads).
+ * The rotation is one fp32 FMA chain per coordinate over k ascending and the
+ * rest the GPU encoder's rounding, so rows match pqkv_ggml_cpy_pq4 bytewise. */
+int pqkv_pq4_quantize_rows_host(const float *x, void *y, int64_t k, int head_dim, const float *R,
+                                const float *codebook);
+int pqkv_pq4_dequantize_rows_host(const void *x, float *y, int64_t k, int head_dim, const float *R,
+                                  const float *codebook);
+/* The default type's rotation: Gram-Schmidt over rand() after srand(42), as
+ * polarquant_init_c builds it (patch:549-579; it re-seeds the C library's
+ * rand() the first time it runs for a head_dim). */
+int pqkv_ggml_pq4_rotation(float *R, int head_dim);
+/* ggml's type-trait signatures (from_float_ref, to_float) for the default
+ * type: head_dim 128, the rotation above, the 4-bit table of patch:978-983
+ * (the one polarquant_init_c uploads). k must be a multiple of 128. */
+void pqkv_ggml_quantize_row_pq4_ref(const float *x, void *y, int64_t k);
+void pqkv_ggml_dequantize_row_pq4(const void *x, float *y, int64_t k);
+
+/* Backend op cpy: f32 / f16 src [ne0][ne1][ne2][ne3] (ne0 fastest, byte
+ * strides nb, nb[0] the element size) into PQ4 rows dst (byte strides
+ * nb_dst, nb_dst[0] = PQKV_GGML_PQ4_TYPE_SIZE) with the state's rotation and
+ * 4-bit codebook (st from polarquant_init_c with n_bits 4). ne0 is whole
+ * heads of st->head_dim. Stream-ordered; the rotation is the FMA chain of
+ * pqkv_rotate, so the bytes equal pqkv_pq4_quantize_rows_host's. */
+int pqkv_ggml_cpy_pq4(const polarquant_state *st, const void *src, int src_type, const int64_t ne[4],
+                      const size_t nb[4], void *dst, const size_t nb_dst[4], void *stream);
+
+/* Backend op flash_attn_ext over PQ4 keys and values, ggml's shapes:
+ *   q    f32 [d][n_q][Hq][n_seq]        (byte strides nb_q, nb_q[0] = 4)
+ *   k, v PQ4 [d][n_kv][Hkv][n_seq_kv]   (nb[1] bytes between tokens, nb[2]
+ *                                        between heads, nb[3] between
+ *                                        sequences; n_seq_kv 1 or n_seq)
+ *   mask f16 [>= n_kv][>= n_q][1][1 or n_seq], additive, or NULL
+ *   dst  f32 [d][Hq][n_q][n_seq], contiguous
+ *   dst = softmax(scale q k^T + mask) v with k, v the rows' values; query
+ *   head h reads kv head h / (Hq / Hkv); a row whose tokens are all masked
+ *   (-inf) is 0. max_bias and logit_softcap must be 0 (PQKV_ERR_UNSUPPORTED
+ *   otherwise: a backend's supports_op declines those). d = st->head_dim.
+ * The workspace (pqkv_ggml_flash_attn_ext_pq4_workspace_bytes, 0 for an
+ * invalid shape) needs no initialisation. Several query rows per sequence
+ * (n_q > 1) each stream the whole key / value sequence. */
+size_t pqkv_ggml_flash_attn_ext_pq4_workspace_bytes(const polarquant_state *st, const int64_t ne_q[4],
+                                                    const int64_t ne_k[4]);
+int pqkv_ggml_flash_attn_ext_pq4(const polarquant_state *st, const float *q, const int64_t ne_q[4],
+                                 const size_t nb_q[4], const void *k, const int64_t ne_k[4], const size_t nb_k[4],
+                                 const void *v, const int64_t ne_v[4], const size_t nb_v[4], const void *mask,
+                                 const int64_t ne_m[4], const size_t nb_m[4], float scale, float max_bias,
+                                 float logit_softcap, float *dst, void *workspace, size_t workspace_bytes,
+                                 void *stream);
 
 #ifdef __cplusplus
 }

@@ -31,6 +31,11 @@ Parity pins (what checks each function besides itself), see tests/test_oracle.py
   group_*              hand-worked codes (round half to even, flat groups,
                        padding), zero vector, the reference tests' cosine
                        thresholds per width (tests/test_quantizer.py:66-82)
+  ggml_pq4_*           the ggml fixture tables, the R = I identity with the
+                       numpy restatement, lossless heads
+  ggml_flash_attn_ext  torch's float64 scaled_dot_product_attention with an
+                       additive mask (causal and padding masks), GQA by
+                       repetition, the all-masked row
 """
 
 from __future__ import annotations
@@ -509,6 +514,69 @@ def group_decompress(r, codes, lo, sc, R: np.ndarray, d: int, group_size: int) -
     g = g * sc.astype(np.float32)[:, None] + lo.astype(np.float32)[:, None]
     y = g.reshape(-1)[:d] * np.float32(r)
     return (y.astype(np.float64) @ R).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# GGML_TYPE_PQ4 and ggml's flash_attn_ext over it
+# ---------------------------------------------------------------------------
+
+def ggml_pq4_encode_rows(x: np.ndarray, d: int, R: np.ndarray, centroids: np.ndarray) -> np.ndarray:
+    """PQ4 rows of x [n, k] float32 (k whole heads of d): per head the fp32
+    FMA-chain rotation (the reference kernels' order, flash_turboquant.cu:
+    132-137, as restated in pq_oracle.c), then quantize_rotated and
+    pack_blocks (the radius tree, division, first-minimum scan, fp16 radius
+    saturated at 65504). The table is the ggml init's (patch:978-983)."""
+    from . import c_rotate_fma
+    x = np.ascontiguousarray(x, np.float32)
+    n, k = x.shape
+    heads = x.reshape(-1, d)
+    xr = c_rotate_fma(heads, R)
+    r, idx = quantize_rotated(xr, centroids)
+    return pack_blocks(r, idx, 4).reshape(n, -1)
+
+
+def ggml_pq4_values(blocks: np.ndarray, d: int, R: np.ndarray, centroids: np.ndarray) -> np.ndarray:
+    """The value of PQ4 heads [..., d/32 * 18] in float64: (r16 c[code]) R,
+    the stored radius times the centroids rotated back (patch:508-544 applies
+    x R to the attention output in the same space)."""
+    b = np.asarray(blocks, np.uint8)
+    lead = b.shape[:-1]
+    rot = dequantize_rotated(b.reshape(-1, b.shape[-1]), d, centroids, 4).astype(np.float64)
+    return (rot @ np.asarray(R, np.float64)).reshape(*lead, d)
+
+
+def ggml_flash_attn_ext(q: np.ndarray, k: np.ndarray, v: np.ndarray, mask, scale: float) -> np.ndarray:
+    """ggml_flash_attn_ext (ggml.h of ggml-org/llama.cpp, the upstream the
+    reference's integration clones, integration/README.md:33; unpinned) in
+    float64, with max_bias = logit_softcap = 0:
+      q [ns][n_q][Hq][d], k / v [ns_k][n_kv][Hkv][d] (ns_k 1 or ns),
+      mask None or [ns_m][n_q][n_kv] additive (ns_m 1 or ns);
+      out[s][i][h] = sum_t w_t v[s][t][h // (Hq / Hkv)],
+      w = softmax_t(scale q[s][i][h] . k[s][t][h // (Hq / Hkv)] + mask[s][i][t]);
+    a row whose logits are all -inf is 0 (ggml's CPU kernel divides by a
+    zero sum as 0). The reference's custom op computes the same attention
+    without a mask (patch:1305-1362)."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    ns, n_q, Hq, d = q.shape
+    Hkv = k.shape[2]
+    G = Hq // Hkv
+    out = np.zeros((ns, n_q, Hq, d))
+    for s in range(ns):
+        ks, vs = k[s if k.shape[0] > 1 else 0], v[s if v.shape[0] > 1 else 0]
+        for i in range(n_q):
+            m = None if mask is None else np.asarray(mask[s if mask.shape[0] > 1 else 0][i], np.float64)
+            for h in range(Hq):
+                logit = scale * (ks[:, h // G] @ q[s, i, h])
+                if m is not None:
+                    logit = logit + m
+                mx = logit.max() if logit.size else -np.inf
+                if not np.isfinite(mx):
+                    continue
+                w = np.exp(logit - mx)
+                out[s, i, h] = (w @ vs[:, h // G]) / w.sum()
+    return out
 
 
 def synth_kv(B: int, H: int, S: int, d: int, seed: int, kind: str = "normal") -> np.ndarray:

@@ -23,7 +23,8 @@ BUILD = os.path.join(HERE, "_build")
 SOURCES = ["pqkv_encode.hip", "pqkv_encode_mfma.hip", "pqkv_decode.hip", "pqkv_decode_mfma.hip",
            "pqkv_decode_mfma_k4v4_shared.hip", "pqkv_decode_mfma_k4v4_own.hip", "pqkv_decode_mfma_k4v2.hip",
            "pqkv_decode_mfma_k2v4.hip", "pqkv_decode_mfma_k2v2.hip", "pqkv_decode_mfma_pair.hip",
-           "pqkv_decode_mfma_soa.hip", "pqkv_prefill.hip", "pqkv_group.hip", "pqkv_api.cpp", "pqkv_compat.cpp", "pqkv_noalloc.hip"]
+           "pqkv_decode_mfma_soa.hip", "pqkv_decode_mfma_ggml.hip", "pqkv_prefill.hip", "pqkv_group.hip",
+           "pqkv_api.cpp", "pqkv_compat.cpp", "pqkv_ggml.cpp", "pqkv_noalloc.hip"]
 
 
 def hipcc() -> str:
@@ -53,8 +54,10 @@ def compile_one(src: str, changed_only: bool = False) -> str:
     if src.endswith(".hip"):
         cmd = [hipcc(), *COMMON, "-x", "hip", "-c", path, "-o", obj]
     else:
-        # host-only units (validation, C ABI): plain g++ against the HIP headers
-        cmd = ["g++", "-O2", "-fPIC", "-std=c++17", "-Wall", "-D__HIP_PLATFORM_AMD__",
+        # host-only units (validation, C ABI, the ggml type's CPU traits): plain
+        # g++ against the HIP headers; no contraction, so host arithmetic
+        # rounds where the source says
+        cmd = ["g++", "-O2", "-fPIC", "-std=c++17", "-Wall", "-ffp-contract=off", "-D__HIP_PLATFORM_AMD__",
                "-I/opt/rocm/include", "-c", path, "-o", obj]
     subprocess.run(cmd, check=True)
     return obj

@@ -99,6 +99,18 @@ std::vector<ProfRecord> g_prof;
 
 namespace pqkv {
 
+int fail_status(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void mfma_split_plan(int64_t streams, int S, int *splits, int *tps) {
+  decode_plan(streams, S > 0 ? S : 1, mfma_target(), splits, tps);
+}
+
 int prof_begin(const char *name, hipStream_t s) {
   std::lock_guard<std::mutex> lk(g_prof_mu);
   if (!g_prof_on) return -1;

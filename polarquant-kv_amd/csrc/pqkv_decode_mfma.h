@@ -272,13 +272,16 @@ constexpr int kNSub = kChunk / kSub;
 // grp*D/4 .. grp*D/4 + D/4 - 1 of token 16 st + col (kWords dwords, loaded
 // at their own, possibly 2 mod 4, offset). r: the radius of token 16 (col / 4) + 4 grp + col % 4 (row
 // broadcasts hand each lane those of its score rows). sg (QJL): sign bytes
-// grp*D/32 .. of token 16 st + col.
-template <int D, int KB, bool QJL>
+// grp*D/32 .. of token 16 st + col. mw (additive-mask mode): MW dwords of
+// fp16 mask values, two per dword, of the tokens whose logits the lane
+// holds in the softmax.
+template <int D, int KB, bool QJL, int MW = 0>
 struct ChunkK {
   static constexpr int kWords = D * KB / 128;
   uint32_t w[kNSub][kWords];
   uint32_t r;
   uint32_t sg[QJL ? kNSub : 1];
+  uint32_t mw[MW > 0 ? MW : 1];
 };
 // Values: for sub-tile kb and e = 0..3, the lane's qs word of token
 // 16 kb + 4 grp + e (4-bit: a dword; 2-bit: a half dword). r as for keys.
@@ -317,16 +320,30 @@ struct DecodeSmem {
 // (coordinate 2i low nibble, 2i + 1 high nibble) in one array and an fp32
 // radius in another (a.k_rad / a.v_rad, S_max per stream), instead of
 // block_pq4 vectors with fp16 radii.
-template <int D, int G, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false>
+// GG (the ggml flash-attn-ext layout): tokens a.k_tok_stride / a.v_tok_stride
+// bytes apart (the heads of a token interleaved), rows b of the batch grouped
+// a.rows_per_seq to a key / value sequence (seq = b / rows_per_seq), and an
+// optional fp16 additive mask (a.mask, row b % rows_per_seq of sequence seq)
+// added to every logit; a row whose tokens are all masked gives zeros.
+template <int D, int G, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GG = false>
 __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem<D, G, KB, VBITS, QJL, VSH> &sm,
                                                  const int split, const int bh) {
   static_assert(!SOA || (KB == 4 && VBITS == 4 && !QJL), "the SoA layout carries 4-bit codes and no QJL signs");
+  static_assert(!GG || (!SOA && !QJL), "the ggml layout has block-encoded keys and values and no QJL signs");
   constexpr int VBK = SOA ? D / 2 : vector_bytes(D, KB), VBV = SOA ? D / 2 : vector_bytes(D, VBITS);
   constexpr int KK = D / 16;     // score MFMAs per 16-token tile
   constexpr int NB = D / 16;     // value n-tiles
   constexpr int NSUB = kNSub;
   constexpr int KQ = D / 32;     // QJL MFMAs per 16-token tile (m = d projections)
-  using CK = ChunkK<D, KB, QJL>;
+  // G <= 4: the softmax runs on the compact layout (below), where a lane
+  // holds 4 consecutive tokens' logits; otherwise 4 per sub-tile.
+  constexpr bool kCompact = G <= 4;
+  constexpr int MW = GG ? (kCompact ? 2 : 2 * NSUB) : 0;  // mask dwords per lane and chunk
+  // Compact, the mask is added after the compaction, one iteration after the
+  // chunk's scores, so its words travel with the scores (MC of them);
+  // otherwise the score product adds it while the chunk's words are loaded.
+  constexpr int MC = GG && kCompact ? MW : 1;
+  using CK = ChunkK<D, KB, QJL, MW>;
   using CV = ChunkV<VBITS>;
 
   const uint2 *lut_k = sm.u.t.k, *lut_v = VSH ? sm.u.t.k : sm.u.t.v, *lut_s = sm.u.t.s;
@@ -337,6 +354,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   const int col = lane & 15, grp = lane >> 4;
   const int b = bh / a.n_heads, hi_ = bh - b * a.n_heads;
   const int h = a.listed ? a.heads[hi_] : hi_;
+  const int seq = GG ? b / a.rows_per_seq : b;   // the key / value sequence of row b
   const int t_begin = split * a.tokens_per_split;
   const int t_end = min(a.S, t_begin + a.tokens_per_split);
   const uint8_t *kstream, *vstream;
@@ -344,11 +362,20 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
     kstream = a.k_cache + b * a.k_batch_stride + a.k_head_off[hi_];
     vstream = a.v_cache + b * a.v_batch_stride + a.v_head_off[hi_];
   } else {
-    kstream = a.k_cache + b * a.k_batch_stride + h * a.k_head_stride;
-    vstream = a.v_cache + b * a.v_batch_stride + h * a.v_head_stride;
+    kstream = a.k_cache + seq * a.k_batch_stride + h * a.k_head_stride;
+    vstream = a.v_cache + seq * a.v_batch_stride + h * a.v_head_stride;
   }
-  const __amdgpu_buffer_rsrc_t kres = stream_rsrc(kstream, (uint32_t)a.S * (uint32_t)VBK);
-  const __amdgpu_buffer_rsrc_t vres = stream_rsrc(vstream, (uint32_t)a.S * (uint32_t)VBV);
+  // bytes between consecutive tokens of a stream
+  const int kts = GG ? (int)a.k_tok_stride : VBK, vts = GG ? (int)a.v_tok_stride : VBV;
+  const __amdgpu_buffer_rsrc_t kres = stream_rsrc(kstream, (uint32_t)a.S * (uint32_t)kts);
+  const __amdgpu_buffer_rsrc_t vres = stream_rsrc(vstream, (uint32_t)a.S * (uint32_t)vts);
+  // GG: the mask row of row b (no mask: an empty buffer, every load reads 0)
+  __amdgpu_buffer_rsrc_t mres = kres;
+  if constexpr (GG) {
+    const uint16_t *mrow = a.mask ? a.mask + seq * a.mask_seq_stride + (b - seq * a.rows_per_seq) * a.mask_row_stride
+                                  : nullptr;
+    mres = stream_rsrc((const uint8_t *)mrow, mrow ? (uint32_t)a.S * 2u : 0u);
+  }
   // radii: fp16 inside the blocks, or (SOA) fp32 arrays of S_max per stream
   __amdgpu_buffer_rsrc_t krres = kres, vrres = vres;
   if constexpr (SOA) {
@@ -356,8 +383,8 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
     krres = stream_rsrc((const uint8_t *)(a.k_rad + ri), (uint32_t)a.S * 4u);
     vrres = stream_rsrc((const uint8_t *)(a.v_rad + ri), (uint32_t)a.S * 4u);
   }
-  auto ld_rad_k = [&](int tok) { return SOA ? bld32(krres, tok * 4) : bld16(kres, tok * VBK); };
-  auto ld_rad_v = [&](int tok) { return SOA ? bld32(vrres, tok * 4) : bld16(vres, tok * VBV); };
+  auto ld_rad_k = [&](int tok) { return SOA ? bld32(krres, tok * 4) : bld16(kres, tok * kts); };
+  auto ld_rad_v = [&](int tok) { return SOA ? bld32(vrres, tok * 4) : bld16(vres, tok * vts); };
   auto rad = [](uint32_t bits) { return SOA ? __builtin_bit_cast(float, bits) : half_bits_to_float(bits); };
   __amdgpu_buffer_rsrc_t sres = kres;
   if constexpr (QJL)
@@ -443,7 +470,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   // as soon as it has read them (and the radii first: they are converted at
   // the start of a step).
   auto load_k_sub = [&](CK &c, int t0, int st) {
-    load_words(kres, (t0 + kSub * st + col) * VBK + kphys, c.w[st]);
+    load_words(kres, (t0 + kSub * st + col) * kts + kphys, c.w[st]);
     if constexpr (QJL) {
       const int so = (t0 + kSub * st + col) * (D / 8) + grp * (D / 32);
       c.sg[st] = D == 128 ? bld32(sres, so) : bld16(sres, so);
@@ -452,12 +479,29 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   auto load_v_sub = [&](CV &c, int t0, int kb) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int off = (t0 + kSub * kb + 4 * grp + e) * VBV + vob;
+      const int off = (t0 + kSub * kb + 4 * grp + e) * vts + vob;
       c.w[kb][e] = VBITS == 4 ? bld32(vres, off) : bld16(vres, off);
     }
   };
+  // GG: the mask values of the chunk's logits this lane holds in the
+  // softmax: compact, tokens 16 (col / 4) + 4 grp .. + 3; otherwise tokens
+  // 16 st + 4 grp .. + 3 of every sub-tile st. One 2-byte load per token,
+  // so a token is either wholly inside the row (S values) or reads 0.
+  auto load_mask = [&](CK &c, int t0) {
+    if constexpr (GG) {
+#pragma unroll
+      for (int j = 0; j < MW; ++j) {
+        const int tok = t0 + kSub * (kCompact ? (col >> 2) : j >> 1) + 4 * grp + 2 * (j & 1);
+        c.mw[j] = bld16(mres, 2 * tok) | (bld16(mres, 2 * tok + 2) << 16);
+      }
+    }
+  };
+  // fp16 mask value j of a lane's mask words, and the logits' exp2 scale
+  constexpr float kLog2eF = 1.4426950408889634f;
+  auto mask_val = [](const uint32_t *mk, int j) { return half_bits_to_float(mk[j >> 1] >> (16 * (j & 1))); };
   auto load_k = [&](CK &c, int t0) {
     c.r = ld_rad_k(t0 + rtok);
+    load_mask(c, t0);
 #pragma unroll
     for (int st = 0; st < NSUB; ++st) load_k_sub(c, t0, st);
   };
@@ -513,7 +557,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   // token 16st + 4grp + i, meaningful in lanes col < G. Lanes of absent heads
   // (q = 0) and the cross lanes (col >= 8) carry finite values that only
   // reach discarded output rows. rkl: this lane's loaded radius.
-  auto kmma = [&](const KTile &kt, float rkl, int st, float4_t &out) {
+  auto kmma = [&](const KTile &kt, float rkl, int st, const uint32_t *mk, float4_t &out) {
     float4_t acc = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) acc = mfma16(pack8(kt.t[kk][0], kt.t[kk][1]), qb[kk], acc);
@@ -534,6 +578,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
         const float q = __builtin_fmaf(row_ror8f(accq[i]), 1.0f / kLoScale, accq[i]);
         v = rk > 0.0f ? v + q : v;  // zero keys get no correction
       }
+      if constexpr (GG) v = __builtin_fmaf(mask_val(mk, 4 * st + i), kLog2eF, v);  // additive mask, exp2 domain
       out[i] = v;
     }
   };
@@ -591,13 +636,14 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   // A operand is spread back by two bank-masked DPP moves per value. The
   // running max and sum are kept per lane of the compact layout (head
   // col % 4; the sum is reduced across the banks at the end).
-  constexpr bool kCompact = G <= 4;
   struct FState {
     float mnew, alpha, psum;
     uint32_t top[kCompact ? 4 : 1], bot[kCompact ? 4 : 1];  // compact weights: (p_hi, 0), (p_lo, p_hi)
   };
-  // rks (kRawScores): this lane's loaded key radius of the chunk in sc.
-  auto fbegin = [&](float (&sv)[NSUB][4], const float4_t (&sc)[NSUB], int ntok, bool partial, float rvl, float rks) {
+  // rks (kRawScores): this lane's loaded key radius of the chunk in sc; mk
+  // (GG): its mask words of that chunk.
+  auto fbegin = [&](float (&sv)[NSUB][4], const float4_t (&sc)[NSUB], int ntok, bool partial, float rvl, float rks,
+                    const uint32_t (&mk)[MC]) {
     FState f;
     float cmax;
     float cv[4];
@@ -617,6 +663,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
           // radius of token 16 j + 4 grp + i: lane 4 j + i of the quad
           c = __builtin_fmaf(x, 1.0f / kLoScale, c) * quad_bcast(rks, i);
         }
+        if constexpr (GG) c = __builtin_fmaf(mask_val(mk, i), kLog2eF, c);  // the logits are in the exp2 domain
         cv[i] = partial && kSub * (col >> 2) + 4 * grp + i >= ntok ? -INFINITY : c;
       }
       cmax = fmaxf(fmaxf(cv[0], cv[1]), fmaxf(cv[2], cv[3]));
@@ -641,9 +688,12 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
         for (int i = 0; i < 4; ++i) cmax = fmaxf(cmax, sv[st][i]);
     }
     // token 0 of the chunk is valid, so after the row reduction every lane's
-    // max is finite; the first chunk has m_run = -inf and alpha = 0.
+    // max is finite; the first chunk has m_run = -inf and alpha = 0. With a
+    // mask (GG) every logit so far can be -inf: the exponentials then take 0
+    // as their reference point (all weights 0) and m_run stays -inf.
     cmax = rows_max(cmax);
-    f.mnew = fmaxf(m_run, cmax);
+    const float mtrue = fmaxf(m_run, cmax);
+    f.mnew = GG && mtrue == -INFINITY ? 0.0f : mtrue;
     f.alpha = __builtin_amdgcn_exp2f(m_run - f.mnew);
     f.psum = 0.0f;
     if constexpr (SOA) {
@@ -659,7 +709,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
         }
       }
     }
-    m_run = f.mnew;
+    m_run = mtrue;
     if constexpr (kCompact) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -730,23 +780,26 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   };
 
   // Scores of a whole chunk (the first one): reads one sub-tile ahead.
-  auto scores = [&](const CK &k, float4_t (&sc)[NSUB], float &rks) {
+  auto scores = [&](const CK &k, float4_t (&sc)[NSUB], float &rks, uint32_t (&mks)[MC]) {
     const float rkl = rad(k.r);
     rks = rkl;
+#pragma unroll
+    for (int j = 0; j < MC; ++j) mks[j] = k.mw[j];
     KTile kt[2];
     kread(k, 0, kt[0]);
 #pragma unroll
     for (int st = 0; st < NSUB; ++st) {
       if (st + 1 < NSUB) kread(k, st + 1, kt[(st + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);
-      kmma(kt[st & 1], rkl, st, sc[st]);
+      kmma(kt[st & 1], rkl, st, k.mw, sc[st]);
     }
   };
   // Softmax update and value product of a whole chunk (the last one).
-  auto finish = [&](const CV &v, const float4_t (&sc)[NSUB], float rks, int ntok, bool partial) {
+  auto finish = [&](const CV &v, const float4_t (&sc)[NSUB], float rks, const uint32_t (&mks)[MC],
+                    int ntok, bool partial) {
     float sv[NSUB][4];
     const float rvl = rad(v.r);
-    FState f = fbegin(sv, sc, ntok, partial, rvl, rks);
+    FState f = fbegin(sv, sc, ntok, partial, rvl, rks, mks);
     VTile vt[2];
     vread(v, 0, vt[0]);
 #pragma unroll
@@ -767,12 +820,14 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   // for the first loads: config 4 28.3 -> 27.3 us); the QJL kernels with
   // G > 4 would spill with that schedule and reload after the iteration.
   constexpr bool kPieceLoads = !QJL || G <= 4;
-  auto step = [&](CK &k, CV &v, const float4_t (&sc)[NSUB], float rks, float4_t (&sn)[NSUB], float &rkn, int tk,
-                  int tv) {
+  auto step = [&](CK &k, CV &v, const float4_t (&sc)[NSUB], float rks, const uint32_t (&mks)[MC],
+                  float4_t (&sn)[NSUB], float &rkn, uint32_t (&mkn)[MC], int tk, int tv) {
     float sv[NSUB][4];
     const float rkl = rad(k.r), rvl = rad(v.r);
     rkn = rkl;
-    FState f = fbegin(sv, sc, kChunk, false, rvl, rks);
+#pragma unroll
+    for (int j = 0; j < MC; ++j) mkn[j] = k.mw[j];
+    FState f = fbegin(sv, sc, kChunk, false, rvl, rks, mks);
 #pragma unroll
     for (int j = 0; j < NSUB; ++j) {
       KTile kt;
@@ -788,15 +843,19 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
           // loads miss again in L2 (+2.6 % HBM traffic)
           k.r = ld_rad_k(tk + rtok);
           v.r = ld_rad_v(tv + rtok);
+          if constexpr (kCompact) load_mask(k, tk);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
       const half8_t pav = fweights(sv[j], rvl, j, f);
       __builtin_amdgcn_sched_barrier(0);
-      kmma(kt, rkl, j, sn[j]);
+      kmma(kt, rkl, j, k.mw, sn[j]);
       vmma(pav, vt);
     }
     l_run = l_run * f.alpha + f.psum;
+    // the mask words of the next chunk, once this one's score products have
+    // read theirs (the compact layout loads them with the radii)
+    if constexpr (GG && !kCompact && kPieceLoads) load_mask(k, tk);
     if constexpr (!kPieceLoads) {
       load_k(k, tk);
       load_v(v, tv);
@@ -819,19 +878,23 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
     load_v(cv, first);
     float4_t sacc[NSUB];
     float rks;
-    scores(ck, sacc, rks);
+    uint32_t mks[MC];
+    scores(ck, sacc, rks, mks);
     // chunk 1 (a repeat of chunk 0 when there is none: an L2 hit)
     load_k(ck, first + min(1, nch - 1) * kStep);
     for (int i = 0; i + 1 < nch; ++i) {
       float4_t snext[NSUB];
       float rkn;
-      step(ck, cv, sacc, rks, snext, rkn, first + min(i + 2, nch - 1) * kStep, first + (i + 1) * kStep);
+      uint32_t mkn[MC];
+      step(ck, cv, sacc, rks, mks, snext, rkn, mkn, first + min(i + 2, nch - 1) * kStep, first + (i + 1) * kStep);
 #pragma unroll
       for (int st = 0; st < NSUB; ++st) sacc[st] = snext[st];
       rks = rkn;
+#pragma unroll
+      for (int j = 0; j < MC; ++j) mks[j] = mkn[j];
     }
     const int tlast = first + (nch - 1) * kStep;
-    finish(cv, sacc, rks, min(kChunk, t_end - tlast), true);
+    finish(cv, sacc, rks, mks, min(kChunk, t_end - tlast), true);
   }
 
   // ---------------- per-wave results ----------------
@@ -886,10 +949,10 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   }
 }
 
-template <int D, int G, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false>
+template <int D, int G, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GG = false>
 __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(const DecodeArgs a) {
   __shared__ DecodeSmem<D, G, KB, VBITS, QJL, VSH> sm;
-  decode_mfma_body<D, G, KB, VBITS, QJL, VSH, SOA>(a, sm, blockIdx.x, blockIdx.y);
+  decode_mfma_body<D, G, KB, VBITS, QJL, VSH, SOA, GG>(a, sm, blockIdx.x, blockIdx.y);
 }
 
 // Mixed widths whose kv heads are either 4-bit keys and values (a4, one
@@ -926,10 +989,10 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_pair_kernel
     default: KERNEL(8, __VA_ARGS__); break;                               \
   }
 
-template <int D, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false>
+template <int D, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GGML = false>
 static void launch_dm(const DecodeArgs &a, int G, hipStream_t s) {
   dim3 grid(a.splits, a.B * a.n_heads);
-#define PQKV_DM_ONE(GG, ...) decode_mfma_kernel<D, GG, KB, VBITS, QJL, VSH, SOA><<<grid, 256, 0, s>>>(a)
+#define PQKV_DM_ONE(GG, ...) decode_mfma_kernel<D, GG, KB, VBITS, QJL, VSH, SOA, GGML><<<grid, 256, 0, s>>>(a)
   PQKV_DM_G_SWITCH(PQKV_DM_ONE, 0)
 #undef PQKV_DM_ONE
 }

@@ -1,0 +1,14 @@
+// Decode kernel instantiations for the ggml flash-attn-ext layout: 4-bit keys
+// and values with one codebook, tokens of a stream a stride apart, batch rows
+// grouped into key / value sequences, fp16 additive mask.
+#include "pqkv_decode_mfma.h"
+
+namespace pqkv {
+
+hipError_t launch_decode_mfma_ggml(const DecodeArgs &a, hipStream_t s) {
+  if (a.d == 128) launch_dm<128, 4, 4, false, true, false, true>(a, a.g, s);
+  else launch_dm<64, 4, 4, false, true, false, true>(a, a.g, s);
+  return hipGetLastError();
+}
+
+}  // namespace pqkv

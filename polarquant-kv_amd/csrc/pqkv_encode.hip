@@ -160,6 +160,19 @@ struct PlainSource {
   const TIN *x;
   __device__ __forceinline__ float operator()(int64_t v, int j) const { return load_as_float(x + v * D + j); }
 };
+// fp32 rows of a strided [n_seq][Hq][n_q] arrangement read in
+// [n_seq][n_q][Hq] order (ggml's flash-attn-ext query: element strides s_q
+// between query rows, s_h between heads, s_s between sequences).
+struct RowsSource {
+  const float *x;
+  int64_t s_q, s_h, s_s;
+  int n_q, Hq;
+  __device__ __forceinline__ float operator()(int64_t v, int j) const {
+    const int64_t rest = v / Hq, h = v - rest * Hq;
+    const int64_t sq = rest / n_q, iq = rest - sq * n_q;
+    return x[sq * s_s + h * s_h + iq * s_q + j];
+  }
+};
 // Block-encoded vectors (block_pq4 / block_pq2): r16 * c[code], the rotated
 // reconstruction the attention kernels use.
 template <int D, int BITS>
@@ -529,6 +542,20 @@ static void rotate_dispatch(const void *x, int xt, const float *R, void *y, int 
     rotate_kernel<D, INV, H, float><<<grid, 256, 0, s>>>(H{(const half_t *)x}, R, (float *)y, n, sc);
   else
     rotate_kernel<D, INV, H, half_t><<<grid, 256, 0, s>>>(H{(const half_t *)x}, R, (half_t *)y, n, sc);
+}
+
+hipError_t launch_rotate_rows(const float *x, int64_t s_q, int64_t s_h, int64_t s_s, int n_q, int Hq, int n_seq,
+                              const float *R, float *y, int d, float out_scale, hipStream_t s) {
+  const int64_t n = (int64_t)n_seq * n_q * Hq;
+  const RowsSource src{x, s_q, s_h, s_s, n_q, Hq};
+  if (d == 128) {
+    const dim3 grid(grid_for(n, kRotVec, 2048), 128 / kRotCols);
+    rotate_kernel<128, false, RowsSource, float><<<grid, 256, 0, s>>>(src, R, y, n, out_scale);
+  } else {
+    const dim3 grid(grid_for(n, kRotVec, 2048), 64 / kRotCols);
+    rotate_kernel<64, false, RowsSource, float><<<grid, 256, 0, s>>>(src, R, y, n, out_scale);
+  }
+  return hipGetLastError();
 }
 
 template <int D, int BITS>

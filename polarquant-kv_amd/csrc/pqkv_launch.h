@@ -59,6 +59,14 @@ struct DecodeArgs {
   int split_base, split_stride;  // this launch's splits are partials split_base .. of split_stride per query head
   int n_heads;                   // heads in this launch
   int listed;                    // 1: heads / offsets below are used
+  // ggml layout (launch_decode_mfma_ggml only): bytes between consecutive
+  // tokens of a stream; batch rows per key / value sequence (the sequence
+  // of row b is b / rows_per_seq, k_batch_stride apart); fp16 additive mask
+  // [seq][row][S] with element strides, or null.
+  int64_t k_tok_stride, v_tok_stride;
+  int rows_per_seq;
+  const uint16_t *mask;
+  int64_t mask_row_stride, mask_seq_stride;
   int16_t heads[kMaxListHeads];
   int64_t k_head_off[kMaxListHeads], v_head_off[kMaxListHeads];
 };
@@ -119,6 +127,11 @@ int decode_segments_run(const void *q, int q_dtype, const float *R, int n_seg, c
 // Sets the thread's error message from a HIP error; returns PQKV_ERR_HIP
 // (PQKV_OK for hipSuccess).
 int report_hip_error(hipError_t e, const char *what);
+// Sets the thread's error message (printf format); returns code.
+int fail_status(int code, const char *fmt, ...);
+// The matrix-core decode kernel's split plan for `streams` (batch, kv-head)
+// streams of S tokens: one balanced round of workgroups.
+void mfma_split_plan(int64_t streams, int S, int *splits, int *tps);
 
 // Event brackets for the measurement hook (pqkv_profile_*): returns a token
 // for prof_end, or -1 when profiling is off.
@@ -133,6 +146,12 @@ hipError_t launch_rotate2(const void *x, int x_dtype, const float *R, const floa
 // R == nullptr: y = x * out_scale (an identity rotation, exactly).
 hipError_t launch_rotate(const void *x, int x_dtype, const float *R, void *y, int y_dtype, int64_t n, int d,
                          int inverse, float out_scale, hipStream_t s);
+// fp32 rows gathered from a strided [n_seq][Hq][n_q] arrangement (element
+// strides: s_q between query rows, s_h between heads, s_s between
+// sequences) into y [n_seq][n_q][Hq][d] fp32, y = (R x) out_scale: the FMA
+// chains of launch_rotate.
+hipError_t launch_rotate_rows(const float *x, int64_t s_q, int64_t s_h, int64_t s_s, int n_q, int Hq, int n_seq,
+                              const float *R, float *y, int d, float out_scale, hipStream_t s);
 // y = (r16 c[code]) R for n block-encoded vectors (inverse rotation, one
 // FMA chain per output as in launch_rotate); fp16 output saturates.
 hipError_t launch_dequantize(const uint8_t *blocks, const float *codebook, int bits, const float *R, void *y,
@@ -162,6 +181,9 @@ hipError_t launch_decode_mfma_pair(const DecodeArgs &a4, const DecodeArgs &a2, h
 // in k_cache / v_cache, fp32 radii in k_rad / v_rad), codebooks of cb_levels
 // entries (one shared table when k_cb == v_cb), no QJL.
 hipError_t launch_decode_mfma_soa(const DecodeArgs &a, hipStream_t s);
+// 4-bit keys and values with one codebook in the ggml flash-attn-ext layout
+// (a.k_tok_stride, a.rows_per_seq, a.mask), no QJL, unlisted heads.
+hipError_t launch_decode_mfma_ggml(const DecodeArgs &a, hipStream_t s);
 // R == nullptr: the normalised rotated output, not rotated back.
 hipError_t launch_decode_merge(const float *part, const float *R, void *out, int out_dtype, int BHq, int splits,
                                int d, hipStream_t s);

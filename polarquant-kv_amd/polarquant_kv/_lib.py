@@ -19,6 +19,8 @@ F32, F16, BF16 = 0, 1, 2
 c_void_p, c_int, c_int64, c_float, c_size_t = (ctypes.c_void_p, ctypes.c_int, ctypes.c_int64,
                                                ctypes.c_float, ctypes.c_size_t)
 c_int_p, c_float_p = ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_float)
+c_int64_4, c_size_4 = ctypes.c_int64 * 4, ctypes.c_size_t * 4      # ggml ne / nb arrays
+c_int64_p, c_size_p = ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_size_t)
 
 # name -> (restype, argtypes); the full exported surface of include/pqkv.h
 SIGNATURES = {
@@ -77,6 +79,17 @@ SIGNATURES = {
     "polarquant_inverse_rotate_cuda_c": (None, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "turboquant_compress": (None, [c_int64] * 5 + [c_int] * 3),
     "turboquant_full_attention": (None, [c_int64] * 12 + [c_int] * 5 + [c_float]),
+    "pqkv_pq4_quantize_rows_host": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p]),
+    "pqkv_pq4_dequantize_rows_host": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p]),
+    "pqkv_ggml_pq4_rotation": (c_int, [c_void_p, c_int]),
+    "pqkv_ggml_quantize_row_pq4_ref": (None, [c_void_p, c_void_p, c_int64]),
+    "pqkv_ggml_dequantize_row_pq4": (None, [c_void_p, c_void_p, c_int64]),
+    "pqkv_ggml_cpy_pq4": (c_int, [c_void_p, c_void_p, c_int, c_int64_p, c_size_p, c_void_p, c_size_p, c_void_p]),
+    "pqkv_ggml_flash_attn_ext_pq4_workspace_bytes": (c_size_t, [c_void_p, c_int64_p, c_int64_p]),
+    "pqkv_ggml_flash_attn_ext_pq4": (c_int, [c_void_p, c_void_p, c_int64_p, c_size_p, c_void_p, c_int64_p, c_size_p,
+                                             c_void_p, c_int64_p, c_size_p, c_void_p, c_int64_p, c_size_p,
+                                             c_float, c_float, c_float, c_void_p, c_void_p, c_size_t,
+                                             c_void_p]),
 }
 
 _lib = None
