@@ -2,7 +2,7 @@
 """PQ4 decode-attention throughput on one MI355X (plus encode tokens/s).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                    [--workload config3|config1|config2|config4|config5]
+                    [--workload config3|config1|config2|config4|config5|ggml]
 
 Default workload (the 32K-context metric config):
 one Llama-3-8B-shaped attention layer, B=8, 32 query / 8 kv heads, d=128,
@@ -318,9 +318,11 @@ def _cpu_obj(gbps, unit, cores, model, blas, sample):
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--workload", choices=("config3", "config1", "config2", "config4", "config5"), default="config3",
-                    help="config3 (default): the metric line; the others: BASELINE.json's remaining "
-                         "configurations, each its own line")
+    ap.add_argument("--workload", choices=("config3", "config1", "config2", "config4", "config5", "ggml"),
+                    default="config3",
+                    help="config3 (default): the metric line; config1/2/4/5: BASELINE.json's remaining "
+                         "configurations, each its own line; ggml: config 3's decode through the ggml "
+                         "flash_attn_ext op over GGML_TYPE_PQ4 in llama.cpp's cache layout")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
@@ -335,7 +337,7 @@ def main() -> int:
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
     return {"config3": run_config3, "config1": run_config1, "config2": run_config2, "config4": run_config4,
-            "config5": run_config5}[args.workload](args)
+            "config5": run_config5, "ggml": run_ggml}[args.workload](args)
 
 
 def run_config3(args) -> int:
@@ -480,6 +482,91 @@ def _decode_line(args, name, metric_workload, B, Hq, Hkv, S, d, kc, vc, q, R, jl
     if extra:
         line.update(extra)
     return line
+
+
+def run_ggml(args) -> int:
+    """Config 3's decode step (8 sequences, 32 query / 8 kv heads, d = 128,
+    32768 cached tokens each, one query token per sequence) through the ggml
+    flash_attn_ext op over GGML_TYPE_PQ4: per-sequence caches in llama.cpp's
+    layout (a token's 8 heads side by side, 576 bytes per token), permuted
+    views, an f16 mask row of zeros (all tokens visible) shared by the
+    sequences. K and V are the config's channel-law data, written by the cpy
+    op. value = (K + V rows + q in + out) / step (hipGraph replays)."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+    from polarquant_kv import _lib, ggml
+
+    dev = "cuda:0"
+    ns, Hq, Hkv, S, d = 8, 32, 8, 32768, 128
+    vb = ggml.row_size(d)
+    st = ggml.State(d, Hkv, Hq)
+    caches = []
+    for seed in (1, 2):
+        x = synth_channel_kv(torch, ns, Hkv, S, d, seed, dev).float().permute(0, 2, 1, 3).reshape(1, ns, S, Hkv * d)
+        c = torch.empty((ns, S, Hkv * vb), dtype=torch.uint8, device=dev)
+        ggml.cpy(st, x.contiguous(), c[None])
+        del x
+        caches.append(c)
+    torch.cuda.synchronize()
+    kv, vv = [c.view(ns, S, Hkv, vb).permute(0, 2, 1, 3) for c in caches]
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    q = torch.randn((ns, 1, Hq, d), generator=g, device=dev).permute(0, 2, 1, 3)
+    mask = torch.zeros((1, 1, 32, S), dtype=torch.float16, device=dev)
+    scale = 1.0 / d ** 0.5
+
+    def step():
+        return ggml.flash_attn_ext(st, q, kv, vv, mask, scale)
+
+    eager_ms, out = timed_eager(torch, step, args.steps, args.warmup)
+    assert torch.isfinite(out).all()
+    graph_ms, _ = timed_graph(torch, step, max(args.steps, 100), 2)
+    km = kernel_means(torch, _lib, step, args.steps, ("ggml_fa_split", "ggml_fa_rotate", "ggml_fa_merge"))
+    cache_bytes = 2 * ns * S * Hkv * vb
+    step_bytes = cache_bytes + ns * Hq * d * 4 * 2
+    kern_bytes = cache_bytes + ns * Hq * d * 4 + S * 2
+    cpu = None
+    if not args.no_cpu:
+        # the oracle on sequence 0 (1/8 of the step): values of its rows, then
+        # ggml's attention in float64
+        cores, model = cpu_info()
+        from threadpoolctl import threadpool_limits
+        R = ggml.rotation(d)
+        table = ggml.default_codebook()
+        kb = kv[0:1].permute(0, 2, 1, 3).contiguous().cpu().numpy()
+        vbt = vv[0:1].permute(0, 2, 1, 3).contiguous().cpu().numpy()
+        qn = q[0:1].permute(0, 2, 1, 3).contiguous().cpu().numpy()
+        with threadpool_limits(limits=cores):
+            t = timed_median(lambda: O.ggml_flash_attn_ext(qn, O.ggml_pq4_values(kb, d, R, table),
+                                                           O.ggml_pq4_values(vbt, d, R, table), None, scale),
+                             runs=args.cpu_runs)
+        cpu = _cpu_obj(cache_bytes / ns / t / 1e9, "GB/s", cores, model, cores,
+                       f"oracle float64 ggml flash_attn_ext of sequence 0 (1/8 of the step: its 32768 tokens x 8 "
+                       f"kv heads, values of the PQ4 rows then attention), median of {args.cpu_runs} runs of "
+                       f"{t:.2f} s")
+    line = {
+        "metric": "ggml flash_attn_ext over GGML_TYPE_PQ4 GB/s at 1 MI355X (config-3 decode shape)",
+        "value": round(step_bytes / (graph_ms / 1e3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(graph_ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u4 codes; f16 hi/lo MFMA, f32 accumulate", "data": "synthetic",
+        "config": {"workload": "ggml: config 3 (8 sequences x 32768 tokens, Hq 32 / Hkv 8, d 128) in llama.cpp's "
+                               "layout, f16 mask row, f32 q / out", "global_batch": ns, "seq_len": S,
+                   "parallelism": "single GPU"},
+        "timing": "hipGraph replays of 10 captured steps; eager step in eager_ms_per_step",
+        "eager_ms_per_step": round(eager_ms, 5), "bytes_per_step": step_bytes,
+        "roofline": {"bound": "hbm", "achieved": round(kern_bytes / (km["ggml_fa_split"] / 1e3) / 1e9, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(kern_bytes / (km["ggml_fa_split"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "decode_mfma_kernel<128,4,4,4,ggml>",
+                     "kernel_ms_events": round(km["ggml_fa_split"], 5), "bytes_per_launch": kern_bytes},
+        "stages_ms_events": {k: round(v, 5) for k, v in km.items()},
+        "cpu_baseline": cpu,
+    }
+    st.close()
+    print(json.dumps(line))
+    return 0
 
 
 def run_config1(args) -> int:

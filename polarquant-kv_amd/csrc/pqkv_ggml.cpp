@@ -362,8 +362,10 @@ int pqkv_ggml_flash_attn_ext_pq4(const polarquant_state *st, const float *q, con
   float *q32 = (float *)((char *)workspace + f.q_off);
   float *part = (float *)((char *)workspace + f.part_off);
   const float kLog2e = 1.4426950408889634f;
+  int tok = pqkv::prof_begin("ggml_fa_rotate", s);
   hipError_t e = pqkv::launch_rotate_rows(q, (int64_t)(nb_q[1] / 4), (int64_t)(nb_q[2] / 4), (int64_t)(nb_q[3] / 4),
                                           f.n_q, f.Hq, f.n_seq, st->rotation, q32, f.d, scale * kLog2e, s);
+  pqkv::prof_end(tok, s);
   if (e != hipSuccess) return pqkv::report_hip_error(e, "ggml flash_attn_ext query rotation");
 
   pqkv::DecodeArgs a;
@@ -403,11 +405,15 @@ int pqkv_ggml_flash_attn_ext_pq4(const polarquant_state *st, const float *q, con
   for (int i = 0; i < n_sub; ++i) {
     a.q_off = off;
     a.g = a.gq / n_sub + (i < a.gq % n_sub ? 1 : 0);
+    tok = pqkv::prof_begin("ggml_fa_split", s);
     e = pqkv::launch_decode_mfma_ggml(a, s);
+    pqkv::prof_end(tok, s);
     if (e != hipSuccess) return pqkv::report_hip_error(e, "ggml flash_attn_ext split launch");
     off += a.g;
   }
+  tok = pqkv::prof_begin("ggml_fa_merge", s);
   e = pqkv::launch_decode_merge(part, st->rotation, dst, PQKV_F32, (int)(rows * f.Hq), f.splits, f.d, s);
+  pqkv::prof_end(tok, s);
   return pqkv::report_hip_error(e, "ggml flash_attn_ext merge launch");
 }
 
