@@ -325,7 +325,12 @@ struct DecodeSmem {
 // a.rows_per_seq to a key / value sequence (seq = b / rows_per_seq), and an
 // optional fp16 additive mask (a.mask, row b % rows_per_seq of sequence seq)
 // added to every logit; a row whose tokens are all masked gives zeros.
-template <int D, int G, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GG = false>
+// HW (heads per wave): bh is this wave's own pair; each wave streams every
+// chunk of the split for its head and writes its partial itself (the four
+// waves of a workgroup take four kv heads of the same tokens, which share
+// cache lines when a token's heads are interleaved). The code tables are
+// built from one codebook shared by all heads (cb_head_stride 0).
+template <int D, int G, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GG = false, bool HW = false>
 __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem<D, G, KB, VBITS, QJL, VSH> &sm,
                                                  const int split, const int bh) {
   static_assert(!SOA || (KB == 4 && VBITS == 4 && !QJL), "the SoA layout carries 4-bit codes and no QJL signs");
@@ -353,12 +358,13 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
   const int b = bh / a.n_heads, hi_ = bh - b * a.n_heads;
-  const int h = a.listed ? a.heads[hi_] : hi_;
+  const bool listed = !GG && a.listed;  // (the ggml layout lists no heads)
+  const int h = listed ? a.heads[hi_] : hi_;
   const int seq = GG ? b / a.rows_per_seq : b;   // the key / value sequence of row b
   const int t_begin = split * a.tokens_per_split;
   const int t_end = min(a.S, t_begin + a.tokens_per_split);
   const uint8_t *kstream, *vstream;
-  if (a.listed) {
+  if (listed) {
     kstream = a.k_cache + b * a.k_batch_stride + a.k_head_off[hi_];
     vstream = a.v_cache + b * a.v_batch_stride + a.v_head_off[hi_];
   } else {
@@ -868,8 +874,8 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   // work. The key registers are reloaded with chunk i + 2 and the value
   // registers with chunk i + 1. Only the last chunk can be partial; it is
   // finished after the loop.
-  constexpr int kStep = kMWaves * kChunk;
-  const int first = t_begin + wave * kChunk;
+  constexpr int kStep = HW ? kChunk : kMWaves * kChunk;
+  const int first = t_begin + (HW ? 0 : wave * kChunk);
   const int nch = first < t_end ? (t_end - first + kStep - 1) / kStep : 0;
   if (nch > 0) {
     CK ck;
@@ -905,6 +911,27 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
     l_run += __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, l_run), 0x128, 0xF, 0xF, true));
   }
   l_run = rows_sum(l_run);
+  if constexpr (HW) {
+    // the wave's partial of its G heads, straight from the registers
+    float *dst = a.part + (((int64_t)(b * a.Hq + h * a.gq + a.q_off) * a.split_stride) + a.split_base + split) * (D + 2);
+    const int64_t hstep = (int64_t)a.split_stride * (D + 2);
+    if (lane < G) {
+      dst[lane * hstep] = m_run;
+      dst[lane * hstep + 1] = l_run;
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float cross = shfl_xor_f(oacc[nb][i], 32);
+        const int head = 4 * grp + i;
+        if (grp < 2 && head < G) {
+          const int coord = D == 128 ? 8 * col + nb : 8 * (col & 7) + 2 * nb + (col >> 3);
+          dst[head * hstep + 2 + coord] = __builtin_fmaf(cross, 1.0f / kLoScale, oacc[nb][i]);
+        }
+      }
+    return;
+  }
   if (lane < G) {
     red_m[wave][lane] = m_run;
     red_l[wave][lane] = l_run;
@@ -949,10 +976,16 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   }
 }
 
-template <int D, int G, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GG = false>
+// HW: workgroup row y takes the pairs 4y .. 4y + 3, one per wave (n_heads a
+// multiple of 4, so the four share the batch row).
+template <int D, int G, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GG = false, bool HW = false>
 __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(const DecodeArgs a) {
   __shared__ DecodeSmem<D, G, KB, VBITS, QJL, VSH> sm;
-  decode_mfma_body<D, G, KB, VBITS, QJL, VSH, SOA, GG>(a, sm, blockIdx.x, blockIdx.y);
+  // (read through a scalar register: the buffer resources built from the
+  // pair must be wave-uniform, or every load becomes a loop over lanes)
+  const int bh = HW ? __builtin_amdgcn_readfirstlane((int)blockIdx.y * kMWaves + (int)(threadIdx.x >> 6))
+                    : (int)blockIdx.y;
+  decode_mfma_body<D, G, KB, VBITS, QJL, VSH, SOA, GG, HW>(a, sm, blockIdx.x, bh);
 }
 
 // Mixed widths whose kv heads are either 4-bit keys and values (a4, one
@@ -989,10 +1022,10 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_pair_kernel
     default: KERNEL(8, __VA_ARGS__); break;                               \
   }
 
-template <int D, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GGML = false>
+template <int D, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GGML = false, bool HW = false>
 static void launch_dm(const DecodeArgs &a, int G, hipStream_t s) {
-  dim3 grid(a.splits, a.B * a.n_heads);
-#define PQKV_DM_ONE(GG, ...) decode_mfma_kernel<D, GG, KB, VBITS, QJL, VSH, SOA, GGML><<<grid, 256, 0, s>>>(a)
+  dim3 grid(a.splits, HW ? a.B * a.n_heads / kMWaves : a.B * a.n_heads);
+#define PQKV_DM_ONE(GG, ...) decode_mfma_kernel<D, GG, KB, VBITS, QJL, VSH, SOA, GGML, HW><<<grid, 256, 0, s>>>(a)
   PQKV_DM_G_SWITCH(PQKV_DM_ONE, 0)
 #undef PQKV_DM_ONE
 }

@@ -5,9 +5,18 @@
 
 namespace pqkv {
 
+// kv heads in fours (n_heads % 4 == 0): one head per wave, so the waves of
+// a workgroup read the same tokens' lines; otherwise the four waves share a
+// head's chunks.
 hipError_t launch_decode_mfma_ggml(const DecodeArgs &a, hipStream_t s) {
-  if (a.d == 128) launch_dm<128, 4, 4, false, true, false, true>(a, a.g, s);
-  else launch_dm<64, 4, 4, false, true, false, true>(a, a.g, s);
+  const bool hw = ggml_heads_per_wave(a.n_heads);
+  if (a.d == 128) {
+    if (hw) launch_dm<128, 4, 4, false, true, false, true, true>(a, a.g, s);
+    else launch_dm<128, 4, 4, false, true, false, true>(a, a.g, s);
+  } else {
+    if (hw) launch_dm<64, 4, 4, false, true, false, true, true>(a, a.g, s);
+    else launch_dm<64, 4, 4, false, true, false, true>(a, a.g, s);
+  }
   return hipGetLastError();
 }
 

@@ -292,7 +292,9 @@ int fa_shape(const polarquant_state *st, const int64_t ne_q[4], const int64_t ne
                              (long long)rows, f->Hkv);
   f->splits = 1;
   f->tps = 0;
-  if (rows > 0 && f->n_kv > 0) pqkv::mfma_split_plan(rows * f->Hkv, f->n_kv, &f->splits, &f->tps);
+  // (a workgroup row per four kv heads when the kernel takes one per wave)
+  const int64_t wg_rows = pqkv::ggml_heads_per_wave(f->Hkv) ? rows * f->Hkv / 4 : rows * f->Hkv;
+  if (rows > 0 && f->n_kv > 0) pqkv::mfma_split_plan(wg_rows, f->n_kv, &f->splits, &f->tps);
   size_t pq_off;
   f->bytes = pqkv::decode_workspace_layout((int)rows, f->Hq, f->splits, d, &f->q_off, &f->part_off, &pq_off);
   return PQKV_OK;

@@ -182,8 +182,12 @@ hipError_t launch_decode_mfma_pair(const DecodeArgs &a4, const DecodeArgs &a2, h
 // entries (one shared table when k_cb == v_cb), no QJL.
 hipError_t launch_decode_mfma_soa(const DecodeArgs &a, hipStream_t s);
 // 4-bit keys and values with one codebook in the ggml flash-attn-ext layout
-// (a.k_tok_stride, a.rows_per_seq, a.mask), no QJL, unlisted heads.
+// (a.k_tok_stride, a.rows_per_seq, a.mask), no QJL, unlisted heads. With
+// ggml_heads_per_wave(n_heads) the grid's rows are B * n_heads / 4 (a
+// workgroup takes four kv heads of the same tokens), so the split plan is
+// made for that many rows.
 hipError_t launch_decode_mfma_ggml(const DecodeArgs &a, hipStream_t s);
+inline bool ggml_heads_per_wave(int n_heads) { return n_heads % 4 == 0; }
 // R == nullptr: the normalised rotated output, not rotated back.
 hipError_t launch_decode_merge(const float *part, const float *R, void *out, int out_dtype, int BHq, int splits,
                                int d, hipStream_t s);
