@@ -367,7 +367,26 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   // (L % CH) ^ swz(vector). Lanes past the end copy the last vector again
   // (into slots no step reads), so the copies need no branch.
   static_assert(NCOPY % kEW == 0, "copy instructions split evenly over the waves");
+  // One contiguous run of vectors (n_outer <= 1): a whole step's copy
+  // sources are the step's base (uniform) plus per-lane byte offsets that
+  // do not change from step to step.
+  // (not for the QJL kernels, which have no registers to spare for it)
+  const bool run_x = !QJL && a.n_outer <= 1;
+  uint32_t xoff[NCOPY / kEW];
+#pragma unroll
+  for (int j = 0; j < NCOPY / kEW; ++j) {
+    const int vl = (wave + kEW * j) * VPI + lane / CH;
+    xoff[j] = (uint32_t)(vl * XB + 16 * ((lane % CH) ^ swz(vl)));
+  }
   auto issue = [&](int64_t g, int b) {
+    if (!QJL && run_x && (uint32_t)g * EG + EG <= n) {
+      const uint8_t *base = (const uint8_t *)x + (int64_t)g * EG * XB;
+#pragma unroll
+      for (int j = 0; j < NCOPY / kEW; ++j)
+        __builtin_amdgcn_global_load_lds((const void *)(base + xoff[j]), (lds_void *)(xs[b] + 1024 * (wave + kEW * j)),
+                                         16, 0, 0);
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < NCOPY / kEW; ++j) {
       const int q = wave + kEW * j;
@@ -509,30 +528,59 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
       const float rt = bperm_f(vl, r), it = bperm_f(vl, inv);
       const bool nzt = rt > 1e-30f;
       int code[MTW][4];
-#pragma unroll
-      for (int mt = 0; mt < MTW; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float yv = y[t][mt][i];
-          if constexpr (kTable) {
-            float d;
-            if constexpr (kFast) {
+      auto dir_of = [&](float yv) {
+        float d;
+        if constexpr (kFast) {
 #pragma clang fp contract(off)
-              const float q0 = yv * it;
-              const float e = __builtin_fmaf(-rt, q0, yv);
-              d = __builtin_fmaf(e, it, q0);
-            } else {
-              d = nzt ? __fdiv_rn(yv, rt) : 0.0f;
-              d = d == d ? d : -2.0f;  // NaN: index 0, as the scan gives
-              d = __builtin_fminf(__builtin_fmaxf(d, -kEClamp), kEClamp);
-            }
+          const float q0 = yv * it;
+          const float e = __builtin_fmaf(-rt, q0, yv);
+          d = __builtin_fmaf(e, it, q0);
+        } else {
+          d = nzt ? __fdiv_rn(yv, rt) : 0.0f;
+          d = d == d ? d : -2.0f;  // NaN: index 0, as the scan gives
+          d = __builtin_fminf(__builtin_fmaxf(d, -kEClamp), kEClamp);
+        }
+        return d;
+      };
+      if constexpr (kTable && QJL) {
+        // (one coordinate at a time: the QJL kernels have no registers to
+        // spare for the batched form below)
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float d = dir_of(y[t][mt][i]);
             const uint2 ce = cells[dir_cell(d)];
             code[mt][i] = (int)ce.x + (d >= __builtin_bit_cast(float, ce.y) ? 1 : 0);
-          } else {
-            const float d = nzt ? __fdiv_rn(yv, rt) : 0.0f;
+          }
+      } else if constexpr (kTable) {
+        // in three passes over the tile's coordinates (directions, cell
+        // reads, codes), so that the lane's cell reads are in flight
+        // together instead of each waiting for the one before
+        float dv[MTW][4];
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dv[mt][i] = dir_of(y[t][mt][i]);
+        uint2 ce[MTW][4];
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ce[mt][i] = cells[dir_cell(dv[mt][i])];
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            code[mt][i] = (int)ce[mt][i].x + (dv[mt][i] >= __builtin_bit_cast(float, ce[mt][i].y) ? 1 : 0);
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float d = nzt ? __fdiv_rn(y[t][mt][i], rt) : 0.0f;
             code[mt][i] = scan_index_rolled(d, cb, NL);
           }
-        }
+      }
       if constexpr (QJL) {
         // residual e = y - r c[code] (fp32 r), times 1 / r (the signs do not
         // change; fp16 planes cannot hold e itself), into ebuf[sb]: four
