@@ -384,11 +384,11 @@ def run_config3(args) -> int:
     vc = quantizer.allocate_cache(B, Hkv, S, d, 4, dev)
 
     # ---- encode (full cache, K and V) ----
-    _lib.profile_enable(True)
     quantizer.compress_pq(K, R, cache=kc, start=0)
     quantizer.compress_pq(V, R, cache=vc, start=0)
     torch.cuda.synchronize()
     settle(torch, lambda: quantizer.compress_pq(K, R, cache=kc, start=0))
+    _lib.profile_enable(True)
     _lib.profile_collect("encode")
     e0, e1 = _events(torch)
     e0.record()
