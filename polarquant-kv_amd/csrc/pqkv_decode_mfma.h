@@ -457,8 +457,18 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
 
   // Key side: the lane group's qs bytes start kphys bytes into the vector
   // (2 mod 4 or 0 mod 4).
-  const int kc0 = grp * (D / 4);
-  const int kphys = SOA ? kc0 / 2 : (kc0 / kBlock) * block_bytes(KB) + 2 + (kc0 % kBlock) * KB / 8;
+  auto kphys_of = [](int g) {
+    const int kc0 = g * (D / 4);
+    return SOA ? kc0 / 2 : (kc0 / kBlock) * block_bytes(KB) + 2 + (kc0 % kBlock) * KB / 8;
+  };
+  // GG: a token's kv heads sit side by side, so the four lanes of a quad
+  // load the four groups of one token (one or two lines) instead of one group
+  // of four tokens (four lines), and a lane permute (kperm) hands each lane
+  // its own group before the table reads: the lane of token t, group g
+  // loads for lane 16 g + t.
+  const int kphys = kphys_of(GG ? (lane & 3) : grp);
+  const int ktok = GG ? (lane >> 2) : col;
+  const int kperm = (4 * col + grp) * 4;
   // Value side: the lane's 8 coordinates (D = 128: 8 col .. + 7; D = 64:
   // 8 (col & 7) .. + 7 with parity col >> 3) as a qs dword (4-bit) or half
   // dword (2-bit) of each token.
@@ -476,7 +486,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   // as soon as it has read them (and the radii first: they are converted at
   // the start of a step).
   auto load_k_sub = [&](CK &c, int t0, int st) {
-    load_words(kres, (t0 + kSub * st + col) * kts + kphys, c.w[st]);
+    load_words(kres, (t0 + kSub * st + ktok) * kts + kphys, c.w[st]);
     if constexpr (QJL) {
       const int so = (t0 + kSub * st + col) * (D / 8) + grp * (D / 32);
       c.sg[st] = D == 128 ? bld32(sres, so) : bld16(sres, so);
@@ -531,7 +541,10 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   };
   auto kread = [&](const CK &k, int st, KTile &kt) {
     // the lane group's qs words of token 16st + col
-    const uint32_t (&qw)[CK::kWords] = k.w[st];
+    uint32_t qw[CK::kWords];
+#pragma unroll
+    for (int i = 0; i < CK::kWords; ++i)
+      qw[i] = GG ? (uint32_t)__builtin_amdgcn_ds_bpermute(kperm, (int)k.w[st][i]) : k.w[st][i];
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       // step kk: coordinates 4kk .. 4kk + 3 of the lane group's range
