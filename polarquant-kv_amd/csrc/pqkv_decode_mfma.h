@@ -335,6 +335,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
                                                  const int split, const int bh) {
   static_assert(!SOA || (KB == 4 && VBITS == 4 && !QJL), "the SoA layout carries 4-bit codes and no QJL signs");
   static_assert(!GG || (!SOA && !QJL), "the ggml layout has block-encoded keys and values and no QJL signs");
+  static_assert(!HW || GG, "one kv head per wave is a mode of the ggml layout (fp16 block radii, no listed heads)");
   constexpr int VBK = SOA ? D / 2 : vector_bytes(D, KB), VBV = SOA ? D / 2 : vector_bytes(D, VBITS);
   constexpr int KK = D / 16;     // score MFMAs per 16-token tile
   constexpr int NB = D / 16;     // value n-tiles
