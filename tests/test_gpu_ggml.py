@@ -98,6 +98,8 @@ def _case(d, Hq, Hkv, n_q, ns, ns_kv, n_kv, kind, seed):
     (64, 6, 2, 3, 1, 1, 1, None),
     (128, 32, 8, 1, 1, 1, 16384, "pad"),
     (128, 32, 8, 3, 2, 2, 500, "causal"),   # one kv head per wave, 3 query rows x 2 sequences
+    (64, 16, 4, 1, 2, 2, 600, "pad"),       # one kv head per wave at d = 64
+    (64, 8, 8, 2, 1, 1, 333, "random"),
 ])
 def test_flash_attn_ext_matches_the_oracle(d, Hq, Hkv, n_q, ns, ns_kv, n_kv, kind):
     print(f"ggml flash_attn_ext d={d} Hq={Hq} Hkv={Hkv} n_q={n_q} ns={ns} ns_kv={ns_kv} n_kv={n_kv} {kind}",
