@@ -1,0 +1,38 @@
+"""Decode parity over seeded random shapes: batch, kv heads, query heads per
+kv head (1..10, so one or two launches per kv head), head_dim, key and value
+widths, stream length (any S, not only whole tiles) and a cache allocated
+longer than the stream, and the three synthetic data laws (i.i.d., per-token
+norm scales, per-channel outliers), against the float64 oracle on the same encoded
+bytes (tolerance of the north-star contract, as in test_gpu_decode)."""
+
+import numpy as np
+import pytest
+import torch
+
+from polarquant_kv import attention
+from test_gpu_decode import _check, _oracle, _setup
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _shape(seed):
+    rng = np.random.default_rng(1000 + seed)
+    B = int(rng.integers(1, 4))
+    Hkv = int(rng.choice([1, 2, 3, 4, 8]))
+    G = int(rng.integers(1, 11))
+    d = int(rng.choice([64, 128]))
+    S = int(rng.integers(1, 2500))
+    S_max = S + int(rng.integers(0, 50))
+    kb, vb = (int(x) for x in rng.choice([2, 4], 2))
+    kind = str(rng.choice(["token_ln", "normal", "channel"]))
+    return B, G * Hkv, Hkv, S, S_max, d, kb, vb, kind
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_decode_random_shapes(seed):
+    B, Hq, Hkv, S, S_max, d, kb, vb, kind = _shape(seed)
+    print(f"sweep seed {seed}: B={B} Hq={Hq} Hkv={Hkv} S={S} S_max={S_max} d={d} k{kb}v{vb} {kind}", flush=True)
+    q, R, Rt, kc, vc, _ = _setup(B, Hq, Hkv, S, d, kb, vb, seed=seed, S_max=S_max, kind=kind)
+    out = attention.decode_attention(torch.from_numpy(q).to(DEV), kc, vc, Rt, out_dtype=torch.float32)
+    _check(out.cpu().numpy(), _oracle(q, R, kc, vc, S))
