@@ -36,3 +36,16 @@ def test_decode_random_shapes(seed):
     q, R, Rt, kc, vc, _ = _setup(B, Hq, Hkv, S, d, kb, vb, seed=seed, S_max=S_max, kind=kind)
     out = attention.decode_attention(torch.from_numpy(q).to(DEV), kc, vc, Rt, out_dtype=torch.float32)
     _check(out.cpu().numpy(), _oracle(q, R, kc, vc, S))
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_decode_qjl_random_shapes(seed):
+    """The same random shapes with the QJL sign sketch on the keys (m = d):
+    the signs the encoder wrote and the projection P go to the oracle."""
+    from oracle import oracle as O
+    B, Hq, Hkv, S, S_max, d, kb, vb, kind = _shape(100 + seed)
+    print(f"qjl sweep seed {seed}: B={B} Hq={Hq} Hkv={Hkv} S={S} S_max={S_max} d={d} k{kb}v{vb} {kind}", flush=True)
+    q, R, Rt, kc, vc, P_rot = _setup(B, Hq, Hkv, S, d, kb, vb, seed=seed, S_max=S_max, kind=kind, qjl=True)
+    out = attention.decode_attention(torch.from_numpy(q).to(DEV), kc, vc, Rt, jl_rot=P_rot, out_dtype=torch.float32)
+    signs = kc.qjl_signs.cpu().numpy()[:, :, :S]
+    _check(out.cpu().numpy(), _oracle(q, R, kc, vc, S, P=O.jl_matrix(d, d, 43), signs=signs))
