@@ -126,3 +126,24 @@ def test_flash_attn_ext_empty_cache_gives_zeros():
         out = ggml.flash_attn_ext(st, q, k, k, None, 0.1)
         torch.cuda.synchronize()
     assert out.shape == (1, 1, Hq, d) and not out.cpu().any()
+
+
+def _sweep_shape(seed):
+    rng = np.random.default_rng(4000 + seed)
+    d = int(rng.choice([64, 128]))
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    Hq = Hkv * int(rng.integers(1, 9))
+    n_q = int(rng.integers(1, 5))
+    ns = int(rng.integers(1, 4))
+    ns_kv = int(rng.choice([1, ns]))
+    n_kv = int(rng.integers(n_q + 20, 3000))
+    kind = [None, "pad", "causal", "random"][int(rng.integers(0, 4))]
+    return d, Hq, Hkv, n_q, ns, ns_kv, n_kv, kind
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_flash_attn_ext_random_shapes(seed):
+    """Seeded random shapes (head_dim, GQA group, query rows, sequences that
+    share one cache or have their own, cache length, mask kind) against the
+    oracle, as test_flash_attn_ext_matches_the_oracle."""
+    test_flash_attn_ext_matches_the_oracle(*_sweep_shape(seed))
