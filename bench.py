@@ -61,6 +61,8 @@ KSTATS_FILE = os.path.join(PROFILES, "decode_mfma_config3_kernel_stats.md")
 GGML_KSTATS_FILE = os.path.join(PROFILES, "ggml_fa_config3_kernel_stats.md")
 C4_KSTATS_FILE = os.path.join(PROFILES, "decode_mfma_config4_kernel_stats.md")
 METRIC = "PQ4 decode-attn GB/s & % HBM peak; encode tokens/s; at 1 MI355X, 32K ctx"
+KSRC = ("live: hipEvents on the launch stream around 20 back-to-back launches of the kernel (idempotent), "
+        "mean per launch")
 
 
 # ---------------------------------------------------------------- inputs
@@ -164,24 +166,31 @@ def cpu_decode_baseline(kc, vc, q, R, d, streams, runs=5, qjl=None, P=None):
     return nbytes / t / 1e9, t, n, model, blas
 
 
-def cpu_encode_baseline(d, n=4096, runs=5):
-    """The C oracle (one thread: FMA-chain rotation + quantiser + packing) on
-    n random vectors; median of `runs`. Returns vectors/s."""
+def cpu_encode_baseline(d, per_thread=4096, runs=5):
+    """The C oracle (FMA-chain rotation + quantiser + packing) on every
+    affinity core: one thread per core, each encoding its own per_thread
+    random vectors (the ctypes calls release the GIL); median of `runs`.
+    Returns (vectors/s, threads)."""
+    from concurrent.futures import ThreadPoolExecutor
+
     import numpy as np
 
     import oracle as OC
     from oracle import oracle as O
 
-    x = np.random.default_rng(0).standard_normal((n, d)).astype(np.float32)
+    n_thr, _ = cpu_info()
+    xs = [np.random.default_rng(i).standard_normal((per_thread, d)).astype(np.float32) for i in range(n_thr)]
     R = O.rotation_matrix(d, 42).astype(np.float32)
     cb = O.lloyd_max_codebook(d, 4)[0]
 
-    def run():
+    def one(x):
         y = OC.c_rotate_fma(x, R)
         r, idx = OC.c_quantize_rotated(y, cb)
         OC.c_pack_blocks(r, idx, 4)
 
-    return n / timed_median(run, runs)
+    with ThreadPoolExecutor(max_workers=n_thr) as ex:
+        t = timed_median(lambda: list(ex.map(one, xs)), runs)
+    return n_thr * per_thread / t, n_thr
 
 
 # ---------------------------------------------------------------- GPU timing helpers
@@ -255,19 +264,33 @@ def best_timing(graph_ms, eager_ms, what=""):
     return eager_ms, f"eager launches{what}; hipGraph replays in graph_ms_per_step"
 
 
-def kernel_means(torch, _lib, fn, steps, names):
-    """Per-step time of each named kernel family from the library's
-    hipEvents on the launch stream (all launches of a step summed)."""
+# Back-to-back launches of each profiled kernel between its two hipEvents in
+# the live kernel measurement (pqkv_profile_repeat): one event pair costs a
+# few microseconds of dispatch latency, which REPEAT launches share.
+REPEAT = 20
+
+
+def kernel_means(torch, _lib, fn, steps, names, repeat=REPEAT):
+    """Live per-launch kernel times: with the library's profiling on, every
+    bracketed kernel of a step (rotation, split, merge, encoder, prefill) is
+    launched `repeat` times back to back between two hipEvents on its launch
+    stream (the kernels are idempotent), for `steps` steps. Returns, per
+    name, the mean ms per launch times the launches one plain step makes."""
+    _lib.profile_repeat(repeat)
     _lib.profile_enable(True)
+    _lib.profile_collect("")
+    settle(torch, fn, 0.1)
     _lib.profile_collect("")
     for _ in range(steps):
         fn()
     torch.cuda.synchronize()
     res = {}
     for n in names:
-        ms, _ = _lib.profile_collect(n)
-        res[n] = ms / steps
+        ms, launches = _lib.profile_collect(n)
+        per_step = launches / (repeat * steps)           # launches of this family in one plain step
+        res[n] = ms / max(launches, 1) * per_step
     _lib.profile_enable(False)
+    _lib.profile_repeat(1)
     return res
 
 
@@ -393,8 +416,6 @@ def run_config3(args) -> int:
     quantizer.compress_pq(V, R, cache=vc, start=0)
     torch.cuda.synchronize()
     settle(torch, lambda: quantizer.compress_pq(K, R, cache=kc, start=0))
-    _lib.profile_enable(True)
-    _lib.profile_collect("encode")
     e0, e1 = _events(torch)
     e0.record()
     for _ in range(args.encode_iters):
@@ -403,11 +424,11 @@ def run_config3(args) -> int:
     e1.record()
     torch.cuda.synchronize()
     enc_ms = e0.elapsed_time(e1) / args.encode_iters
-    enc_kernel_ms, enc_launches = _lib.profile_collect("encode")
-    _lib.profile_enable(False)
+    # live kernel time: REPEAT back-to-back launches per event pair
+    enc_kernel_each = kernel_means(torch, _lib, lambda: quantizer.compress_pq(K, R, cache=kc, start=0),
+                                   args.encode_iters, ("encode",))["encode"]
     enc_tokens_s = B * S / (enc_ms / 1e3)
     enc_bytes = 2 * (K.numel() * 2 + kc.blocks.numel())
-    enc_kernel_each = enc_kernel_ms / max(enc_launches, 1)
     del K, V
 
     # ---- decode ----
@@ -429,9 +450,8 @@ def run_config3(args) -> int:
     value = step_bytes / (step_ms / 1e3) / 1e9
     kern_bytes = cache_bytes + B * Hq * d * 4                      # compressed K+V + fp32 rotated query
     kernel = "decode_mfma_kernel<128,4,4,4>"
-    ev_ms = km["decode_split"]
+    kern_ms = km["decode_split"]
     rp_us = committed_kernel_us(kernel)
-    kern_ms = rp_us / 1e3 if rp_us is not None else ev_ms
     achieved = kern_bytes / (kern_ms / 1e3) / 1e9
     sr = stream_read_gbps(torch, _lib, (kc.blocks, vc.blocks))
 
@@ -441,12 +461,13 @@ def run_config3(args) -> int:
     cpu = None
     if not args.no_cpu:
         gbs, t, n, model, blas = cpu_decode_baseline(kc, vc, q, R, d, streams=B * Hkv, runs=args.cpu_runs)
-        enc_vs = cpu_encode_baseline(d, runs=args.cpu_runs)
+        enc_vs, enc_thr = cpu_encode_baseline(d, runs=args.cpu_runs)
         cpu = _cpu_obj(gbs, "GB/s", n, model, blas,
                        f"oracle float64 numpy decode of one whole step (all 64 (batch, kv-head) streams of the "
                        f"cache, S=32768, {Hq // Hkv} query heads each), BLAS on {n} threads, "
                        f"median of {args.cpu_runs} runs of {t:.2f} s; encode: C oracle FMA rotation + quantiser "
-                       f"+ packing, one thread, median of {args.cpu_runs}: {enc_vs:.0f} vectors/s = "
+                       f"+ packing on {enc_thr} threads (4096 vectors each), median of {args.cpu_runs}: "
+                       f"{enc_vs:.0f} vectors/s = "
                        f"{enc_vs / (2 * Hkv):.0f} tokens/s (K+V of {Hkv} kv heads)")
 
     line = {
@@ -461,18 +482,19 @@ def run_config3(args) -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic(kernel),
                      "kernel": kernel, "kernel_ms": round(kern_ms, 5),
-                     "kernel_ms_source": "rocprofv3 kernel trace (profiles/decode_mfma_config3_kernel_stats.md)"
-                     if rp_us is not None else "library hipEvents (no committed trace for this kernel)",
-                     "kernel_ms_events": round(ev_ms, 5),
-                     "achieved_events": round(kern_bytes / (ev_ms / 1e3) / 1e9, 2),
+                     "kernel_ms_source": KSRC,
+                     "kernel_us_rocprof_committed": rp_us,
+                     "kernel_us_rocprof_source": "profiles/decode_mfma_config3_kernel_stats.md (committed summary, "
+                                                 "not this run)",
                      "bytes_per_launch": kern_bytes,
                      "stream_read_GBps": round(sr, 1), "pct_of_stream_read": round(100 * achieved / sr, 2)},
-        "stages_ms": {"query_rotate": round(km["decode_rotate"], 5), "split": round(ev_ms, 5),
-                      "merge": round(km["decode_merge"], 5)},
+        "stages_ms": {"query_rotate": round(km["decode_rotate"], 5), "split": round(kern_ms, 5),
+                      "merge": round(km["decode_merge"], 5), "source": KSRC},
         "encode": {"tokens_per_s": round(enc_tokens_s), "ms": round(enc_ms, 4),
                    "kernel_ms": round(enc_kernel_each, 4), "GB_per_s": round(enc_bytes / (enc_ms / 1e3) / 1e9, 2),
                    "vectors": 2 * B * Hkv * S,
                    "kernel": "encode_mfma_kernel (matrix-core rotation, bit-exact quantiser)",
+                   "kernel_ms_source": KSRC,
                    "roofline": {"bound": "hbm", "bytes": enc_bytes,
                                 "achieved_GBps": round(enc_bytes / (enc_kernel_each * 2 / 1e3) / 1e9, 2),
                                 "frac": round(enc_bytes / (enc_kernel_each * 2 / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}},
@@ -503,9 +525,8 @@ def _decode_line(args, name, metric_workload, B, Hq, Hkv, S, d, kc, vc, q, R, jl
     step_bytes = cache_bytes + B * Hq * d * 2 * 2
     kern_bytes = cache_bytes + B * Hq * d * 4
     step_ms, timing = best_timing(graph_ms, eager_ms, " (the configuration is launch-bound)")
-    # the split kernel's time: the committed rocprofv3 mean when there is one
     rp_us = committed_kernel_us(kernel, kstats) if kstats else None
-    kern_ms = rp_us / 1e3 if rp_us is not None else km["decode_split"]
+    kern_ms = km["decode_split"]
     line = {
         "metric": name, "value": round(step_bytes / (step_ms / 1e3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "settle_s": SETTLE_S, "ms_per_step": round(step_ms, 5), "higher_is_better": True,
@@ -517,11 +538,11 @@ def _decode_line(args, name, metric_workload, B, Hq, Hkv, S, d, kc, vc, q, R, jl
         "roofline": {"bound": "hbm", "achieved": round(kern_bytes / (kern_ms / 1e3) / 1e9, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(kern_bytes / (kern_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": kernel, "kernel_ms": round(kern_ms, 5),
-                     "kernel_ms_source": f"rocprofv3 kernel trace (profiles/{os.path.basename(kstats)})"
-                     if rp_us is not None else "library hipEvents (no committed trace for this kernel)",
-                     "kernel_ms_events": round(km["decode_split"], 5)},
-        "stages_ms_events": {k: round(v, 5) for k, v in km.items()},
+                     "kernel": kernel, "kernel_ms": round(kern_ms, 5), "kernel_ms_source": KSRC,
+                     "kernel_us_rocprof_committed": rp_us,
+                     "kernel_us_rocprof_source": f"profiles/{os.path.basename(kstats)} (committed summary, not this "
+                                                 f"run)" if rp_us is not None else None},
+        "stages_ms": {**{k: round(v, 5) for k, v in km.items()}, "source": KSRC},
     }
     if extra:
         line.update(extra)
@@ -591,11 +612,9 @@ def run_ggml(args) -> int:
                        f"kv heads, values of the PQ4 rows then attention), median of {args.cpu_runs} runs of "
                        f"{t:.2f} s")
     step_ms, timing = best_timing(graph_ms, eager_ms)
-    # the split kernel's time: the committed rocprofv3 mean for this kernel
-    # when there is one (events carry dispatch latency), else the events
     gg_kernel = "decode_mfma_kernel<128,4,4,4,ggml>"
     rp_us = committed_kernel_us(gg_kernel, GGML_KSTATS_FILE)
-    gg_ms = rp_us / 1e3 if rp_us is not None else km["ggml_fa_split"]
+    gg_ms = km["ggml_fa_split"]
     gg_achieved = kern_bytes / (gg_ms / 1e3) / 1e9
     line = {
         "metric": "ggml flash_attn_ext over GGML_TYPE_PQ4 GB/s at 1 MI355X (config-3 decode shape)",
@@ -610,11 +629,12 @@ def run_ggml(args) -> int:
         "roofline": {"bound": "hbm", "achieved": round(gg_achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gg_achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": gg_kernel, "kernel_ms": round(gg_ms, 5),
-                     "kernel_ms_source": "rocprofv3 kernel trace (profiles/ggml_fa_config3_kernel_stats.md)"
-                     if rp_us is not None else "library hipEvents (no committed trace for this kernel)",
-                     "kernel_ms_events": round(km["ggml_fa_split"], 5), "bytes_per_launch": kern_bytes},
-        "stages_ms_events": {k: round(v, 5) for k, v in km.items()},
+                     "traffic": None, "kernel": gg_kernel, "kernel_ms": round(gg_ms, 5), "kernel_ms_source": KSRC,
+                     "kernel_us_rocprof_committed": rp_us,
+                     "kernel_us_rocprof_source": "profiles/ggml_fa_config3_kernel_stats.md (committed summary, not "
+                                                 "this run)",
+                     "bytes_per_launch": kern_bytes},
+        "stages_ms": {**{k: round(v, 5) for k, v in km.items()}, "source": KSRC},
         "cpu_baseline": cpu,
     }
     st.close()
@@ -768,7 +788,7 @@ def run_config4(args) -> int:
                                "(P seed 43); variants 2bit (block_pq2 K+V) and mixed (kv heads 0-3 PQ4, 4-7 PQ2)",
                    "global_batch": B, "seq_len": S, "parallelism": "single GPU"},
         "variants": {k: {kk: vv for kk, vv in r.items() if kk in ("value", "ms_per_step", "eager_ms_per_step",
-                                                                 "bytes_per_step", "roofline", "stages_ms_events")}
+                                                                 "bytes_per_step", "roofline", "stages_ms")}
                      for k, r in res.items()},
         "cpu_baseline": cpu,
     })
@@ -843,10 +863,11 @@ def run_config5(args) -> int:
                    "global_batch": B, "seq_len": S, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(kern_tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "prefill_mfma_kernel<128,4,4,false>", "kernel_ms_events": round(km["prefill_attn"], 4),
+                     "kernel": "prefill_mfma_kernel<128,4,4,false>", "kernel_ms": round(km["prefill_attn"], 4),
+                     "kernel_ms_source": KSRC,
                      "flops_per_launch": flops,
                      "note": "fp32-grade products cost 3 fp16 MFMAs each: this arithmetic tops out at 1/3"},
-        "stages_ms": {k: round(v, 4) for k, v in km.items()},
+        "stages_ms": {**{k: round(v, 4) for k, v in km.items()}, "source": KSRC},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -265,6 +265,13 @@ int pqkv_blocks_to_soa(const uint8_t *blocks, uint8_t *packed, float *radius,
  * bench.py; off by default, and costs nothing when off. */
 int pqkv_profile_enable(int on);
 int pqkv_profile_collect(const char *name, double *total_ms, int64_t *launches);
+/* While profiling is on, each bracketed kernel (decode rotation, split and
+ * merge; the encoders; prefill; the ggml ops) is launched n times back to
+ * back between its two events (1 <= n <= 1000; default 1), so that the
+ * per-launch mean pqkv_profile_collect gives carries the events' dispatch
+ * latency once per n launches. Those kernels are idempotent: a repeat
+ * rewrites the same outputs from the same inputs. */
+int pqkv_profile_repeat(int n);
 /* A plain streaming read of `bytes` (a multiple of 16) at p with 16-byte
  * loads by `blocks` workgroups (the data is XOR-folded; sink, of `blocks`
  * words, is written only on a fold that never occurs in practice): the

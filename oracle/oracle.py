@@ -336,6 +336,17 @@ def qjl_signs_rotated(x_rot: np.ndarray, radius: np.ndarray, idx: np.ndarray,
     return bit_pack_lsb(proj >= 0), np.linalg.norm(e, axis=-1)
 
 
+def qjl_zero_residual(packed: np.ndarray, m: int) -> np.ndarray:
+    """Keys whose residual is zero, as far as the stored sketch tells: a zero
+    residual projects to P 0 = 0 >= 0, so every one of its m signs is 1
+    (qjl_kernel.py:31, qjl.py:32). The CPU guard returns correction 0 for a
+    zero residual (qjl.py:50-51, the reference test AC-3.5 at
+    tests/test_qjl.py:139-154); a block cache keeps no residual norm, so the
+    all-ones sketch stands for it (a non-zero residual has all signs 1 with
+    probability 2^-m). packed [..., ceil(m/8)] -> bool [...]."""
+    return np.all(bit_unpack_lsb(np.asarray(packed), m), axis=-1)
+
+
 def qjl_correction(q: np.ndarray, packed: np.ndarray, P: np.ndarray) -> np.ndarray:
     """(1/m) sum_i (2 s_i - 1) (P q)_i, qjl.py:53-55 / attention_kernel.py:99-106.
     q [..., d] against packed [S, m/8] -> [..., S]."""
@@ -360,7 +371,8 @@ def decode_attention(q: np.ndarray, k_blocks: np.ndarray, v_blocks: np.ndarray,
     Semantics (flash_turboquant.cu:27-105, patch:277-389, attention_kernel.py:
     74-113, benchmark_turboquant.py:102,120): q_rot = q R^T; s_t = scale *
     r_k,t * q_rot . c[idx_t] (+ scale * QJL correction when signs given, with
-    correction 0 for zero keys, qjl.py:50-51); w = softmax(s);
+    correction 0 for a zero residual, i.e. an all-ones sketch, qjl.py:50-51,
+    see qjl_zero_residual); w = softmax(s);
     o = (sum_t w_t r_v,t c[vidx_t]) R. GQA: q-head h reads kv-head h // (Hq/Hkv).
     S = 0 gives zeros (attention_kernel.py:38-39).
     """
@@ -386,8 +398,7 @@ def decode_attention(q: np.ndarray, k_blocks: np.ndarray, v_blocks: np.ndarray,
             s = (qs @ K.T) * scale
             if qjl_signs is not None and P is not None:
                 corr = qjl_correction(q[b, h * grp:(h + 1) * grp], qjl_signs[b, h, :S], P)
-                rk, _ = unpack_blocks(k_blocks[b, h, :S], d, kb[h])
-                corr = np.where(rk.astype(np.float64)[None, :] > 0, corr, 0.0)
+                corr = np.where(qjl_zero_residual(qjl_signs[b, h, :S], P.shape[0])[None, :], 0.0, corr)
                 s = s + corr * scale
             s = s - s.max(axis=-1, keepdims=True)
             w = np.exp(s)

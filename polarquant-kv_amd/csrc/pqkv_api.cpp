@@ -90,9 +90,11 @@ struct ProfRecord {
   std::string name;
   hipEvent_t start, stop;
   bool closed;
+  int launches;   // launches between the two events (the repeat count in force)
 };
 std::mutex g_prof_mu;
 bool g_prof_on = false;
+int g_prof_repeat = 1;
 std::vector<ProfRecord> g_prof;
 
 }  // namespace
@@ -111,14 +113,19 @@ void mfma_split_plan(int64_t streams, int S, int *splits, int *tps) {
   decode_plan(streams, S > 0 ? S : 1, mfma_target(), splits, tps);
 }
 
-int prof_begin(const char *name, hipStream_t s) {
+int prof_begin(const char *name, hipStream_t s, bool repeated) {
   std::lock_guard<std::mutex> lk(g_prof_mu);
   if (!g_prof_on) return -1;
-  ProfRecord r{name, nullptr, nullptr, false};
+  ProfRecord r{name, nullptr, nullptr, false, repeated ? g_prof_repeat : 1};
   if (hipEventCreate(&r.start) != hipSuccess || hipEventCreate(&r.stop) != hipSuccess) return -1;
   if (hipEventRecord(r.start, s) != hipSuccess) return -1;
   g_prof.push_back(r);
   return (int)g_prof.size() - 1;
+}
+
+int prof_repeats() {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  return g_prof_on ? g_prof_repeat : 1;
 }
 
 void prof_end(int token, hipStream_t s) {
@@ -137,6 +144,13 @@ int pqkv_profile_enable(int on) {
   return PQKV_OK;
 }
 
+int pqkv_profile_repeat(int n) {
+  if (n < 1 || n > 1000) return fail(PQKV_ERR_INVALID, "profile_repeat: n=%d (1..1000)", n);
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_prof_repeat = n;
+  return PQKV_OK;
+}
+
 int pqkv_profile_collect(const char *name, double *total_ms, int64_t *launches) {
   if (!name || !total_ms || !launches) return fail(PQKV_ERR_INVALID, "profile_collect: null pointer");
   std::lock_guard<std::mutex> lk(g_prof_mu);
@@ -152,7 +166,7 @@ int pqkv_profile_collect(const char *name, double *total_ms, int64_t *launches) 
       float ms = 0.0f;
       if (hipEventElapsedTime(&ms, r.start, r.stop) == hipSuccess) {
         tot += ms;
-        ++n;
+        n += r.launches;
       }
     }
     (void)hipEventDestroy(r.start);
@@ -364,12 +378,16 @@ int pqkv_encode(const void *x, int x_dtype, int64_t x_outer_stride, const float 
   hipError_t e;
   if (!exact && fast_encode_ok(x, x_dtype, x_outer_stride, n_outer, n_inner, R, p_rot, qjl, qjl_outer_stride, blocks,
                                  blocks_outer_stride)) {
-    const int tok = pqkv::prof_begin("encode_mfma", (hipStream_t)stream);
-    e = pqkv::launch_encode_mfma(a, nullptr, nullptr, device_cus(), (hipStream_t)stream);
+    const int tok = pqkv::prof_begin("encode_mfma", (hipStream_t)stream, true);
+    e = hipSuccess;
+    for (int rep = 0, nrep = pqkv::prof_repeats(); rep < nrep && e == hipSuccess; ++rep)
+      e = pqkv::launch_encode_mfma(a, nullptr, nullptr, device_cus(), (hipStream_t)stream);
     pqkv::prof_end(tok, (hipStream_t)stream);
   } else {
-    const int tok = pqkv::prof_begin("encode_exact", (hipStream_t)stream);
-    e = pqkv::launch_encode_exact(a, x_dtype, (hipStream_t)stream);
+    const int tok = pqkv::prof_begin("encode_exact", (hipStream_t)stream, true);
+    e = hipSuccess;
+    for (int rep = 0, nrep = pqkv::prof_repeats(); rep < nrep && e == hipSuccess; ++rep)
+      e = pqkv::launch_encode_exact(a, x_dtype, (hipStream_t)stream);
     pqkv::prof_end(tok, (hipStream_t)stream);
   }
   return hip_status(e, "encode launch");
@@ -556,11 +574,13 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
   float *part = (float *)((char *)workspace + part_off);
   float *pq32 = (float *)((char *)workspace + pq_off);
   const float kLog2e = 1.4426950408889634f;
-  int tok = prof_begin("decode_rotate", st);
-  // QJL: the projections P_rot q_rot / m (m == d) come from the same launch
-  hipError_t e = qjl_signs ? launch_rotate2(q, q_dtype, R, p_rot, q32, pq32, (int64_t)B * Hq, d, scale * kLog2e,
-                                            1.0f / (float)m, st)
-                           : launch_rotate(q, q_dtype, R, q32, PQKV_F32, (int64_t)B * Hq, d, 0, scale * kLog2e, st);
+  int tok = prof_begin("decode_rotate", st, true);
+  hipError_t e = hipSuccess;
+  for (int rep = 0, nrep = prof_repeats(); rep < nrep && e == hipSuccess; ++rep)
+    // QJL: the projections P_rot q_rot / m (m == d) come from the same launch
+    e = qjl_signs ? launch_rotate2(q, q_dtype, R, p_rot, q32, pq32, (int64_t)B * Hq, d, scale * kLog2e,
+                                   1.0f / (float)m, st)
+                  : launch_rotate(q, q_dtype, R, q32, PQKV_F32, (int64_t)B * Hq, d, 0, scale * kLog2e, st);
   prof_end(tok, st);
   if (e != hipSuccess) return hip_status(e, "decode query rotation");
 
@@ -617,10 +637,12 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
     e = for_each_subgroup([&](int off, int g) {
       a.q_off = off;
       a.g = g;
-      const int t = prof_begin("decode_split", st);
-      const hipError_t r = soa    ? launch_decode_mfma_soa(a, st)
-                           : mfma ? launch_decode_mfma(a, k_bits, v_bits, st)
-                                  : launch_decode_split(a, k_bits, v_bits, st);
+      const int t = prof_begin("decode_split", st, true);
+      hipError_t r = hipSuccess;
+      for (int rep = 0, nrep = prof_repeats(); rep < nrep && r == hipSuccess; ++rep)
+        r = soa    ? launch_decode_mfma_soa(a, st)
+            : mfma ? launch_decode_mfma(a, k_bits, v_bits, st)
+                   : launch_decode_split(a, k_bits, v_bits, st);
       prof_end(t, st);
       return r;
     });
@@ -652,8 +674,10 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
       e = for_each_subgroup([&](int off, int g) {
         a.q_off = a2.q_off = off;
         a.g = a2.g = g;
-        const int t = prof_begin("decode_split", st);
-        const hipError_t r = launch_decode_mfma_pair(a, a2, st);
+        const int t = prof_begin("decode_split", st, true);
+        hipError_t r = hipSuccess;
+        for (int rep = 0, nrep = prof_repeats(); rep < nrep && r == hipSuccess; ++rep)
+          r = launch_decode_mfma_pair(a, a2, st);
         prof_end(t, st);
         return r;
       });
@@ -674,9 +698,10 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
           e = for_each_subgroup([&](int off, int g) {
             a.q_off = off;
             a.g = g;
-            const int t = prof_begin("decode_split", st);
-            const hipError_t r =
-                mfma ? launch_decode_mfma(a, kbits, vbits, st) : launch_decode_split(a, kbits, vbits, st);
+            const int t = prof_begin("decode_split", st, true);
+            hipError_t r = hipSuccess;
+            for (int rep = 0, nrep = prof_repeats(); rep < nrep && r == hipSuccess; ++rep)
+              r = mfma ? launch_decode_mfma(a, kbits, vbits, st) : launch_decode_split(a, kbits, vbits, st);
             prof_end(t, st);
             return r;
           });
@@ -684,8 +709,9 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
         }
     }
   }
-  tok = prof_begin("decode_merge", st);
-  e = launch_decode_merge(part, R, out, out_dtype, B * Hq, splits, d, st);
+  tok = prof_begin("decode_merge", st, true);
+  for (int rep = 0, nrep = prof_repeats(); rep < nrep && e == hipSuccess; ++rep)
+    e = launch_decode_merge(part, R, out, out_dtype, B * Hq, splits, d, st);
   prof_end(tok, st);
   return hip_status(e, "decode merge launch");
 }
@@ -907,8 +933,10 @@ int pqkv_prefill_attn(const void *q, int q_dtype, const float *R, const uint8_t 
     a.k_batch_stride = a.k_head_stride * Hkv;
     a.v_batch_stride = a.v_head_stride * Hkv;
     a.n_heads = Hkv;
-    tok = pqkv::prof_begin("prefill_attn", st);
-    e = pqkv::launch_prefill(a, k_bits, v_bits, st);
+    tok = pqkv::prof_begin("prefill_attn", st, true);
+    e = hipSuccess;
+    for (int rep = 0, nrep = pqkv::prof_repeats(); rep < nrep && e == hipSuccess; ++rep)
+      e = pqkv::launch_prefill(a, k_bits, v_bits, st);
     pqkv::prof_end(tok, st);
     if (e != hipSuccess) return hip_status(e, "prefill launch");
   } else {
@@ -935,8 +963,10 @@ int pqkv_prefill_attn(const void *q, int q_dtype, const float *R, const uint8_t 
           }
         if (n == 0) continue;
         a.n_heads = n;
-        tok = pqkv::prof_begin("prefill_attn", st);
-        e = pqkv::launch_prefill(a, kbits, vbits, st);
+        tok = pqkv::prof_begin("prefill_attn", st, true);
+        e = hipSuccess;
+        for (int rep = 0, nrep = pqkv::prof_repeats(); rep < nrep && e == hipSuccess; ++rep)
+          e = pqkv::launch_prefill(a, kbits, vbits, st);
         pqkv::prof_end(tok, st);
         if (e != hipSuccess) return hip_status(e, "prefill launch");
       }

@@ -216,8 +216,12 @@ __global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int hh = 0; hh < G; ++hh) s[hh] *= rk;
     if (QJL) {
-      // + (1/m) sum_i (2 sign_i - 1) (P q)_i, skipped for zero keys.
-      if (valid && rk > 0.0f) {
+      // + (1/m) sum_i (2 sign_i - 1) (P q)_i, skipped for a zero residual
+      // (an all-ones sketch: P 0 = 0 >= 0 sets every sign).
+      bool zero_res = true;
+#pragma unroll
+      for (int wd = 0; wd < M / 32; ++wd) zero_res = zero_res && sg[wd] == 0xFFFFFFFFu;
+      if (valid && !zero_res) {
 #pragma unroll
         for (int wd = 0; wd < M / 32; ++wd) {
           const uint32_t bits = sg[wd];

@@ -35,10 +35,13 @@
 // 2-bit codes: a nibble holds two codes, so the same operand shapes come from
 // 16-entry tables (nibble -> (c_hi, c_lo, c_hi', c_lo')); value tokens pair
 // up as two crumbs per nibble.
-// QJL: s += [r_k > 0] sum_i (2 sign_i - 1) pq_i with pq = P_rot q / m, a
+// QJL: s += [e != 0] sum_i (2 sign_i - 1) pq_i with pq = P_rot q / m, a
 // second product on the matrix cores: A = the signs as +-1 (a 16-entry table
 // maps 4 sign bits to 4 halves), B = pq as (hi | lo) columns, 32 projections
-// per MFMA.
+// per MFMA. A zero residual e projects to P 0 = 0 >= 0, all m signs 1; the
+// block cache keeps no residual norm, so an all-ones sketch is read as e = 0
+// and gets no correction (the reference's guard, python/polarquant_kv/
+// qjl.py:50-51): one ballot per sub-tile, its four lane-group slices ANDed.
 // Operands come straight from HBM in MFMA lane order (no LDS staging): a key
 // lane loads its lane group's qs bytes of one token (lane group grp owns
 // coordinates grp*D/4 .. grp*D/4 + D/4 - 1, so they are contiguous), a value
@@ -539,6 +542,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   struct KTile {
     uint2 t[KK][2];
     uint2 s[QJL ? KQ : 1][2];
+    uint32_t zf;   // QJL: bit i set = the lane's score row i has an all-ones sketch
   };
   auto kread = [&](const CK &k, int st, KTile &kt) {
     // the lane group's qs words of token 16st + col
@@ -563,6 +567,13 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
       }
     }
     if constexpr (QJL) {
+      // token 16 st + col has an all-ones sketch when the four lane groups'
+      // sign words of it are all ones: bit col of the ballot's four 16-lane
+      // slices ANDed; the lane's score rows are tokens 4 grp .. 4 grp + 3
+      const uint32_t full = D == 128 ? 0xFFFFFFFFu : 0xFFFFu;
+      const uint64_t bal = __builtin_amdgcn_ballot_w64(k.sg[st] == full);
+      const uint32_t ones = (uint32_t)(bal & (bal >> 16) & (bal >> 32) & (bal >> 48)) & 0xFFFFu;
+      kt.zf = ones >> (4 * grp);
       // sign byte kq: low nibble, high nibble
       const uint32_t slo = nib_lo(k.sg[st]), shi = nib_hi(k.sg[st]);
 #pragma unroll
@@ -573,7 +584,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
     }
   };
   // Score products of key sub-tile st, finished to the exp2-domain logit:
-  // s = (D[t][h] + 2^-11 D[t][h + 8]) r_k (+ the QJL term when r_k > 0) for
+  // s = (D[t][h] + 2^-11 D[t][h + 8]) r_k (+ the QJL term unless e = 0) for
   // token 16st + 4grp + i, meaningful in lanes col < G. Lanes of absent heads
   // (q = 0) and the cross lanes (col >= 8) carry finite values that only
   // reach discarded output rows. rkl: this lane's loaded radius.
@@ -596,7 +607,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
       float v = __builtin_fmaf(row_ror8f(acc[i]), 1.0f / kLoScale, acc[i]) * rk;
       if constexpr (QJL) {
         const float q = __builtin_fmaf(row_ror8f(accq[i]), 1.0f / kLoScale, accq[i]);
-        v = rk > 0.0f ? v + q : v;  // zero keys get no correction
+        v = ((kt.zf >> i) & 1u) ? v : v + q;  // zero residuals get no correction
       }
       if constexpr (GG) v = __builtin_fmaf(mask_val(mk, 4 * st + i), kLog2eF, v);  // additive mask, exp2 domain
       out[i] = v;

@@ -407,14 +407,18 @@ int pqkv_ggml_flash_attn_ext_pq4(const polarquant_state *st, const float *q, con
   for (int i = 0; i < n_sub; ++i) {
     a.q_off = off;
     a.g = a.gq / n_sub + (i < a.gq % n_sub ? 1 : 0);
-    tok = pqkv::prof_begin("ggml_fa_split", s);
-    e = pqkv::launch_decode_mfma_ggml(a, s);
+    tok = pqkv::prof_begin("ggml_fa_split", s, true);
+    e = hipSuccess;
+    for (int rep = 0, nrep = pqkv::prof_repeats(); rep < nrep && e == hipSuccess; ++rep)
+      e = pqkv::launch_decode_mfma_ggml(a, s);
     pqkv::prof_end(tok, s);
     if (e != hipSuccess) return pqkv::report_hip_error(e, "ggml flash_attn_ext split launch");
     off += a.g;
   }
-  tok = pqkv::prof_begin("ggml_fa_merge", s);
-  e = pqkv::launch_decode_merge(part, st->rotation, dst, PQKV_F32, (int)(rows * f.Hq), f.splits, f.d, s);
+  tok = pqkv::prof_begin("ggml_fa_merge", s, true);
+  e = hipSuccess;
+  for (int rep = 0, nrep = pqkv::prof_repeats(); rep < nrep && e == hipSuccess; ++rep)
+    e = pqkv::launch_decode_merge(part, st->rotation, dst, PQKV_F32, (int)(rows * f.Hq), f.splits, f.d, s);
   pqkv::prof_end(tok, s);
   return pqkv::report_hip_error(e, "ggml flash_attn_ext merge launch");
 }

@@ -135,8 +135,13 @@ void mfma_split_plan(int64_t streams, int S, int *splits, int *tps);
 
 // Event brackets for the measurement hook (pqkv_profile_*): returns a token
 // for prof_end, or -1 when profiling is off.
-int prof_begin(const char *name, hipStream_t s);
+// repeated: the bracket holds prof_repeats() launches of the kernel.
+int prof_begin(const char *name, hipStream_t s, bool repeated = false);
 void prof_end(int token, hipStream_t s);
+// Launches of a profiled kernel per event bracket: the pqkv_profile_repeat
+// count while profiling is on, else 1. The kernels bracketed this way are
+// idempotent (each repeat rewrites the same outputs from the same inputs).
+int prof_repeats();
 
 hipError_t launch_quantize_rotated(const float *x_rot, const float *codebook, int bits, uint8_t *blocks,
                                    float *radius_out, int64_t n, int d, hipStream_t s);

@@ -26,9 +26,11 @@
 //
 // 2-bit codes: a nibble holds two codes, so 16-entry tables give the same
 // operand pairs as the 4-bit byte tables.
-// QJL: s += [r_k > 0] sum_i (2 sign_i - 1) pq_i, pq = P_rot q_rot / m, a
+// QJL: s += [e != 0] sum_i (2 sign_i - 1) pq_i, pq = P_rot q_rot / m, a
 // second product per score tile: A = the signs as +-1 halves (a 16-entry
-// table maps 4 sign bits to 4 halves; a zero-radius key reads a zero entry),
+// table maps 4 sign bits to 4 halves; a key whose sketch is all ones, which
+// is what a zero residual e gives, reads a zero entry: the reference's guard,
+// python/polarquant_kv/qjl.py:50-51),
 // B = pq hi / lo. The key radius then scales the code product before the
 // sign product is added (in the matrix stage instead of the softmax).
 //
@@ -421,7 +423,7 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
       al = al_n;
     }
     if constexpr (QJL) {
-      // s = r_k (q . c) + [r_k > 0] sum_i (2 s_i - 1) pq_i: the radius
+      // s = r_k (q . c) + [e != 0] sum_i (2 s_i - 1) pq_i: the radius
       // scaling moves here, then the sign products accumulate on top
       const float *rk = rads[it & 1];
       const uint8_t *sg = raw_s[it % 3];
@@ -436,12 +438,23 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
           sacc[rt][tt][3] *= r4.w;
         }
         // A: signs of token 16 tt + col, projections 32 ks + 8 grp .. + 7
-        // (sign byte 4 ks + grp); the zero half of the table for r_k = 0
+        // (sign byte 4 ks + grp); the zero half of the table for an all-ones
+        // sketch (the four lane groups' bytes of the token all 0xFF: bit col
+        // of the ballot's four 16-lane slices ANDed)
         const int tok = 16 * tt + col;
-        const int zoff = rk[tok] > 0.0f ? 0 : 16;
+        uint32_t sb[KS];
+        uint32_t all = 0xFFu;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          const uint32_t byte = sg[tok * SGB + 4 * ks + grp];
+          sb[ks] = sg[tok * SGB + 4 * ks + grp];
+          all &= sb[ks];
+        }
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(all == 0xFFu);
+        const uint32_t ones = (uint32_t)(bal & (bal >> 16) & (bal >> 32) & (bal >> 48));
+        const int zoff = ((ones >> col) & 1u) ? 16 : 0;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const uint32_t byte = sb[ks];
           const uint2 lo = lut_s[zoff + (byte & 15)], hi = lut_s[zoff + (byte >> 4)];
           const half8_t as = pack8u((u32x2){lo.x, lo.y}, (u32x2){hi.x, hi.y});
 #pragma unroll

@@ -65,6 +65,7 @@ SIGNATURES = {
     "pqkv_soa_to_blocks": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p]),
     "pqkv_blocks_to_soa": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p]),
     "pqkv_profile_enable": (c_int, [c_int]),
+    "pqkv_profile_repeat": (c_int, [c_int]),
     "pqkv_profile_stream_read": (c_int, [c_void_p, c_size_t, c_void_p, c_int, c_void_p]),
     "pqkv_profile_collect": (c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                      ctypes.POINTER(ctypes.c_int64)]),
@@ -163,6 +164,10 @@ def int_array(values):
 
 def profile_enable(on: bool = True) -> None:
     check(lib().pqkv_profile_enable(int(on)))
+
+
+def profile_repeat(n: int) -> None:
+    check(lib().pqkv_profile_repeat(int(n)))
 
 
 def profile_collect(name: str):

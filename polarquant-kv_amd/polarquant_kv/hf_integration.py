@@ -88,11 +88,20 @@ def _layer_class():
             return self.get_seq_length() + query_length, 0
 
         def crop(self, tokens_to_remove: int) -> None:
-            if self.kc is None:
+            """DynamicLayer.crop's rule (transformers 5): a negative value
+            removes that many tokens, a positive one is the legacy absolute
+            length to keep (nothing happens when it is not below the current
+            length), and 0 does nothing."""
+            if self.kc is None or tokens_to_remove == 0:
                 return
             S = self.kc.seq_len
-            keep = tokens_to_remove if tokens_to_remove >= 0 else S + tokens_to_remove
-            self.kc.seq_len = self.vc.seq_len = max(0, min(S, keep))
+            if tokens_to_remove > 0:
+                if tokens_to_remove >= S:
+                    return
+                keep = tokens_to_remove
+            else:
+                keep = max(0, S + tokens_to_remove)
+            self.kc.seq_len = self.vc.seq_len = keep
 
         def reset(self) -> None:
             if self.kc is not None:

@@ -19,9 +19,12 @@ Differences, all on purpose:
     reference manager stores its per-group min/scale format);
   - with enable_qjl the keys carry the QJL sign sketch and attention adds
     the correction (the reference manager never writes signs, kv_cache.py:112);
-  - the attention layer applies the causal rule to a multi-token chunk
-    (query i of a chunk at positions p0.. sees positions <= p0 + i); the
-    reference's compressed path attends every query to the whole cache.
+  - CompressedMultiHeadAttention applies the causal rule to a multi-token
+    chunk on every path (query i of a chunk at positions p0.. sees positions
+    <= p0 + i): the compressed cache, the uncompressed cache and no cache.
+    The reference calls non-causal SDPA / compressed attention on all three
+    (inference/attention.py:63-92), so a chunk's queries see its later
+    tokens; causal=False reproduces that.
 All GPU work goes through libpqkv_hip.so.
 """
 
@@ -190,9 +193,11 @@ class CompressedMultiHeadAttention(torch.nn.Module):
     """Multi-head (GQA) attention whose KV cache is the compressed one
     (src/polarquant_kv_cuda/inference/attention.py:12-95)."""
 
-    def __init__(self, config: PolarQuantConfig, embed_dim: int, num_heads: int, num_kv_heads: int | None = None):
+    def __init__(self, config: PolarQuantConfig, embed_dim: int, num_heads: int, num_kv_heads: int | None = None,
+                 causal: bool = True):
         super().__init__()
         self.config = config
+        self.causal = causal
         self.embed_dim = embed_dim
         self.num_heads = num_heads
         self.num_kv_heads = num_kv_heads or num_heads
@@ -205,20 +210,22 @@ class CompressedMultiHeadAttention(torch.nn.Module):
     def forward(self, x: torch.Tensor, cache_manager: KVCacheManager | None = None) -> torch.Tensor:
         """x [batch, seq_len, embed_dim] -> [batch, seq_len, embed_dim]. With a
         cache manager the new keys and values are appended and the queries
-        attend causally to everything cached."""
+        attend to everything cached (causally unless causal=False)."""
         B, T, _ = x.shape
         q = self.q_proj(x).reshape(B, T, self.num_heads, self.head_dim).transpose(1, 2).half()
         k = self.k_proj(x).reshape(B, T, self.num_kv_heads, self.head_dim).transpose(1, 2).half()
         v = self.v_proj(x).reshape(B, T, self.num_kv_heads, self.head_dim).transpose(1, 2).half()
         if cache_manager is not None:
             cache_manager.append(k.contiguous(), v.contiguous())
-            out = cache_manager.attend(q.contiguous(), causal=True)
+            out = cache_manager.attend(q.contiguous(), causal=self.causal)
         else:
             rep = self.num_heads // self.num_kv_heads
             kk = k.float().repeat_interleave(rep, 1)
             vv = v.float().repeat_interleave(rep, 1)
             s = torch.matmul(q.float(), kk.transpose(-1, -2).contiguous()) / math.sqrt(self.head_dim)
-            mask = torch.ones(T, T, dtype=torch.bool, device=x.device).triu(1)
-            out = torch.matmul(torch.softmax(s.masked_fill(mask, float("-inf")), -1), vv).half()
+            if self.causal:
+                mask = torch.ones(T, T, dtype=torch.bool, device=x.device).triu(1)
+                s = s.masked_fill(mask, float("-inf"))
+            out = torch.matmul(torch.softmax(s, -1), vv).half()
         out = out.transpose(1, 2).reshape(B, T, -1)
         return self.o_proj(out.to(self.o_proj.weight.dtype))

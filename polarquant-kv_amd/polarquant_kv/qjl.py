@@ -94,14 +94,20 @@ def compute_signatures_gpu(residual, jl_matrix):
 def compute_correction_gpu(query, packed_signs, residual_norms, jl_matrix):
     """Device version of the correction (src/polarquant_kv_cuda/qjl_kernel.py:40-70):
     query [..., d] against packed signs [..., m/8] of the same leading shape
-    -> [...] = (1/m) sum_i (2 s_i - 1) (P q)_i. residual_norms is accepted for
-    the reference's signature and, as there, not used."""
+    -> [...] = (1/m) sum_i (2 s_i - 1) (P q)_i, and 0 where the residual norm
+    is 0 (the CPU guard of python/polarquant_kv/qjl.py:50-51, the reference's
+    AC-3.5; the reference's device function leaves the norms unread).
+    residual_norms None: an all-ones sketch (what a zero residual gives) is
+    read as a zero residual."""
     import torch
 
     from .rotation import rotate
     P = jl_matrix if isinstance(jl_matrix, torch.Tensor) else torch.from_numpy(np.asarray(jl_matrix, np.float32))
     P = P.to(device=query.device, dtype=torch.float32)
     m = P.shape[0]
-    s = bit_unpack(packed_signs, m).to(torch.float32) * 2.0 - 1.0
+    bits = bit_unpack(packed_signs, m)
+    s = bits.to(torch.float32) * 2.0 - 1.0
     qp = rotate(query.to(torch.float32).contiguous(), P)
-    return (s * qp).sum(-1) / m
+    corr = (s * qp).sum(-1) / m
+    zero = bits.all(-1) if residual_norms is None else residual_norms.to(corr.device).float() <= 1e-30
+    return torch.where(zero, torch.zeros_like(corr), corr)

@@ -62,7 +62,8 @@ def allocate_cache(batch: int, num_heads: int, max_seq_len: int, head_dim: int, 
 
 def compress_pq(kv: torch.Tensor, rotation_matrix: torch.Tensor, n_bits=4, cache: PQCache | None = None,
                 start: int | None = None, jl_rot: torch.Tensor | None = None) -> PQCache:
-    """Encode kv [B, H, T, d] (fp16/fp32, device) into a PQ cache.
+    """Encode kv [B, H, T, d] (fp16 or fp32; other float types such as bf16
+    are widened to fp32; device) into a PQ cache.
 
     With `cache`, positions start .. start+T-1 (default: cache.seq_len) are
     written in place and seq_len grows to cover them; otherwise a new cache of
@@ -84,7 +85,10 @@ def compress_pq(kv: torch.Tensor, rotation_matrix: torch.Tensor, n_bits=4, cache
         raise ValueError("cache was allocated without QJL signs")
     if T == 0:
         return cache
-    x = kv.contiguous()
+    # the encoders read fp16 or fp32; other floating types (bf16 models) are
+    # widened to fp32 first, as the reference's kv.float() does
+    # (src/polarquant_kv_cuda/compress_kernel.py:135)
+    x = (kv if kv.dtype in (torch.float16, torch.float32) else kv.to(torch.float32)).contiguous()
     R = rotation_matrix.to(torch.float32).contiguous()
     P = None if jl_rot is None else jl_rot.to(torch.float32).contiguous()
     stream = _lib.stream_of(x)

@@ -372,17 +372,19 @@ def qjl_rule_cache(d=64, S=6, seed=12, key_scale=1.0):
     return kb[None, None], vb[None, None], signs[None, None], P, R, c, xr
 
 
-def test_qjl_zero_key_gets_no_correction_lossless_key_does():
-    """The rule: a key whose radius is 0 (the zero key, where the CPU guard of
-    python/polarquant_kv/qjl.py:50-51 fires) adds no correction; every other
-    key adds (1/m) sum_i (2 s_i - 1) (P q)_i, as the GPU path does
-    (src/polarquant_kv_cuda/attention_kernel.py:95-107), including a lossless
-    key whose rotated-space residual is 0 and whose stored signs are all 1.
-    Scores assembled by hand here; a kernel that dropped the guard (zero key
-    corrected) or guarded on the all-ones sketch (lossless key not corrected)
-    fails."""
+def test_qjl_zero_residual_keys_get_no_correction():
+    """The rule (reference AC-3.5, tests/test_qjl.py:139-154, guard at
+    python/polarquant_kv/qjl.py:50-51): a key whose residual is zero adds no
+    correction. Key 0 is the zero vector and key 1 is lossless (rotated-space
+    residual 0); both store an all-ones sketch (P 0 = 0 >= 0), and a block
+    cache keeps no residual norm, so the all-ones sketch marks them. Every
+    other key adds (1/m) sum_i (2 s_i - 1) (P q)_i
+    (src/polarquant_kv_cuda/attention_kernel.py:95-107). Scores assembled by
+    hand here; a kernel that dropped the guard (both corrected) or guarded on
+    the radius only (lossless key corrected) fails."""
     d, S, G = 64, 6, 2
     kb, vb, signs, P, R, c, xr = qjl_rule_cache(d, S)
+    assert np.array_equal(O.qjl_zero_residual(signs[0, 0], d), [True, True] + [False] * (S - 2))
     q = np.random.default_rng(3).standard_normal((1, G, d))
     got = O.decode_attention(q, kb, vb, R, c, c, qjl_signs=signs, P=P)
     r16, idx = O.unpack_blocks(kb[0, 0], d, 4)
@@ -393,15 +395,26 @@ def test_qjl_zero_key_gets_no_correction_lossless_key_does():
     for g in range(G):
         qr = R @ q[0, g]
         pq = P @ q[0, g]
-        s = np.array([qr @ K[t] + (0.0 if t == 0 else bits[t] @ pq / d) for t in range(S)]) * scale
+        s = np.array([qr @ K[t] + (0.0 if t < 2 else bits[t] @ pq / d) for t in range(S)]) * scale
         assert s[0] == 0.0
-        assert abs(s[1] - scale * (qr @ K[1] + pq.sum() / d)) < 1e-12
+        assert abs(s[1] - scale * (qr @ K[1])) < 1e-12
         w = np.exp(s - s.max())
         w /= w.sum()
         np.testing.assert_allclose(got[0, g], (w @ Vr) @ R, atol=1e-12)
-    # the other rules give different outputs on this cache
-    no_guard = np.array([[R @ q[0, g] @ K[t] + bits[t] @ (P @ q[0, g]) / d for t in range(S)] for g in range(G)])
-    assert abs(no_guard[0, 0]) > 1e-3
+    # the other rules give different scores on this cache
+    pq0 = P @ q[0, 0]
+    assert abs(bits[0] @ pq0 / d) > 1e-3 and abs(bits[1] @ pq0 / d) > 1e-3
+
+
+def test_qjl_zero_residual_needs_every_sign():
+    """One clear bit anywhere in the sketch (any byte, any bit) means a
+    non-zero residual: the mask is an AND over all m signs."""
+    m = 64
+    full = np.full((m + 1, m // 8), 0xFF, np.uint8)
+    for i in range(m):
+        full[i + 1, i // 8] &= ~np.uint8(1 << (i % 8))
+    z = O.qjl_zero_residual(full, m)
+    assert z[0] and not z[1:].any()
 
 
 def test_bit_pack_lsb_round_trip():

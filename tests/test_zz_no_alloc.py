@@ -66,12 +66,32 @@ def test_noalloc_decode_matches_workspace_decode_twice():
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+def _scratch_bytes():
+    """PQKV_NOALLOC_SCRATCH_BYTES as include/pqkv.h defines it."""
+    import os
+    import re
+    hdr = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "pqkv.h")
+    m = re.search(r"#define PQKV_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", open(hdr).read())
+    return int(m.group(1)) << int(m.group(2))
+
+
 def test_noalloc_refuses_a_plan_larger_than_the_scratch():
+    """A shape whose rotated queries alone (B Hq d fp32) exceed the scratch
+    array, on real (zeroed) device buffers of that shape: the call is refused
+    before any launch, and were the refusal ever lost the kernels would read
+    valid memory, not fault."""
     print("noalloc oversized plan", flush=True)
     L = _lib.lib()
-    FAKE = 0x1000     # never dereferenced: the call is refused before any launch
-    B, Hq, Hkv, S, d = 256, 64, 8, 4096, 128
-    rc = L.pqkv_decode_attn_noalloc(FAKE, _lib.F16, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 4, None, None, None, None, 0,
-                                    B, Hq, Hkv, S, S, d, 0.088, FAKE, _lib.F32, None)
+    B, Hq, Hkv, S, d = 1024, 64, 8, 64, 128
+    assert B * Hq * d * 4 > _scratch_bytes()
+    q = torch.zeros(B, Hq, d, dtype=torch.float16, device=DEV)
+    R = torch.eye(d, device=DEV)
+    kc = quantizer.allocate_cache(B, Hkv, S, d, 4, DEV)
+    vc = quantizer.allocate_cache(B, Hkv, S, d, 4, DEV)
+    kc.seq_len = vc.seq_len = S
+    out = torch.zeros(B, Hq, d, device=DEV)
+    rc = L.pqkv_decode_attn_noalloc(*_args(q, R, kc, vc, None, out), _lib.stream_of(q))
+    torch.cuda.synchronize()
     assert rc == _lib.ERR_WORKSPACE
     assert b"scratch" in L.pqkv_last_error()
+    assert not out.any()
