@@ -215,6 +215,71 @@ int pqkv_group_compress(const void *x, int x_dtype, const double *R, int64_t n, 
 int pqkv_group_decompress(const float *radius, const uint8_t *codes, const float *mins, const float *scales,
                           const double *R, int64_t n, int d, int group_size, float *out, void *stream);
 
+/* ---- the reference's GPU group format (CompressedKVCacheGPU) -------------
+ * The format of src/polarquant_kv_cuda/compress_kernel.py:100-189: per
+ * vector y = clamp(x, +-65000) R^T (fp32), r = |y|, u = y / max(r, 1e-30)
+ * (0 where r < 1e-30) zero-padded to d_pad = ceil(d / group_size) *
+ * group_size, per group lo = min, s = (max - lo) / (2^n_bits - 1) (1 for a
+ * flat group), code = round_half_even(clamp((u - lo) / s, 0, 2^n_bits - 1)).
+ * Stored: radius [n] (saturated at 65504), mins / scales [n][ng] in
+ * param_dtype (PQKV_F16 as the reference, or PQKV_F32), codes [n][row]
+ * packed as the reference packs them: 4-bit d_pad/2 bytes (coordinate 2i
+ * low nibble), 2-bit d_pad/4 bytes (v0 | v1<<2 | v2<<4 | v3<<6), every
+ * other width one byte per code. x fp32 / fp16 / bf16 [n][d]; R [d][d] fp32
+ * and Rt = R^T (both device); 1 <= d <= 256, 2 <= n_bits <= 8. residual
+ * (nullable, needs R) receives the QJL residual e = (y - (code s + lo)
+ * max(r, 1e-30)) R [n][d] fp32 with the unrounded lo and s
+ * (compress_kernel.py:166-175). Replaces compress_gpu. */
+int pqkv_group_gpu_compress(const void *x, int x_dtype, const float *R, const float *Rt, int64_t n, int d,
+                            int n_bits, int group_size, void *radius, uint8_t *codes, void *mins, void *scales,
+                            int param_dtype, float *residual, void *stream);
+/* x^ = clamp(((code s + lo) r) R, +-65504) [n][d] in out_dtype (fp16 as the
+ * reference's decompress_gpu, src/polarquant_kv_cuda/decompress_kernel.py:
+ * 10-51, or fp32). */
+int pqkv_group_gpu_decompress(const void *radius, const uint8_t *codes, const void *mins, const void *scales,
+                              int param_dtype, const float *R, int64_t n, int d, int n_bits, int group_size,
+                              void *out, int out_dtype, void *stream);
+/* QJL sketch (compute_signatures_gpu, src/polarquant_kv_cuda/qjl_kernel.py:
+ * 6-37; compute_signatures, python/polarquant_kv/qjl.py:25-35): e = x - x_hat
+ * (x_hat nullable: e = x) in fp32, signs (P e >= 0) summed in fp64 against
+ * Pt = P^T [d][m] fp64, packed LSB first into ceil(m/8) bytes per vector
+ * (bits past m zero), and |e| in norm_dtype. */
+int pqkv_qjl_sketch(const void *x, int x_dtype, const float *x_hat, const double *Pt, int64_t n, int d, int m,
+                    uint8_t *signs, void *norms, int norm_dtype, void *stream);
+/* Attention straight on group-format caches (compressed_attention_gpu,
+ * src/polarquant_kv_cuda/attention_kernel.py:11-113, whose fallback
+ * decompresses both caches; the reference's fused kernels,
+ * csrc/polarquant_full.cu:45-111, read the same fields): q [B][Hq][d]
+ * (original space; several query tokens per head are Hq*Sq rows ordered
+ * [B][Hq][Sq], each attending to all S positions), caches [B][Hkv][S_max][..]
+ * as pqkv_group_gpu_compress writes them with S valid positions; row h of a
+ * batch reads kv head h / (Hq / Hkv). s_t = scale r_t sum_g (s_tg q_rot.c_tg
+ * + lo_tg sum_{j in g} q_rot_j), plus, with qjl_signs ([B][Hkv][S_max][m/8])
+ * and P ([m][d] fp32), scale (1/m) sum_i (2 sign_i - 1) (P q)_i, which is 0
+ * where residual_norms ([B][Hkv][S_max] in param_dtype, nullable) is 0, or,
+ * without norms, where the sketch is all ones (the reference's zero-residual
+ * guard, python/polarquant_kv/qjl.py:50-51). out [B][Hq][d] = softmax(s)
+ * (code s + lo) r, rotated back. The fused kernel needs group_size a
+ * multiple of 8 (16 for 2-bit codes), d_pad <= 256 and, with QJL, m a
+ * multiple of 32 up to 256 (PQKV_ERR_UNSUPPORTED otherwise). */
+size_t pqkv_group_attn_workspace_bytes(int B, int Hq, int Hkv, int S, int d, int group_size, int m);
+int pqkv_group_attn(const void *q, int q_dtype, const float *R, const float *P, int m, const uint8_t *k_codes,
+                    const void *k_radius, const void *k_mins, const void *k_scales, const uint8_t *v_codes,
+                    const void *v_radius, const void *v_mins, const void *v_scales, const uint8_t *qjl_signs,
+                    const void *residual_norms, int n_bits, int param_dtype, int B, int Hq, int Hkv, int S,
+                    int S_max, int d, int group_size, float scale, void *out, int out_dtype, void *workspace,
+                    size_t workspace_bytes, void *stream);
+/* Codebook attention on the reference kernels' SoA cache (packed 4-bit codes
+ * [Hkv][S][d/2], fp32 radii [Hkv][S], a table of `levels` <= 16 entries;
+ * csrc/flash_turboquant.cu:27-105, patch:277-389) at any d that is a
+ * multiple of 8 up to 256, by the group kernel in its codebook mode: q_rot
+ * [Hq][d] already rotated, out [Hq][d] rotated. The compat entry points use
+ * it for the head dims the matrix-core kernels are not built for. */
+size_t pqkv_soa_attn_generic_workspace_bytes(int Hq, int Hkv, int S, int d);
+int pqkv_soa_attn_generic(const float *q_rot, const uint8_t *k_codes, const float *k_radius, const uint8_t *v_codes,
+                          const float *v_radius, const float *codebook, int levels, int Hq, int Hkv, int S, int d,
+                          float scale, float *out, void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---- chunked prefill attention -------------------------------------------
  * Sq query tokens per sequence (absolute positions q_start .. q_start+Sq-1)
  * against a cache that already holds them (append-then-attend,
@@ -347,6 +412,19 @@ void turboquant_full_attention(int64_t q_ptr, int64_t R_ptr, int64_t pk_ptr, int
                                int64_t out_ptr, int64_t q_rot_ptr, int64_t score_ptr,
                                int64_t attn_out_ptr, int total_heads, int total_kv, int S, int D,
                                int n_levels, float scale);
+/* The reference's pybind module polarquant_full
+ * (csrc/polarquant_full.cu:142-186, called by
+ * scripts/benchmark_turboquant.py:63-69): q [total_heads][D] fp32 in the
+ * original space, group-format keys and values with 4-bit packed codes
+ * [total_kv][S][D/2], fp32 group minima and scales [total_kv][S][num_groups]
+ * and fp32 radii [total_kv][S]; out [total_heads][D] fp32, rotated back.
+ * q_rot and attn_out are not needed; score ([total_heads][S] fp32) is used
+ * as scratch when large enough. Runs pqkv_group_attn on the null stream. */
+void full_compressed_attention(int64_t q_ptr, int64_t R_ptr, int64_t pk_ptr, int64_t km_ptr, int64_t ks_ptr,
+                               int64_t kr_ptr, int64_t pv_ptr, int64_t vm_ptr, int64_t vs_ptr, int64_t vr_ptr,
+                               int64_t out_ptr, int64_t q_rot_ptr, int64_t score_ptr, int64_t attn_out_ptr,
+                               int total_heads, int total_kv, int S, int D, int group_size, int num_groups,
+                               float scale);
 
 /* ---- GGML_TYPE_PQ4: a ggml type and its HIP backend ops -------------------
  * No counterpart exists in the reference: its llama.cpp integration keeps the

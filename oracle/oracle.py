@@ -31,6 +31,12 @@ Parity pins (what checks each function besides itself), see tests/test_oracle.py
   group_*              hand-worked codes (round half to even, flat groups,
                        padding), zero vector, the reference tests' cosine
                        thresholds per width (tests/test_quantizer.py:66-82)
+  gpu_group_*          hand-worked codes and packing (4-, 2-bit, bytes), the
+                       zero vector, the reference tests' round-trip cosine
+                       thresholds (tests/cuda/test_compress_decompress.py:
+                       66-80), the residual identity e = x - x^ for R = I
+  group_attention      textbook SDPA (torch fp64) on the same decompressed
+                       caches, the zero-residual guard by hand
   ggml_pq4_*           the ggml fixture tables, the R = I identity with the
                        numpy restatement, lossless heads
   ggml_flash_attn_ext  torch's float64 scaled_dot_product_attention with an
@@ -525,6 +531,163 @@ def group_decompress(r, codes, lo, sc, R: np.ndarray, d: int, group_size: int) -
     g = g * sc.astype(np.float32)[:, None] + lo.astype(np.float32)[:, None]
     y = g.reshape(-1)[:d] * np.float32(r)
     return (y.astype(np.float64) @ R).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# The reference's GPU group format (CompressedKVCacheGPU)
+# ---------------------------------------------------------------------------
+
+def gpu_group_store_bits(n_bits: int) -> int:
+    """4- and 2-bit codes are packed, every other width keeps one byte per
+    code (compress_kernel.py:17-63: 3- and 6-bit "simplified" to bytes)."""
+    return 4 if n_bits == 4 else 2 if n_bits == 2 else 8
+
+
+def gpu_group_pack(codes: np.ndarray, n_bits: int) -> np.ndarray:
+    """[..., d_pad] uint8 -> packed rows (compress_kernel.py:17-63): 4-bit
+    (high << 4) | low of the pair (2i, 2i + 1); 2-bit v0 | v1<<2 | v2<<4 |
+    v3<<6; other widths unchanged."""
+    c = np.asarray(codes).astype(np.uint32)
+    if n_bits == 4:
+        return (c[..., 0::2] | (c[..., 1::2] << 4)).astype(np.uint8)
+    if n_bits == 2:
+        return (c[..., 0::4] | (c[..., 1::4] << 2) | (c[..., 2::4] << 4) | (c[..., 3::4] << 6)).astype(np.uint8)
+    return c.astype(np.uint8)
+
+
+def gpu_group_unpack(packed: np.ndarray, n_bits: int) -> np.ndarray:
+    """Inverse of gpu_group_pack (compress_kernel.py:66-97)."""
+    p = np.asarray(packed).astype(np.uint32)
+    if n_bits == 4:
+        out = np.empty(p.shape[:-1] + (2 * p.shape[-1],), np.uint8)
+        out[..., 0::2] = p & 15
+        out[..., 1::2] = p >> 4
+        return out
+    if n_bits == 2:
+        out = np.empty(p.shape[:-1] + (4 * p.shape[-1],), np.uint8)
+        for k in range(4):
+            out[..., k::4] = (p >> (2 * k)) & 3
+        return out
+    return p.astype(np.uint8)
+
+
+def gpu_group_quantize(y: np.ndarray, n_bits: int, group_size: int):
+    """The quantiser of compress_gpu on rotated vectors y [n, d] float32
+    (src/polarquant_kv_cuda/compress_kernel.py:137-163), fp32 elementwise:
+    r = |y| (fp32 of the fp64 sum of squares), safe = max(r, 1e-30), u =
+    y / safe and 0 where r < 1e-30, zero-padded to whole groups; per group
+    lo = min, range = max - lo, s = range / L where range > 0 else 1 (L =
+    2^bits - 1); code = round_half_even(clip((u - lo) / s, 0, L)).
+    Returns (r, safe, codes [n, d_pad] uint8, lo [n, ng], s [n, ng]), lo and
+    s unrounded fp32."""
+    y = np.asarray(y, np.float32)
+    n, d = y.shape
+    ng = math.ceil(d / group_size)
+    r = np.sqrt((y.astype(np.float64) ** 2).sum(-1)).astype(np.float32)
+    zero = r < np.float32(1e-30)
+    safe = np.where(zero, np.float32(1e-30), r).astype(np.float32)
+    u = np.zeros((n, ng * group_size), np.float32)
+    u[:, :d] = np.where(zero[:, None], np.float32(0.0), y / safe[:, None])
+    g = u.reshape(n, ng, group_size)
+    lo = g.min(-1)
+    rng = (g.max(-1) - lo).astype(np.float32)
+    L = np.float32((1 << n_bits) - 1)
+    sc = np.where(rng > 0, rng / L, np.float32(1.0)).astype(np.float32)
+    t = ((g - lo[..., None]) / sc[..., None]).astype(np.float32)
+    codes = np.rint(np.clip(t, np.float32(0.0), L)).astype(np.uint8).reshape(n, -1)
+    return r, safe, codes, lo, sc
+
+
+def gpu_group_compress(x: np.ndarray, R: np.ndarray, n_bits: int, group_size: int, P=None, rotate_fn=None):
+    """compress_gpu (compress_kernel.py:100-189) on x [n, d]: y = clamp(x,
+    +-65000) R^T in fp32 (rotate_fn(x, R), default the fp32 product in
+    coordinate order, see the C restatement), the quantiser above, and the
+    stored fields: radius fp16 (saturated at 65504), codes packed, lo and s
+    fp16. With P ([m, d]): the QJL residual e = (y - (code s + lo)[:d] safe)
+    R with the unrounded lo and s (fp32, two roundings each; the product back
+    in fp32 by rotate_fn(., R, inverse)), signs (P e >= 0) in fp64 packed LSB
+    first, and fp16 |e| (qjl_kernel.py:6-37). Returns a dict."""
+    x = np.clip(np.asarray(x, np.float32), np.float32(-65000.0), np.float32(65000.0))
+    n, d = x.shape
+    if rotate_fn is None:
+        def rotate_fn(v, M, inverse=False):
+            M64 = np.asarray(M, np.float32).astype(np.float64)
+            return (v.astype(np.float64) @ (M64 if inverse else M64.T)).astype(np.float32)
+    y = rotate_fn(x, R)
+    r, safe, codes, lo, sc = gpu_group_quantize(y, n_bits, group_size)
+    out = {"radius": np.minimum(r, np.float32(65504.0)).astype(np.float16),
+           "codes": gpu_group_pack(codes, n_bits), "mins": lo.astype(np.float16), "scales": sc.astype(np.float16),
+           "codes_unpacked": codes, "y": y, "lo32": lo, "sc32": sc}
+    if P is not None:
+        ng = lo.shape[1]
+        dq = (codes.reshape(n, ng, -1).astype(np.float32) * sc[..., None]).astype(np.float32) + lo[..., None]
+        hat = dq.reshape(n, -1)[:, :d].astype(np.float32) * safe[:, None]
+        e = rotate_fn((y - hat).astype(np.float32), R, inverse=True)
+        proj = e.astype(np.float64) @ np.asarray(P, np.float64).T
+        out["residual"] = e
+        out["signs"] = bit_pack_lsb(proj >= 0)
+        out["res_norms"] = np.sqrt((e.astype(np.float64) ** 2).sum(-1)).astype(np.float16)
+    return out
+
+
+def gpu_group_rotated(radius, codes_packed, mins, scales, d: int, n_bits: int) -> np.ndarray:
+    """The rotated-space reconstruction (code s + lo)[:d] r of the stored
+    fields, fp32 with two roundings for code s + lo and one for the product
+    (decompress_kernel.py:34-43). [n, d] float32."""
+    codes = gpu_group_unpack(codes_packed, n_bits).astype(np.float32)
+    n = codes.shape[0]
+    ng = np.asarray(mins).shape[-1]
+    dq = (codes.reshape(n, ng, -1) * np.asarray(scales, np.float32)[..., None]).astype(np.float32) \
+        + np.asarray(mins, np.float32)[..., None]
+    return dq.reshape(n, -1)[:, :d].astype(np.float32) * np.asarray(radius, np.float32).reshape(n)[:, None]
+
+
+def gpu_group_decompress(radius, codes_packed, mins, scales, R: np.ndarray, d: int, n_bits: int, group_size: int,
+                         rotate_fn=None):
+    """decompress_gpu (decompress_kernel.py:10-51): the rotated
+    reconstruction above times R (rotate_fn(y, R, inverse=True), default the
+    fp64 product), clamped to +-65504, fp16. Returns [n, d] float16."""
+    y = gpu_group_rotated(radius, codes_packed, mins, scales, d, n_bits)
+    if rotate_fn is None:
+        out = y.astype(np.float64) @ np.asarray(R, np.float32).astype(np.float64)
+    else:
+        out = rotate_fn(y, R, inverse=True)
+    return np.clip(out, -65504.0, 65504.0).astype(np.float16)
+
+
+def group_attention(q: np.ndarray, K_hat: np.ndarray, V_hat: np.ndarray, scale: float | None = None,
+                    signs=None, res_norms=None, P=None) -> np.ndarray:
+    """compressed_attention_gpu's arithmetic after decompression
+    (src/polarquant_kv_cuda/attention_kernel.py:62-113) and the CPU path's
+    (python/polarquant_kv/attention.py:111-163), in float64: q [B, Hq, Sq, d]
+    against K_hat / V_hat [B, Hkv, S, d] (the decompressed caches), GQA by
+    repetition, s = q K_hat^T scale (+ scale (1/m) sum_i (2 sign_i - 1) (P q)_i
+    with signs [B, Hkv, S, m/8], 0 where res_norms is 0: the guard of
+    python/polarquant_kv/qjl.py:50-51), softmax over all S, w V_hat. S = 0
+    gives zeros."""
+    q = np.asarray(q, np.float64)
+    B, Hq, Sq, d = q.shape
+    Hkv, S = K_hat.shape[1], K_hat.shape[2]
+    if S == 0:
+        return np.zeros_like(q)
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    rep = Hq // Hkv
+    K = np.repeat(np.asarray(K_hat, np.float64), rep, axis=1)
+    V = np.repeat(np.asarray(V_hat, np.float64), rep, axis=1)
+    s = np.einsum("bhqd,bhsd->bhqs", q, K) * scale
+    if signs is not None and P is not None:
+        m = P.shape[0]
+        sv = 2.0 * bit_unpack_lsb(np.repeat(np.asarray(signs), rep, axis=1), m).astype(np.float64) - 1.0
+        qp = q @ np.asarray(P, np.float64).T
+        corr = np.einsum("bhqm,bhsm->bhqs", qp, sv) / m
+        if res_norms is not None:
+            live = np.repeat(np.asarray(res_norms, np.float64), rep, axis=1) > 1e-30
+            corr = corr * live[:, :, None, :]
+        s = s + corr * scale
+    s = s - s.max(-1, keepdims=True)
+    w = np.exp(s)
+    w /= w.sum(-1, keepdims=True)
+    return np.einsum("bhqs,bhsd->bhqd", w, V)
 
 
 # ---------------------------------------------------------------------------

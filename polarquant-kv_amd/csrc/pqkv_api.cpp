@@ -109,6 +109,12 @@ int fail_status(int code, const char *fmt, ...) {
   return code;
 }
 
+void decode_plan_for(int64_t streams, int S, int target, int *splits, int *tps) {
+  decode_plan(streams, S, target, splits, tps);
+}
+
+int device_compute_units() { return device_cus(); }
+
 void mfma_split_plan(int64_t streams, int S, int *splits, int *tps) {
   decode_plan(streams, S > 0 ? S : 1, mfma_target(), splits, tps);
 }

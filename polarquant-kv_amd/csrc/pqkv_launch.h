@@ -204,6 +204,43 @@ hipError_t launch_group_compress(const void *x, int x_dtype, const double *R, in
                                  float *radius, uint8_t *codes, float *mins, float *scales, hipStream_t s);
 hipError_t launch_group_decompress(const float *radius, const uint8_t *codes, const float *mins, const float *scales,
                                    const double *R, int64_t n, int d, int gs, float *out, hipStream_t s);
+// The reference's GPU group format (CompressedKVCacheGPU): d <= 256, any
+// 1 <= gs <= d; radius, lo and s in pdt (fp16 or fp32); codes packed 4-bit,
+// 2-bit, or one byte per code for the other widths, [n][d_pad * sb / 8].
+// Rt = R^T; resid (nullable) receives the QJL residual e [n][d] fp32.
+hipError_t launch_group_gpu_compress(const void *x, int x_dtype, const float *Rt, const float *R, int64_t n, int d,
+                                     int bits, int gs, void *radius, uint8_t *codes, void *mins, void *scales,
+                                     int pdt, float *resid, hipStream_t s);
+hipError_t launch_group_gpu_decompress(const void *radius, const uint8_t *codes, const void *mins,
+                                       const void *scales, int pdt, const float *R, int64_t n, int d, int bits,
+                                       int gs, void *out, int out_dtype, hipStream_t s);
+// QJL signs of e = x - x_hat (x_hat nullable) against P given as Pt [d][m]
+// fp64, and |e| in norm_dtype.
+hipError_t launch_qjl_sketch(const void *x, int x_dtype, const float *x_hat, const double *Pt, int64_t n, int d,
+                             int m, uint8_t *signs, void *norms, int norm_dtype, hipStream_t s);
+// Fused attention on the group format: query rows rotated (q_rot [rows][dpad],
+// x qs, zero-padded) with P q x qs / m beside them, the split kernel, the merge.
+hipError_t launch_group_qprep(const void *q, int q_dtype, const float *R, const float *P, int64_t rows, int d,
+                              int dpad, int m, float qs, float *q_rot, float *pq, hipStream_t s);
+struct GroupAttnArgsHost {
+  const float *q, *pq;
+  const uint8_t *k_codes, *v_codes;
+  const void *k_rad, *v_rad, *k_lo, *k_sc, *v_lo, *v_sc;
+  const uint8_t *qjl;
+  const void *res_norm;
+  const float *cb;               // codebook mode (SoA caches): c[code], one group of dpad, no lo / s
+  int cb_levels;
+  float *part;
+  int B, Hq, Hkv, S, S_max, d, dpad, gs, bits, pdt, m;
+  int splits, tps;
+};
+hipError_t launch_group_attn(const GroupAttnArgsHost &a, hipStream_t s);
+hipError_t launch_group_merge(const float *part, const float *R, void *out, int out_dtype, int64_t rows, int splits,
+                              int d, hipStream_t s);
+// The split plan of the decode kernels (splits of tps tokens, a multiple of
+// 64) for `streams` streams of S tokens and `target` workgroups.
+void decode_plan_for(int64_t streams, int S, int target, int *splits, int *tps);
+int device_compute_units();
 // Measurement: read `bytes` (a multiple of 16) from p once, XOR into sink[block].
 hipError_t launch_stream_read(const void *p, size_t bytes, uint32_t *sink, int blocks, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs &a, int k_bits, int v_bits, hipStream_t s);

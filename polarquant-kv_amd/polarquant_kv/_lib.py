@@ -56,6 +56,20 @@ SIGNATURES = {
                                     c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "pqkv_group_decompress": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int,
                                       c_void_p, c_void_p]),
+    "pqkv_group_gpu_compress": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_int64, c_int, c_int, c_int,
+                                        c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
+    "pqkv_group_gpu_decompress": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int64, c_int,
+                                          c_int, c_int, c_void_p, c_int, c_void_p]),
+    "pqkv_qjl_sketch": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_int64, c_int, c_int, c_void_p, c_void_p,
+                                c_int, c_void_p]),
+    "pqkv_group_attn_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
+    "pqkv_group_attn": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p, c_int,
+                                c_void_p, c_size_t, c_void_p]),
+    "pqkv_soa_attn_generic_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "pqkv_soa_attn_generic": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                      c_int, c_int, c_int, c_float, c_void_p, c_void_p, c_size_t, c_void_p]),
     "pqkv_prefill_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "pqkv_prefill_attn": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_int, c_int, c_int_p, c_int_p, c_void_p, c_void_p, c_int,
@@ -80,6 +94,7 @@ SIGNATURES = {
     "polarquant_inverse_rotate_cuda_c": (None, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "turboquant_compress": (None, [c_int64] * 5 + [c_int] * 3),
     "turboquant_full_attention": (None, [c_int64] * 12 + [c_int] * 5 + [c_float]),
+    "full_compressed_attention": (None, [c_int64] * 14 + [c_int] * 6 + [c_float]),
     "pqkv_pq4_quantize_rows_host": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p]),
     "pqkv_pq4_dequantize_rows_host": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p]),
     "pqkv_ggml_pq4_rotation": (c_int, [c_void_p, c_int]),

@@ -260,20 +260,23 @@ def compressed_attention(query, key, value, rotation_matrix, jl_matrix=None, n_b
                          group_size: int = 32, enable_qjl: bool = True, num_kv_heads: int | None = None,
                          return_scores: bool = False):
     """The reference's compressed attention on arrays
-    (python/polarquant_kv/attention.py:83-191): compress key and value, then
-    attend on the compressed data, with the QJL score correction when a JL
-    matrix is given. Shapes as standard_attention; returns float32 numpy
-    (or {"output", "scores"} for 2-D input with return_scores).
+    (python/polarquant_kv/attention.py:83-191), in its format and semantics:
+    every key and value is compressed by the group (min / scale) quantizer
+    (quantizer.compress: fp64 rotation, fp32 radius, per-group min / scale,
+    one byte per code), scores are q . k_hat / sqrt(d) with k_hat the
+    decompressed key, plus, with a JL matrix, (1/m) sum_i (2 s_i - 1) (P q)_i
+    / sqrt(d) for the signs of P (k - k_hat) (0 for a zero residual,
+    qjl.py:50-51); softmax over all keys; output w v_hat. Shapes as
+    standard_attention; float32 numpy out (or {"output", "scores"} for 2-D
+    input with return_scores).
 
-    Here the key and value go to the GPU, are encoded in the codebook format
-    (block_pq4 / block_pq2, Lloyd-Max centroids, the north-star format; the
-    reference's CPU function uses its per-group min/scale quantiser) by the
-    HIP encoder, and attended by the HIP decode (one query token) or prefill
-    (several, no mask) kernels. group_size is checked as the reference
-    checks it."""
+    Computed on the GPU: pqkv_group_compress encodes the keys and values,
+    pqkv_group_decompress and pqkv_qjl_sketch give the QJL signs of the
+    original-space residuals, and pqkv_group_attn attends straight on the
+    codes (the reference decompresses and runs numpy products)."""
     import numpy as np
+    from . import _lib as L
     from . import quantizer
-    from .qjl import rotated_jl_matrix
 
     q_np, k_np, v_np = (np.asarray(a) for a in (query, key, value))
     two_d = q_np.ndim == 2 and k_np.ndim == 2
@@ -296,34 +299,69 @@ def compressed_attention(query, key, value, rotation_matrix, jl_matrix=None, n_b
     dev = torch.device("cuda", torch.cuda.current_device()) if torch.cuda.is_available() else None
     if dev is None:
         raise RuntimeError("compressed_attention runs on the GPU (the hot path has no CPU fallback)")
-    R = torch.from_numpy(np.asarray(rotation_matrix, np.float32)).to(dev)
-    kt = torch.from_numpy(np.ascontiguousarray(k_np, np.float32))[None].to(dev)
-    vt = torch.from_numpy(np.ascontiguousarray(v_np, np.float32))[None].to(dev)
-    qt = torch.from_numpy(np.ascontiguousarray(q_np, np.float32))[None].to(dev)
+    lib = L.lib()
+    ng = -(-d // group_size)
+    dpad = ng * group_size
+    R64 = torch.from_numpy(np.ascontiguousarray(rotation_matrix, np.float64)).to(dev)
+    R32 = R64.to(torch.float32)
+
+    def to_dev(a):
+        a = np.ascontiguousarray(a if a.dtype in (np.float16, np.float32) else a.astype(np.float32))
+        return torch.from_numpy(a).to(dev)
+
+    kt, vt, qt = to_dev(k_np), to_dev(v_np), to_dev(q_np)
+    n = hkv * S
+    stream = L.stream_of(kt)
+    fields = []
+    for x in (kt, vt):
+        r = torch.empty(n, dtype=torch.float32, device=dev)
+        c = torch.empty(n, dpad, dtype=torch.uint8, device=dev)
+        lo = torch.empty(n, ng, dtype=torch.float32, device=dev)
+        sc = torch.empty(n, ng, dtype=torch.float32, device=dev)
+        L.check(lib.pqkv_group_compress(x.data_ptr(), L.dtype_code(x.dtype), R64.data_ptr(), n, d, n_bits, group_size,
+                                        r.data_ptr(), c.data_ptr(), lo.data_ptr(), sc.data_ptr(), stream))
+        fields.append((r, c, lo, sc))
     use_qjl = enable_qjl and jl_matrix is not None
-    P_rot = rotated_jl_matrix(jl_matrix, np.asarray(rotation_matrix), dev) if use_qjl else None
-    kc = quantizer.compress_pq(kt, R, n_bits, jl_rot=P_rot)
-    vc = quantizer.compress_pq(vt, R, n_bits)
-    if sq == 1:
-        out = decode_attention(qt[:, :, 0], kc, vc, R, jl_rot=P_rot, out_dtype=torch.float32)[:, :, None]
-    else:
-        out = prefill_attention(qt, kc, vc, R, q_start=0, causal=False, jl_rot=P_rot, out_dtype=torch.float32)
-    out = out[0].cpu().numpy()
+    signs = norms = P32 = k_hat = None
+    m = 0
+    if use_qjl or return_scores:
+        r, c, lo, sc = fields[0]
+        k_hat = torch.empty(n, d, dtype=torch.float32, device=dev)
+        L.check(lib.pqkv_group_decompress(r.data_ptr(), c.data_ptr(), lo.data_ptr(), sc.data_ptr(), R64.data_ptr(),
+                                          n, d, group_size, k_hat.data_ptr(), stream))
+    if use_qjl:
+        P64 = torch.from_numpy(np.ascontiguousarray(jl_matrix, np.float64)).to(dev)
+        m = P64.shape[0]
+        P32 = P64.to(torch.float32).contiguous()
+        signs = torch.empty(n, (m + 7) // 8, dtype=torch.uint8, device=dev)
+        norms = torch.empty(n, dtype=torch.float32, device=dev)
+        L.check(lib.pqkv_qjl_sketch(kt.data_ptr(), L.dtype_code(kt.dtype), k_hat.data_ptr(),
+                                    P64.t().contiguous().data_ptr(), n, d, m, signs.data_ptr(), norms.data_ptr(),
+                                    L.F32, stream))
+    (kr, kc, klo, ksc), (vr, vc, vlo, vsc) = fields
+    rows = hq * sq
+    out = torch.empty(rows, d, dtype=torch.float32, device=dev)
+    ws = torch.empty(lib.pqkv_group_attn_workspace_bytes(1, rows, hkv, S, d, group_size, m), dtype=torch.uint8,
+                     device=dev)
+    # one byte per code: the attention reads the codes as 8-bit storage
+    L.check(lib.pqkv_group_attn(qt.data_ptr(), L.dtype_code(qt.dtype), R32.data_ptr(), L.ptr(P32), m, kc.data_ptr(),
+                                kr.data_ptr(), klo.data_ptr(), ksc.data_ptr(), vc.data_ptr(), vr.data_ptr(),
+                                vlo.data_ptr(), vsc.data_ptr(), L.ptr(signs), L.ptr(norms), 8, L.F32, 1, rows, hkv, S,
+                                S, d, group_size, float(d) ** -0.5, out.data_ptr(), L.F32, ws.data_ptr(), ws.numel(),
+                                stream))
+    res = out.reshape(hq, sq, d).cpu().numpy()
     if not two_d:
-        return out
-    out = out[0]
+        return res
+    res = res[0]
     if not return_scores:
-        return out
-    # scores s = q_rot . k_hat_rot / sqrt(d) (+ the QJL term), from the
-    # rotated-space reconstruction of the same cache
-    Kr = quantizer.dequantize(kc, None, torch.float32)[0, 0]                # [S, d] rotated
-    from .rotation import rotate
-    q_rot = rotate(qt[0, 0].contiguous(), R)                                # [sq, d]
-    s = q_rot @ Kr.T
+        return res
+    # the 2-D scores: q . k_hat / sqrt(d) (+ the QJL term), from the same
+    # decompressed keys and signs
+    q32 = qt[0].float()
+    s = q32 @ k_hat.T
     if use_qjl:
         from .qjl import bit_unpack
-        signs = bit_unpack(kc.qjl_signs[0, 0, :S], d).to(torch.float32) * 2 - 1
-        pq = rotate(q_rot.contiguous(), P_rot) / d
-        rk = (Kr.norm(dim=-1) > 0).to(torch.float32)
-        s = s + (pq @ signs.T) * rk
-    return {"output": out, "scores": (s / math.sqrt(d)).cpu().numpy()}
+        sv = bit_unpack(signs, m).to(torch.float32) * 2 - 1
+        corr = (q32 @ P32.T) @ sv.T / m
+        s = s + torch.where((norms > 1e-30)[None, :], corr, torch.zeros_like(corr))
+    return {"output": res, "scores": (s / math.sqrt(d)).cpu().numpy()}

@@ -76,19 +76,29 @@ def compute_correction(query, signatures, jl_matrix) -> float:
 
 def compute_signatures_gpu(residual, jl_matrix):
     """Device version (src/polarquant_kv_cuda/qjl_kernel.py:6-37): residual
-    [..., d] fp32 on the GPU, jl_matrix [m, d] with m == d -> (packed signs
-    [..., m/8] uint8 LSB-first, residual norms [...] fp16). The projections
-    run on the HIP rotate kernel (P e as one FMA chain per row)."""
+    [..., d] on the GPU, jl_matrix [m, d] -> (packed signs [..., ceil(m/8)]
+    uint8 LSB-first, residual norms [...] fp16), by pqkv_qjl_sketch (P e
+    summed in fp64; the reference's fp32 product agrees up to projections
+    within rounding of 0)."""
     import torch
 
-    from .rotation import rotate
-    P = jl_matrix if isinstance(jl_matrix, torch.Tensor) else torch.from_numpy(np.asarray(jl_matrix, np.float32))
-    P = P.to(device=residual.device, dtype=torch.float32)
-    if P.shape[0] != P.shape[1] or P.shape[1] != residual.shape[-1]:
-        raise ValueError("the device sketch takes a square JL matrix (m == d)")
-    e = residual.to(torch.float32).contiguous()
-    proj = rotate(e, P)                          # e P^T = (P e) per vector
-    return bit_pack(proj >= 0), torch.linalg.vector_norm(e, dim=-1).half()
+    from . import _lib
+    _lib.require_device(residual)
+    P = jl_matrix if isinstance(jl_matrix, torch.Tensor) else torch.from_numpy(np.asarray(jl_matrix))
+    P = P.to(device=residual.device, dtype=torch.float64)
+    m, d = P.shape
+    if residual.shape[-1] != d:
+        raise ValueError(f"residual dim {residual.shape[-1]} != JL matrix dim {d}")
+    e = residual if residual.dtype in (torch.float16, torch.float32, torch.bfloat16) else residual.float()
+    e = e.contiguous()
+    lead = e.shape[:-1]
+    n = e.numel() // d
+    signs = torch.empty(*lead, (m + 7) // 8, dtype=torch.uint8, device=e.device)
+    norms = torch.empty(*lead, dtype=torch.float16, device=e.device)
+    code = {torch.float16: _lib.F16, torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}[e.dtype]
+    _lib.check(_lib.lib().pqkv_qjl_sketch(e.data_ptr(), code, None, P.t().contiguous().data_ptr(), n, d, m,
+                                          signs.data_ptr(), norms.data_ptr(), _lib.F16, _lib.stream_of(e)))
+    return signs, norms
 
 
 def compute_correction_gpu(query, packed_signs, residual_norms, jl_matrix):

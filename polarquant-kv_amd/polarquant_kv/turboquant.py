@@ -37,3 +37,15 @@ def turboquant_full_attention(q_ptr: int, R_ptr: int, pk_ptr: int, kr_ptr: int, 
                                          int(vr_ptr), int(k_cb_ptr), int(v_cb_ptr), int(out_ptr), int(q_rot_ptr),
                                          int(score_ptr), int(attn_out_ptr), int(total_heads), int(total_kv),
                                          int(S), int(D), int(n_levels), float(scale))
+
+
+def full_compressed_attention(q_ptr: int, R_ptr: int, pk_ptr: int, km_ptr: int, ks_ptr: int, kr_ptr: int,
+                              pv_ptr: int, vm_ptr: int, vs_ptr: int, vr_ptr: int, out_ptr: int, q_rot_ptr: int,
+                              score_ptr: int, attn_out_ptr: int, total_heads: int, total_kv: int, S: int, D: int,
+                              group_size: int, num_groups: int, scale: float) -> None:
+    """polarquant_full.full_compressed_attention (csrc/polarquant_full.cu:142-186):
+    group-format attention of original-space fp32 queries, output rotated
+    back; device pointers as ints, asynchronous on the null stream."""
+    _lib.lib().full_compressed_attention(q_ptr, R_ptr, pk_ptr, km_ptr, ks_ptr, kr_ptr, pv_ptr, vm_ptr, vs_ptr,
+                                         vr_ptr, out_ptr, q_rot_ptr, score_ptr, attn_out_ptr, total_heads, total_kv,
+                                         S, D, group_size, num_groups, float(scale))

@@ -20,7 +20,8 @@ def declared_functions():
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     names = re.findall(r"\b([a-z_][a-z0-9_]*)\s*\(", text)
     keywords = {"if", "sizeof", "defined", "return"}
-    return sorted({n for n in names if n not in keywords and n.startswith(("pqkv_", "polarquant_", "turboquant_"))})
+    return sorted({n for n in names if n not in keywords and (n.startswith(("pqkv_", "polarquant_", "turboquant_"))
+                                                                or n == "full_compressed_attention")})
 
 
 def test_header_declares_the_surface():

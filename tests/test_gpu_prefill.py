@@ -213,53 +213,21 @@ def test_compressed_attention_gpu_multi_token_with_qjl():
     _check(out.float().cpu().numpy(), _oracle_w(q, R, kc, vc, S, S - Sq, True, P=P))
 
 
-def test_array_api_compressed_and_standard_attention():
-    """polarquant_kv.attention.compressed_attention / standard_attention on
-    numpy arrays (the reference's CPU API names), 2-D and 3-D GQA shapes, with
-    and without QJL; checked against the oracle on the bytes the GPU encoder
-    wrote and, loosely, against uncompressed attention."""
+def test_array_api_standard_attention():
+    """polarquant_kv.attention.standard_attention on numpy arrays (the
+    reference's CPU API name, python/polarquant_kv/attention.py:20-73), 2-D
+    and 3-D GQA shapes, against the textbook SDPA; compressed_attention (the
+    group format) is checked in test_gpu_group_gpu.py."""
     rng = np.random.default_rng(0)
     d, S = 64, 200
-    R = O.rotation_matrix(d, 42)
-    P = O.jl_matrix(d, d, 43)
     k2 = rng.standard_normal((S, d)).astype(np.float32)
     v2 = rng.standard_normal((S, d)).astype(np.float32)
     q2 = rng.standard_normal((5, d)).astype(np.float32)
-    std = attention.standard_attention(q2, k2, v2)
-    np.testing.assert_allclose(std, O.sdpa(q2, k2, v2), atol=1e-5)
-    for jl in (None, P):
-        res = attention.compressed_attention(q2, k2, v2, R, jl_matrix=jl, return_scores=True)
-        out, scores = res["output"], res["scores"]
-        assert out.dtype == np.float32 and out.shape == (5, d) and scores.shape == (5, S)
-        # the oracle on the same encoded bytes
-        Rt = torch.from_numpy(R.astype(np.float32)).to(DEV)
-        P_rot = None if jl is None else torch.from_numpy((jl @ R.T).astype(np.float32)).to(DEV)
-        kc = quantizer.compress_pq(torch.from_numpy(k2)[None, None].to(DEV), Rt, 4, jl_rot=P_rot)
-        vc = quantizer.compress_pq(torch.from_numpy(v2)[None, None].to(DEV), Rt, 4)
-        cb = O.lloyd_max_codebook(d, 4)[0]
-        signs = None if jl is None else kc.qjl_signs.cpu().numpy()
-        ref = O.prefill_attention(q2[None, None].astype(np.float64), kc.blocks.cpu().numpy(),
-                                  vc.blocks.cpu().numpy(), R, cb, cb, q_start=0, causal=False,
-                                  qjl_signs=signs, P=jl)[0, 0]
-        _check(out, ref)
-        # scores: softmax of them with the dequantised values gives the output
-        w = np.exp(scores - scores.max(-1, keepdims=True))
-        w /= w.sum(-1, keepdims=True)
-        V = O.inverse_rotate(O.dequantize_rotated(vc.blocks.cpu().numpy()[0, 0], d, cb), R)
-        np.testing.assert_allclose(w @ V, ref, atol=2e-4)
-        cos = (out * std).sum() / np.linalg.norm(out) / np.linalg.norm(std)
-        assert cos > 0.95
-    # 3-D GQA, one query token per head (decode path) and several (prefill path)
+    np.testing.assert_allclose(attention.standard_attention(q2, k2, v2), O.sdpa(q2, k2, v2), atol=1e-5)
     k3 = rng.standard_normal((2, S, d)).astype(np.float32)
     v3 = rng.standard_normal((2, S, d)).astype(np.float32)
-    for sq in (1, 7):
-        q3 = rng.standard_normal((8, sq, d)).astype(np.float32)
-        out3 = attention.compressed_attention(q3, k3, v3, R, jl_matrix=P, num_kv_heads=2)
-        std3 = attention.standard_attention(q3, k3, v3, num_kv_heads=2)
-        assert out3.shape == (8, sq, d)
-        cos = (out3 * std3).sum() / np.linalg.norm(out3) / np.linalg.norm(std3)
-        assert cos > 0.95
-    with pytest.raises(ValueError):
-        attention.compressed_attention(q2, k2, v2, R, n_bits=9)
-    empty = attention.compressed_attention(q2, k2[:0], v2[:0], R)
-    assert empty.shape == (5, d) and not empty.any()
+    q3 = rng.standard_normal((8, 7, d)).astype(np.float32)
+    std3 = attention.standard_attention(q3, k3, v3, num_kv_heads=2)
+    want = np.stack([O.sdpa(q3[h], k3[h // 4], v3[h // 4]) for h in range(8)])
+    np.testing.assert_allclose(std3, want, atol=1e-5)
+    assert not attention.standard_attention(q2, k2[:0], v2[:0]).any()
