@@ -33,7 +33,7 @@ extern "C" {
 
 polarquant_state *polarquant_init_c(int head_dim, int n_kv_heads, int n_q_heads, int n_layers, int n_kv_max,
                                     int n_bits) {
-  if ((head_dim != 64 && head_dim != 128) || n_kv_heads <= 0 || n_q_heads <= 0 || n_layers <= 0 ||
+  if (head_dim < 2 || head_dim > 256 || head_dim % 2 || n_kv_heads <= 0 || n_q_heads <= 0 || n_layers <= 0 ||
       n_kv_max <= 0) {
     fprintf(stderr, "PolarQuant (HIP): init: unsupported head_dim=%d n_kv_heads=%d n_q_heads=%d n_layers=%d "
                     "n_kv_max=%d\n", head_dim, n_kv_heads, n_q_heads, n_layers, n_kv_max);
@@ -108,37 +108,52 @@ void polarquant_free_c(polarquant_state *st) {
 void polarquant_compress_cuda_c(const float *input, const float *rotation, const float *codebook,
                                 float *radius_out, uint8_t *packed_out, int N, int D, int n_levels, void *stream) {
   if (N <= 0 || D <= 0) return;
-  if ((D != 64 && D != 128) || n_levels < 2 || n_levels > 16) {
-    fprintf(stderr, "PolarQuant (HIP): compress: unsupported D=%d n_levels=%d\n", D, n_levels);
+  if (D % 2 || D > 256 || n_levels < 2 || n_levels > 16) {
+    fprintf(stderr, "PolarQuant (HIP): compress: unsupported D=%d n_levels=%d (even D up to 256)\n", D, n_levels);
     return;
   }
-  report(pqkv::launch_encode_soa(input, rotation, codebook, n_levels, radius_out, packed_out, N, D,
-                                 (hipStream_t)stream),
-         "compress launch");
+  // head dims 64 and 128: the fixed-d encoder; any other even D <= 256: the
+  // generic one (same arithmetic, a 128- or 256-slot radius tree)
+  if (D == 64 || D == 128)
+    report(pqkv::launch_encode_soa(input, rotation, codebook, n_levels, radius_out, packed_out, N, D,
+                                   (hipStream_t)stream),
+           "compress launch");
+  else
+    report(pqkv::launch_encode_soa_generic(input, rotation, codebook, n_levels, radius_out, packed_out, N, D,
+                                           (hipStream_t)stream),
+           "compress launch");
 }
 
 void polarquant_rotate_query_cuda_c(const float *q_input, const float *rotation, float *q_rotated,
                                     int total_q_heads, int D, void *stream) {
   if (total_q_heads <= 0 || D <= 0) return;
-  if (D != 64 && D != 128) {
-    fprintf(stderr, "PolarQuant (HIP): rotate: unsupported D=%d\n", D);
+  if (D > 256) {
+    fprintf(stderr, "PolarQuant (HIP): rotate: unsupported D=%d (up to 256)\n", D);
     return;
   }
-  report(pqkv::launch_rotate(q_input, PQKV_F32, rotation, q_rotated, PQKV_F32, total_q_heads, D, 0, 1.0f,
-                             (hipStream_t)stream),
-         "rotate launch");
+  if (D == 64 || D == 128)
+    report(pqkv::launch_rotate(q_input, PQKV_F32, rotation, q_rotated, PQKV_F32, total_q_heads, D, 0, 1.0f,
+                               (hipStream_t)stream),
+           "rotate launch");
+  else
+    report(pqkv::launch_rotate_generic(q_input, rotation, q_rotated, total_q_heads, D, 0, (hipStream_t)stream),
+           "rotate launch");
 }
 
 void polarquant_inverse_rotate_cuda_c(const float *input, const float *rotation, float *output, int total_q_heads,
                                       int D, void *stream) {
   if (total_q_heads <= 0 || D <= 0) return;
-  if (D != 64 && D != 128) {
-    fprintf(stderr, "PolarQuant (HIP): inverse rotate: unsupported D=%d\n", D);
+  if (D > 256) {
+    fprintf(stderr, "PolarQuant (HIP): inverse rotate: unsupported D=%d (up to 256)\n", D);
     return;
   }
-  report(pqkv::launch_rotate(input, PQKV_F32, rotation, output, PQKV_F32, total_q_heads, D, 1, 1.0f,
-                             (hipStream_t)stream),
-         "inverse rotate launch");
+  if (D == 64 || D == 128)
+    report(pqkv::launch_rotate(input, PQKV_F32, rotation, output, PQKV_F32, total_q_heads, D, 1, 1.0f,
+                               (hipStream_t)stream),
+           "inverse rotate launch");
+  else
+    report(pqkv::launch_rotate_generic(input, rotation, output, total_q_heads, D, 1, (hipStream_t)stream),
+           "inverse rotate launch");
 }
 
 void polarquant_fused_attention_cuda_c(const float *q_rotated, const uint8_t *packed_k, const float *k_radius,
@@ -146,16 +161,27 @@ void polarquant_fused_attention_cuda_c(const float *q_rotated, const uint8_t *pa
                                        float *output, int total_q_heads, int total_kv_heads, int S, int D,
                                        int n_levels, float scale, void *stream) {
   if (total_q_heads <= 0 || S <= 0 || D <= 0) return;
-  if ((D != 64 && D != 128) || total_kv_heads <= 0 || total_q_heads % total_kv_heads || n_levels < 2 ||
+  if (D % 8 || D > 256 || total_kv_heads <= 0 || total_q_heads % total_kv_heads || n_levels < 2 ||
       n_levels > 16) {
-    fprintf(stderr, "PolarQuant (HIP): attention: unsupported Hq=%d Hkv=%d D=%d n_levels=%d\n", total_q_heads,
-            total_kv_heads, D, n_levels);
+    fprintf(stderr, "PolarQuant (HIP): attention: unsupported Hq=%d Hkv=%d D=%d n_levels=%d (D a multiple of 8 "
+                    "up to 256)\n", total_q_heads, total_kv_heads, D, n_levels);
     return;
   }
   // Stream-ordered scratch for the split partials, like the reference's
   // attention dispatcher, which allocates its temporaries per call
   // (patch:869-870); no host synchronisation.
   hipStream_t st = (hipStream_t)stream;
+  if (D != 64 && D != 128) {
+    // other head dims: the group kernel in its codebook mode (VALU)
+    const size_t gws = pqkv_soa_attn_generic_workspace_bytes(total_q_heads, total_kv_heads, S, D);
+    void *gwork = nullptr;
+    if (!report(hipMallocAsync(&gwork, gws, st), "hipMallocAsync")) return;
+    const int grc = pqkv_soa_attn_generic(q_rotated, packed_k, k_radius, packed_v, v_radius, codebook, n_levels,
+                                          total_q_heads, total_kv_heads, S, D, scale, output, gwork, gws, stream);
+    if (grc != PQKV_OK) fprintf(stderr, "PolarQuant (HIP): attention: %s\n", pqkv_last_error());
+    report(hipFreeAsync(gwork, st), "hipFreeAsync");
+    return;
+  }
   const size_t ws = pqkv_decode_workspace_bytes(1, total_q_heads, total_kv_heads, S, D);
   void *work = nullptr;
   if (!report(hipMallocAsync(&work, ws, st), "hipMallocAsync")) return;
@@ -189,9 +215,28 @@ void turboquant_full_attention(int64_t q_ptr, int64_t R_ptr, int64_t pk_ptr, int
   (void)R_ptr;
   (void)out_ptr;
   if (total_heads <= 0 || S <= 0 || D <= 0) return;
-  if ((D != 64 && D != 128) || total_kv <= 0 || total_heads % total_kv || n_levels < 2 || n_levels > 16) {
-    fprintf(stderr, "PolarQuant (HIP): turboquant_full_attention: unsupported heads=%d kv=%d D=%d n_levels=%d\n",
-            total_heads, total_kv, D, n_levels);
+  if (D % 8 || D > 256 || total_kv <= 0 || total_heads % total_kv || n_levels < 2 || n_levels > 16) {
+    fprintf(stderr, "PolarQuant (HIP): turboquant_full_attention: unsupported heads=%d kv=%d D=%d n_levels=%d "
+                    "(D a multiple of 8 up to 256)\n", total_heads, total_kv, D, n_levels);
+    return;
+  }
+  if (D != 64 && D != 128) {
+    // other head dims: the group kernel in its codebook mode; the keys and
+    // values share one codebook there (k_cb), as the reference's callers pass
+    void *score = (void *)score_ptr;
+    const size_t need = pqkv_soa_attn_generic_workspace_bytes(total_heads, total_kv, S, D);
+    const size_t have = (size_t)total_heads * S * sizeof(float);
+    void *work = score;
+    if (!score || (uintptr_t)score % 256 || have < need) {
+      work = nullptr;
+      if (!report(hipMallocAsync(&work, need, nullptr), "hipMallocAsync")) return;
+    }
+    const int grc = pqkv_soa_attn_generic((const float *)q_rot_ptr, (const uint8_t *)pk_ptr, (const float *)kr_ptr,
+                                          (const uint8_t *)pv_ptr, (const float *)vr_ptr, (const float *)k_cb_ptr,
+                                          n_levels, total_heads, total_kv, S, D, scale, (float *)attn_out_ptr, work,
+                                          work == score ? have : need, nullptr);
+    if (grc != PQKV_OK) fprintf(stderr, "PolarQuant (HIP): turboquant_full_attention: %s\n", pqkv_last_error());
+    if (work != score) report(hipFreeAsync(work, nullptr), "hipFreeAsync");
     return;
   }
   const pqkv::SoaCache soa{(const float *)kr_ptr, (const float *)vr_ptr, n_levels};

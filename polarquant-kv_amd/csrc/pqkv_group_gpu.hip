@@ -666,12 +666,121 @@ __global__ void __launch_bounds__(256) group_merge_kernel(const float *part, con
 }
 
 // ---------------------------------------------------------------------------
+// The reference kernels' SoA encoder at any even d <= 256 (the compat entry
+// points use it for the head dims the fixed-d encoders are not built for):
+// integration/polarquant-kv.patch:193-269 with blockDim = max(d, 128):
+// y_j = sum_k x_k R[j][k] as one fp32 FMA chain in k order, |y|^2 by a
+// pairwise tree over T slots (slot t holds y_t^2, zeros past d; step s adds
+// slot t + s into slot t for s = T/2 .. 1), r = correctly rounded sqrt,
+// u = y / r (IEEE) or 0 where r <= 1e-30, code = first index of the
+// smallest |u - c_i| (strict <, running minimum from 1e30), two codes per
+// byte (coordinate 2i low nibble). T is 128 for d <= 128 and 256 above: the
+// reference's tree over a non-power-of-two block drops slots for 128 < d <
+// 256, which this encoder does not reproduce. One wave per vector.
+__global__ void __launch_bounds__(kGW * 64)
+    encode_soa_generic_kernel(const float *x, const float *R, const float *codebook, int nl, float *radius_out,
+                              uint8_t *packed_out, int64_t n, int d) {
+  __shared__ float xs[kGW][kGMax];
+  __shared__ uint8_t cq[kGW][kGMax];
+  __shared__ float cb[16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (threadIdx.x < 16) cb[threadIdx.x] = (int)threadIdx.x < nl ? codebook[threadIdx.x] : 0.0f;
+  __syncthreads();
+  for (int64_t v = (int64_t)blockIdx.x * kGW + w; v < n; v += (int64_t)gridDim.x * kGW) {
+    for (int k = lane; k < d; k += 64) xs[w][k] = x[v * d + k];
+    __builtin_amdgcn_wave_barrier();
+    float y[kGPer];
+#pragma unroll
+    for (int i = 0; i < kGPer; ++i) {
+      const int j = lane + 64 * i;
+      float acc = 0.0f;
+      if (j < d)
+        for (int k = 0; k < d; ++k) acc = __builtin_fmaf(xs[w][k], R[(int64_t)j * d + k], acc);
+      y[i] = acc;
+    }
+    float sq;
+    {
+#pragma clang fp contract(off)
+      const float q0 = y[0] * y[0], q1 = y[1] * y[1];
+      if (d > 128) {
+        const float q2 = y[2] * y[2], q3 = y[3] * y[3];
+        sq = (q0 + q2) + (q1 + q3);   // s = 128, then s = 64
+      } else {
+        sq = q0 + q1;                 // s = 64
+      }
+#pragma unroll
+      for (int s = 32; s > 0; s >>= 1) sq = sq + shfl_down_f(sq, s);
+    }
+    const float r = (float)__builtin_sqrt((double)__shfl(sq, 0, 64));
+    const bool nz = r > 1e-30f;
+#pragma unroll
+    for (int i = 0; i < kGPer; ++i) {
+      const int j = lane + 64 * i;
+      if (j < d) {
+        const float u = nz ? __fdiv_rn(y[i], r) : 0.0f;
+        int best = 0;
+        float mb = 1e30f;
+        for (int c = 0; c < nl; ++c) {
+          const float e = fabsf(u - cb[c]);
+          if (e < mb) {
+            mb = e;
+            best = c;
+          }
+        }
+        cq[w][j] = (uint8_t)best;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    for (int i = lane; i < d / 2; i += 64)
+      packed_out[v * (d / 2) + i] = (uint8_t)(cq[w][2 * i] | (cq[w][2 * i + 1] << 4));
+    if (lane == 0) radius_out[v] = r;
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// Rotation of n rows at any d <= 256: y = x R^T (forward, y_j = sum_k x_k
+// R[j][k]) or y = x R (inverse, sum_k x_k R[k][j]), one fp32 FMA chain per
+// output in k order (the reference's loops, patch:395-437,508-544).
+__global__ void __launch_bounds__(kGW * 64)
+    rotate_generic_kernel(const float *x, const float *R, float *y, int64_t n, int d, int inverse) {
+  __shared__ float xs[kGW][kGMax];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int64_t v = (int64_t)blockIdx.x * kGW + w; v < n; v += (int64_t)gridDim.x * kGW) {
+    for (int k = lane; k < d; k += 64) xs[w][k] = x[v * d + k];
+    __builtin_amdgcn_wave_barrier();
+    for (int j = lane; j < d; j += 64) {
+      float acc = 0.0f;
+      if (inverse)
+        for (int k = 0; k < d; ++k) acc = __builtin_fmaf(xs[w][k], R[(int64_t)k * d + j], acc);
+      else
+        for (int k = 0; k < d; ++k) acc = __builtin_fmaf(xs[w][k], R[(int64_t)j * d + k], acc);
+      y[v * d + j] = acc;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// ---------------------------------------------------------------------------
 namespace {
 int grid_for(int64_t n) {
   const int64_t blocks = (n + kGW - 1) / kGW;
   return (int)(blocks < 8192 ? (blocks > 0 ? blocks : 1) : 8192);
 }
 }  // namespace
+
+hipError_t launch_encode_soa_generic(const float *x, const float *R, const float *codebook, int n_levels,
+                                     float *radius, uint8_t *packed, int64_t n, int d, hipStream_t s) {
+  if (d < 2 || d > kGMax || d % 2 || n_levels < 1 || n_levels > 16) return hipErrorInvalidValue;
+  encode_soa_generic_kernel<<<grid_for(n), kGW * 64, 0, s>>>(x, R, codebook, n_levels, radius, packed, n, d);
+  return hipGetLastError();
+}
+
+hipError_t launch_rotate_generic(const float *x, const float *R, float *y, int64_t n, int d, int inverse,
+                                 hipStream_t s) {
+  if (d < 1 || d > kGMax) return hipErrorInvalidValue;
+  rotate_generic_kernel<<<grid_for(n), kGW * 64, 0, s>>>(x, R, y, n, d, inverse);
+  return hipGetLastError();
+}
 
 hipError_t launch_group_gpu_compress(const void *x, int x_dtype, const float *Rt, const float *R, int64_t n, int d,
                                      int bits, int gs, void *radius, uint8_t *codes, void *mins, void *scales,

@@ -237,6 +237,12 @@ struct GroupAttnArgsHost {
 hipError_t launch_group_attn(const GroupAttnArgsHost &a, hipStream_t s);
 hipError_t launch_group_merge(const float *part, const float *R, void *out, int out_dtype, int64_t rows, int splits,
                               int d, hipStream_t s);
+// The reference kernels' SoA encoder and fp32 rotations at any head dim
+// (even d <= 256 / d <= 256), for the compat entry points.
+hipError_t launch_encode_soa_generic(const float *x, const float *R, const float *codebook, int n_levels,
+                                     float *radius, uint8_t *packed, int64_t n, int d, hipStream_t s);
+hipError_t launch_rotate_generic(const float *x, const float *R, float *y, int64_t n, int d, int inverse,
+                                 hipStream_t s);
 // The split plan of the decode kernels (splits of tps tokens, a multiple of
 // 64) for `streams` streams of S tokens and `target` workgroups.
 void decode_plan_for(int64_t streams, int S, int target, int *splits, int *tps);

@@ -232,3 +232,84 @@ def test_turboquant_full_attention(case):
     if vcb_kind != "scaled":
         cos = (o * full).sum() / np.linalg.norm(o) / np.linalg.norm(full)
         assert cos > 0.98, cos
+
+
+# ---- head dims other than 64 and 128 (the patch's D-generic kernels) ----
+
+@pytest.mark.parametrize("d", [80, 96, 48, 256, 160])
+def test_generic_head_dim_compress_and_rotations_bit_exact(d):
+    """polarquant_compress_cuda_c, polarquant_rotate_query_cuda_c and
+    polarquant_inverse_rotate_cuda_c at head dims the fixed-d kernels are not
+    built for (integration/polarquant-kv.patch:193-269,395-437,508-544 take
+    any D): codes and fp32 radii equal the oracle's on the FMA-chain rotation
+    (the radius tree over 128 slots up to d = 128, 256 above)."""
+    print(f"compat generic d={d}", flush=True)
+    rng = np.random.default_rng(d)
+    n = 301
+    x = (rng.standard_normal((n, d)) * rng.lognormal(0, 1, (n, 1))).astype(np.float32)
+    x[0] = 0
+    cb = np.asarray(O.lloyd_max_codebook(128, 4)[0], np.float32)
+    R = O.rotation_matrix(d, 42).astype(np.float32)
+    xt, Rt, cbt = (torch.from_numpy(a).to(DEV) for a in (x, R, cb))
+    radius = torch.empty(n, device=DEV)
+    packed = torch.empty(n, d // 2, dtype=torch.uint8, device=DEV)
+    L = _lib.lib()
+    L.polarquant_compress_cuda_c(xt.data_ptr(), Rt.data_ptr(), cbt.data_ptr(), radius.data_ptr(), packed.data_ptr(),
+                                 n, d, 16, _stream())
+    y = torch.empty_like(xt)
+    z = torch.empty_like(xt)
+    L.polarquant_rotate_query_cuda_c(xt.data_ptr(), Rt.data_ptr(), y.data_ptr(), n, d, _stream())
+    L.polarquant_inverse_rotate_cuda_c(y.data_ptr(), Rt.data_ptr(), z.data_ptr(), n, d, _stream())
+    torch.cuda.synchronize()
+    yr = OC.c_rotate_fma(x, R)
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), yr.view(np.uint32))
+    assert np.array_equal(z.cpu().numpy().view(np.uint32), OC.c_rotate_fma(yr, R, inverse=True).view(np.uint32))
+    r_ref, idx = O.quantize_rotated(yr, cb)
+    assert np.array_equal(radius.cpu().numpy().view(np.uint32), r_ref.view(np.uint32))
+    assert np.array_equal(packed.cpu().numpy(), (idx[:, 0::2] | (idx[:, 1::2] << 4)).astype(np.uint8))
+
+
+@pytest.mark.parametrize("case", [(8, 2, 300, 80), (12, 4, 1000, 96), (4, 4, 129, 256), (6, 1, 700, 48)])
+def test_generic_head_dim_attention(case):
+    """polarquant_fused_attention_cuda_c and turboquant_full_attention at
+    head dims 48, 80, 96 and 256 (the group kernel in its codebook mode):
+    within 2e-3 of the SoA oracle on the same codes and fp32 radii; and
+    polarquant_init_c accepts the head dim."""
+    Hq, Hkv, S, d = case
+    print(f"compat generic attention {case}", flush=True)
+    rng = np.random.default_rng(S + d)
+    cb = np.asarray(O.lloyd_max_codebook(128, 4)[0], np.float32)
+    R = O.rotation_matrix(d, 42).astype(np.float32)
+    k = rng.standard_normal((Hkv * S, d)).astype(np.float32)
+    v = rng.standard_normal((Hkv * S, d)).astype(np.float32)
+    L = _lib.lib()
+    Rt, cbt = torch.from_numpy(R).to(DEV), torch.from_numpy(cb).to(DEV)
+    enc = []
+    for a in (k, v):
+        at = torch.from_numpy(a).to(DEV)
+        rad = torch.empty(Hkv * S, device=DEV)
+        pk = torch.empty(Hkv * S, d // 2, dtype=torch.uint8, device=DEV)
+        L.polarquant_compress_cuda_c(at.data_ptr(), Rt.data_ptr(), cbt.data_ptr(), rad.data_ptr(), pk.data_ptr(),
+                                     Hkv * S, d, 16, _stream())
+        enc.append((pk, rad))
+    (pk, kr), (pv, vr) = enc
+    q_rot = torch.from_numpy(rng.standard_normal((Hq, d)).astype(np.float32)).to(DEV)
+    scale = 1.0 / math.sqrt(d)
+    out1 = torch.full((Hq, d), float("nan"), device=DEV)
+    L.polarquant_fused_attention_cuda_c(q_rot.data_ptr(), pk.data_ptr(), kr.data_ptr(), pv.data_ptr(), vr.data_ptr(),
+                                        cbt.data_ptr(), out1.data_ptr(), Hq, Hkv, S, d, 16, scale, _stream())
+    out2 = torch.full((Hq, d), float("nan"), device=DEV)
+    score = torch.zeros(Hq, S, device=DEV)
+    L.turboquant_full_attention(0, Rt.data_ptr(), pk.data_ptr(), kr.data_ptr(), pv.data_ptr(), vr.data_ptr(),
+                                cbt.data_ptr(), cbt.data_ptr(), 0, q_rot.data_ptr(), score.data_ptr(), out2.data_ptr(),
+                                Hq, Hkv, S, d, 16, scale)
+    torch.cuda.synchronize()
+    want = O.decode_attention_soa(q_rot.cpu().numpy(), pk.cpu().numpy(), kr.cpu().numpy(), pv.cpu().numpy(),
+                                  vr.cpu().numpy(), cb, Hkv, scale)
+    for got in (out1, out2):
+        g = got.cpu().numpy().astype(np.float64)
+        assert np.abs(g - want).max() <= 2e-3
+        assert (g * want).sum() / np.linalg.norm(g) / np.linalg.norm(want) >= 0.9999
+    st = L.polarquant_init_c(d, Hkv, Hq, 2, 64, 4)
+    assert st
+    L.polarquant_free_c(st)
