@@ -196,6 +196,53 @@ int pqkv_decode_attn_segments(const void *q, int q_dtype, const float *R, int n_
                               void *out, int out_dtype,
                               void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- paged caches --------------------------------------------------------
+ * A paged cache keeps each (batch, kv-head) stream s = b * Hkv + h in pages
+ * of page_tokens vectors (a power of two, 64 <= page_tokens <= 65536):
+ * position t of stream s is vector t % page_tokens of the page whose device
+ * address is pages[s * max_pages + t / page_tokens]. k_pages, v_pages and
+ * (QJL keys) qjl_pages are device arrays of B * Hkv * max_pages addresses; a
+ * key page and its sign page share an index. A page holds page_tokens
+ * vectors of the cache's width (block_pq4 / block_pq2) or of m/8 sign bytes
+ * and is 16-byte aligned; pages may sit anywhere in device memory, so a cache
+ * grows by adding pages and writing their addresses, with no copy of what it
+ * holds. Entries for pages that no valid position reaches are not read.
+ * Replace the reference cache's grow-by-concatenation, which copies the
+ * whole cache on every append (src/polarquant_kv_cuda/inference/kv_cache.py:
+ * 93-112), and the attention on it (inference/attention.py:59-61). */
+
+/* pqkv_encode into a paged cache: x as in pqkv_encode with n_streams rows
+ * (x + o * x_outer_stride elements) of n_tokens vectors; vector (o, i) is
+ * written to position start + i of stream o (blocks, and with p_rot its QJL
+ * signs in qjl_pages). Same encoders and results as pqkv_encode. */
+int pqkv_encode_paged(const void *x, int x_dtype, int64_t x_outer_stride,
+                      const float *R, const float *codebook, int n_bits,
+                      uint8_t *const *pages, int page_tokens, int max_pages, int64_t start,
+                      int64_t n_streams, int64_t n_tokens, int d,
+                      const float *p_rot, int m, uint8_t *const *qjl_pages, void *stream);
+
+/* pqkv_decode_attn on a paged cache of S valid positions per stream, keys and
+ * values of n_bits each (one codebook each; the same pointer for both lets
+ * one LDS table serve them), QJL when qjl_pages and p_rot are given. The
+ * workspace is pqkv_decode_workspace_bytes(B, Hq, Hkv, S, d). */
+int pqkv_decode_attn_paged(const void *q, int q_dtype, const float *R,
+                           const uint8_t *const *k_pages, const uint8_t *const *v_pages,
+                           int page_tokens, int max_pages,
+                           const float *k_codebook, const float *v_codebook, int n_bits,
+                           const uint8_t *const *qjl_pages, const float *p_rot, int m,
+                           int B, int Hq, int Hkv, int S, int d, float scale,
+                           void *out, int out_dtype, void *workspace, size_t workspace_bytes, void *stream);
+
+/* pqkv_prefill_attn on a paged cache (as pqkv_decode_attn_paged); the
+ * workspace is pqkv_prefill_workspace_bytes(B, Hq, Hkv, Sq, S, d). */
+int pqkv_prefill_attn_paged(const void *q, int q_dtype, const float *R,
+                            const uint8_t *const *k_pages, const uint8_t *const *v_pages,
+                            int page_tokens, int max_pages,
+                            const float *k_codebook, const float *v_codebook, int n_bits,
+                            const uint8_t *const *qjl_pages, const float *p_rot, int m,
+                            int B, int Hq, int Hkv, int Sq, int q_start, int S, int d, float scale, int causal,
+                            void *out, int out_dtype, void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---- group (min / scale) format ------------------------------------------
  * The reference's CPU quantizer format (python/polarquant_kv/quantizer.py:
  * 25-158, behind polarquant_kv.quantizer.compress / decompress /

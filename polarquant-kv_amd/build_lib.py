@@ -23,7 +23,8 @@ BUILD = os.path.join(HERE, "_build")
 SOURCES = ["pqkv_encode.hip", "pqkv_encode_mfma.hip", "pqkv_decode.hip", "pqkv_decode_mfma.hip",
            "pqkv_decode_mfma_k4v4_shared.hip", "pqkv_decode_mfma_k4v4_own.hip", "pqkv_decode_mfma_k4v2.hip",
            "pqkv_decode_mfma_k2v4.hip", "pqkv_decode_mfma_k2v2.hip", "pqkv_decode_mfma_pair.hip",
-           "pqkv_decode_mfma_soa.hip", "pqkv_decode_mfma_ggml.hip", "pqkv_prefill.hip", "pqkv_group.hip", "pqkv_group_gpu.hip", "pqkv_group_api.cpp",
+           "pqkv_decode_mfma_soa.hip", "pqkv_decode_mfma_paged_k4v4_shared.hip", "pqkv_decode_mfma_paged_k4v4_own.hip",
+           "pqkv_decode_mfma_paged_k2v2.hip", "pqkv_decode_mfma_ggml.hip", "pqkv_prefill.hip", "pqkv_group.hip", "pqkv_group_gpu.hip", "pqkv_group_api.cpp",
            "pqkv_api.cpp", "pqkv_compat.cpp", "pqkv_ggml.cpp", "pqkv_noalloc.hip"]
 
 

@@ -513,7 +513,7 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
                     const int *k_head_bits, const int *v_head_bits, const uint8_t *qjl_signs, const float *p_rot,
                     int m, int B, int Hq, int Hkv, int S, int S_max, int d, float scale, void *out, int out_dtype,
                     void *workspace, size_t workspace_bytes, bool plan_sized, const SoaCache *soa,
-                    void *stream) {
+                    void *stream, const PagedCache *pg) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S < 0 || S_max < S)
     return fail(PQKV_ERR_INVALID, "decode: B=%d Hq=%d Hkv=%d S=%d S_max=%d", B, Hq, Hkv, S, S_max);
   if (Hq % Hkv) return fail(PQKV_ERR_INVALID, "decode: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
@@ -532,23 +532,29 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
       if (!supported_bits(kb[h]) || !supported_bits(vb[h]))
         return fail(PQKV_ERR_UNSUPPORTED, "decode: head %d widths k=%d v=%d", h, kb[h], vb[h]);
     }
-  if ((qjl_signs == nullptr) != (p_rot == nullptr)) return fail(PQKV_ERR_INVALID, "decode: qjl and p_rot go together");
-  if (qjl_signs && m != d) return fail(PQKV_ERR_UNSUPPORTED, "decode: QJL needs m == d");
+  // QJL signs: an array, or (paged) sign pages
+  const bool has_qjl = qjl_signs != nullptr || (pg && pg->s_pages != nullptr);
+  if (has_qjl != (p_rot != nullptr)) return fail(PQKV_ERR_INVALID, "decode: qjl and p_rot go together");
+  if (has_qjl && m != d) return fail(PQKV_ERR_UNSUPPORTED, "decode: QJL needs m == d");
   if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(PQKV_ERR_INVALID, "decode: scale must be > 0");
+  if (pg && (mixed || soa || k_bits != v_bits))
+    return fail(PQKV_ERR_UNSUPPORTED, "decode: paged caches take uniform widths with k_bits == v_bits");
   if (!q || (!R && !soa) || !out) return fail(PQKV_ERR_INVALID, "decode: null pointer");
   if ((uintptr_t)R % 16) return fail(PQKV_ERR_INVALID, "decode: R must be 16-byte aligned");
   if (soa && (mixed || k_bits != 4 || v_bits != 4 || qjl_signs || soa->levels < 1 || soa->levels > 16 ||
               (S > 0 && (!soa->k_rad || !soa->v_rad))))
     return fail(PQKV_ERR_UNSUPPORTED, "decode: the SoA layout takes 4-bit codes and no QJL signs");
   if ((uintptr_t)p_rot % 16) return fail(PQKV_ERR_INVALID, "decode: p_rot must be 16-byte aligned");
-  if (S > 0 && (!k_cache || !v_cache || !k_codebooks || !v_codebooks))
-    return fail(PQKV_ERR_INVALID, "decode: null cache or codebook");
+  if (S > 0 && (pg ? (!pg->k_pages || !pg->v_pages) : (!k_cache || !v_cache)))
+    return fail(PQKV_ERR_INVALID, "decode: null cache");
+  if (S > 0 && (!k_codebooks || !v_codebooks)) return fail(PQKV_ERR_INVALID, "decode: null codebook");
 
   // One split plan serves every launch (they share the partials layout); it
   // is sized for the largest launch: all kv heads, or with mixed widths the
   // largest group of heads sharing (k bits, v bits). Heads that are all 4/4
   // (one shared codebook) or 2/2 run as one launch.
-  const bool mfma = use_mfma() || soa != nullptr;
+  // (the paged and SoA modes exist only in the matrix-core kernel)
+  const bool mfma = use_mfma() || soa != nullptr || pg != nullptr;
   int group = Hkv;
   bool pair = false;
   if (mixed) {
@@ -584,8 +590,8 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
   hipError_t e = hipSuccess;
   for (int rep = 0, nrep = prof_repeats(); rep < nrep && e == hipSuccess; ++rep)
     // QJL: the projections P_rot q_rot / m (m == d) come from the same launch
-    e = qjl_signs ? launch_rotate2(q, q_dtype, R, p_rot, q32, pq32, (int64_t)B * Hq, d, scale * kLog2e,
-                                   1.0f / (float)m, st)
+    e = has_qjl ? launch_rotate2(q, q_dtype, R, p_rot, q32, pq32, (int64_t)B * Hq, d, scale * kLog2e,
+                                 1.0f / (float)m, st)
                   : launch_rotate(q, q_dtype, R, q32, PQKV_F32, (int64_t)B * Hq, d, 0, scale * kLog2e, st);
   prof_end(tok, st);
   if (e != hipSuccess) return hip_status(e, "decode query rotation");
@@ -603,8 +609,15 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
   a.v_rad = soa ? soa->v_rad : nullptr;
   a.qjl = qjl_signs;
   a.p_rot = p_rot;
-  a.pq = qjl_signs ? pq32 : nullptr;
+  a.pq = has_qjl ? pq32 : nullptr;
   a.part = part;
+  if (pg) {
+    a.k_pages = pg->k_pages;
+    a.v_pages = pg->v_pages;
+    a.s_pages = pg->s_pages;
+    a.page_shift = pg->page_shift;
+    a.max_pages = pg->max_pages;
+  }
   a.B = B;
   a.Hq = Hq;
   a.Hkv = Hkv;
@@ -646,7 +659,8 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
       const int t = prof_begin("decode_split", st, true);
       hipError_t r = hipSuccess;
       for (int rep = 0, nrep = prof_repeats(); rep < nrep && r == hipSuccess; ++rep)
-        r = soa    ? launch_decode_mfma_soa(a, st)
+        r = pg     ? launch_decode_mfma_paged(a, k_bits, st)
+            : soa  ? launch_decode_mfma_soa(a, st)
             : mfma ? launch_decode_mfma(a, k_bits, v_bits, st)
                    : launch_decode_split(a, k_bits, v_bits, st);
       prof_end(t, st);
@@ -855,11 +869,26 @@ int pqkv_prefill_attn(const void *q, int q_dtype, const float *R, const uint8_t 
                       const int *k_head_bits, const int *v_head_bits, const uint8_t *qjl_signs, const float *p_rot,
                       int m, int B, int Hq, int Hkv, int Sq, int q_start, int S, int S_max, int d, float scale,
                       int causal, void *out, int out_dtype, void *workspace, size_t workspace_bytes, void *stream) {
+  return pqkv::prefill_attn_run(q, q_dtype, R, k_cache, v_cache, k_codebooks, v_codebooks, k_bits, v_bits,
+                                k_head_bits, v_head_bits, qjl_signs, p_rot, m, B, Hq, Hkv, Sq, q_start, S, S_max, d,
+                                scale, causal, out, out_dtype, workspace, workspace_bytes, stream, nullptr);
+}
+
+}  // extern "C"
+
+namespace pqkv {
+
+int prefill_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k_cache, const uint8_t *v_cache,
+                     const float *k_codebooks, const float *v_codebooks, int k_bits, int v_bits,
+                     const int *k_head_bits, const int *v_head_bits, const uint8_t *qjl_signs, const float *p_rot,
+                     int m, int B, int Hq, int Hkv, int Sq, int q_start, int S, int S_max, int d, float scale,
+                     int causal, void *out, int out_dtype, void *workspace, size_t workspace_bytes, void *stream,
+                     const PagedCache *pg) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || S < 0 || S_max < S || q_start < 0)
     return fail(PQKV_ERR_INVALID, "prefill: B=%d Hq=%d Hkv=%d Sq=%d S=%d S_max=%d q_start=%d", B, Hq, Hkv, Sq, S,
                 S_max, q_start);
   if (Hq % Hkv) return fail(PQKV_ERR_INVALID, "prefill: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
-  const bool qjl = qjl_signs != nullptr;
+  const bool qjl = qjl_signs != nullptr || (pg && pg->s_pages != nullptr);
   if (Hq / Hkv > pqkv::prefill_rows_per_block(qjl))
     return fail(PQKV_ERR_UNSUPPORTED, "prefill: group size %d", Hq / Hkv);
   if (causal && (int64_t)q_start + Sq > S)
@@ -879,7 +908,9 @@ int pqkv_prefill_attn(const void *q, int q_dtype, const float *R, const uint8_t 
       if (!supported_bits(kb[h]) || !supported_bits(vb[h]))
         return fail(PQKV_ERR_UNSUPPORTED, "prefill: head %d widths k=%d v=%d", h, kb[h], vb[h]);
     }
-  if ((qjl_signs == nullptr) != (p_rot == nullptr)) return fail(PQKV_ERR_INVALID, "prefill: qjl and p_rot go together");
+  if (qjl != (p_rot != nullptr)) return fail(PQKV_ERR_INVALID, "prefill: qjl and p_rot go together");
+  if (pg && (mixed || k_bits != v_bits))
+    return fail(PQKV_ERR_UNSUPPORTED, "prefill: paged caches take uniform widths with k_bits == v_bits");
   if (qjl && m != d) return fail(PQKV_ERR_UNSUPPORTED, "prefill: QJL needs m == d");
   if (!float_dtype(q_dtype) || !float_dtype(out_dtype)) return fail(PQKV_ERR_UNSUPPORTED, "prefill: dtype");
   if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(PQKV_ERR_INVALID, "prefill: scale must be > 0");
@@ -892,7 +923,7 @@ int pqkv_prefill_attn(const void *q, int q_dtype, const float *R, const uint8_t 
     const size_t ob = (size_t)B * Hq * Sq * d * (out_dtype == PQKV_F32 ? 4 : 2);
     return hip_status(pqkv::launch_fill_zero(out, ob, st), "prefill zero fill");
   }
-  if (!k_cache || !v_cache || !k_codebooks || !v_codebooks)
+  if ((pg ? (!pg->k_pages || !pg->v_pages) : (!k_cache || !v_cache)) || !k_codebooks || !v_codebooks)
     return fail(PQKV_ERR_INVALID, "prefill: null cache or codebook");
   const size_t need = pqkv_prefill_workspace_bytes(B, Hq, Hkv, Sq, S, d);
   if (!workspace || workspace_bytes < need)
@@ -933,6 +964,13 @@ int pqkv_prefill_attn(const void *q, int q_dtype, const float *R, const uint8_t 
   a.d = d;
   a.causal = causal ? 1 : 0;
   a.qt = pqkv::prefill_rows_per_block(qjl) / a.G;
+  if (pg) {
+    a.k_pages = pg->k_pages;
+    a.v_pages = pg->v_pages;
+    a.s_pages = pg->s_pages;
+    a.page_shift = pg->page_shift;
+    a.max_pages = pg->max_pages;
+  }
   if (!mixed) {
     a.k_head_stride = (int64_t)S_max * pqkv_vector_bytes(d, k_bits);
     a.v_head_stride = (int64_t)S_max * pqkv_vector_bytes(d, v_bits);
@@ -981,6 +1019,113 @@ int pqkv_prefill_attn(const void *q, int q_dtype, const float *R, const uint8_t 
   e = pqkv::launch_rotate(o32, PQKV_F32, R, out, out_dtype, nvec, d, 1, 1.0f, st);
   pqkv::prof_end(tok, st);
   return hip_status(e, "prefill output rotation");
+}
+
+}  // namespace pqkv
+
+// ---- paged caches ----
+
+namespace {
+
+// log2 of a page size that is a power of two in [64, 65536], else -1
+int page_shift_of(int page_tokens) {
+  if (page_tokens < 64 || page_tokens > 65536 || (page_tokens & (page_tokens - 1))) return -1;
+  int s = 0;
+  while ((1 << s) < page_tokens) ++s;
+  return s;
+}
+
+// Shared checks of the paged entry points: the page size, and a table wide
+// enough for `positions` tokens per stream. Returns the page shift, or a
+// negative status.
+int paged_validate(const char *what, int page_tokens, int max_pages, int64_t positions) {
+  const int shift = page_shift_of(page_tokens);
+  if (shift < 0)
+    return fail(PQKV_ERR_INVALID, "%s: page_tokens=%d is not a power of two in 64..65536", what, page_tokens);
+  if (max_pages <= 0) return fail(PQKV_ERR_INVALID, "%s: max_pages=%d", what, max_pages);
+  const int64_t need = (positions + page_tokens - 1) >> shift;
+  if (need > max_pages)
+    return fail(PQKV_ERR_INVALID, "%s: %lld positions need %lld pages per stream, the table has %d", what,
+                (long long)positions, (long long)need, max_pages);
+  return shift;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pqkv_encode_paged(const void *x, int x_dtype, int64_t x_outer_stride, const float *R, const float *codebook,
+                      int n_bits, uint8_t *const *pages, int page_tokens, int max_pages, int64_t start,
+                      int64_t n_streams, int64_t n_tokens, int d, const float *p_rot, int m,
+                      uint8_t *const *qjl_pages, void *stream) {
+  if (start < 0) return fail(PQKV_ERR_INVALID, "encode_paged: start=%lld", (long long)start);
+  if (n_streams < 0 || n_tokens < 0) return fail(PQKV_ERR_INVALID, "encode_paged: negative count");
+  const int shift = paged_validate("encode_paged", page_tokens, max_pages, start + n_tokens);
+  if (shift < 0) return shift;
+  // the row checks of pqkv_encode with the page tables standing in for the
+  // block and sign rows
+  const int64_t vb = pqkv_vector_bytes(d, n_bits);
+  const int v = encode_validate(x, x_dtype, x_outer_stride, R, codebook, n_bits, (uint8_t *)pages, n_tokens * vb,
+                                n_streams, n_tokens, d, p_rot, m, (uint8_t *)qjl_pages, n_tokens * (m / 8));
+  if (v <= 0) return v;
+  pqkv::EncodeArgs a;
+  memset(&a, 0, sizeof(a));
+  a.x = x;
+  a.x_outer_stride = x_outer_stride;
+  a.R = R;
+  a.codebook = codebook;
+  a.bits = n_bits;
+  a.n_outer = n_streams;
+  a.n_inner = n_tokens;
+  a.d = d;
+  a.p_rot = p_rot;
+  a.m = m;
+  a.pages = pages;
+  a.qjl_pages = qjl_pages;
+  a.page_shift = shift;
+  a.max_pages = max_pages;
+  a.page_start = start;
+  const char *env = getenv("PQKV_ENCODE_KERNEL");
+  const bool exact = env && strcmp(env, "exact") == 0;
+  hipError_t e;
+  if (!exact && fast_encode_ok(x, x_dtype, x_outer_stride, n_streams, n_tokens, R, p_rot, (const uint8_t *)qjl_pages,
+                                 0, nullptr, 0)) {
+    const int tok = pqkv::prof_begin("encode_mfma", (hipStream_t)stream);
+    e = pqkv::launch_encode_mfma(a, nullptr, nullptr, device_cus(), (hipStream_t)stream);
+    pqkv::prof_end(tok, (hipStream_t)stream);
+  } else {
+    const int tok = pqkv::prof_begin("encode_exact", (hipStream_t)stream);
+    e = pqkv::launch_encode_exact(a, x_dtype, (hipStream_t)stream);
+    pqkv::prof_end(tok, (hipStream_t)stream);
+  }
+  return hip_status(e, "encode_paged launch");
+}
+
+int pqkv_decode_attn_paged(const void *q, int q_dtype, const float *R, const uint8_t *const *k_pages,
+                           const uint8_t *const *v_pages, int page_tokens, int max_pages, const float *k_codebook,
+                           const float *v_codebook, int n_bits, const uint8_t *const *qjl_pages, const float *p_rot,
+                           int m, int B, int Hq, int Hkv, int S, int d, float scale, void *out, int out_dtype,
+                           void *workspace, size_t workspace_bytes, void *stream) {
+  const int shift = paged_validate("decode_paged", page_tokens, max_pages, S);
+  if (shift < 0) return shift;
+  const pqkv::PagedCache pg{k_pages, v_pages, qjl_pages, shift, max_pages};
+  return pqkv::decode_attn_run(q, q_dtype, R, nullptr, nullptr, k_codebook, v_codebook, n_bits, n_bits, nullptr,
+                               nullptr, nullptr, p_rot, m, B, Hq, Hkv, S, S, d, scale, out, out_dtype, workspace,
+                               workspace_bytes, false, nullptr, stream, &pg);
+}
+
+int pqkv_prefill_attn_paged(const void *q, int q_dtype, const float *R, const uint8_t *const *k_pages,
+                            const uint8_t *const *v_pages, int page_tokens, int max_pages, const float *k_codebook,
+                            const float *v_codebook, int n_bits, const uint8_t *const *qjl_pages, const float *p_rot,
+                            int m, int B, int Hq, int Hkv, int Sq, int q_start, int S, int d, float scale,
+                            int causal, void *out, int out_dtype, void *workspace, size_t workspace_bytes,
+                            void *stream) {
+  const int shift = paged_validate("prefill_paged", page_tokens, max_pages, S);
+  if (shift < 0) return shift;
+  const pqkv::PagedCache pg{k_pages, v_pages, qjl_pages, shift, max_pages};
+  return pqkv::prefill_attn_run(q, q_dtype, R, nullptr, nullptr, k_codebook, v_codebook, n_bits, n_bits, nullptr,
+                                nullptr, nullptr, p_rot, m, B, Hq, Hkv, Sq, q_start, S, S, d, scale, causal, out,
+                                out_dtype, workspace, workspace_bytes, stream, &pg);
 }
 
 int pqkv_dequantize(const uint8_t *blocks, const float *codebook, int n_bits, const float *R, void *out,

@@ -333,12 +333,18 @@ struct DecodeSmem {
 // waves of a workgroup take four kv heads of the same tokens, which share
 // cache lines when a token's heads are interleaved). The code tables are
 // built from one codebook shared by all heads (cb_head_stride 0).
-template <int D, int G, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GG = false, bool HW = false>
+// PG (paged caches): a stream's positions live in pages of 2^page_shift
+// tokens (>= 64, so a 64-token chunk lies in one page) found through the
+// page tables a.k_pages / a.v_pages / a.s_pages; each chunk's loads go
+// through a buffer over its own page.
+template <int D, int G, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GG = false, bool HW = false,
+          bool PG = false>
 __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem<D, G, KB, VBITS, QJL, VSH> &sm,
                                                  const int split, const int bh) {
   static_assert(!SOA || (KB == 4 && VBITS == 4 && !QJL), "the SoA layout carries 4-bit codes and no QJL signs");
   static_assert(!GG || (!SOA && !QJL), "the ggml layout has block-encoded keys and values and no QJL signs");
   static_assert(!HW || GG, "one kv head per wave is a mode of the ggml layout (fp16 block radii, no listed heads)");
+  static_assert(!PG || (!SOA && !GG), "paged caches hold block-encoded vectors, one token per vector slot");
   constexpr int VBK = SOA ? D / 2 : vector_bytes(D, KB), VBV = SOA ? D / 2 : vector_bytes(D, VBITS);
   constexpr int KK = D / 16;     // score MFMAs per 16-token tile
   constexpr int NB = D / 16;     // value n-tiles
@@ -393,12 +399,27 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
     krres = stream_rsrc((const uint8_t *)(a.k_rad + ri), (uint32_t)a.S * 4u);
     vrres = stream_rsrc((const uint8_t *)(a.v_rad + ri), (uint32_t)a.S * 4u);
   }
-  auto ld_rad_k = [&](int tok) { return SOA ? bld32(krres, tok * 4) : bld16(kres, tok * kts); };
-  auto ld_rad_v = [&](int tok) { return SOA ? bld32(vrres, tok * 4) : bld16(vres, tok * vts); };
+  auto ld_rad_k = [&](__amdgpu_buffer_rsrc_t kr, int tok) { return SOA ? bld32(krres, tok * 4) : bld16(kr, tok * kts); };
+  auto ld_rad_v = [&](__amdgpu_buffer_rsrc_t vr, int tok) { return SOA ? bld32(vrres, tok * 4) : bld16(vr, tok * vts); };
   auto rad = [](uint32_t bits) { return SOA ? __builtin_bit_cast(float, bits) : half_bits_to_float(bits); };
   __amdgpu_buffer_rsrc_t sres = kres;
-  if constexpr (QJL)
+  if constexpr (QJL && !PG)
     sres = stream_rsrc(a.qjl + ((int64_t)(b * a.Hkv + h) * a.S_max) * (D / 8), (uint32_t)a.S * (uint32_t)(D / 8));
+  // The buffer that chunk t0 loads through and t0's position in it: the
+  // whole stream, or (PG) the chunk's page, over the page's valid tokens (so
+  // loads past S still read 0). The page address is wave-uniform (a scalar
+  // load).
+  const int64_t prow = PG ? (int64_t)(b * a.Hkv + h) * a.max_pages : 0;
+  auto chunk_rsrc = [&](const uint8_t *const *pages, int t0, uint32_t vb, __amdgpu_buffer_rsrc_t whole, int &rel) {
+    if constexpr (PG) {
+      const int pg = t0 >> a.page_shift, p0 = pg << a.page_shift;
+      rel = t0 - p0;
+      return stream_rsrc(pages[prow + pg], (uint32_t)min(a.S - p0, 1 << a.page_shift) * vb);
+    } else {
+      rel = t0;
+      return whole;
+    }
+  };
 
   if constexpr (KB == 4) build_sliced4(sm.u.t.k, a.k_cb + h * a.cb_head_stride, tid, SOA ? a.cb_levels : 16);
   else build_sliced2(sm.u.t.k, a.k_cb + h * a.cb_head_stride, tid);
@@ -489,18 +510,19 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   // Per sub-tile pieces, so that a step can reload each sub-tile's registers
   // as soon as it has read them (and the radii first: they are converted at
   // the start of a step).
-  auto load_k_sub = [&](CK &c, int t0, int st) {
-    load_words(kres, (t0 + kSub * st + ktok) * kts + kphys, c.w[st]);
+  // (kr / vr / sr: the chunk's buffers, t0 its position in them)
+  auto load_k_sub = [&](CK &c, __amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t sr, int t0, int st) {
+    load_words(kr, (t0 + kSub * st + ktok) * kts + kphys, c.w[st]);
     if constexpr (QJL) {
       const int so = (t0 + kSub * st + col) * (D / 8) + grp * (D / 32);
-      c.sg[st] = D == 128 ? bld32(sres, so) : bld16(sres, so);
+      c.sg[st] = D == 128 ? bld32(sr, so) : bld16(sr, so);
     }
   };
-  auto load_v_sub = [&](CV &c, int t0, int kb) {
+  auto load_v_sub = [&](CV &c, __amdgpu_buffer_rsrc_t vr, int t0, int kb) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int off = (t0 + kSub * kb + 4 * grp + e) * vts + vob;
-      c.w[kb][e] = VBITS == 4 ? bld32(vres, off) : bld16(vres, off);
+      c.w[kb][e] = VBITS == 4 ? bld32(vr, off) : bld16(vr, off);
     }
   };
   // GG: the mask values of the chunk's logits this lane holds in the
@@ -519,16 +541,32 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   // fp16 mask value j of a lane's mask words, and the logits' exp2 scale
   constexpr float kLog2eF = 1.4426950408889634f;
   auto mask_val = [](const uint32_t *mk, int j) { return half_bits_to_float(mk[j >> 1] >> (16 * (j & 1))); };
+  // the key (and sign) buffers of chunk t0 and its position in them (key
+  // and sign pages share the page index)
+  auto key_rsrc = [&](int t0, __amdgpu_buffer_rsrc_t &sr, int &rel) {
+    if constexpr (QJL && PG) {
+      int srel;
+      sr = chunk_rsrc(a.s_pages, t0, D / 8, sres, srel);
+    } else {
+      sr = sres;
+    }
+    return chunk_rsrc(a.k_pages, t0, VBK, kres, rel);
+  };
   auto load_k = [&](CK &c, int t0) {
-    c.r = ld_rad_k(t0 + rtok);
+    int rel;
+    __amdgpu_buffer_rsrc_t sr;
+    const __amdgpu_buffer_rsrc_t kr = key_rsrc(t0, sr, rel);
+    c.r = ld_rad_k(kr, rel + rtok);
     load_mask(c, t0);
 #pragma unroll
-    for (int st = 0; st < NSUB; ++st) load_k_sub(c, t0, st);
+    for (int st = 0; st < NSUB; ++st) load_k_sub(c, kr, sr, rel, st);
   };
   auto load_v = [&](CV &c, int t0) {
-    c.r = ld_rad_v(t0 + rtok);
+    int rel;
+    const __amdgpu_buffer_rsrc_t vr = chunk_rsrc(a.v_pages, t0, VBV, vres, rel);
+    c.r = ld_rad_v(vr, rel + rtok);
 #pragma unroll
-    for (int kb = 0; kb < NSUB; ++kb) load_v_sub(c, t0, kb);
+    for (int kb = 0; kb < NSUB; ++kb) load_v_sub(c, vr, rel, kb);
   };
   __syncthreads();
 
@@ -856,6 +894,13 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
     float sv[NSUB][4];
     const float rkl = rad(k.r), rvl = rad(v.r);
     rkn = rkl;
+    // the buffers of the chunks this iteration loads
+    int tkr = tk, tvr = tv;
+    __amdgpu_buffer_rsrc_t kr = kres, vr = vres, sr = sres;
+    if constexpr (kPieceLoads) {
+      kr = key_rsrc(tk, sr, tkr);
+      vr = chunk_rsrc(a.v_pages, tv, VBV, vres, tvr);
+    }
 #pragma unroll
     for (int j = 0; j < MC; ++j) mkn[j] = k.mw[j];
     FState f = fbegin(sv, sc, kChunk, false, rvl, rks, mks);
@@ -866,14 +911,14 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
       kread(k, j, kt);
       vread(v, j, vt);
       if constexpr (kPieceLoads) {
-        load_k_sub(k, tk, j);
-        load_v_sub(v, tv, j);
+        load_k_sub(k, kr, sr, tkr, j);
+        load_v_sub(v, vr, tvr, j);
         if (j == 0) {
           // the radii with the first pieces: issued at the start of the
           // iteration they fetch lines that some of the chunk's later code
           // loads miss again in L2 (+2.6 % HBM traffic)
-          k.r = ld_rad_k(tk + rtok);
-          v.r = ld_rad_v(tv + rtok);
+          k.r = ld_rad_k(kr, tkr + rtok);
+          v.r = ld_rad_v(vr, tvr + rtok);
           if constexpr (kCompact) load_mask(k, tk);
         }
       }
@@ -900,7 +945,9 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
   // registers with chunk i + 1. Only the last chunk can be partial; it is
   // finished after the loop.
   constexpr int kStep = HW ? kChunk : kMWaves * kChunk;
-  const int first = t_begin + (HW ? 0 : wave * kChunk);
+  // (PG: through a scalar register, so that the chunk positions and with
+  // them the page addresses are known to be wave-uniform)
+  const int first = t_begin + (HW ? 0 : (PG ? __builtin_amdgcn_readfirstlane(wave) : wave) * kChunk);
   const int nch = first < t_end ? (t_end - first + kStep - 1) / kStep : 0;
   if (nch > 0) {
     CK ck;
@@ -1003,14 +1050,15 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
 
 // HW: workgroup row y takes the pairs 4y .. 4y + 3, one per wave (n_heads a
 // multiple of 4, so the four share the batch row).
-template <int D, int G, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GG = false, bool HW = false>
+template <int D, int G, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GG = false, bool HW = false,
+          bool PG = false>
 __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_kernel(const DecodeArgs a) {
   __shared__ DecodeSmem<D, G, KB, VBITS, QJL, VSH> sm;
   // (read through a scalar register: the buffer resources built from the
   // pair must be wave-uniform, or every load becomes a loop over lanes)
   const int bh = HW ? __builtin_amdgcn_readfirstlane((int)blockIdx.y * kMWaves + (int)(threadIdx.x >> 6))
                     : (int)blockIdx.y;
-  decode_mfma_body<D, G, KB, VBITS, QJL, VSH, SOA, GG, HW>(a, sm, blockIdx.x, bh);
+  decode_mfma_body<D, G, KB, VBITS, QJL, VSH, SOA, GG, HW, PG>(a, sm, blockIdx.x, bh);
 }
 
 // Mixed widths whose kv heads are either 4-bit keys and values (a4, one
@@ -1047,24 +1095,26 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_pair_kernel
     default: KERNEL(8, __VA_ARGS__); break;                               \
   }
 
-template <int D, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GGML = false, bool HW = false>
+template <int D, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GGML = false, bool HW = false,
+          bool PG = false>
 static void launch_dm(const DecodeArgs &a, int G, hipStream_t s) {
   dim3 grid(a.splits, HW ? a.B * a.n_heads / kMWaves : a.B * a.n_heads);
-#define PQKV_DM_ONE(GG, ...) decode_mfma_kernel<D, GG, KB, VBITS, QJL, VSH, SOA, GGML, HW><<<grid, 256, 0, s>>>(a)
+#define PQKV_DM_ONE(GG, ...) decode_mfma_kernel<D, GG, KB, VBITS, QJL, VSH, SOA, GGML, HW, PG><<<grid, 256, 0, s>>>(a)
   PQKV_DM_G_SWITCH(PQKV_DM_ONE, 0)
 #undef PQKV_DM_ONE
 }
 
-// One width pair on both head dims, with or without QJL.
-template <int KB, int VBITS, bool VSH = false>
+// One width pair on both head dims, with or without QJL (PG: paged caches,
+// whose QJL signs come through a.s_pages).
+template <int KB, int VBITS, bool VSH = false, bool PG = false>
 static hipError_t launch_dm_widths(const DecodeArgs &a, hipStream_t s) {
-  const bool qjl = a.qjl != nullptr;
+  const bool qjl = PG ? a.s_pages != nullptr : a.qjl != nullptr;
   if (a.d == 128) {
-    if (qjl) launch_dm<128, KB, VBITS, true, VSH>(a, a.g, s);
-    else launch_dm<128, KB, VBITS, false, VSH>(a, a.g, s);
+    if (qjl) launch_dm<128, KB, VBITS, true, VSH, false, false, false, PG>(a, a.g, s);
+    else launch_dm<128, KB, VBITS, false, VSH, false, false, false, PG>(a, a.g, s);
   } else {
-    if (qjl) launch_dm<64, KB, VBITS, true, VSH>(a, a.g, s);
-    else launch_dm<64, KB, VBITS, false, VSH>(a, a.g, s);
+    if (qjl) launch_dm<64, KB, VBITS, true, VSH, false, false, false, PG>(a, a.g, s);
+    else launch_dm<64, KB, VBITS, false, VSH, false, false, false, PG>(a, a.g, s);
   }
   return hipGetLastError();
 }
@@ -1075,5 +1125,10 @@ hipError_t launch_dm_k4v4_own(const DecodeArgs &a, hipStream_t s);     // a valu
 hipError_t launch_dm_k4v2(const DecodeArgs &a, hipStream_t s);
 hipError_t launch_dm_k2v4(const DecodeArgs &a, hipStream_t s);
 hipError_t launch_dm_k2v2(const DecodeArgs &a, hipStream_t s);
+// Paged caches (uniform widths): 4/4 with one shared table or a value
+// codebook of its own, and 2/2.
+hipError_t launch_dm_paged_k4v4_shared(const DecodeArgs &a, hipStream_t s);
+hipError_t launch_dm_paged_k4v4_own(const DecodeArgs &a, hipStream_t s);
+hipError_t launch_dm_paged_k2v2(const DecodeArgs &a, hipStream_t s);
 
 }  // namespace pqkv

@@ -395,13 +395,13 @@ __global__ void __launch_bounds__(256) encode_exact_kernel(EncodeArgs a) {
         const float x1 = D == 128 ? ys[wave][lane + 64] : 0.0f;
         float r;
         uint32_t codes;
-        quantize_store_wave<D, BITS>(x0, x1, cb, a.blocks + qo * a.blocks_outer_stride + qi * VB,
+        quantize_store_wave<D, BITS>(x0, x1, cb, encode_out_addr(a, a.blocks, a.pages, a.blocks_outer_stride, qo, qi, VB),
                                      nullptr, &r, &codes);
         cs[wave][lane] = codes;
         if (lane == 0) rs[wave] = r;
       }
     }
-    if (a.qjl != nullptr) {
+    if (a.qjl != nullptr || a.qjl_pages != nullptr) {
       __syncthreads();
       // Residual e = y - r * c[code] in LDS (overwrites xs), then sign of
       // p_rot[i] . e for i = j (m = D projections, one per thread).
@@ -419,7 +419,7 @@ __global__ void __launch_bounds__(256) encode_exact_kernel(EncodeArgs a) {
       const uint64_t bits = __ballot(proj >= 0.0f);
       if (v < n && lane == 0) {
         const int64_t qo = v / a.n_inner, qi = v - qo * a.n_inner;
-        uint8_t *dst = a.qjl + qo * a.qjl_outer_stride + qi * (D / 8) + (j / 64) * 8;
+        uint8_t *dst = encode_out_addr(a, a.qjl, a.qjl_pages, a.qjl_outer_stride, qo, qi, D / 8) + (j / 64) * 8;
         if (D == 64) {
           *(uint64_t *)dst = bits;
         } else {

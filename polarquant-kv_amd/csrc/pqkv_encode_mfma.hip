@@ -400,7 +400,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   };
   // Step g's blocks from stage[sb] to memory: one run of 16-byte pieces when
   // the blocks are one aligned run, else dword by dword.
-  const bool run16 = a.n_outer <= 1 && ((uintptr_t)a.blocks & 15) == 0;
+  const bool run16 = a.n_outer <= 1 && a.pages == nullptr && ((uintptr_t)a.blocks & 15) == 0;
   auto flush = [&](int64_t g, int sb) {
     const lds_u8 *stg = (const lds_u8 *)stage[sb];
     if (run16) {
@@ -429,7 +429,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
           uint32_t vo, vi;
           split(v, vo, vi);
           const uint32_t w = *(const lds_u32 *)(stg + vl * VB + 4 * c);
-          *(uint32_t *)(a.blocks + (int64_t)vo * a.blocks_outer_stride + (int64_t)vi * VB + 4 * c) = w;
+          *(uint32_t *)(encode_out_addr(a, a.blocks, a.pages, a.blocks_outer_stride, vo, vi, VB) + 4 * c) = w;
         }
       }
     }
@@ -668,7 +668,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
       }
     }
   };
-  const bool run16q = a.n_outer <= 1 && ((uintptr_t)a.qjl & 15) == 0;
+  const bool run16q = a.n_outer <= 1 && a.pages == nullptr && ((uintptr_t)a.qjl & 15) == 0;
   auto flush_signs = [&](int64_t g, int sb) {
     const lds_u8 *stg = (const lds_u8 *)sstage[sb];
     if (run16q) {
@@ -691,7 +691,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
       if (v < n) {
         uint32_t vo, vi;
         split(v, vo, vi);
-        *(uint32_t *)(a.qjl + (int64_t)vo * a.qjl_outer_stride + (int64_t)vi * SB + 4 * c) =
+        *(uint32_t *)(encode_out_addr(a, a.qjl, a.qjl_pages, a.qjl_outer_stride, vo, vi, SB) + 4 * c) =
             *(const lds_u32 *)(stg + vl * SB + 4 * c);
       }
     }
@@ -813,7 +813,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
 }
 
 hipError_t launch_encode_mfma(const EncodeArgs &a, float *rot_out, float *radius_out, int cus, hipStream_t s) {
-  const bool qjl = a.qjl != nullptr;
+  const bool qjl = a.qjl != nullptr || a.qjl_pages != nullptr;
   const int64_t n = a.n_outer * a.n_inner;
   const int eg = qjl ? 32 : kEG;
   const int64_t groups = (n + eg - 1) / eg;

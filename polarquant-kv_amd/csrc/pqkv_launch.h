@@ -35,7 +35,24 @@ struct EncodeArgs {
   int m;
   uint8_t *qjl;                // or null
   int64_t qjl_outer_stride;    // bytes
+  // Paged output (pages != null; blocks and the outer strides unused): vector
+  // (o, i) is position page_start + i of stream o, stored as vector
+  // (pos & (2^page_shift - 1)) of page pages[o * max_pages + (pos >> page_shift)];
+  // its signs likewise in qjl_pages.
+  uint8_t *const *pages;
+  uint8_t *const *qjl_pages;
+  int page_shift, max_pages;
+  int64_t page_start;
 };
+
+// Output address of vector (o, i) of an encode: row o of the blocks (or
+// signs) `stride` bytes apart, or (paged) its page slot; vb bytes per vector.
+__device__ __forceinline__ uint8_t *encode_out_addr(const EncodeArgs &a, uint8_t *base, uint8_t *const *pages,
+                                                    int64_t stride, int64_t o, int64_t i, int vb) {
+  if (a.pages == nullptr) return base + o * stride + i * vb;
+  const int64_t pos = a.page_start + i;
+  return pages[o * a.max_pages + (pos >> a.page_shift)] + (pos & ((1 << a.page_shift) - 1)) * vb;
+}
 
 // One launch of the split-K decode kernel covers B x n_heads (batch, kv-head)
 // streams with the same K and V bit widths.
@@ -67,6 +84,12 @@ struct DecodeArgs {
   int rows_per_seq;
   const uint16_t *mask;
   int64_t mask_row_stride, mask_seq_stride;
+  // Paged caches (the kernels' PG mode; k_cache / v_cache / qjl unused):
+  // position t of stream s = b * Hkv + h is vector t & (2^page_shift - 1) of
+  // page k_pages[s * max_pages + (t >> page_shift)] (v_pages, and the sign
+  // pages s_pages, alike); page_shift >= 6, so a 64-token chunk lies in one page.
+  const uint8_t *const *k_pages, *const *v_pages, *const *s_pages;
+  int page_shift, max_pages;
   int16_t heads[kMaxListHeads];
   int64_t k_head_off[kMaxListHeads], v_head_off[kMaxListHeads];
 };
@@ -88,6 +111,10 @@ struct PrefillArgs {
   int B, Hq, Hkv, G, Sq, q_start, S, S_max, d, causal;
   int qt;                        // query tokens per workgroup (rows / G)
   int n_heads, listed;
+  // Paged caches (k_pages != null; k_cache / v_cache / qjl unused), as in
+  // DecodeArgs: a 64-token tile lies in one page.
+  const uint8_t *const *k_pages, *const *v_pages, *const *s_pages;
+  int page_shift, max_pages;
   int16_t heads[kMaxListHeads];
   int64_t k_head_off[kMaxListHeads], v_head_off[kMaxListHeads];
 };
@@ -103,6 +130,13 @@ struct SoaCache {
   const float *k_rad, *v_rad;
   int levels;
 };
+// A paged cache (pqkv_*_paged): page address tables of B * Hkv * max_pages
+// entries for keys, values and (nullable) QJL signs; pages of 2^page_shift
+// tokens.
+struct PagedCache {
+  const uint8_t *const *k_pages, *const *v_pages, *const *s_pages;
+  int page_shift, max_pages;
+};
 // The validated decode call behind pqkv_decode_attn (plan_sized = false: the
 // workspace must hold pqkv_decode_workspace_bytes) and the allocation-free
 // entry point (plan_sized = true: the workspace must hold this call's plan).
@@ -113,7 +147,14 @@ int decode_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k
                     const int *k_head_bits, const int *v_head_bits, const uint8_t *qjl_signs, const float *p_rot,
                     int m, int B, int Hq, int Hkv, int S, int S_max, int d, float scale, void *out, int out_dtype,
                     void *workspace, size_t workspace_bytes, bool plan_sized, const SoaCache *soa,
-                    void *stream);
+                    void *stream, const PagedCache *pg = nullptr);
+// The validated call behind pqkv_prefill_attn (pg: pqkv_prefill_attn_paged).
+int prefill_attn_run(const void *q, int q_dtype, const float *R, const uint8_t *k_cache, const uint8_t *v_cache,
+                     const float *k_codebooks, const float *v_codebooks, int k_bits, int v_bits,
+                     const int *k_head_bits, const int *v_head_bits, const uint8_t *qjl_signs, const float *p_rot,
+                     int m, int B, int Hq, int Hkv, int Sq, int q_start, int S, int S_max, int d, float scale,
+                     int causal, void *out, int out_dtype, void *workspace, size_t workspace_bytes, void *stream,
+                     const PagedCache *pg);
 // The validated call behind pqkv_decode_attn_segments, and the split plans
 // it makes (one per segment, sharing one partials layout; returns their
 // total).
@@ -179,6 +220,9 @@ hipError_t launch_decode_split(const DecodeArgs &a, int k_bits, int v_bits, hipS
 // Matrix-core variant for 2- and 4-bit keys and values, with or without QJL
 // (same workspace).
 hipError_t launch_decode_mfma(const DecodeArgs &a, int k_bits, int v_bits, hipStream_t s);
+// Paged caches (a.k_pages, a.v_pages, a.s_pages; uniform widths, keys and
+// values of `bits` each).
+hipError_t launch_decode_mfma_paged(const DecodeArgs &a, int bits, hipStream_t s);
 // Mixed widths with kv heads of exactly two kinds, 4-bit K and V sharing one
 // codebook (a4) and 2-bit K and V (a2): one launch over both head lists.
 hipError_t launch_decode_mfma_pair(const DecodeArgs &a4, const DecodeArgs &a2, hipStream_t s);

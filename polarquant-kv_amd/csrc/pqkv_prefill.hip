@@ -573,8 +573,20 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
   // group 1's values of tile it - 1 (stage 2 it + 1). Each is read from the
   // stage after its decode on, and radii follow their half.
   const int ntiles = (kv_end + kPT - 1) / kPT;
-  const __amdgpu_buffer_rsrc_t gres = group == 0 ? kres : vres;  // this group's stream
   uint8_t(&graw)[2][RawTile<D>::kAlloc] = raw[group];
+  // The buffer tile t0 is copied from and t0's position in it: the whole
+  // stream, or with paged caches (pages != null, a wave-uniform test) the
+  // tile's page over its valid tokens; a 64-token tile lies in one page.
+  const int64_t prow = (int64_t)(b * a.Hkv + h) * a.max_pages;
+  auto tile_rsrc = [&](const uint8_t *const *pages, __amdgpu_buffer_rsrc_t whole, int t0, int vb, int &rel) {
+    if (pages == nullptr) {
+      rel = t0;
+      return whole;
+    }
+    const int pg = t0 >> a.page_shift, p0 = pg << a.page_shift;
+    rel = t0 - p0;
+    return stream_rsrc(pages[prow + pg], (uint32_t)min(a.S - p0, 1 << a.page_shift) * (uint32_t)vb);
+  };
   auto decode = [&](int it) {  // this group's half of tile it, from graw[it & 1]
     if (group == 0) decode_k<D, KB>(graw[it & 1], tiles[it & 1], rads[it & 1], lut_k, gtid);
     else decode_v<D, VBITS>(graw[it & 1], tiles[it & 1], rads[it & 1], lut_v, gtid);
@@ -582,15 +594,17 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
   // this group's raw tile it into graw[it & 1] (group 0: K, and with QJL the
   // signs into raw_s[it % 3], one wave instruction)
   auto dma = [&](int it) {
+    int rel;
     if (group == 0) {
-      dma_raw<VBK>(gres, graw[it & 1], it * kPT, gw, lane);
+      dma_raw<VBK>(tile_rsrc(a.k_pages, kres, it * kPT, VBK, rel), graw[it & 1], rel, gw, lane);
       if constexpr (QJL) {
+        const __amdgpu_buffer_rsrc_t sr = tile_rsrc(a.s_pages, sres, it * kPT, SGB, rel);
         if (gw == 0 && 16 * lane < kPT * SGB)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(sres, (__attribute__((address_space(3))) void *)raw_s[it % 3], 16,
-                                                   it * kPT * SGB + 16 * lane, 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (__attribute__((address_space(3))) void *)raw_s[it % 3], 16,
+                                                   rel * SGB + 16 * lane, 0, 0, 0);
       }
     } else {
-      dma_raw<VBV>(gres, graw[it & 1], it * kPT, gw, lane);
+      dma_raw<VBV>(tile_rsrc(a.v_pages, vres, it * kPT, VBV, rel), graw[it & 1], rel, gw, lane);
     }
   };
   auto wait_dma = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
@@ -667,7 +681,7 @@ __global__ void __launch_bounds__(kPW * 64, 1) prefill_mfma_kernel(const Prefill
 
 template <int D, int KB, int VBITS>
 static void launch_pw(const PrefillArgs &a, dim3 grid, hipStream_t s) {
-  if (a.qjl != nullptr) prefill_mfma_kernel<D, KB, VBITS, true><<<grid, kPW * 64, 0, s>>>(a);
+  if (a.qjl != nullptr || a.s_pages != nullptr) prefill_mfma_kernel<D, KB, VBITS, true><<<grid, kPW * 64, 0, s>>>(a);
   else prefill_mfma_kernel<D, KB, VBITS, false><<<grid, kPW * 64, 0, s>>>(a);
 }
 

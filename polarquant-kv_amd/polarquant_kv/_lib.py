@@ -52,6 +52,15 @@ SIGNATURES = {
                                           c_int_p, c_int_p, c_int_p, c_int_p,
                                           c_int, c_int, c_int, c_int, c_float,
                                           c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
+    "pqkv_encode_paged": (c_int, [c_void_p, c_int, c_int64, c_void_p, c_void_p, c_int, c_void_p, c_int, c_int,
+                                  c_int64, c_int64, c_int64, c_int, c_void_p, c_int, c_void_p, c_void_p]),
+    "pqkv_decode_attn_paged": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p,
+                                       c_void_p, c_int, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                       c_int, c_float, c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
+    "pqkv_prefill_attn_paged": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p,
+                                        c_void_p, c_int, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                        c_int, c_int, c_int, c_float, c_int, c_void_p, c_int, c_void_p, c_size_t,
+                                        c_void_p]),
     "pqkv_group_compress": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int, c_int, c_int,
                                     c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "pqkv_group_decompress": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int,

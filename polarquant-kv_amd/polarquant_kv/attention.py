@@ -17,7 +17,7 @@ import math
 import torch
 
 from . import _lib
-from .types import PQCache, vector_bytes
+from .types import PagedPQCache, PQCache, vector_bytes
 
 
 def _rotated_p(jl_matrix, rotation_matrix, device):
@@ -55,13 +55,46 @@ def check_shapes(B: int, Hq: int, d: int, keys: PQCache, values: PQCache, rotati
     return Hkv
 
 
+def check_paged(B: int, Hq: int, d: int, keys: PagedPQCache, values: PagedPQCache, rotation_matrix=None) -> int:
+    """check_shapes for paged caches: the same geometry, uniform and equal
+    widths, one page size, pages covering seq_len. Returns Hkv."""
+    if not isinstance(keys, PagedPQCache) or not isinstance(values, PagedPQCache):
+        raise ValueError("keys and values must both be paged caches, or both PQCache")
+    Hkv = keys.num_heads
+    if keys.head_dim != d or values.head_dim != d:
+        raise ValueError(f"head_dim: query {d}, keys {keys.head_dim}, values {values.head_dim}")
+    if values.num_heads != Hkv or keys.batch != B or values.batch != B:
+        raise ValueError("keys and values must match the query's batch and each other's heads")
+    if keys.seq_len != values.seq_len:
+        raise ValueError("keys and values hold different numbers of positions")
+    if keys.n_bits != values.n_bits:
+        raise ValueError("paged caches take keys and values of one width")
+    if keys.page_tokens != values.page_tokens:
+        raise ValueError("keys and values must share page_tokens")
+    for c in (keys, values):
+        if c.capacity < c.seq_len:
+            raise ValueError("paged cache holds fewer pages than its seq_len needs")
+    # one table width for both (the kernels take one row stride)
+    width = max(keys.max_pages, values.max_pages)
+    keys._widen(width)
+    values._widen(width)
+    if Hq % Hkv:
+        raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
+    if rotation_matrix is not None and tuple(rotation_matrix.shape) != (d, d):
+        raise ValueError(f"rotation matrix must be ({d}, {d}), got {tuple(rotation_matrix.shape)}")
+    return Hkv
+
+
 def decode_attention(query: torch.Tensor, keys: PQCache, values: PQCache, rotation_matrix: torch.Tensor,
                      scale: float | None = None, jl_rot: torch.Tensor | None = None,
                      out_dtype: torch.dtype | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """query [B, Hq, d] (original space) -> out [B, Hq, d] (original space)."""
+    """query [B, Hq, d] (original space) -> out [B, Hq, d] (original space).
+    keys / values: PQCache, or PagedPQCache (pqkv_decode_attn_paged)."""
     if query.dim() != 3:
         raise ValueError(f"query must be [B, Hq, d], got {tuple(query.shape)}")
     B, Hq, d = query.shape
+    if isinstance(keys, PagedPQCache) or isinstance(values, PagedPQCache):
+        return _decode_paged(query, keys, values, rotation_matrix, scale, jl_rot, out_dtype, workspace)
     Hkv = check_shapes(B, Hq, d, keys, values, rotation_matrix)
     _lib.require_device(query, rotation_matrix, jl_rot)
     scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
@@ -87,6 +120,32 @@ def decode_attention(query: torch.Tensor, keys: PQCache, values: PQCache, rotati
         kcb.data_ptr(), vcb.data_ptr(), keys.head_bits()[0], values.head_bits()[0], kbits, vbits,
         _lib.ptr(qjl), _lib.ptr(P), d if P is not None else 0, B, Hq, Hkv, S, keys.max_seq_len, d, scale,
         out.data_ptr(), _lib.dtype_code(out_dtype), workspace.data_ptr(), workspace.numel(), _lib.stream_of(q)))
+    return out
+
+
+def _decode_paged(query, keys, values, rotation_matrix, scale, jl_rot, out_dtype, workspace):
+    B, Hq, d = query.shape
+    Hkv = check_paged(B, Hq, d, keys, values, rotation_matrix)
+    _lib.require_device(query, rotation_matrix, jl_rot)
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    out_dtype = query.dtype if out_dtype is None else out_dtype
+    q = query.contiguous()
+    R = rotation_matrix.to(torch.float32).contiguous()
+    out = torch.empty(B, Hq, d, dtype=out_dtype, device=q.device)
+    lib = _lib.lib()
+    S = keys.seq_len
+    need = lib.pqkv_decode_workspace_bytes(B, Hq, Hkv, max(S, 1), d)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    if jl_rot is not None and keys.sign_table is None:
+        raise ValueError("QJL correction requested but the key cache has no signs")
+    P = None if jl_rot is None else jl_rot.to(torch.float32).contiguous()
+    _lib.check(lib.pqkv_decode_attn_paged(
+        q.data_ptr(), _lib.dtype_code(q.dtype), R.data_ptr(), keys.table.data_ptr(), values.table.data_ptr(),
+        keys.page_tokens, keys.max_pages, keys.codebooks.data_ptr(),
+        values.codebooks.data_ptr(), keys.n_bits, keys.sign_table.data_ptr() if P is not None else None,
+        _lib.ptr(P), d if P is not None else 0, B, Hq, Hkv, S, d, scale, out.data_ptr(), _lib.dtype_code(out_dtype),
+        workspace.data_ptr(), workspace.numel(), _lib.stream_of(q)))
     return out
 
 
@@ -141,6 +200,8 @@ def prefill_attention(query: torch.Tensor, keys: PQCache, values: PQCache, rotat
     if query.dim() != 4:
         raise ValueError(f"query must be [B, Hq, Sq, d], got {tuple(query.shape)}")
     B, Hq, Sq, d = query.shape
+    if isinstance(keys, PagedPQCache) or isinstance(values, PagedPQCache):
+        return _prefill_paged(query, keys, values, rotation_matrix, q_start, causal, scale, out_dtype, jl_rot)
     Hkv = check_shapes(B, Hq, d, keys, values, rotation_matrix)
     _lib.require_device(query, rotation_matrix, jl_rot)
     scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
@@ -166,6 +227,31 @@ def prefill_attention(query: torch.Tensor, keys: PQCache, values: PQCache, rotat
         _lib.ptr(qjl), _lib.ptr(P), d if P is not None else 0, B, Hq, Hkv, Sq, q_start, S, keys.max_seq_len, d,
         scale, int(causal), out.data_ptr(), _lib.dtype_code(out_dtype), ws.data_ptr(), ws.numel(),
         _lib.stream_of(q)))
+    return out
+
+
+def _prefill_paged(query, keys, values, rotation_matrix, q_start, causal, scale, out_dtype, jl_rot):
+    B, Hq, Sq, d = query.shape
+    Hkv = check_paged(B, Hq, d, keys, values, rotation_matrix)
+    _lib.require_device(query, rotation_matrix, jl_rot)
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    out_dtype = query.dtype if out_dtype is None else out_dtype
+    q = query.contiguous()
+    R = rotation_matrix.to(torch.float32).contiguous()
+    out = torch.empty(B, Hq, Sq, d, dtype=out_dtype, device=q.device)
+    lib = _lib.lib()
+    S = keys.seq_len
+    need = lib.pqkv_prefill_workspace_bytes(B, Hq, Hkv, Sq, max(S, 1), d)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    if jl_rot is not None and keys.sign_table is None:
+        raise ValueError("QJL correction requested but the key cache has no signs")
+    P = None if jl_rot is None else jl_rot.to(torch.float32).contiguous()
+    _lib.check(lib.pqkv_prefill_attn_paged(
+        q.data_ptr(), _lib.dtype_code(q.dtype), R.data_ptr(), keys.table.data_ptr(), values.table.data_ptr(),
+        keys.page_tokens, keys.max_pages, keys.codebooks.data_ptr(),
+        values.codebooks.data_ptr(), keys.n_bits, keys.sign_table.data_ptr() if P is not None else None,
+        _lib.ptr(P), d if P is not None else 0, B, Hq, Hkv, Sq, q_start, S, d, scale, int(causal), out.data_ptr(),
+        _lib.dtype_code(out_dtype), ws.data_ptr(), ws.numel(), _lib.stream_of(q)))
     return out
 
 

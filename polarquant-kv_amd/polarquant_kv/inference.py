@@ -11,10 +11,14 @@ the reference with the same names and arguments:
                                (attention.py:12-95)
 
 Differences, all on purpose:
-  - the caches are allocated once for max_seq_len positions and append
-    encodes the new positions in place (the reference concatenates the whole
-    cache with torch.cat on every append, kv_cache.py:96-116), so a decode
-    step costs O(new tokens), not O(S);
+  - the compressed caches are paged (PagedPQCache): they grow by pages of
+    page_tokens positions as the sequence grows, and append encodes the new
+    positions straight into their pages through the page table
+    (pqkv_encode_paged), never copying what is cached (the reference
+    concatenates the whole cache with torch.cat on every append,
+    kv_cache.py:96-116), so a decode step costs O(new tokens), not O(S), and
+    memory follows the sequence, not max_seq_len (a limit only); attention
+    runs the paged decode / chunked-prefill kernels;
   - the layout is block_pq4 / block_pq2 with Lloyd-Max centroids (the
     reference manager stores its per-group min/scale format);
   - with enable_qjl the keys carry the QJL sign sketch and attention adds
@@ -36,7 +40,7 @@ from dataclasses import dataclass
 import torch
 
 from . import attention, quantizer
-from .types import PQCache
+from .types import PagedPQCache
 
 
 @dataclass
@@ -49,18 +53,20 @@ class PolarQuantConfig:
 
 
 class KVCacheManager:
-    """Compressed KV cache of one attention layer: [batch, num_heads,
-    max_seq_len] positions, filled by prefill (several tokens) and decode
+    """Compressed KV cache of one attention layer: up to max_seq_len
+    positions per (batch, head), kept in pages of page_tokens positions
+    (a power of two, >= 64), filled by prefill (several tokens) and decode
     (one token) appends."""
 
     def __init__(self, config: PolarQuantConfig, max_seq_len: int, batch: int, num_heads: int, head_dim: int,
-                 device: str = "cuda", rotation_seed: int = 42):
+                 device: str = "cuda", rotation_seed: int = 42, page_tokens: int = 256):
         from .rotation import generate_rotation_matrix
         if config.enable_compression:
             quantizer._validate_params(config.n_bits, config.group_size, head_dim)
             if config.n_bits not in (2, 4):
                 raise ValueError(f"the codebook format stores 2- or 4-bit codes, got n_bits={config.n_bits}")
         self.config = config
+        self.page_tokens = int(page_tokens)
         self.max_seq_len = int(max_seq_len)
         self.batch = batch
         self.num_heads = num_heads
@@ -75,8 +81,8 @@ class KVCacheManager:
             from .qjl import generate_jl_matrix, rotated_jl_matrix
             self.jl_matrix = generate_jl_matrix(config.jl_dim, head_dim, seed=rotation_seed + 1)
             self.jl_rot = rotated_jl_matrix(self.jl_matrix, self.R.cpu().numpy(), device)
-        self._keys: PQCache | None = None
-        self._values: PQCache | None = None
+        self._keys: PagedPQCache | None = None
+        self._values: PagedPQCache | None = None
         self._key_cache: torch.Tensor | None = None
         self._value_cache: torch.Tensor | None = None
         self._seq_len = 0
@@ -84,10 +90,10 @@ class KVCacheManager:
     # ---- allocation ----
     def _allocate(self):
         if self.config.enable_compression:
-            B, H, S, d, bits = self.batch, self.num_heads, self.max_seq_len, self.head_dim, self.config.n_bits
-            self._keys = quantizer.allocate_cache(B, H, S, d, bits, self.device,
-                                                  jl_dim=d if self.jl_rot is not None else 0)
-            self._values = quantizer.allocate_cache(B, H, S, d, bits, self.device)
+            B, H, d, bits = self.batch, self.num_heads, self.head_dim, self.config.n_bits
+            self._keys = quantizer.allocate_paged_cache(B, H, d, bits, self.device, page_tokens=self.page_tokens,
+                                                        jl_dim=d if self.jl_rot is not None else 0)
+            self._values = quantizer.allocate_paged_cache(B, H, d, bits, self.device, page_tokens=self.page_tokens)
         else:
             shape = (self.batch, self.num_heads, self.max_seq_len, self.head_dim)
             self._key_cache = torch.zeros(shape, dtype=torch.float16, device=self.device)
@@ -113,7 +119,8 @@ class KVCacheManager:
 
     @property
     def allocated_bytes(self) -> int:
-        """Device bytes held for all max_seq_len positions."""
+        """Device bytes held: the pages allocated so far (and their tables);
+        uncompressed, the max_seq_len-position arrays."""
         if self.config.enable_compression:
             return 0 if self._keys is None else self._keys.memory_bytes() + self._values.memory_bytes()
         return 0 if self._key_cache is None else 2 * self._key_cache.numel() * 2
@@ -128,7 +135,8 @@ class KVCacheManager:
     # ---- writes ----
     def append(self, key: torch.Tensor, value: torch.Tensor) -> None:
         """key / value [batch, num_heads, new_seq, head_dim] (fp16 or fp32) at
-        positions seq_len .. seq_len + new_seq - 1, encoded in place."""
+        positions seq_len .. seq_len + new_seq - 1, encoded into their pages
+        (pages are added as the positions need them)."""
         if key.shape != value.shape or key.dim() != 4:
             raise ValueError("key and value must both be [batch, num_heads, new_seq, head_dim]")
         B, H, T, d = key.shape
@@ -148,7 +156,7 @@ class KVCacheManager:
         self._seq_len += T
 
     def get_kv(self):
-        """Compressed: the two PQCache objects (seq_len positions valid);
+        """Compressed: the two PagedPQCache objects (seq_len positions valid);
         uncompressed: views of the first seq_len positions."""
         if not self.config.enable_compression:
             if self._key_cache is None:
@@ -157,7 +165,7 @@ class KVCacheManager:
         return self._keys, self._values
 
     def reset(self) -> None:
-        """Forget the cached positions (the allocation is kept for reuse)."""
+        """Forget the cached positions (the pages are kept for reuse)."""
         self._seq_len = 0
         for c in (self._keys, self._values):
             if c is not None:

@@ -18,7 +18,7 @@ import torch
 
 from . import _lib
 from .lloyd_max import padded_codebook_torch, stacked_codebooks_torch
-from .types import PQCache, vector_bytes
+from .types import PagedPQCache, PQCache, vector_bytes
 
 
 def quantize_rotated(x_rot: torch.Tensor, codebook: torch.Tensor, n_bits: int = 4):
@@ -73,6 +73,8 @@ def compress_pq(kv: torch.Tensor, rotation_matrix: torch.Tensor, n_bits=4, cache
     if kv.dim() != 4:
         raise ValueError("kv must be [B, H, T, d]")
     B, H, T, d = kv.shape
+    if isinstance(cache, PagedPQCache):
+        return _compress_paged(kv, rotation_matrix, cache, start, jl_rot)
     if cache is None:
         cache = allocate_cache(B, H, T, d, n_bits, kv.device, jl_dim=d if jl_rot is not None else 0)
         start = 0
@@ -124,6 +126,41 @@ def compress_pq(kv: torch.Tensor, rotation_matrix: torch.Tensor, n_bits=4, cache
     return cache
 
 
+def _compress_paged(kv, rotation_matrix, cache: PagedPQCache, start, jl_rot):
+    """compress_pq into a paged cache: pages are added as needed, then one
+    pqkv_encode_paged call writes positions start .. start + T - 1 of every
+    stream through the page table."""
+    B, H, T, d = kv.shape
+    start = cache.seq_len if start is None else int(start)
+    if cache.head_dim != d or cache.batch != B or cache.num_heads != H:
+        raise ValueError("cache shape does not match kv")
+    if start < 0:
+        raise ValueError(f"start {start} < 0")
+    if jl_rot is not None and cache.sign_table is None:
+        raise ValueError("cache was allocated without QJL signs")
+    if T == 0:
+        return cache
+    cache.ensure(start + T)
+    x = (kv if kv.dtype in (torch.float16, torch.float32) else kv.to(torch.float32)).contiguous()
+    R = rotation_matrix.to(torch.float32).contiguous()
+    P = None if jl_rot is None else jl_rot.to(torch.float32).contiguous()
+    _lib.check(_lib.lib().pqkv_encode_paged(
+        x.data_ptr(), _lib.dtype_code(x.dtype), T * d, R.data_ptr(), cache.codebooks.data_ptr(), cache.n_bits,
+        cache.table.data_ptr(), cache.page_tokens, cache.max_pages, start, B * H, T, d, _lib.ptr(P),
+        d if P is not None else 0, cache.sign_table.data_ptr() if P is not None else None, _lib.stream_of(x)))
+    cache.seq_len = max(cache.seq_len, start + T)
+    return cache
+
+
+def allocate_paged_cache(batch: int, num_heads: int, head_dim: int, n_bits: int = 4, device="cuda",
+                         page_tokens: int = 256, jl_dim: int = 0, codebooks=None) -> PagedPQCache:
+    """Empty paged cache (no pages yet; compress_pq adds them)."""
+    if codebooks is None:
+        codebooks = padded_codebook_torch(head_dim, n_bits, device)
+    return PagedPQCache(batch, num_heads, head_dim, n_bits, codebooks, device, page_tokens=page_tokens,
+                        jl_dim=jl_dim)
+
+
 def _validate_params(n_bits: int, group_size: int, d: int) -> None:
     """The reference's argument checks (python/polarquant_kv/quantizer.py:15-22,
     src/polarquant_kv_cuda/compress_kernel.py:13-20), same messages' meaning."""
@@ -164,7 +201,10 @@ def dequantize(cache: PQCache, rotation_matrix: torch.Tensor | None, out_dtype=t
     """Reconstruction r16 c[code] of the first `positions` (default seq_len)
     positions of every (batch, head), rotated back with R (pqkv_dequantize):
     [B, H, positions, d] of out_dtype. rotation_matrix None leaves the
-    rotated-space reconstruction (R = I, exact)."""
+    rotated-space reconstruction (R = I, exact). A paged cache is gathered
+    into one array first."""
+    if isinstance(cache, PagedPQCache):
+        cache = cache.to_contiguous(positions)
     S = cache.seq_len if positions is None else int(positions)
     B, H, d = cache.batch, cache.num_heads, cache.head_dim
     dev = cache.blocks.device

@@ -150,3 +150,58 @@ def test_zero_sized_calls_are_no_ops():
     assert L.pqkv_quantize_rotated(None, None, 4, None, None, 0, 64, None) == 0
     assert L.pqkv_encode(None, 0, 0, None, None, 4, None, 0, 0, 5, 128, None, 0, None, 0, None) == 0
     assert L.pqkv_soa_to_blocks(None, None, None, 0, 128, None) == 0
+
+
+def test_paged_validation():
+    """The paged entry points check the page size, the table width and the
+    widths in host code (fake pointers never reach a launch)."""
+    L = _lib.lib()
+    # pqkv_encode_paged(x, dt, xs, R, cb, bits, pages, P, max_pages, start, streams, tokens, d, p, m, qjl, stream)
+    def enc(**k):
+        a = dict(x=FAKE, dt=1, xs=1280, R=FAKE, cb=FAKE, bits=4, pages=FAKE, P=64, mp=4, start=0, ns=2, nt=10,
+                 d=128, p=None, m=0, qjl=None)
+        a.update(k)
+        return L.pqkv_encode_paged(a["x"], a["dt"], a["xs"], a["R"], a["cb"], a["bits"], a["pages"], a["P"],
+                                   a["mp"], a["start"], a["ns"], a["nt"], a["d"], a["p"], a["m"], a["qjl"], None)
+    _status(enc(P=48), _lib.ERR_INVALID)                       # not a power of two
+    _status(enc(P=32), _lib.ERR_INVALID)                       # below one 64-token chunk
+    _status(enc(P=1 << 17), _lib.ERR_INVALID)
+    _status(enc(mp=0), _lib.ERR_INVALID)
+    _status(enc(start=250, mp=4), _lib.ERR_INVALID)            # 260 positions need 5 pages of 64
+    _status(enc(start=-1), _lib.ERR_INVALID)
+    _status(enc(bits=3), _lib.ERR_UNSUPPORTED)
+    _status(enc(xs=100), _lib.ERR_INVALID)                     # rows overlap
+    _status(enc(p=FAKE, m=128), _lib.ERR_INVALID)              # projection without sign pages
+    assert enc(nt=0, start=0) == 0                             # nothing to write
+
+    def dec(**k):
+        a = dict(q=FAKE, qt=1, R=FAKE, kp=FAKE, vp=FAKE, P=64, mp=4, kcb=FAKE, vcb=FAKE, bits=4, qjl=None, p=None,
+                 m=0, B=1, Hq=8, Hkv=2, S=200, d=128, scale=0.088, out=FAKE, ot=1, ws=FAKE, wsb=1 << 20)
+        a.update(k)
+        return L.pqkv_decode_attn_paged(a["q"], a["qt"], a["R"], a["kp"], a["vp"], a["P"], a["mp"], a["kcb"],
+                                        a["vcb"], a["bits"], a["qjl"], a["p"], a["m"], a["B"], a["Hq"], a["Hkv"],
+                                        a["S"], a["d"], a["scale"], a["out"], a["ot"], a["ws"], a["wsb"], None)
+    _status(dec(P=100), _lib.ERR_INVALID)
+    _status(dec(S=300), _lib.ERR_INVALID)                      # 300 positions need 5 pages of 64
+    _status(dec(bits=3), _lib.ERR_UNSUPPORTED)
+    _status(dec(qjl=FAKE), _lib.ERR_INVALID)                   # sign pages without projection
+    _status(dec(kp=None), _lib.ERR_INVALID)
+    _status(dec(wsb=16), _lib.ERR_WORKSPACE)
+    _status(dec(Hq=6, Hkv=4), _lib.ERR_INVALID)
+
+    def pre(**k):
+        a = dict(q=FAKE, qt=1, R=FAKE, kp=FAKE, vp=FAKE, P=64, mp=4, kcb=FAKE, vcb=FAKE, bits=4, qjl=None, p=None,
+                 m=0, B=1, Hq=8, Hkv=2, Sq=16, q0=184, S=200, d=128, scale=0.088, causal=1, out=FAKE, ot=1,
+                 ws=FAKE, wsb=1 << 24)
+        a.update(k)
+        return L.pqkv_prefill_attn_paged(a["q"], a["qt"], a["R"], a["kp"], a["vp"], a["P"], a["mp"], a["kcb"],
+                                         a["vcb"], a["bits"], a["qjl"], a["p"], a["m"], a["B"], a["Hq"], a["Hkv"],
+                                         a["Sq"], a["q0"], a["S"], a["d"], a["scale"], a["causal"], a["out"],
+                                         a["ot"], a["ws"], a["wsb"], None)
+    _status(pre(P=96), _lib.ERR_INVALID)
+    _status(pre(S=257, q0=241), _lib.ERR_INVALID)              # table too narrow
+    _status(pre(q0=190), _lib.ERR_INVALID)                     # causal queries past the cache
+    _status(pre(bits=3), _lib.ERR_UNSUPPORTED)
+    _status(pre(vp=None), _lib.ERR_INVALID)
+    _status(pre(wsb=1024), _lib.ERR_WORKSPACE)
+    assert pre(Sq=0) == 0

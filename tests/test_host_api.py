@@ -197,3 +197,39 @@ def test_inference_config_validation():
     assert m.seq_len == 0 and m.memory_bytes == 0 and m.compression_ratio == 0.0
     with pytest.raises(ValueError):
         m.append(torch.zeros(1, 3, 4, 64), torch.zeros(1, 3, 4, 64))   # wrong head count
+
+
+def test_paged_cache_tables_on_the_host():
+    """PagedPQCache bookkeeping (no kernel): page groups are added as
+    positions need them, table entry (stream, p) is page p's address for
+    that stream, widening the table keeps the entries, and adopt() checks
+    caller-managed tables."""
+    import torch
+    from polarquant_kv.types import PagedPQCache, vector_bytes
+    cb = torch.zeros(16)
+    c = PagedPQCache(2, 3, 64, 4, cb, "cpu", page_tokens=64, jl_dim=64, max_pages=2)
+    assert c.capacity == 0 and c.qjl_signs is not None
+    c.ensure(1)
+    c.ensure(64)
+    assert len(c.groups) == 1
+    c.ensure(65)
+    c.ensure(200)                                   # 4 pages: the table widens from 2 to 4
+    assert len(c.groups) == 4 and c.max_pages == 4 and c.capacity == 256
+    vb = vector_bytes(64, 4)
+    for p, g in enumerate(c.groups):
+        assert tuple(g.shape) == (2, 3, 64, vb)
+        want = torch.tensor([g.data_ptr() + s * 64 * vb for s in range(6)])
+        assert torch.equal(c.table[:, p], want)
+        assert torch.equal(c.sign_table[:, p], torch.tensor([c.sign_groups[p].data_ptr() + s * 64 * 8
+                                                             for s in range(6)]))
+    with pytest.raises(ValueError):
+        PagedPQCache(1, 1, 64, 4, cb, "cpu", page_tokens=96)
+    a = PagedPQCache(1, 2, 64, 4, cb, "cpu", page_tokens=64)
+    with pytest.raises(ValueError):
+        a.adopt(torch.zeros(3, 4, dtype=torch.int64), 256, [])          # wrong stream count
+    with pytest.raises(ValueError):
+        a.adopt(torch.zeros(2, 4, dtype=torch.int64), 300, [])          # more than the table holds
+    a.adopt(torch.zeros(2, 4, dtype=torch.int64), 256, [])
+    assert a.capacity == 256
+    with pytest.raises(ValueError):
+        a.ensure(257)
