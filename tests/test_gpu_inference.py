@@ -161,6 +161,13 @@ def test_hf_fused_attention_on_a_tiny_llama():
         assert (step - step_r).abs().max() < 1e-3 * step_r.abs().max()
         nxt = step[:, -1:].argmax(-1)
     assert cache.get_seq_length() == 44
+    # generate() drives the same path (its masks are None for an unpadded batch)
+    gen = model.generate(ids, past_key_values=hf_integration.create_compressed_cache(model), max_new_tokens=6,
+                         do_sample=False)
+    model.set_attn_implementation("sdpa")
+    gen_r = model.generate(ids, past_key_values=hf_integration.CompressedDynamicCache(n_bits=4), max_new_tokens=6,
+                           do_sample=False)
+    assert torch.equal(gen, gen_r)
 
 
 @torch.no_grad()
