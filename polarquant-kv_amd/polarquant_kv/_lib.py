@@ -11,7 +11,9 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "_lib", "libpqkv_hip.so")
+# PQKV_LIBRARY selects another build of the library (same ABI), e.g. one
+# compiled with different kernel options
+LIB_PATH = os.environ.get("PQKV_LIBRARY") or os.path.join(_HERE, "_lib", "libpqkv_hip.so")
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_HIP = 0, -1, -2, -3, -4
 F32, F16, BF16 = 0, 1, 2
