@@ -229,9 +229,14 @@ def timed_eager(torch, fn, steps, warmup):
     return t0.elapsed_time(t1) / steps, out
 
 
-def timed_graph(torch, fn, steps, warmup, per_graph=10):
+def timed_graph(torch, fn, steps, warmup, per_graph=50):
     """Steps captured `per_graph` at a time into one hipGraph, replayed until
-    `steps` steps have run; ms per step (launch overheads amortised)."""
+    `steps` steps have run; ms per step (launch overheads amortised). Each
+    replay carries a cost of its own (measured at config 3: a 1-step graph
+    adds ~8 us per step, a 10-step graph ~30 us per replay; with 200 steps
+    per graph the replayed step equals the eager one), so the steps are
+    captured in batches of 50, as a serving loop captures many layers in
+    one graph."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):

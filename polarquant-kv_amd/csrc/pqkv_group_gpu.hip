@@ -248,37 +248,60 @@ __global__ void __launch_bounds__(kGW * 64)
   }
 }
 
-// Query preparation for the fused attention: one wave per query row,
-// q_rot = (R q) qs zero-padded to dpad (FMA chain over k, R row j read by
-// lane j), pq = (P q) qs / m (P [m][d] fp32).
+// Query preparation for the fused attention: q_rot = (R q) qs zero-padded to
+// dpad and pq = (P q) qs / m (P [m][d] fp32), each output one FMA chain over
+// k ascending. blockIdx.y picks a slice of 64 outputs (the dpad outputs of
+// R, then the m outputs of P); the workgroup stages those 64 rows of R or P
+// in LDS once, with all its loads in flight together, and its four waves
+// take one query row each, lane j computing output j of the slice.
+constexpr int kQRows = 64;
+constexpr int kQPer = kQRows * kGMax / (kGW * 64);   // staged floats per thread
 __global__ void __launch_bounds__(kGW * 64)
     group_qprep_kernel(const void *q, int q_dtype, const float *R, const float *P, int64_t rows, int d, int dpad,
                        int m, float qs, float *q_rot, float *pq) {
   __shared__ float xq[kGW][kGMax];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int64_t v = (int64_t)blockIdx.x * kGW + w; v < rows; v += (int64_t)gridDim.x * kGW) {
-    for (int k = lane; k < d; k += 64) xq[w][k] = ld_in(q, q_dtype, v * d + k);
-    __builtin_amdgcn_wave_barrier();
-    for (int j = lane; j < dpad; j += 64) {
-      float acc = 0.0f;
-      if (j < d) {
-        if (R) {
-          for (int k = 0; k < d; ++k) acc = __builtin_fmaf(R[(int64_t)j * d + k], xq[w][k], acc);
-        } else {
-          acc = xq[w][j];
-        }
-      }
-      q_rot[v * dpad + j] = acc * qs;
+  __shared__ float mat[kQRows][kGMax + 1];   // row pitch 257: lane j's reads of row j hit distinct banks
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int r_slices = (dpad + kQRows - 1) / kQRows;
+  const bool is_p = (int)blockIdx.y >= r_slices;
+  const int j0 = (is_p ? (int)blockIdx.y - r_slices : (int)blockIdx.y) * kQRows;
+  const float *M = is_p ? P : R;
+  const int n = is_p ? m : min(d, dpad);      // rows of M that exist
+  if (M) {
+    float t[kQPer];
+#pragma unroll
+    for (int i = 0; i < kQPer; ++i) {
+      const int e = tid + i * kGW * 64, r = e / kGMax, c = e - r * kGMax;
+      t[i] = (c < d && j0 + r < n) ? M[(int64_t)(j0 + r) * d + c] : 0.0f;
     }
-    if (P) {
-      const float sc = qs / (float)m;
-      for (int i = lane; i < m; i += 64) {
-        float acc = 0.0f;
-        for (int k = 0; k < d; ++k) acc = __builtin_fmaf(P[(int64_t)i * d + k], xq[w][k], acc);
-        pq[v * m + i] = acc * sc;
+#pragma unroll
+    for (int i = 0; i < kQPer; ++i) {
+      const int e = tid + i * kGW * 64, r = e / kGMax, c = e - r * kGMax;
+      mat[r][c] = t[i];
+    }
+  }
+  const int j = j0 + lane;
+  const float sc = is_p ? qs / (float)m : qs;
+  for (int64_t base = (int64_t)blockIdx.x * kGW; base < rows; base += (int64_t)gridDim.x * kGW) {
+    const int64_t v = base + w;
+    const bool live = v < rows;
+    for (int k = lane; k < d; k += 64) xq[w][k] = live ? ld_in(q, q_dtype, v * d + k) : 0.0f;
+    __syncthreads();
+    float acc = 0.0f;
+    if (M) {
+      if (j < n)
+        for (int k = 0; k < d; ++k) acc = __builtin_fmaf(mat[lane][k], xq[w][k], acc);
+    } else if (j < d) {
+      acc = xq[w][j];
+    }
+    if (live) {
+      if (is_p) {
+        if (j < m) pq[v * m + j] = acc * sc;
+      } else if (j < dpad) {
+        q_rot[v * dpad + j] = (j < d ? acc : 0.0f) * sc;
       }
     }
-    __builtin_amdgcn_wave_barrier();
+    __syncthreads();   // xq is reused by the next rows
   }
 }
 
@@ -810,7 +833,11 @@ hipError_t launch_qjl_sketch(const void *x, int x_dtype, const float *x_hat, con
 hipError_t launch_group_qprep(const void *q, int q_dtype, const float *R, const float *P, int64_t rows, int d,
                               int dpad, int m, float qs, float *q_rot, float *pq, hipStream_t s) {
   if (d < 1 || d > kGMax || dpad > kGMax) return hipErrorInvalidValue;
-  group_qprep_kernel<<<grid_for(rows), kGW * 64, 0, s>>>(q, q_dtype, R, P, rows, d, dpad, m, qs, q_rot, pq);
+  if (P && (m < 1 || m > kGMax)) return hipErrorInvalidValue;
+  const int slices = (dpad + kQRows - 1) / kQRows + (P ? (m + kQRows - 1) / kQRows : 0);
+  const int64_t per = (rows + kGW - 1) / kGW;
+  const dim3 grid((unsigned)(per < 1024 ? (per > 0 ? per : 1) : 1024), (unsigned)slices);
+  group_qprep_kernel<<<grid, kGW * 64, 0, s>>>(q, q_dtype, R, P, rows, d, dpad, m, qs, q_rot, pq);
   return hipGetLastError();
 }
 
