@@ -349,18 +349,58 @@ hipError_t launch_rotate2(const void *x, int x_dtype, const float *R, const floa
 }
 
 // ---------------------------------------------------------------------------
-// Exact fused encoder: the rotation above (bit-identical FMA chain) followed by
-// the per-wave quantiser, plus the optional QJL sign sketch. 256 threads, NV
-// vectors per iteration.
+// Exact fused encoders: the rotation above (bit-identical FMA chain) followed
+// by the per-wave quantiser. 256 threads; a tile is EV = kExactChains *
+// (256 / D) vectors. Thread (j, g) = (tid % D, tid / D) keeps row j of R in
+// registers and runs kExactChains independent chains, for vectors g,
+// g + 256 / D, ... of the tile, each over k ascending: the arithmetic of one
+// chain per vector, with several chains' latencies overlapped in a thread.
+// Each wave then quantises EV / 4 of the tile's vectors. The next tile's
+// inputs are loaded into registers while this one is rotated.
 // ---------------------------------------------------------------------------
+constexpr int kExactChains = 4;
+
+template <int D>
+struct ExactTile {
+  static constexpr int TG = 256 / D;              // threads per output coordinate
+  static constexpr int EV = TG * kExactChains;    // vectors per tile
+  static constexpr int QW = EV / 4;               // vectors each wave quantises
+};
+
+// The tile's rotation: ys[t][j] = FMA chain over k of xs[t][k] R[j][k] for
+// t = g + TG i.
+template <int D>
+__device__ __forceinline__ void rotate_tile(const float (*xs)[D], float (*ys)[D + 1], const float (&rr)[D], int j,
+                                            int g) {
+  constexpr int TG = ExactTile<D>::TG;
+  float acc[kExactChains];
+#pragma unroll
+  for (int i = 0; i < kExactChains; ++i) acc[i] = 0.0f;
+#pragma unroll
+  for (int k4 = 0; k4 < D / 4; ++k4) {
+#pragma unroll
+    for (int i = 0; i < kExactChains; ++i) {
+      const float4 x4 = *(const float4 *)&xs[g + TG * i][4 * k4];
+      acc[i] = __builtin_fmaf(x4.x, rr[4 * k4], acc[i]);
+      acc[i] = __builtin_fmaf(x4.y, rr[4 * k4 + 1], acc[i]);
+      acc[i] = __builtin_fmaf(x4.z, rr[4 * k4 + 2], acc[i]);
+      acc[i] = __builtin_fmaf(x4.w, rr[4 * k4 + 3], acc[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kExactChains; ++i) ys[g + TG * i][j] = acc[i];
+}
+
+// block_pq4 / block_pq2 output (strided, paged), fp32 or fp16 input, plus
+// the optional QJL sign sketch.
 template <int D, int BITS, typename TIN>
 __global__ void __launch_bounds__(256) encode_exact_kernel(EncodeArgs a) {
-  constexpr int NV = 256 / D;
+  constexpr int TG = ExactTile<D>::TG, EV = ExactTile<D>::EV, QW = ExactTile<D>::QW;
   constexpr int VB = vector_bytes(D, BITS);
-  __shared__ float xs[NV][D];
-  __shared__ float ys[NV][D + 1];
-  __shared__ float rs[NV];
-  __shared__ uint32_t cs[NV][64];
+  __shared__ __align__(16) float xs[EV][D];
+  __shared__ float ys[EV][D + 1];
+  __shared__ float rs[EV];
+  __shared__ uint32_t cs[EV][64];
   __shared__ float cb[16];
   const int tid = threadIdx.x;
   const int j = tid % D, g = tid / D;
@@ -370,60 +410,77 @@ __global__ void __launch_bounds__(256) encode_exact_kernel(EncodeArgs a) {
   load_r_row<D, false>(a.R, j, rr);
   const TIN *x = (const TIN *)a.x;
   const int64_t n = a.n_outer * a.n_inner;
-  for (int64_t base = (int64_t)blockIdx.x * NV; base < n; base += (int64_t)gridDim.x * NV) {
-    const int64_t v = base + g;
-    int64_t vo = 0, vi = 0;
-    if (v < n) {
-      vo = v / a.n_inner;
-      vi = v - vo * a.n_inner;
-      xs[g][j] = load_as_float(x + vo * a.x_outer_stride + vi * D + j);
-    }
-    __syncthreads();
-    if (v < n) {
-      float acc = 0.0f;
+  const int64_t stride = (int64_t)gridDim.x * EV;
+  const bool qjl = a.qjl != nullptr || a.qjl_pages != nullptr;
+  float xv[kExactChains];
+  auto load_x = [&](int64_t base) {
 #pragma unroll
-      for (int k = 0; k < D; ++k) acc = __builtin_fmaf(xs[g][k], rr[k], acc);
-      ys[g][j] = acc;
+    for (int i = 0; i < kExactChains; ++i) {
+      const int64_t v = base + g + TG * i;
+      float t = 0.0f;
+      if (v < n) {
+        const int64_t vo = v / a.n_inner, vi = v - vo * a.n_inner;
+        t = load_as_float(x + vo * a.x_outer_stride + vi * D + j);
+      }
+      xv[i] = t;
     }
+  };
+  load_x((int64_t)blockIdx.x * EV);
+  for (int64_t base = (int64_t)blockIdx.x * EV; base < n; base += stride) {
+#pragma unroll
+    for (int i = 0; i < kExactChains; ++i) xs[g + TG * i][j] = xv[i];
     __syncthreads();
-    // Quantise: wave w < NV handles vector base + w.
-    if (wave < NV) {
-      const int64_t qv = base + wave;
+    if (base + stride < n) load_x(base + stride);
+    rotate_tile<D>(xs, ys, rr, j, g);
+    __syncthreads();
+    // Quantise: wave w handles vectors QW w .. QW w + QW - 1 of the tile.
+#pragma unroll
+    for (int q = 0; q < QW; ++q) {
+      const int t = QW * wave + q;
+      const int64_t qv = base + t;
       if (qv < n) {
         const int64_t qo = qv / a.n_inner, qi = qv - qo * a.n_inner;
-        const float x0 = ys[wave][lane];
-        const float x1 = D == 128 ? ys[wave][lane + 64] : 0.0f;
+        const float x0 = ys[t][lane];
+        const float x1 = D == 128 ? ys[t][lane + 64] : 0.0f;
         float r;
         uint32_t codes;
         quantize_store_wave<D, BITS>(x0, x1, cb, encode_out_addr(a, a.blocks, a.pages, a.blocks_outer_stride, qo, qi, VB),
                                      nullptr, &r, &codes);
-        cs[wave][lane] = codes;
-        if (lane == 0) rs[wave] = r;
+        cs[t][lane] = codes;
+        if (lane == 0) rs[t] = r;
       }
     }
-    if (a.qjl != nullptr || a.qjl_pages != nullptr) {
+    if (qjl) {
       __syncthreads();
       // Residual e = y - r * c[code] in LDS (overwrites xs), then sign of
       // p_rot[i] . e for i = j (m = D projections, one per thread).
-      if (v < n) {
-        const uint32_t cw = cs[g][j & 63];
-        const int code = D == 128 ? ((j < 64) ? (cw & 15) : (cw >> 4)) : (cw & 15);
-        xs[g][j] = ys[g][j] - rs[g] * cb[code];
+#pragma unroll
+      for (int i = 0; i < kExactChains; ++i) {
+        const int t = g + TG * i;
+        if (base + t < n) {
+          const uint32_t cw = cs[t][j & 63];
+          const int code = D == 128 ? ((j < 64) ? (cw & 15) : (cw >> 4)) : (cw & 15);
+          xs[t][j] = ys[t][j] - rs[t] * cb[code];
+        }
       }
       __syncthreads();
-      float proj = 0.0f;
-      if (v < n) {
+      float proj[kExactChains];
+#pragma unroll
+      for (int i = 0; i < kExactChains; ++i) proj[i] = 0.0f;
 #pragma unroll 8
-        for (int k = 0; k < D; ++k) proj = __builtin_fmaf(a.p_rot[j * D + k], xs[g][k], proj);
+      for (int k = 0; k < D; ++k) {
+        const float pk = a.p_rot[j * D + k];
+#pragma unroll
+        for (int i = 0; i < kExactChains; ++i) proj[i] = __builtin_fmaf(pk, xs[g + TG * i][k], proj[i]);
       }
-      const uint64_t bits = __ballot(proj >= 0.0f);
-      if (v < n && lane == 0) {
-        const int64_t qo = v / a.n_inner, qi = v - qo * a.n_inner;
-        uint8_t *dst = encode_out_addr(a, a.qjl, a.qjl_pages, a.qjl_outer_stride, qo, qi, D / 8) + (j / 64) * 8;
-        if (D == 64) {
-          *(uint64_t *)dst = bits;
-        } else {
-          *(uint64_t *)dst = bits;
+#pragma unroll
+      for (int i = 0; i < kExactChains; ++i) {
+        const int64_t v = base + g + TG * i;
+        const uint64_t bits = __ballot(proj[i] >= 0.0f);
+        if (v < n && lane == 0) {
+          const int64_t qo = v / a.n_inner, qi = v - qo * a.n_inner;
+          *(uint64_t *)(encode_out_addr(a, a.qjl, a.qjl_pages, a.qjl_outer_stride, qo, qi, D / 8) + (j / 64) * 8) =
+              bits;
         }
       }
     }
@@ -431,19 +488,17 @@ __global__ void __launch_bounds__(256) encode_exact_kernel(EncodeArgs a) {
   }
 }
 
-// ---------------------------------------------------------------------------
 // Reference-format encoder (fp32 input, SoA output, any level count <= 16):
 // the exact rotation and quantiser above, written as packed nibbles plus fp32
 // radius, i.e. the output of turboquant_compress_kernel.
-// ---------------------------------------------------------------------------
 template <int D>
 __global__ void __launch_bounds__(256) encode_soa_kernel(const float *__restrict__ x, const float *__restrict__ R,
                                                          const float *__restrict__ codebook, int nl,
                                                          float *__restrict__ radius_out,
                                                          uint8_t *__restrict__ packed_out, int64_t n) {
-  constexpr int NV = 256 / D;
-  __shared__ float xs[NV][D];
-  __shared__ float ys[NV][D + 1];
+  constexpr int TG = ExactTile<D>::TG, EV = ExactTile<D>::EV, QW = ExactTile<D>::QW;
+  __shared__ __align__(16) float xs[EV][D];
+  __shared__ float ys[EV][D + 1];
   __shared__ float cb[16];
   const int tid = threadIdx.x;
   const int j = tid % D, g = tid / D;
@@ -451,22 +506,32 @@ __global__ void __launch_bounds__(256) encode_soa_kernel(const float *__restrict
   if (tid < 16) cb[tid] = tid < nl ? codebook[tid] : 0.0f;
   float rr[D];
   load_r_row<D, false>(R, j, rr);
-  for (int64_t base = (int64_t)blockIdx.x * NV; base < n; base += (int64_t)gridDim.x * NV) {
-    const int64_t v = base + g;
-    if (v < n) xs[g][j] = x[v * D + j];
-    __syncthreads();
-    if (v < n) {
-      float acc = 0.0f;
+  const int64_t stride = (int64_t)gridDim.x * EV;
+  float xv[kExactChains];
+  auto load_x = [&](int64_t base) {
 #pragma unroll
-      for (int k = 0; k < D; ++k) acc = __builtin_fmaf(xs[g][k], rr[k], acc);
-      ys[g][j] = acc;
+    for (int i = 0; i < kExactChains; ++i) {
+      const int64_t v = base + g + TG * i;
+      xv[i] = v < n ? x[v * D + j] : 0.0f;
     }
+  };
+  load_x((int64_t)blockIdx.x * EV);
+  for (int64_t base = (int64_t)blockIdx.x * EV; base < n; base += stride) {
+#pragma unroll
+    for (int i = 0; i < kExactChains; ++i) xs[g + TG * i][j] = xv[i];
     __syncthreads();
-    if (wave < NV && base + wave < n) {
-      const int64_t qv = base + wave;
-      int b0, b1;
-      const float r = quantize_wave<D>(ys[wave][lane], D == 128 ? ys[wave][lane + 64] : 0.0f, cb, nl, &b0, &b1);
-      store_soa_wave<D>(b0, b1, r, packed_out + qv * (D / 2), radius_out + qv);
+    if (base + stride < n) load_x(base + stride);
+    rotate_tile<D>(xs, ys, rr, j, g);
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < QW; ++q) {
+      const int t = QW * wave + q;
+      const int64_t qv = base + t;
+      if (qv < n) {
+        int b0, b1;
+        const float r = quantize_wave<D>(ys[t][lane], D == 128 ? ys[t][lane + 64] : 0.0f, cb, nl, &b0, &b1);
+        store_soa_wave<D>(b0, b1, r, packed_out + qv * (D / 2), radius_out + qv);
+      }
     }
     __syncthreads();
   }
@@ -597,9 +662,16 @@ hipError_t launch_rotate(const void *x, int x_dtype, const float *R, void *y, in
   return hipGetLastError();
 }
 
+// The exact encoders keep a row of R in each thread's registers, loaded once
+// per workgroup: one resident round of workgroups loops over the tiles (two
+// per CU at d = 128, whose kernels take 2 waves per SIMD; three at d = 64).
+static int exact_grid(int64_t n, int d) {
+  return grid_for(n, kExactChains * (256 / d), (d == 128 ? 2 : 3) * device_compute_units());
+}
+
 hipError_t launch_encode_exact(const EncodeArgs &a, int x_dtype, hipStream_t s) {
   const int64_t n = a.n_outer * a.n_inner;
-  const int grid = grid_for(n, 256 / a.d, 4096);
+  const int grid = exact_grid(n, a.d);
 #define PQKV_EE(DD, BB)                                                            \
   do {                                                                             \
     if (x_dtype == 0) encode_exact_kernel<DD, BB, float><<<grid, 256, 0, s>>>(a);  \
@@ -615,7 +687,7 @@ hipError_t launch_encode_exact(const EncodeArgs &a, int x_dtype, hipStream_t s) 
 
 hipError_t launch_encode_soa(const float *x, const float *R, const float *codebook, int n_levels, float *radius,
                              uint8_t *packed, int64_t n, int d, hipStream_t s) {
-  const int grid = grid_for(n, 256 / d, 4096);
+  const int grid = exact_grid(n, d);
   if (d == 128) encode_soa_kernel<128><<<grid, 256, 0, s>>>(x, R, codebook, n_levels, radius, packed, n);
   else encode_soa_kernel<64><<<grid, 256, 0, s>>>(x, R, codebook, n_levels, radius, packed, n);
   return hipGetLastError();
