@@ -15,15 +15,18 @@ the timed region. R and P come from the package's own generators
 (polarquant_kv.rotation / qjl).
 
 value = algorithmic bytes per step (compressed K+V read once, query read,
-output written) / step time, K eager steps bracketed by events.
+output written) / step time: the faster of K eager steps bracketed by events
+and hipGraph replays of captured step batches (the line's `timing` names it).
 
 roofline: the split-K decode kernel's algorithmic bytes per launch (302 120 960
 at config 3) over its mean duration. Two durations are reported:
-  kernel_ms          the rocprofv3 kernel-trace mean of the committed summary
-                     (profiles/decode_mfma_config3_kernel_stats.md, the same
-                     command on the same build) -- achieved / frac use it;
-  kernel_ms_events   the library's hipEvents around each launch, live in this
-                     run (they also count the launch's dispatch latency).
+  kernel_ms          live in this run: the library's hipEvents on the launch
+                     stream around 20 back-to-back launches of the kernel
+                     (idempotent), mean per launch -- achieved / frac use it;
+  kernel_us_rocprof_committed
+                     the rocprofv3 kernel-trace mean of the committed summary
+                     (profiles/decode_mfma_config3_kernel_stats.md), a
+                     cross-check from an earlier run of the same command.
 roofline.traffic: HBM bytes per launch from the committed counter summary
 (profiles/decode_mfma_config3_hbm_traffic.md: FETCH_SIZE and WRITE_SIZE, each
 scaled by the counter's reading on a plain 1 GiB copy, which --calibrate adds
@@ -249,7 +252,8 @@ def timed_graph(torch, fn, steps, warmup, per_graph=50):
         for _ in range(per_graph):
             out = fn()
     reps = max(1, steps // per_graph)
-    g.replay()
+    for _ in range(3):   # the first replays of a new graph run slower
+        g.replay()
     torch.cuda.synchronize()
     t0, t1 = _events(torch)
     t0.record()
@@ -265,7 +269,7 @@ def best_timing(graph_ms, eager_ms, what=""):
     replayed, or eager launches; both are ways a caller runs the step), with
     a label naming it and where the other one is reported."""
     if graph_ms <= eager_ms:
-        return graph_ms, f"hipGraph replays of 10 captured steps{what}; eager step in eager_ms_per_step"
+        return graph_ms, f"hipGraph replays of captured step batches{what}; eager step in eager_ms_per_step"
     return eager_ms, f"eager launches{what}; hipGraph replays in graph_ms_per_step"
 
 
