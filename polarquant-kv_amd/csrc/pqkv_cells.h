@@ -1,0 +1,179 @@
+// Nearest-centroid lookup table shared by the encoders.
+//
+// The reference quantiser (csrc/flash_turboquant.cu:162-170) scans
+// |dir - c_i| over the codebook and keeps the first minimum. For a strictly
+// increasing codebook that index is a step function of dir: it equals the
+// number of switch points theta_i <= dir, where theta_i is the smallest fp32
+// value the scan maps to i + 1. build_cell_table() finds the switch points by
+// bisection over fp32 values with the scan itself, then fills a table over
+// 1027 direction cells holding (index at the cell start, the switch point
+// inside the cell or +inf): one LDS read and one compare per coordinate. The
+// cell of dir is round(512 dir) + 513, read from the low bits of
+// fma(dir, 512, 1.5 * 2^23), monotone in dir; the table is built with the same
+// function. A codebook that is not strictly increasing, with a switch point
+// outside (-1, 1), two switch points in one cell or one below 2^-60 in
+// magnitude clears the table's flag, and its callers then use the scan.
+//
+// table_code() takes a direction from the same division the reference makes
+// or, for a radius in the range where it is exact, from the Markstein
+// quotient q0 + fma(-r, q0, y) / r with one correctly rounded reciprocal per
+// vector (dir_markstein()).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pqkv {
+
+constexpr int kECells = 1024;           // direction cells over [-1, 1], 1/512 wide
+constexpr int kECellSlots = kECells + 3;
+constexpr int kECellOff = 513;          // cell of dir = round(512 dir) + 513
+constexpr float kEMagic = 12582912.0f;  // 1.5 * 2^23: ulp 1, so fma(d, 512, kEMagic) holds round(512 d) in its low bits
+constexpr float kEClamp = 1.001f;       // |dir| of the table path stays below; beyond, no switch point lies
+
+// The reference quantiser: first i minimising |d - c_i| (strict '<').
+__device__ __forceinline__ int scan_index(float d, const float *cb, int nl) {
+#pragma clang fp contract(off)
+  int b = 0;
+  float m = 1e30f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if (i < nl) {
+      const float e = fabsf(d - cb[i]);
+      if (e < m) {
+        m = e;
+        b = i;
+      }
+    }
+  }
+  return b;
+}
+
+// The same scan as a rolled loop over the LDS codebook: the fallback path's
+// form, which keeps the codebook out of registers.
+__device__ __forceinline__ int scan_index_rolled(float d, const float *cb, int nl) {
+#pragma clang fp contract(off)
+  int b = 0;
+  float m = 1e30f;
+#pragma nounroll
+  for (int i = 0; i < nl; ++i) {
+    const float e = fabsf(d - cb[i]);
+    if (e < m) {
+      m = e;
+      b = i;
+    }
+  }
+  return b;
+}
+
+// Direction cell, monotone in d: round(512 d) + 513, for |d| <= kEClamp in
+// 0 .. kECellSlots - 1.
+__device__ __forceinline__ uint32_t cell_bits(float d) {
+  return __builtin_bit_cast(uint32_t, __builtin_fmaf(d, 512.0f, kEMagic));
+}
+__device__ __forceinline__ int dir_cell(float d) {
+  return (int)(cell_bits(d) - __builtin_bit_cast(uint32_t, kEMagic)) + kECellOff;
+}
+
+// Order-preserving map between fp32 values and integers.
+__device__ __forceinline__ int64_t fkey(float f) {
+  const int32_t i = __builtin_bit_cast(int32_t, f);
+  return i >= 0 ? (int64_t)i : -(int64_t)(i & 0x7FFFFFFF);
+}
+__device__ __forceinline__ float kfloat(int64_t k) {
+  return k >= 0 ? __builtin_bit_cast(float, (int32_t)k) : __builtin_bit_cast(float, (int32_t)(0x80000000u | (uint32_t)(-k)));
+}
+
+// Builds the table for the nl-level codebook cb[0..15] (in LDS, written and
+// made visible before the call) with a 256-thread workgroup; all threads
+// call it. On return (after a barrier) *table_ok says whether cells[] holds
+// the table; thr[] and ucell[] are 16-entry LDS work arrays.
+__device__ __forceinline__ void build_cell_table(const float *cb, int nl, int tid, uint2 *cells, float *thr,
+                                                 int *ucell, int *table_ok) {
+  if (tid == 0) *table_ok = 1;
+  __syncthreads();
+  // Switch points: 16 lanes per point i search (c_i, c_{i+1}] 16-ary; lane j
+  // tests the (j + 1)/16 point of the range, and the first that the scan maps
+  // to i + 1 or more closes it. Keys of fp32 values differ by < 2^33, so 9
+  // steps reach a range of one.
+  {
+    const int i = tid >> 4, j = tid & 15;
+    const bool act = i < nl - 1;
+    bool ok = act;
+    int64_t lo = 0, hi = 0;
+    if (act) {
+      ok = cb[i] < cb[i + 1] && scan_index(cb[i], cb, nl) <= i && scan_index(cb[i + 1], cb, nl) >= i + 1;
+      lo = fkey(cb[i]);
+      hi = fkey(cb[i + 1]);
+    }
+    for (int step = 0; step < 10; ++step) {
+      const int64_t span = hi - lo;
+      const int64_t cand = j == 15 ? hi : lo + ((span * (j + 1)) >> 4);
+      const bool p = ok && span > 1 && scan_index(kfloat(cand), cb, nl) >= i + 1;
+      const uint32_t gm = (uint32_t)(__builtin_amdgcn_ballot_w64(p) >> (16 * (i & 3))) & 0xFFFFu;
+      const int k = gm ? __builtin_ctz(gm) : 15;
+      if (ok && span > 1) {
+        const int64_t nhi = k == 15 ? hi : lo + ((span * (k + 1)) >> 4);
+        lo = k == 0 ? lo : lo + ((span * k) >> 4);
+        hi = nhi;
+      }
+    }
+    if (act && j == 0) {
+      if (!ok || hi - lo != 1) {
+        *table_ok = 0;
+      } else {
+        const float t = kfloat(hi);
+        thr[i] = t;
+        if (!(fabsf(t) >= 0x1p-60f) || !(fabsf(t) < 1.0f)) *table_ok = 0;
+        else ucell[i] = dir_cell(t);
+      }
+    }
+  }
+  __syncthreads();
+  if (*table_ok != 0) {
+    for (int u = tid; u < kECellSlots; u += 256) {
+      int base = 0, inside = -1, count = 0;
+      for (int i = 0; i < nl - 1; ++i) {
+        if (ucell[i] < u) ++base;
+        else if (ucell[i] == u) {
+          inside = i;
+          ++count;
+        }
+      }
+      if (count > 1) *table_ok = 0;
+      cells[u] = make_uint2((uint32_t)base, inside >= 0 ? __builtin_bit_cast(uint32_t, thr[inside]) : 0x7F800000u);
+    }
+  }
+  __syncthreads();
+}
+
+// Radii for which the Markstein quotient gives the reference's index:
+// zero-like (dir = 0, reached through inv = 0 on finite y) or finite and
+// >= 2^-40 (quotient exact wherever a switch point is within a factor of two,
+// |dir| <= 1 + 11 ulp).
+__device__ __forceinline__ bool markstein_radius(float r) {
+  return r <= 1e-30f || (r >= 0x1p-40f && r < __builtin_inff());
+}
+
+// dir = RN(y / r) for a radius markstein_radius() accepts, inv = RN(1 / r)
+// (0 for a zero-like radius).
+__device__ __forceinline__ float dir_markstein(float y, float r, float inv) {
+#pragma clang fp contract(off)
+  const float q0 = y * inv;
+  const float e = __builtin_fmaf(-r, q0, y);
+  return __builtin_fmaf(e, inv, q0);
+}
+
+// dir = RN(y / r) by division, mapped into the table's range: NaN to -2
+// (index 0, as the scan gives), then clamped to +-kEClamp.
+__device__ __forceinline__ float dir_divided(float y, float r) {
+  float d = r > 1e-30f ? __fdiv_rn(y, r) : 0.0f;
+  d = d == d ? d : -2.0f;
+  return __builtin_fminf(__builtin_fmaxf(d, -kEClamp), kEClamp);
+}
+
+__device__ __forceinline__ int table_code(const uint2 *cells, float d) {
+  const uint2 ce = cells[dir_cell(d)];
+  return (int)ce.x + (d >= __builtin_bit_cast(float, ce.y) ? 1 : 0);
+}
+
+}  // namespace pqkv

@@ -10,6 +10,7 @@
 // lane (x[t]^2 + x[t+64]^2), the remaining steps are shuffle-downs. The file
 // is compiled without FP contraction inside the quantiser so squares and adds
 // round separately, as in the reference.
+#include "pqkv_cells.h"
 #include "pqkv_device.h"
 #include "pqkv_launch.h"
 
@@ -18,10 +19,15 @@ namespace pqkv {
 // ---------------------------------------------------------------------------
 // Per-wave quantiser of one vector held as lane t -> (x0 = y[t], x1 = y[t+64])
 // for D = 128, or x0 = y[t] for D = 64. Returns the fp32 radius (all lanes)
-// and this lane's two codes; nl <= 16 levels, strict '<' scan.
+// and this lane's two codes; nl <= 16 levels, strict '<' scan. With TABLE the
+// index comes from the switch-point cell table (cells, built for cb), and the
+// direction from the Markstein quotient where the radius allows it: the same
+// indices with one division per vector instead of one per coordinate and a
+// table read instead of the scan.
 // ---------------------------------------------------------------------------
-template <int D>
-__device__ __forceinline__ float quantize_wave(float x0, float x1, const float *cb, int nl, int *c0, int *c1) {
+template <int D, bool TABLE = false>
+__device__ __forceinline__ float quantize_wave(float x0, float x1, const float *cb, int nl, int *c0, int *c1,
+                                               const uint2 *cells = nullptr) {
 #pragma clang fp contract(off)
   float v = x0 * x0;
   if (D == 128) {
@@ -34,6 +40,20 @@ __device__ __forceinline__ float quantize_wave(float x0, float x1, const float *
   // 1 ulp, so take the fp64 root (correctly rounded) and round once to fp32,
   // which gives the correctly rounded fp32 root of an fp32 argument.
   const float r = (float)__builtin_sqrt((double)__shfl(v, 0, kWave));
+  if constexpr (TABLE) {
+    float d0, d1;
+    if (markstein_radius(r)) {
+      const float inv = r > 1e-30f ? __fdiv_rn(1.0f, r) : 0.0f;
+      d0 = dir_markstein(x0, r, inv);
+      d1 = dir_markstein(x1, r, inv);
+    } else {
+      d0 = dir_divided(x0, r);
+      d1 = dir_divided(x1, r);
+    }
+    *c0 = table_code(cells, d0);
+    *c1 = D == 128 ? table_code(cells, d1) : 0;
+    return r;
+  }
   const bool nz = r > 1e-30f;
   const float d0 = nz ? __fdiv_rn(x0, r) : 0.0f;
   const float d1 = nz ? __fdiv_rn(x1, r) : 0.0f;
@@ -97,11 +117,12 @@ __device__ __forceinline__ void store_soa_wave(int b0, int b1, float r, uint8_t 
   if (lane == 0) *radius = r;
 }
 
-template <int D, int BITS>
+template <int D, int BITS, bool TABLE = false>
 __device__ __forceinline__ void quantize_store_wave(float x0, float x1, const float *cb, uint8_t *out_vec,
-                                                    float *radius_out, float *r_f32, uint32_t *codes) {
+                                                    float *radius_out, float *r_f32, uint32_t *codes,
+                                                    const uint2 *cells = nullptr) {
   int b0, b1;
-  const float r = quantize_wave<D>(x0, x1, cb, 1 << BITS, &b0, &b1);
+  const float r = quantize_wave<D, TABLE>(x0, x1, cb, 1 << BITS, &b0, &b1, cells);
   store_blocks_wave<D, BITS>(b0, b1, r, out_vec);
   *r_f32 = r;
   *codes = (uint32_t)(b0 | (b1 << 4));
@@ -401,11 +422,17 @@ __global__ void __launch_bounds__(256) encode_exact_kernel(EncodeArgs a) {
   __shared__ float ys[EV][D + 1];
   __shared__ float rs[EV];
   __shared__ uint32_t cs[EV][64];
-  __shared__ float cb[16];
+  __shared__ float cb[16], thr[16];
+  __shared__ int ucell[16];
+  __shared__ int table_ok;
+  __shared__ uint2 cells[kECellSlots];
   const int tid = threadIdx.x;
   const int j = tid % D, g = tid / D;
   const int lane = tid & 63, wave = tid >> 6;
-  if (tid < (1 << BITS)) cb[tid] = a.codebook[tid];
+  if (tid < 16) cb[tid] = tid < (1 << BITS) ? a.codebook[tid] : 0.0f;
+  __syncthreads();
+  build_cell_table(cb, 1 << BITS, tid, cells, thr, ucell, &table_ok);
+  const bool use_table = table_ok != 0;
   float rr[D];
   load_r_row<D, false>(a.R, j, rr);
   const TIN *x = (const TIN *)a.x;
@@ -444,8 +471,9 @@ __global__ void __launch_bounds__(256) encode_exact_kernel(EncodeArgs a) {
         const float x1 = D == 128 ? ys[t][lane + 64] : 0.0f;
         float r;
         uint32_t codes;
-        quantize_store_wave<D, BITS>(x0, x1, cb, encode_out_addr(a, a.blocks, a.pages, a.blocks_outer_stride, qo, qi, VB),
-                                     nullptr, &r, &codes);
+        uint8_t *out = encode_out_addr(a, a.blocks, a.pages, a.blocks_outer_stride, qo, qi, VB);
+        if (use_table) quantize_store_wave<D, BITS, true>(x0, x1, cb, out, nullptr, &r, &codes, cells);
+        else quantize_store_wave<D, BITS>(x0, x1, cb, out, nullptr, &r, &codes);
         cs[t][lane] = codes;
         if (lane == 0) rs[t] = r;
       }
@@ -499,11 +527,17 @@ __global__ void __launch_bounds__(256) encode_soa_kernel(const float *__restrict
   constexpr int TG = ExactTile<D>::TG, EV = ExactTile<D>::EV, QW = ExactTile<D>::QW;
   __shared__ __align__(16) float xs[EV][D];
   __shared__ float ys[EV][D + 1];
-  __shared__ float cb[16];
+  __shared__ float cb[16], thr[16];
+  __shared__ int ucell[16];
+  __shared__ int table_ok;
+  __shared__ uint2 cells[kECellSlots];
   const int tid = threadIdx.x;
   const int j = tid % D, g = tid / D;
   const int lane = tid & 63, wave = tid >> 6;
   if (tid < 16) cb[tid] = tid < nl ? codebook[tid] : 0.0f;
+  __syncthreads();
+  build_cell_table(cb, nl, tid, cells, thr, ucell, &table_ok);
+  const bool use_table = table_ok != 0;
   float rr[D];
   load_r_row<D, false>(R, j, rr);
   const int64_t stride = (int64_t)gridDim.x * EV;
@@ -529,7 +563,9 @@ __global__ void __launch_bounds__(256) encode_soa_kernel(const float *__restrict
       const int64_t qv = base + t;
       if (qv < n) {
         int b0, b1;
-        const float r = quantize_wave<D>(ys[t][lane], D == 128 ? ys[t][lane + 64] : 0.0f, cb, nl, &b0, &b1);
+        const float y0 = ys[t][lane], y1 = D == 128 ? ys[t][lane + 64] : 0.0f;
+        const float r = use_table ? quantize_wave<D, true>(y0, y1, cb, nl, &b0, &b1, cells)
+                                  : quantize_wave<D>(y0, y1, cb, nl, &b0, &b1);
         store_soa_wave<D>(b0, b1, r, packed_out + qv * (D / 2), radius_out + qv);
       }
     }

@@ -20,24 +20,11 @@
 // with slots 4 w + i. Those 16 partial sums per vector go through LDS, and
 // lane L of every wave finishes the steps s = 8 .. 1 of vector L.
 //
-// Nearest centroid: the reference scans |dir - c_i| and keeps the first
-// minimum. For a sorted codebook that index is a step function of dir, so it
-// equals the number of switch points theta_i <= dir, where theta_i is the
-// smallest fp32 value the scan maps to i + 1. Each workgroup finds the
-// switch points by bisection over fp32 values with the scan itself, then
-// builds a table over 1027 direction cells holding (index at the cell start,
-// the switch point inside the cell): one LDS read and one compare per
-// coordinate. The cell of dir is round(512 dir) + 513, read from the low bits
-// of fma(dir, 512, 1.5 * 2^23) (monotone in dir; the table is built with the
-// same function). A codebook that is not strictly increasing, with a switch
-// point outside (-1, 1), two switch points in one cell or one below 2^-60 in
-// magnitude falls back to the scan.
-//
-// Direction on the table path: dir = q0 + e * inv with inv = RN(1 / r) (one
-// correctly rounded division per vector), q0 = RN(y * inv) and the residual
-// e = fma(-r, q0, y). By Markstein's theorem this is RN(y / r), the
-// reference's division, whenever e is exact, which holds when
-// exp(r) + exp(q0) - 46 >= -149. The fast form is taken per 64-vector step
+// Nearest centroid: the switch-point cell table of pqkv_cells.h, built by
+// each workgroup at launch (the scan when the codebook does not allow it).
+// The direction is the Markstein quotient (one correctly rounded 1 / r per
+// vector): RN(y / r) whenever its residual is exact, which holds when
+// exp(r) + exp(q0) - 46 >= -149. That form is taken per 64-vector step
 // when every radius is finite and >= 2^-40 (or zero-like, dir = 0): then
 // every direction within a factor of two of a switch point (>= 2^-60) is
 // exact, and a direction off by an ulp elsewhere crosses no switch point, so
@@ -60,6 +47,7 @@
 // a wave's matrix-core products rotate step k, its vector ALUs quantise step
 // k - 1 (rotation held in registers); step k + 1's input is in flight and
 // step k - 2's blocks are being written.
+#include "pqkv_cells.h"
 #include "pqkv_device.h"
 #include "pqkv_launch.h"
 
@@ -80,11 +68,6 @@ constexpr int kEW = 4;              // waves per workgroup
 constexpr int kET = PQKV_ENC_TILES; // 16-vector tiles per workgroup step
 constexpr int kEG = 16 * kET;       // vectors per workgroup step
 constexpr int kEBlocksPerCU = PQKV_ENC_BLOCKS;  // resident workgroups per compute unit
-constexpr int kECells = 1024;       // direction cells over [-1, 1], 1/512 wide
-constexpr int kECellSlots = kECells + 3;
-constexpr int kECellOff = 513;      // cell of dir = round(512 dir) + 513
-constexpr float kEMagic = 12582912.0f;  // 1.5 * 2^23: ulp 1, so fma(d, 512, kEMagic) holds round(512 d) in its low bits
-constexpr float kEClamp = 1.001f;   // |dir| of the table path stays below; beyond, no switch point lies
 constexpr int kEPart = 20;          // floats per vector in the partial-sum exchange (16 used; 80-byte rows
                                     // put the 16-byte reads of lanes 0..15 in distinct banks)
 
@@ -110,50 +93,6 @@ __device__ __forceinline__ float bperm_f(int src_lane, float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane * 4, __builtin_bit_cast(int, v)));
 }
 
-// The reference quantiser: first i minimising |d - c_i| (strict '<').
-__device__ __forceinline__ int scan_index(float d, const float *cb, int nl) {
-#pragma clang fp contract(off)
-  int b = 0;
-  float m = 1e30f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if (i < nl) {
-      const float e = fabsf(d - cb[i]);
-      if (e < m) {
-        m = e;
-        b = i;
-      }
-    }
-  }
-  return b;
-}
-
-// The same scan as a rolled loop over the LDS codebook: the fallback path's
-// form, which keeps the codebook out of registers.
-__device__ __forceinline__ int scan_index_rolled(float d, const float *cb, int nl) {
-#pragma clang fp contract(off)
-  int b = 0;
-  float m = 1e30f;
-#pragma nounroll
-  for (int i = 0; i < nl; ++i) {
-    const float e = fabsf(d - cb[i]);
-    if (e < m) {
-      m = e;
-      b = i;
-    }
-  }
-  return b;
-}
-
-// Direction cell, monotone in d: round(512 d) + 513, for |d| <= kEClamp in
-// 0 .. kECellSlots - 1.
-__device__ __forceinline__ uint32_t cell_bits(float d) {
-  return __builtin_bit_cast(uint32_t, __builtin_fmaf(d, 512.0f, kEMagic));
-}
-__device__ __forceinline__ int dir_cell(float d) {
-  return (int)(cell_bits(d) - __builtin_bit_cast(uint32_t, kEMagic)) + kECellOff;
-}
-
 // Unsigned division by a divisor fixed per launch (Granlund and Montgomery,
 // "Division by invariant integers using multiplication", 1994, round-up
 // multiplier with the add-back step): exact for every 32-bit numerator.
@@ -177,15 +116,6 @@ template <bool B>
 struct TableFlag {
   static constexpr bool on = B;
 };
-
-// Order-preserving map between fp32 values and integers.
-__device__ __forceinline__ int64_t fkey(float f) {
-  const int32_t i = __builtin_bit_cast(int32_t, f);
-  return i >= 0 ? (int64_t)i : -(int64_t)(i & 0x7FFFFFFF);
-}
-__device__ __forceinline__ float kfloat(int64_t k) {
-  return k >= 0 ? __builtin_bit_cast(float, (int32_t)k) : __builtin_bit_cast(float, (int32_t)(0x80000000u | (uint32_t)(-k)));
-}
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -296,61 +226,8 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   }
 
   if (tid < 16) cb[tid] = tid < NL ? a.codebook[tid] : 0.0f;
-  if (tid == 0) table_ok = 1;
   __syncthreads();
-  // ---- switch points: 16 lanes per point i search (c_i, c_{i+1}] 16-ary:
-  // lane j tests the (j + 1)/16 point of the range, the first that the scan
-  // maps to i + 1 or more closes it. Keys of fp32 values differ by < 2^33,
-  // so 9 steps reach a range of one. ----
-  {
-    const int i = tid >> 4, j = tid & 15;
-    const bool act = i < NL - 1;
-    bool ok = act;
-    int64_t lo = 0, hi = 0;
-    if (act) {
-      ok = cb[i] < cb[i + 1] && scan_index(cb[i], cb, NL) <= i && scan_index(cb[i + 1], cb, NL) >= i + 1;
-      lo = fkey(cb[i]);
-      hi = fkey(cb[i + 1]);
-    }
-    for (int step = 0; step < 10; ++step) {
-      const int64_t span = hi - lo;
-      const int64_t cand = j == 15 ? hi : lo + ((span * (j + 1)) >> 4);
-      const bool p = ok && span > 1 && scan_index(kfloat(cand), cb, NL) >= i + 1;
-      const uint32_t gm = (uint32_t)(__builtin_amdgcn_ballot_w64(p) >> (16 * (i & 3))) & 0xFFFFu;
-      const int k = gm ? __builtin_ctz(gm) : 15;
-      if (ok && span > 1) {
-        const int64_t nhi = k == 15 ? hi : lo + ((span * (k + 1)) >> 4);
-        lo = k == 0 ? lo : lo + ((span * k) >> 4);
-        hi = nhi;
-      }
-    }
-    if (act && j == 0) {
-      if (!ok || hi - lo != 1) {
-        table_ok = 0;
-      } else {
-        const float t = kfloat(hi);
-        thr[i] = t;
-        if (!(fabsf(t) >= 0x1p-60f) || !(fabsf(t) < 1.0f)) table_ok = 0;
-        else ucell[i] = dir_cell(t);
-      }
-    }
-  }
-  __syncthreads();
-  if (table_ok != 0) {
-    for (int u = tid; u < kECellSlots; u += kEW * 64) {
-      int base = 0, inside = -1, count = 0;
-      for (int i = 0; i < NL - 1; ++i) {
-        if (ucell[i] < u) ++base;
-        else if (ucell[i] == u) {
-          inside = i;
-          ++count;
-        }
-      }
-      if (count > 1) table_ok = 0;
-      cells[u] = make_uint2((uint32_t)base, inside >= 0 ? __builtin_bit_cast(uint32_t, thr[inside]) : 0x7F800000u);
-    }
-  }
-  __syncthreads();
+  build_cell_table(cb, NL, tid, cells, thr, ucell, &table_ok);
 
   const half_t *x = (const half_t *)a.x;
   // vector v = n_inner * vo + vi; the host keeps n below 2^32 (a single row
@@ -509,7 +386,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
       inv = nz ? __fdiv_rn(1.0f, r) : 0.0f;
       // zero-like (dir = 0, reached through inv = 0 on finite y) or finite
       // and >= 2^-40 (Markstein quotient exact, |dir| <= 1 + 11 ulp)
-      fast = r <= 1e-30f || (r >= 0x1p-40f && r < __builtin_inff());
+      fast = markstein_radius(r);
     }
     if (vme < n && lane < EG) {
       if (wave < D / 32) stage_st16((lds_u8 *)stage[sb] + lv * VB + wave * BB, radius_half_bits(r));
@@ -529,18 +406,8 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
       const bool nzt = rt > 1e-30f;
       int code[MTW][4];
       auto dir_of = [&](float yv) {
-        float d;
-        if constexpr (kFast) {
-#pragma clang fp contract(off)
-          const float q0 = yv * it;
-          const float e = __builtin_fmaf(-rt, q0, yv);
-          d = __builtin_fmaf(e, it, q0);
-        } else {
-          d = nzt ? __fdiv_rn(yv, rt) : 0.0f;
-          d = d == d ? d : -2.0f;  // NaN: index 0, as the scan gives
-          d = __builtin_fminf(__builtin_fmaxf(d, -kEClamp), kEClamp);
-        }
-        return d;
+        if constexpr (kFast) return dir_markstein(yv, rt, it);
+        else return dir_divided(yv, rt);
       };
       if constexpr (kTable && QJL) {
         // (one coordinate at a time: the QJL kernels have no registers to
@@ -549,9 +416,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
         for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float d = dir_of(y[t][mt][i]);
-            const uint2 ce = cells[dir_cell(d)];
-            code[mt][i] = (int)ce.x + (d >= __builtin_bit_cast(float, ce.y) ? 1 : 0);
+            code[mt][i] = table_code(cells, dir_of(y[t][mt][i]));
           }
       } else if constexpr (kTable) {
         // in three passes over the tile's coordinates (directions, cell

@@ -148,6 +148,49 @@ def test_init_and_free():
         L.polarquant_free_c(st)
 
 
+def _soa_codebook(d, kind):
+    cb = O.lloyd_max_codebook(d, 4)[0].astype(np.float32)
+    rng = np.random.default_rng(11)
+    if kind == "unsorted":                   # not increasing: the scan
+        return cb[rng.permutation(16)]
+    if kind == "repeated":                   # two equal centroids: the scan
+        cb = cb.copy()
+        cb[9] = cb[8]
+        return cb
+    if kind == "wide":                       # switch points beyond +-1: the scan
+        return np.linspace(-3, 3, 16).astype(np.float32)
+    if kind == "random":                     # arbitrary switch points: the table
+        return np.sort(rng.uniform(-0.4, 0.4, 16)).astype(np.float32)
+    return cb
+
+
+@pytest.mark.parametrize("kind", ["lloyd", "unsorted", "repeated", "wide", "random"])
+@pytest.mark.parametrize("d", [128, 64])
+def test_compress_soa_codebooks_and_radii(d, kind):
+    """The SoA encoder's quantiser on codebooks that its switch-point table
+    refuses (falling back to the scan) or accepts, over radii from zero to
+    infinite: the reference's first-minimum scan of the division, bit for
+    bit."""
+    print(f"compress_soa d={d} codebook={kind}", flush=True)
+    rng = np.random.default_rng(d)
+    scales = [0.0, 1e-25, 1e-20, 1e-14, 2.0 ** -40 / np.sqrt(d), 1e-12, 1.0, 1e18, 1e20]
+    x = np.concatenate([rng.standard_normal((20, d)) * s for s in scales]
+                       + [rng.standard_normal((300, d)) * rng.lognormal(0, 1, (300, 1))]).astype(np.float32)
+    x[-1, 3] = np.inf
+    n = x.shape[0]
+    cb = _soa_codebook(d, kind)
+    R = O.rotation_matrix(d, 42).astype(np.float32)
+    xt, Rt, cbt = (torch.from_numpy(a).to(DEV) for a in (x, R, cb))
+    radius = torch.empty(n, device=DEV)
+    packed = torch.empty(n, d // 2, dtype=torch.uint8, device=DEV)
+    _lib.lib().polarquant_compress_cuda_c(xt.data_ptr(), Rt.data_ptr(), cbt.data_ptr(), radius.data_ptr(),
+                                          packed.data_ptr(), n, d, 16, _stream())
+    torch.cuda.synchronize()
+    r_ref, idx = OC.c_quantize_rotated(OC.c_rotate_fma(x, R), cb)
+    assert np.array_equal(radius.cpu().numpy().view(np.uint32), r_ref.view(np.uint32))
+    assert np.array_equal(packed.cpu().numpy(), (idx[:, 0::2] | (idx[:, 1::2] << 4)).astype(np.uint8))
+
+
 # ---- the raw-pointer binding (polarquant_turboquant, flash_turboquant.cu:180-230) ----
 
 @pytest.mark.parametrize("d", [128, 64])

@@ -114,6 +114,36 @@ def test_encode_mixed_widths_bit_exact(monkeypatch):
         assert np.array_equal(seg, want), f"head {h}"
 
 
+def _radius_ladder(d, seed):
+    """Rows whose radii cover every branch of the exact encoders' quantiser:
+    zero and below the 1e-30 guard, (1e-30, 2^-40) where directions are
+    divided per coordinate, the 2^-40 edge, the normal range, squares that
+    overflow to an infinite radius, and an infinite coordinate (NaN
+    directions)."""
+    rng = np.random.default_rng(seed)
+    base = _inputs(40, d, seed)
+    edge = 2.0 ** -40 / np.sqrt(d)                         # radii about 2^-40
+    scales = [1e-25, 1e-20, 1e-16, 1e-14, edge, 1.1 * edge, 1e-12, 1.0, 1e15, 1e18, 1e19, 1e20]
+    rows = [rng.standard_normal((3, d)) * s for s in scales]
+    inf_row = rng.standard_normal((1, d))
+    inf_row[0, 7] = np.inf
+    return np.concatenate([base] + rows + [inf_row]).astype(np.float32)
+
+
+@pytest.mark.parametrize("d,bits", [(128, 4), (64, 4), (128, 2)])
+def test_encode_cache_exact_special_radii(d, bits, monkeypatch):
+    print(f"exact encode radius ladder d={d} bits={bits}", flush=True)
+    monkeypatch.setenv("PQKV_ENCODE_KERNEL", "exact")
+    x = _radius_ladder(d, d + bits)
+    n = x.shape[0]
+    R32 = O.rotation_matrix(d, 42).astype(np.float32)
+    cache = quantizer.allocate_cache(1, 1, n, d, bits, DEV)
+    with np.errstate(invalid="ignore", over="ignore"):
+        quantizer.compress_pq(torch.from_numpy(x).to(DEV).view(1, 1, n, d), torch.from_numpy(R32).to(DEV), cache=cache)
+        want, *_ = _oracle_encode(x, R32, bits)
+    assert np.array_equal(cache.blocks.cpu().numpy().reshape(n, -1), want)
+
+
 def test_encode_qjl_signs(monkeypatch):
     """The exact encoder's QJL signs (fp32 FMA-chain rotation)."""
     monkeypatch.setenv("PQKV_ENCODE_KERNEL", "exact")
