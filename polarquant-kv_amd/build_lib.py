@@ -20,7 +20,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "polarquant_kv", "_lib")
 LIB = os.path.join(OUT_DIR, "libpqkv_hip.so")
 BUILD = os.path.join(HERE, "_build")
-SOURCES = ["pqkv_encode.hip", "pqkv_encode_mfma.hip", "pqkv_decode.hip", "pqkv_decode_mfma.hip",
+SOURCES = ["pqkv_encode.hip", "pqkv_encode_tiled.hip", "pqkv_encode_mfma.hip", "pqkv_decode.hip", "pqkv_decode_mfma.hip",
            "pqkv_decode_mfma_k4v4_shared.hip", "pqkv_decode_mfma_k4v4_own.hip", "pqkv_decode_mfma_k4v2.hip",
            "pqkv_decode_mfma_k2v4.hip", "pqkv_decode_mfma_k2v2.hip", "pqkv_decode_mfma_pair.hip",
            "pqkv_decode_mfma_soa.hip", "pqkv_decode_mfma_paged_k4v4_shared.hip", "pqkv_decode_mfma_paged_k4v4_own.hip",

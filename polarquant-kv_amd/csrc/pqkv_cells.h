@@ -84,13 +84,15 @@ __device__ __forceinline__ float kfloat(int64_t k) {
 }
 
 // Builds the table for the nl-level codebook cb[0..15] (in LDS, written and
-// made visible before the call) with a 256-thread workgroup; all threads
-// call it. On return (after a barrier) *table_ok says whether cells[] holds
-// the table; thr[] and ucell[] are 16-entry LDS work arrays.
+// made visible before the call) with a workgroup of NT >= 256 threads; all
+// threads call it. On return (after a barrier) *table_ok says whether
+// cells[] holds the table; thr[] and ucell[] are 16-entry LDS work arrays.
+template <int NT = 256>
 __device__ __forceinline__ void build_cell_table(const float *cb, int nl, int tid, uint2 *cells, float *thr,
                                                  int *ucell, int *table_ok) {
   if (tid == 0) *table_ok = 1;
   __syncthreads();
+  static_assert(NT >= 256 && NT % 64 == 0, "16 lanes for each of up to 15 switch points");
   // Switch points: 16 lanes per point i search (c_i, c_{i+1}] 16-ary; lane j
   // tests the (j + 1)/16 point of the range, and the first that the scan maps
   // to i + 1 or more closes it. Keys of fp32 values differ by < 2^33, so 9
@@ -130,7 +132,7 @@ __device__ __forceinline__ void build_cell_table(const float *cb, int nl, int ti
   }
   __syncthreads();
   if (*table_ok != 0) {
-    for (int u = tid; u < kECellSlots; u += 256) {
+    for (int u = tid; u < kECellSlots; u += NT) {
       int base = 0, inside = -1, count = 0;
       for (int i = 0; i < nl - 1; ++i) {
         if (ucell[i] < u) ++base;

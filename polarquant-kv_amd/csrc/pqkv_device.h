@@ -37,6 +37,25 @@ __device__ __forceinline__ uint16_t radius_half_bits(float r) {
   return float_to_half_bits(r > 65504.0f ? 65504.0f : r);
 }
 
+// Unsigned division by a divisor fixed per launch (Granlund and Montgomery,
+// "Division by invariant integers using multiplication", 1994, round-up
+// multiplier with the add-back step): exact for every 32-bit numerator.
+struct FastDiv {
+  uint32_t d, m;
+  int s1, s2;
+  __device__ explicit FastDiv(uint32_t div) : d(div) {
+    int l = 0;
+    while (l < 32 && (1ull << l) < div) ++l;
+    m = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << l) - div)) / div + 1);
+    s1 = l < 1 ? l : 1;
+    s2 = l > 1 ? l - 1 : 0;
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    const uint32_t t = __umulhi(m, n);
+    return (t + ((n - t) >> s1)) >> s2;
+  }
+};
+
 __device__ __forceinline__ float shfl_down_f(float v, int s) { return __shfl_down(v, s, kWave); }
 __device__ __forceinline__ float shfl_xor_f(float v, int s) { return __shfl_xor(v, s, kWave); }
 

@@ -706,6 +706,7 @@ static int exact_grid(int64_t n, int d) {
 }
 
 hipError_t launch_encode_exact(const EncodeArgs &a, int x_dtype, hipStream_t s) {
+  if (tiled_encode_ok(a, x_dtype)) return launch_encode_tiled(a, x_dtype, s);
   const int64_t n = a.n_outer * a.n_inner;
   const int grid = exact_grid(n, a.d);
 #define PQKV_EE(DD, BB)                                                            \
@@ -723,6 +724,7 @@ hipError_t launch_encode_exact(const EncodeArgs &a, int x_dtype, hipStream_t s) 
 
 hipError_t launch_encode_soa(const float *x, const float *R, const float *codebook, int n_levels, float *radius,
                              uint8_t *packed, int64_t n, int d, hipStream_t s) {
+  if (tiled_soa_ok(x, R, packed, n, d)) return launch_encode_soa_tiled(x, R, codebook, n_levels, radius, packed, n, d, s);
   const int grid = exact_grid(n, d);
   if (d == 128) encode_soa_kernel<128><<<grid, 256, 0, s>>>(x, R, codebook, n_levels, radius, packed, n);
   else encode_soa_kernel<64><<<grid, 256, 0, s>>>(x, R, codebook, n_levels, radius, packed, n);

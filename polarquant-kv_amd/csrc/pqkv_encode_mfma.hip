@@ -93,25 +93,6 @@ __device__ __forceinline__ float bperm_f(int src_lane, float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane * 4, __builtin_bit_cast(int, v)));
 }
 
-// Unsigned division by a divisor fixed per launch (Granlund and Montgomery,
-// "Division by invariant integers using multiplication", 1994, round-up
-// multiplier with the add-back step): exact for every 32-bit numerator.
-struct FastDiv {
-  uint32_t d, m;
-  int s1, s2;
-  __device__ explicit FastDiv(uint32_t div) : d(div) {
-    int l = 0;
-    while (l < 32 && (1ull << l) < div) ++l;
-    m = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << l) - div)) / div + 1);
-    s1 = l < 1 ? l : 1;
-    s2 = l > 1 ? l - 1 : 0;
-  }
-  __device__ __forceinline__ uint32_t div(uint32_t n) const {
-    const uint32_t t = __umulhi(m, n);
-    return (t + ((n - t) >> s1)) >> s2;
-  }
-};
-
 template <bool B>
 struct TableFlag {
   static constexpr bool on = B;

@@ -203,6 +203,14 @@ hipError_t launch_rotate_rows(const float *x, int64_t s_q, int64_t s_h, int64_t 
 hipError_t launch_dequantize(const uint8_t *blocks, const float *codebook, int bits, const float *R, void *y,
                              int y_dtype, int64_t n, int d, hipStream_t s);
 hipError_t launch_encode_exact(const EncodeArgs &a, int x_dtype, hipStream_t s);
+// Register-blocked form of the exact encoder (same rotation, same indices)
+// for inputs it reads in 16-byte pieces, without QJL signs; the exact
+// launchers take it where tiled_encode_ok / tiled_soa_ok hold.
+bool tiled_encode_ok(const EncodeArgs &a, int x_dtype);
+hipError_t launch_encode_tiled(const EncodeArgs &a, int x_dtype, hipStream_t s);
+bool tiled_soa_ok(const float *x, const float *R, const uint8_t *packed, int64_t n, int d);
+hipError_t launch_encode_soa_tiled(const float *x, const float *R, const float *codebook, int n_levels,
+                                   float *radius, uint8_t *packed, int64_t n, int d, hipStream_t s);
 // Matrix-core encoder for fp16 input (with the QJL signs when a.qjl is set;
 // rot_out and radius_out are for keys without them); rot_out and radius_out
 // (nullable) receive the fp32 rotated vectors the quantiser saw, [n][d], and

@@ -191,6 +191,33 @@ def test_compress_soa_codebooks_and_radii(d, kind):
     assert np.array_equal(packed.cpu().numpy(), (idx[:, 0::2] | (idx[:, 1::2] << 4)).astype(np.uint8))
 
 
+@pytest.mark.parametrize("case", ["many_steps", "misaligned"])
+def test_compress_soa_long_and_misaligned_inputs(case):
+    """The SoA encoder over enough vectors that each workgroup of the
+    register-blocked kernel takes several steps (a partial last one), and on
+    input 4 bytes off a 16-byte boundary (the four-chain kernel)."""
+    print(f"compress_soa {case}", flush=True)
+    d = 128
+    n = 256 * 128 * 2 + 77 if case == "many_steps" else 999
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal((n, d)) * rng.lognormal(0, 1, (n, 1))).astype(np.float32)
+    cb = O.lloyd_max_codebook(d, 4)[0].astype(np.float32)
+    R = O.rotation_matrix(d, 42).astype(np.float32)
+    buf = torch.zeros(n * d + 1, dtype=torch.float32, device=DEV)
+    xt = buf[1:] if case == "misaligned" else buf[:-1]
+    xt.copy_(torch.from_numpy(x).flatten())
+    assert (xt.data_ptr() % 16 == 4) == (case == "misaligned")
+    Rt, cbt = torch.from_numpy(R).to(DEV), torch.from_numpy(cb).to(DEV)
+    radius = torch.empty(n, device=DEV)
+    packed = torch.empty(n, d // 2, dtype=torch.uint8, device=DEV)
+    _lib.lib().polarquant_compress_cuda_c(xt.data_ptr(), Rt.data_ptr(), cbt.data_ptr(), radius.data_ptr(),
+                                          packed.data_ptr(), n, d, 16, _stream())
+    torch.cuda.synchronize()
+    r_ref, idx = OC.c_quantize_rotated(OC.c_rotate_fma(x, R), cb)
+    assert np.array_equal(radius.cpu().numpy().view(np.uint32), r_ref.view(np.uint32))
+    assert np.array_equal(packed.cpu().numpy(), (idx[:, 0::2] | (idx[:, 1::2] << 4)).astype(np.uint8))
+
+
 # ---- the raw-pointer binding (polarquant_turboquant, flash_turboquant.cu:180-230) ----
 
 @pytest.mark.parametrize("d", [128, 64])

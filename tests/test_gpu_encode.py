@@ -144,6 +144,45 @@ def test_encode_cache_exact_special_radii(d, bits, monkeypatch):
     assert np.array_equal(cache.blocks.cpu().numpy().reshape(n, -1), want)
 
 
+@pytest.mark.parametrize("layout", ["paged", "misaligned", "many_steps"])
+def test_encode_exact_layouts(layout, monkeypatch):
+    """fp32 input on the exact encoders' other routes: paged appends (the
+    register-blocked kernel's per-vector dword stores into pages), rows that
+    start 4 bytes off a 16-byte boundary (the four-chain kernel, which reads
+    element by element), and enough vectors that every workgroup of the
+    register-blocked kernel takes several steps with a partial last one."""
+    print(f"exact encode layout={layout}", flush=True)
+    d, bits = 128, 4
+    R32 = O.rotation_matrix(d, 42).astype(np.float32)
+    Rt = torch.from_numpy(R32).to(DEV)
+    if layout == "paged":
+        B, H, T = 2, 3, 300
+        x = _inputs(B * H * T, d, 77).reshape(B, H, T, d)
+        c = quantizer.allocate_paged_cache(B, H, d, bits, DEV, page_tokens=64)
+        xt = torch.from_numpy(x).to(DEV)
+        for lo, hi in ((0, 1), (1, 100), (100, 300)):
+            quantizer.compress_pq(xt[:, :, lo:hi].contiguous(), Rt, cache=c)
+        got = c.to_contiguous().blocks.cpu().numpy().reshape(-1, 72)
+    elif layout == "misaligned":
+        B, H, T = 1, 2, 333
+        x = _inputs(B * H * T, d, 78).reshape(B, H, T, d)
+        buf = torch.zeros(x.size + 1, dtype=torch.float32, device=DEV)
+        xt = buf[1:].view(B, H, T, d)
+        xt.copy_(torch.from_numpy(x))
+        assert xt.data_ptr() % 16 == 4
+        c = quantizer.allocate_cache(B, H, T, d, bits, DEV)
+        quantizer.compress_pq(xt, Rt, cache=c)
+        got = c.blocks.cpu().numpy().reshape(-1, 72)
+    else:
+        n = 256 * 128 * 2 + 77
+        x = _inputs(n, d, 79)
+        c = quantizer.allocate_cache(1, 1, n, d, bits, DEV)
+        quantizer.compress_pq(torch.from_numpy(x).to(DEV).view(1, 1, n, d), Rt, cache=c)
+        got = c.blocks.cpu().numpy().reshape(-1, 72)
+    want, *_ = _oracle_encode(x.reshape(-1, d), R32, bits)
+    assert np.array_equal(got, want)
+
+
 def test_encode_qjl_signs(monkeypatch):
     """The exact encoder's QJL signs (fp32 FMA-chain rotation)."""
     monkeypatch.setenv("PQKV_ENCODE_KERNEL", "exact")
