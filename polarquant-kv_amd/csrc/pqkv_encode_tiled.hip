@@ -4,8 +4,9 @@
 // quantiser of csrc/flash_turboquant.cu:141-170 on the values in registers.
 //
 // Work split. A workgroup of 8 waves takes VS vectors per step (128 at
-// d = 128, 256 at d = 64). Lane row tv = tid / 16 owns VT consecutive
-// vectors of the step (4 / 8) and lane tj = tid % 16 of the row owns output
+// d = 128, 256 at d = 64; half that when full-size steps would leave compute
+// units without one). Lane row tv = tid / 16 owns VT consecutive vectors of
+// the step (4 / 8, or 2 / 4) and lane tj = tid % 16 of the row owns output
 // coordinates j = 64 g + 4 tj + i (g < d / 64, i < 4): 32 accumulators per
 // thread, each the chain of one (vector, coordinate) over k ascending, so
 // every rotated value is bit-identical to the one-chain form. Per k a thread
@@ -48,12 +49,14 @@ constexpr int kTK = 32;             // input coordinates per staged chunk
 constexpr int kTXP = kTK + 4;       // floats per staged vector chunk (padded: 16-byte aligned rows in
                                     // different banks)
 
-template <int D>
+// HALF: half the vectors per thread and step, for launches with fewer
+// full-size steps than compute units.
+template <int D, bool HALF>
 struct TiledShape {
-  static constexpr int NG = D / 64;      // 64-coordinate groups per thread
-  static constexpr int VT = 8 / NG;      // vectors per thread
-  static constexpr int VS = 32 * VT;     // vectors per step (32 rows of 16 lanes)
-  static constexpr int NC = D / kTK;     // chunks per step
+  static constexpr int NG = D / 64;               // 64-coordinate groups per thread
+  static constexpr int VT = (8 / NG) >> HALF;     // vectors per thread
+  static constexpr int VS = 32 * VT;              // vectors per step (32 rows of 16 lanes)
+  static constexpr int NC = D / kTK;              // chunks per step
 };
 
 // Lane l of a 16-lane row receives lane (l + N) % 16's value (DPP row_ror).
@@ -70,16 +73,17 @@ typedef __attribute__((address_space(3))) uint32_t lds_u32;
 // OUT: 4 / 2 = block_pq4 / block_pq2 vectors through a's output addressing;
 // 0 = SoA codes at a.blocks (d / 2 bytes per vector) and fp32 radii at
 // soa_radius, one run of n_inner vectors. nl levels (<= 16).
-template <int D, int OUT, typename TIN>
+template <int D, int OUT, typename TIN, bool HALF>
 __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a, const int nl, float *soa_radius) {
-  using S = TiledShape<D>;
+  using S = TiledShape<D, HALF>;
   constexpr int NG = S::NG, VT = S::VT, VS = S::VS, NC = S::NC;
   constexpr int VB = OUT == 0 ? D / 2 : vector_bytes(D, OUT);   // output bytes per vector
   constexpr int BB = OUT == 0 ? 0 : block_bytes(OUT);
   constexpr int PPV = kTK * (int)sizeof(TIN) / 16;               // 16-byte input pieces per vector chunk
   constexpr int EPP = 16 / (int)sizeof(TIN);                     // input elements per piece
-  constexpr int NP = VS * PPV / kTT;                             // pieces per thread per chunk
-  static_assert(VS * PPV % kTT == 0, "input pieces split evenly over the threads");
+  constexpr int NPC = VS * PPV;                                  // input pieces per chunk
+  constexpr int NP = (NPC + kTT - 1) / kTT;                      // pieces per thread per chunk
+  static_assert(NPC % kTT == 0 || NP == 1, "threads past the chunk's pieces take none");
   static_assert(NC % 2 == 0, "chunk c of every step in buffer c % 2");
   __shared__ __attribute__((aligned(16))) float rt[D * D];           // rt[k * D + j] = R[j][k]
   __shared__ __attribute__((aligned(16))) float xs[2][VS * kTXP];    // xs[b][v * kTXP + kk]
@@ -117,7 +121,7 @@ __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a
     for (int p = 0; p < NP; ++p) {
       const int q = tid + kTT * p;
       const uint32_t v = s * VS + q / PPV;
-      if (v < n) {
+      if (q < NPC && v < n) {
         const uint32_t vo = by_inner.div(v), vi = v - vo * (uint32_t)a.n_inner;
         src[p] = x + (int64_t)vo * a.x_outer_stride + (int64_t)vi * D + EPP * (q % PPV);
       } else {
@@ -134,6 +138,7 @@ __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       const int q = tid + kTT * p;
+      if (q >= NPC) continue;
       float *dst = &xs[b][(q / PPV) * kTXP + EPP * (q % PPV)];
       if constexpr (sizeof(TIN) == 4) {
         *(float4_t *)dst = __builtin_bit_cast(float4_t, pre[p]);
@@ -339,20 +344,31 @@ bool tiled_encode_ok(const EncodeArgs &a, int x_dtype) {
   return true;
 }
 
-static int tiled_grid(int64_t n, int d) {
-  const int vs = d == 128 ? TiledShape<128>::VS : TiledShape<64>::VS;
+// Vectors per step: full-size steps, or half-size ones when full-size steps
+// would leave compute units without one.
+static int tiled_step(int64_t n, int d) {
+  const int full = d == 128 ? TiledShape<128, false>::VS : TiledShape<64, false>::VS;
+  return (n + full - 1) / full < device_compute_units() ? full / 2 : full;
+}
+
+static int tiled_grid(int64_t n, int vs) {
   const int64_t steps = (n + vs - 1) / vs;
   const int64_t cap = device_compute_units();
   return (int)(steps < cap ? steps : cap);
 }
 
 hipError_t launch_encode_tiled(const EncodeArgs &a, int x_dtype, hipStream_t s) {
-  const int grid = tiled_grid(a.n_outer * a.n_inner, a.d);
+  const int64_t n = a.n_outer * a.n_inner;
+  const int vs = tiled_step(n, a.d);
+  const bool half = vs < (a.d == 128 ? TiledShape<128, false>::VS : TiledShape<64, false>::VS);
+  const int grid = tiled_grid(n, vs);
   const int nl = 1 << a.bits;
-#define PQKV_ET(DD, BB)                                                                              \
-  do {                                                                                               \
-    if (x_dtype == 0) encode_tiled_kernel<DD, BB, float><<<grid, kTT, 0, s>>>(a, nl, nullptr);       \
-    else encode_tiled_kernel<DD, BB, half_t><<<grid, kTT, 0, s>>>(a, nl, nullptr);                   \
+#define PQKV_ET(DD, BB)                                                                                  \
+  do {                                                                                                   \
+    if (x_dtype == 0 && !half) encode_tiled_kernel<DD, BB, float, false><<<grid, kTT, 0, s>>>(a, nl, nullptr); \
+    else if (x_dtype == 0) encode_tiled_kernel<DD, BB, float, true><<<grid, kTT, 0, s>>>(a, nl, nullptr);     \
+    else if (!half) encode_tiled_kernel<DD, BB, half_t, false><<<grid, kTT, 0, s>>>(a, nl, nullptr);          \
+    else encode_tiled_kernel<DD, BB, half_t, true><<<grid, kTT, 0, s>>>(a, nl, nullptr);                      \
   } while (0)
   if (a.d == 128 && a.bits == 4) PQKV_ET(128, 4);
   else if (a.d == 128) PQKV_ET(128, 2);
@@ -378,9 +394,13 @@ hipError_t launch_encode_soa_tiled(const float *x, const float *R, const float *
   a.n_outer = 1;
   a.n_inner = n;
   a.d = d;
-  const int grid = tiled_grid(n, d);
-  if (d == 128) encode_tiled_kernel<128, 0, float><<<grid, kTT, 0, s>>>(a, n_levels, radius);
-  else encode_tiled_kernel<64, 0, float><<<grid, kTT, 0, s>>>(a, n_levels, radius);
+  const int vs = tiled_step(n, d);
+  const bool half = vs < (d == 128 ? TiledShape<128, false>::VS : TiledShape<64, false>::VS);
+  const int grid = tiled_grid(n, vs);
+  if (d == 128 && !half) encode_tiled_kernel<128, 0, float, false><<<grid, kTT, 0, s>>>(a, n_levels, radius);
+  else if (d == 128) encode_tiled_kernel<128, 0, float, true><<<grid, kTT, 0, s>>>(a, n_levels, radius);
+  else if (!half) encode_tiled_kernel<64, 0, float, false><<<grid, kTT, 0, s>>>(a, n_levels, radius);
+  else encode_tiled_kernel<64, 0, float, true><<<grid, kTT, 0, s>>>(a, n_levels, radius);
   return hipGetLastError();
 }
 
