@@ -503,7 +503,9 @@ def run_config3(args) -> int:
         "encode": {"tokens_per_s": round(enc_tokens_s), "ms": round(enc_ms, 4),
                    "kernel_ms": round(enc_kernel_each, 4), "GB_per_s": round(enc_bytes / (enc_ms / 1e3) / 1e9, 2),
                    "vectors": 2 * B * Hkv * S,
-                   "kernel": "encode_mfma_kernel (matrix-core rotation, bit-exact quantiser)",
+                   "kernel": ("encode_tiled_kernel (PQKV_ENCODE_KERNEL=exact: the reference's FMA-chain rotation, "
+                              "register-blocked)" if os.environ.get("PQKV_ENCODE_KERNEL") == "exact" else
+                              "encode_mfma_kernel (matrix-core rotation, bit-exact quantiser)"),
                    "kernel_ms_source": KSRC,
                    "roofline": {"bound": "hbm", "bytes": enc_bytes,
                                 "achieved_GBps": round(enc_bytes / (enc_kernel_each * 2 / 1e3) / 1e9, 2),
