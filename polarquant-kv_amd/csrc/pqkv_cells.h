@@ -83,15 +83,22 @@ __device__ __forceinline__ float kfloat(int64_t k) {
   return k >= 0 ? __builtin_bit_cast(float, (int32_t)k) : __builtin_bit_cast(float, (int32_t)(0x80000000u | (uint32_t)(-k)));
 }
 
+// Workgroup barrier for LDS hand-offs: each wave waits for its own LDS
+// operations only, so its global loads and global->LDS copies stay in flight
+// across it (__syncthreads would drain them).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Builds the table for the nl-level codebook cb[0..15] (in LDS, written and
 // made visible before the call) with a workgroup of NT >= 256 threads; all
 // threads call it. On return (after a barrier) *table_ok says whether
 // cells[] holds the table; thr[] and ucell[] are 16-entry LDS work arrays.
+// Its barriers are LDS-only, so loads the caller issued before it keep
+// running meanwhile.
 template <int NT = 256>
 __device__ __forceinline__ void build_cell_table(const float *cb, int nl, int tid, uint2 *cells, float *thr,
                                                  int *ucell, int *table_ok) {
   if (tid == 0) *table_ok = 1;
-  __syncthreads();
+  lds_barrier();
   static_assert(NT >= 256 && NT % 64 == 0, "16 lanes for each of up to 15 switch points");
   // Switch points: 16 lanes per point i search (c_i, c_{i+1}] 16-ary; lane j
   // tests the (j + 1)/16 point of the range, and the first that the scan maps
@@ -130,7 +137,7 @@ __device__ __forceinline__ void build_cell_table(const float *cb, int nl, int ti
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (*table_ok != 0) {
     for (int u = tid; u < kECellSlots; u += NT) {
       int base = 0, inside = -1, count = 0;
@@ -145,7 +152,7 @@ __device__ __forceinline__ void build_cell_table(const float *cb, int nl, int ti
       cells[u] = make_uint2((uint32_t)base, inside >= 0 ? __builtin_bit_cast(uint32_t, thr[inside]) : 0x7F800000u);
     }
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // Radii for which the Markstein quotient gives the reference's index:

@@ -169,22 +169,32 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   // ---- A operand, in registers for the launch: row p of tile mt is output
   // coordinate j = 16 (4 mt + p / 4) + 4 wave + p % 4; lane (p, grp) holds
   // R[j][32 ks + 8 grp .. + 7] ----
+  // (loaded here, split after the set-up below so that the loads' latency
+  // overlaps it)
   half8_t ah[MTW][KS], al[MTW][KS];
+  float4_t rraw[MTW][KS][2];
 #pragma unroll
   for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int j = 16 * (4 * mt + (col >> 2)) + 4 * wave + (col & 3);
-      const float4 *rr = (const float4 *)(a.R + (int64_t)j * D + 32 * ks + 8 * grp);
-      const float4 r0 = rr[0], r1 = rr[1];
-      const float rv[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const half_t h = (half_t)rv[e];
-        ah[mt][ks][e] = h;
-        al[mt][ks][e] = (half_t)(rv[e] - (float)h);
-      }
+      const float4_t *rr = (const float4_t *)(a.R + (int64_t)j * D + 32 * ks + 8 * grp);
+      rraw[mt][ks][0] = rr[0];
+      rraw[mt][ks][1] = rr[1];
     }
+  auto split_r = [&] {
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float rv = rraw[mt][ks][e >> 2][e & 3];
+          const half_t h = (half_t)rv;
+          ah[mt][ks][e] = h;
+          al[mt][ks][e] = (half_t)(rv - (float)h);
+        }
+  };
   // QJL: P_rot = P R^T as the A operand of the sign product, the same way:
   // row p of tile mt is projection (d / 4) wave + 16 mt + p
   half8_t ph[QJL ? MTW : 1][KS], pl[QJL ? MTW : 1][KS];
@@ -207,8 +217,6 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   }
 
   if (tid < 16) cb[tid] = tid < NL ? a.codebook[tid] : 0.0f;
-  __syncthreads();
-  build_cell_table(cb, NL, tid, cells, thr, ucell, &table_ok);
 
   const half_t *x = (const half_t *)a.x;
   // vector v = n_inner * vo + vi; the host keeps n below 2^32 (a single row
@@ -552,8 +560,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
     constexpr bool kTable = decltype(table_flag)::on;
     const int64_t g0 = blockIdx.x;
     const int64_t steps = (groups - g0 + g_step - 1) / g_step;  // this workgroup's steps
-    Tile acc, accp;
-    issue(g0, 0);
+    Tile acc, accp;   // (step g0's input was issued before the set-up)
     for (int64_t k = 0; k < steps + 3; ++k) {
       const int b = (int)(k & 1);
       const int64_t gk = g0 + k * g_step;
@@ -591,8 +598,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   auto run = [&](auto table_flag) {
     constexpr bool kTable = decltype(table_flag)::on;
     int64_t g = blockIdx.x;
-    Tile acc, accp;
-    issue(g, 0);
+    Tile acc, accp;   // (step g's input was issued before the set-up)
     wait_mem();
     barrier();
     rotate(0, acc);
@@ -649,6 +655,12 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
     barrier();
     flush(gp, b);
   };
+  // Set-up: the first step's input copies and R's loads are in flight while
+  // the centroid table is built (its barriers wait for LDS only).
+  issue(blockIdx.x, 0);
+  lds_barrier();
+  build_cell_table(cb, NL, tid, cells, thr, ucell, &table_ok);
+  split_r();
   if constexpr (QJL) {
     if (table_ok != 0) run_qjl(TableFlag<true>{});
     else run_qjl(TableFlag<false>{});

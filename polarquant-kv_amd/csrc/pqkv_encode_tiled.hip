@@ -99,19 +99,7 @@ __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a
   const uint32_t steps = (n + VS - 1) / VS;
   const FastDiv by_inner((uint32_t)a.n_inner);
   const TIN *x = (const TIN *)a.x;
-
-  if (tid < 16) cb[tid] = tid < nl ? a.codebook[tid] : 0.0f;
-  // R^T: consecutive lanes take consecutive rows j of one 4-column slice, so
-  // the transposed LDS writes fall in distinct banks
-  for (int q = tid; q < D * D / 4; q += kTT) {
-    const int j = q % D, k4 = q / D;
-    const float4_t r = *(const float4_t *)(a.R + (int64_t)j * D + 4 * k4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) rt[(4 * k4 + e) * D + j] = r[e];
-  }
-  __syncthreads();
-  build_cell_table<kTT>(cb, nl, tid, cells, thr, ucell, &table_ok);
-  const bool use_table = table_ok != 0;
+  bool use_table = false;   // whether the switch-point table holds (set after its build)
 
   // ---- input: piece p of this thread is piece q % PPV of vector q / PPV of
   // the step, q = tid + kTT p ----
@@ -302,7 +290,19 @@ __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a
   // barrier per chunk. The host launches at most `steps` workgroups. ----
   uint32_t s = blockIdx.x;
   set_rows(s);
-  load(0);
+  load(0);   // in flight during the set-up below
+  if (tid < 16) cb[tid] = tid < nl ? a.codebook[tid] : 0.0f;
+  // R^T: consecutive lanes take consecutive rows j of one 4-column slice, so
+  // the transposed LDS writes fall in distinct banks
+  for (int q = tid; q < D * D / 4; q += kTT) {
+    const int j = q % D, k4 = q / D;
+    const float4_t r = *(const float4_t *)(a.R + (int64_t)j * D + 4 * k4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rt[(4 * k4 + e) * D + j] = r[e];
+  }
+  lds_barrier();
+  build_cell_table<kTT>(cb, nl, tid, cells, thr, ucell, &table_ok);
+  use_table = table_ok != 0;
   store_x(0);
   __syncthreads();
   for (; s < steps; s += gridDim.x) {
