@@ -86,7 +86,9 @@ int pqkv_quantize_rotated(const float *x_rot, const float *codebook, int n_bits,
                           int64_t n, int d, void *stream);
 
 /* Fused encoder: rotate, quantise and pack n_outer x n_inner vectors.
- * x: fp16 or fp32, vector (o, i) at x + (o * x_outer_stride + i * d) elements.
+ * x: fp16, fp32 or bf16 (PQKV_BF16, widened exactly to fp32, as the
+ * reference's kv.float()), vector (o, i) at x + (o * x_outer_stride + i * d)
+ * elements.
  * blocks: vector (o, i) at blocks + o * blocks_outer_stride + i * vector_bytes.
  * Optional QJL sign sketch of the key residual (p_rot = P R^T, [m][d] fp32,
  * m = d): signs at qjl + o * qjl_outer_stride + i * (m/8), bit i of the

@@ -324,7 +324,7 @@ int encode_validate(const void *x, int x_dtype, int64_t x_outer_stride, const fl
   if (n_outer < 0 || n_inner < 0) return fail(PQKV_ERR_INVALID, "encode: negative count");
   if (!supported_d(d) || !supported_bits(n_bits))
     return fail(PQKV_ERR_UNSUPPORTED, "encode: d=%d bits=%d", d, n_bits);
-  if (!float_dtype(x_dtype)) return fail(PQKV_ERR_UNSUPPORTED, "encode: x dtype %d", x_dtype);
+  if (!float_dtype(x_dtype) && x_dtype != PQKV_BF16) return fail(PQKV_ERR_UNSUPPORTED, "encode: x dtype %d", x_dtype);
   if ((qjl == nullptr) != (p_rot == nullptr)) return fail(PQKV_ERR_INVALID, "encode: qjl and p_rot go together");
   if (qjl && m != d) return fail(PQKV_ERR_UNSUPPORTED, "encode: QJL needs m == d (m=%d, d=%d)", m, d);
   if (n_outer * n_inner == 0) return PQKV_OK;

@@ -16,6 +16,12 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// bfloat16 storage: the upper half of an fp32, so widening is exact.
+struct bf16_t {
+  uint16_t bits;
+};
+__device__ __forceinline__ float bf16_to_float(uint32_t bits16) { return __builtin_bit_cast(float, bits16 << 16); }
+
 constexpr int kWave = 64;
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {

@@ -165,6 +165,7 @@ __device__ __forceinline__ void load_r_row(const float *__restrict__ R, int j, f
 
 template <typename T>
 __device__ __forceinline__ float load_as_float(const T *p) { return (float)*p; }
+__device__ __forceinline__ float load_as_float(const bf16_t *p) { return bf16_to_float(p->bits); }
 
 // y = R x (forward) or R^T x (inverse) for n vectors, each output one fp32
 // FMA chain over k ascending (the encoder's order, so both agree bit for bit).
@@ -712,7 +713,8 @@ hipError_t launch_encode_exact(const EncodeArgs &a, int x_dtype, hipStream_t s) 
 #define PQKV_EE(DD, BB)                                                            \
   do {                                                                             \
     if (x_dtype == 0) encode_exact_kernel<DD, BB, float><<<grid, 256, 0, s>>>(a);  \
-    else encode_exact_kernel<DD, BB, half_t><<<grid, 256, 0, s>>>(a);              \
+    else if (x_dtype == 1) encode_exact_kernel<DD, BB, half_t><<<grid, 256, 0, s>>>(a); \
+    else encode_exact_kernel<DD, BB, bf16_t><<<grid, 256, 0, s>>>(a);              \
   } while (0)
   if (a.d == 128 && a.bits == 4) PQKV_EE(128, 4);
   else if (a.d == 128 && a.bits == 2) PQKV_EE(128, 2);

@@ -130,6 +130,12 @@ __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a
       float *dst = &xs[b][(q / PPV) * kTXP + EPP * (q % PPV)];
       if constexpr (sizeof(TIN) == 4) {
         *(float4_t *)dst = __builtin_bit_cast(float4_t, pre[p]);
+      } else if constexpr (__is_same(TIN, bf16_t)) {
+        const u32x4 w = pre[p];
+        *(float4_t *)dst = float4_t{bf16_to_float(w[0] & 0xFFFFu), bf16_to_float(w[0] >> 16),
+                                    bf16_to_float(w[1] & 0xFFFFu), bf16_to_float(w[1] >> 16)};
+        *(float4_t *)(dst + 4) = float4_t{bf16_to_float(w[2] & 0xFFFFu), bf16_to_float(w[2] >> 16),
+                                          bf16_to_float(w[3] & 0xFFFFu), bf16_to_float(w[3] >> 16)};
       } else {
         const half8_t h = __builtin_bit_cast(half8_t, pre[p]);
         *(float4_t *)dst = float4_t{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
@@ -363,18 +369,23 @@ hipError_t launch_encode_tiled(const EncodeArgs &a, int x_dtype, hipStream_t s) 
   const bool half = vs < (a.d == 128 ? TiledShape<128, false>::VS : TiledShape<64, false>::VS);
   const int grid = tiled_grid(n, vs);
   const int nl = 1 << a.bits;
-#define PQKV_ET(DD, BB)                                                                                  \
-  do {                                                                                                   \
-    if (x_dtype == 0 && !half) encode_tiled_kernel<DD, BB, float, false><<<grid, kTT, 0, s>>>(a, nl, nullptr); \
-    else if (x_dtype == 0) encode_tiled_kernel<DD, BB, float, true><<<grid, kTT, 0, s>>>(a, nl, nullptr);     \
-    else if (!half) encode_tiled_kernel<DD, BB, half_t, false><<<grid, kTT, 0, s>>>(a, nl, nullptr);          \
-    else encode_tiled_kernel<DD, BB, half_t, true><<<grid, kTT, 0, s>>>(a, nl, nullptr);                      \
+#define PQKV_ET_T(DD, BB, TT)                                                                     \
+  do {                                                                                            \
+    if (!half) encode_tiled_kernel<DD, BB, TT, false><<<grid, kTT, 0, s>>>(a, nl, nullptr);       \
+    else encode_tiled_kernel<DD, BB, TT, true><<<grid, kTT, 0, s>>>(a, nl, nullptr);              \
+  } while (0)
+#define PQKV_ET(DD, BB)                          \
+  do {                                           \
+    if (x_dtype == 0) PQKV_ET_T(DD, BB, float);  \
+    else if (x_dtype == 1) PQKV_ET_T(DD, BB, half_t); \
+    else PQKV_ET_T(DD, BB, bf16_t);              \
   } while (0)
   if (a.d == 128 && a.bits == 4) PQKV_ET(128, 4);
   else if (a.d == 128) PQKV_ET(128, 2);
   else if (a.bits == 4) PQKV_ET(64, 4);
   else PQKV_ET(64, 2);
 #undef PQKV_ET
+#undef PQKV_ET_T
   return hipGetLastError();
 }
 

@@ -62,8 +62,9 @@ def allocate_cache(batch: int, num_heads: int, max_seq_len: int, head_dim: int, 
 
 def compress_pq(kv: torch.Tensor, rotation_matrix: torch.Tensor, n_bits=4, cache: PQCache | None = None,
                 start: int | None = None, jl_rot: torch.Tensor | None = None) -> PQCache:
-    """Encode kv [B, H, T, d] (fp16 or fp32; other float types such as bf16
-    are widened to fp32; device) into a PQ cache.
+    """Encode kv [B, H, T, d] (fp16, fp32 or bf16, which the encoder widens
+    exactly to fp32; other float types are widened here; device) into a PQ
+    cache.
 
     With `cache`, positions start .. start+T-1 (default: cache.seq_len) are
     written in place and seq_len grows to cover them; otherwise a new cache of
@@ -87,10 +88,12 @@ def compress_pq(kv: torch.Tensor, rotation_matrix: torch.Tensor, n_bits=4, cache
         raise ValueError("cache was allocated without QJL signs")
     if T == 0:
         return cache
-    # the encoders read fp16 or fp32; other floating types (bf16 models) are
-    # widened to fp32 first, as the reference's kv.float() does
-    # (src/polarquant_kv_cuda/compress_kernel.py:135)
-    x = (kv if kv.dtype in (torch.float16, torch.float32) else kv.to(torch.float32)).contiguous()
+    # the encoders read fp16, fp32 and bf16 (widened exactly to fp32 on the
+    # device, as the reference's kv.float() does,
+    # src/polarquant_kv_cuda/compress_kernel.py:135); other floating types
+    # are widened here
+    x = (kv if kv.dtype in (torch.float16, torch.float32, torch.bfloat16) else kv.to(torch.float32)).contiguous()
+    x_code = _lib.BF16 if x.dtype == torch.bfloat16 else _lib.dtype_code(x.dtype)
     R = rotation_matrix.to(torch.float32).contiguous()
     P = None if jl_rot is None else jl_rot.to(torch.float32).contiguous()
     stream = _lib.stream_of(x)
@@ -105,7 +108,7 @@ def compress_pq(kv: torch.Tensor, rotation_matrix: torch.Tensor, n_bits=4, cache
             m8 = cache.qjl_signs.shape[-1]
             qjl_ptr = cache.qjl_signs.data_ptr() + start * m8
             qjl_stride = cache.max_seq_len * m8
-        _lib.check(lib.pqkv_encode(x.data_ptr(), _lib.dtype_code(x.dtype), T * d, R.data_ptr(),
+        _lib.check(lib.pqkv_encode(x.data_ptr(), x_code, T * d, R.data_ptr(),
                                    cache.codebooks.data_ptr(), cache.n_bits,
                                    cache.blocks.data_ptr() + start * vb, cache.max_seq_len * vb, B * H, T, d,
                                    _lib.ptr(P), d if P is not None else 0, qjl_ptr, qjl_stride, stream))
@@ -119,7 +122,7 @@ def compress_pq(kv: torch.Tensor, rotation_matrix: torch.Tensor, n_bits=4, cache
                 m8 = cache.qjl_signs.shape[-1]
                 qjl_ptr = cache.qjl_signs.data_ptr() + ((h * cache.max_seq_len) + start) * m8
                 qjl_stride = H * cache.max_seq_len * m8
-            _lib.check(lib.pqkv_encode(xq, _lib.dtype_code(x.dtype), H * T * d, R.data_ptr(),
+            _lib.check(lib.pqkv_encode(xq, x_code, H * T * d, R.data_ptr(),
                                        cache.codebooks[h].data_ptr(), bits, base, cache.blocks.shape[1], B, T, d,
                                        _lib.ptr(P), d if P is not None else 0, qjl_ptr, qjl_stride, stream))
     cache.seq_len = max(cache.seq_len, start + T)
@@ -141,11 +144,12 @@ def _compress_paged(kv, rotation_matrix, cache: PagedPQCache, start, jl_rot):
     if T == 0:
         return cache
     cache.ensure(start + T)
-    x = (kv if kv.dtype in (torch.float16, torch.float32) else kv.to(torch.float32)).contiguous()
+    x = (kv if kv.dtype in (torch.float16, torch.float32, torch.bfloat16) else kv.to(torch.float32)).contiguous()
+    x_code = _lib.BF16 if x.dtype == torch.bfloat16 else _lib.dtype_code(x.dtype)
     R = rotation_matrix.to(torch.float32).contiguous()
     P = None if jl_rot is None else jl_rot.to(torch.float32).contiguous()
     _lib.check(_lib.lib().pqkv_encode_paged(
-        x.data_ptr(), _lib.dtype_code(x.dtype), T * d, R.data_ptr(), cache.codebooks.data_ptr(), cache.n_bits,
+        x.data_ptr(), x_code, T * d, R.data_ptr(), cache.codebooks.data_ptr(), cache.n_bits,
         cache.table.data_ptr(), cache.page_tokens, cache.max_pages, start, B * H, T, d, _lib.ptr(P),
         d if P is not None else 0, cache.sign_table.data_ptr() if P is not None else None, _lib.stream_of(x)))
     cache.seq_len = max(cache.seq_len, start + T)

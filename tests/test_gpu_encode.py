@@ -183,6 +183,53 @@ def test_encode_exact_layouts(layout, monkeypatch):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("layout", ["contiguous", "paged", "misaligned", "qjl"])
+def test_encode_bf16_bit_exact(layout):
+    """bf16 input (a bf16 model's states) goes to the exact encoders as is,
+    widened to fp32 on the device: the blocks equal the oracle's encode of
+    x.float(), the reference's kv.float() path, bit for bit. Contiguous and
+    paged rows take the register-blocked kernel, rows 2 bytes off a 16-byte
+    boundary and QJL keys the four-chain kernel."""
+    print(f"bf16 encode layout={layout}", flush=True)
+    d, bits = 128, 4
+    R = O.rotation_matrix(d, 42)
+    R32 = R.astype(np.float32)
+    Rt = torch.from_numpy(R32).to(DEV)
+    B, H, T = 2, 2, 157
+    xb = torch.from_numpy(_inputs(B * H * T, d, 91)).to(DEV).bfloat16().view(B, H, T, d)
+    xf = xb.float().cpu().numpy()
+    if layout == "paged":
+        c = quantizer.allocate_paged_cache(B, H, d, bits, DEV, page_tokens=64)
+        quantizer.compress_pq(xb[:, :, :70].contiguous(), Rt, cache=c)
+        quantizer.compress_pq(xb[:, :, 70:].contiguous(), Rt, cache=c)
+        got = c.to_contiguous().blocks.cpu().numpy().reshape(-1, 72)
+    elif layout == "misaligned":
+        buf = torch.zeros(xb.numel() + 1, dtype=torch.bfloat16, device=DEV)
+        xm = buf[1:].view(B, H, T, d)
+        xm.copy_(xb)
+        assert xm.data_ptr() % 16 == 2
+        c = quantizer.allocate_cache(B, H, T, d, bits, DEV)
+        quantizer.compress_pq(xm, Rt, cache=c)
+        got = c.blocks.cpu().numpy().reshape(-1, 72)
+    else:
+        jl = layout == "qjl"
+        P_rot = (O.jl_matrix(d, d, 43) @ R.T).astype(np.float32)
+        c = quantizer.allocate_cache(B, H, T, d, bits, DEV, jl_dim=d if jl else 0)
+        quantizer.compress_pq(xb, Rt, cache=c, jl_rot=torch.from_numpy(P_rot).to(DEV) if jl else None)
+        got = c.blocks.cpu().numpy().reshape(-1, 72)
+    want, y, r, idx, cb = _oracle_encode(xf.reshape(-1, d), R32, bits)
+    assert np.array_equal(got, want)
+    if layout == "qjl":
+        e = y.astype(np.float64) - r[:, None].astype(np.float64) * cb[idx].astype(np.float64)
+        proj = e @ P_rot.astype(np.float64).T
+        sg = O.bit_unpack_lsb(c.qjl_signs.cpu().numpy().reshape(-1, d // 8), d)
+        want_s = O.bit_unpack_lsb(O.bit_pack_lsb(proj >= 0), d)
+        # sign ties: projections within fp32 summation error of zero
+        tol = 1e-5 * np.linalg.norm(e, axis=1, keepdims=True) * np.linalg.norm(P_rot, axis=1)[None]
+        assert not ((sg != want_s) & (np.abs(proj) > tol)).any()
+        assert (sg != want_s).mean() < 1e-3
+
+
 def test_encode_qjl_signs(monkeypatch):
     """The exact encoder's QJL signs (fp32 FMA-chain rotation)."""
     monkeypatch.setenv("PQKV_ENCODE_KERNEL", "exact")
