@@ -183,6 +183,24 @@ def test_encode_exact_layouts(layout, monkeypatch):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("d,bits", [(128, 4), (128, 2), (64, 4), (64, 2)])
+def test_encode_exact_full_steps(d, bits, dtype, monkeypatch):
+    """The register-blocked exact encoder with full-size steps (4 vectors
+    per thread at d = 128, 8 at d = 64; the launches above take half-size
+    ones): enough vectors for several steps on every compute unit, the last
+    one partial, in every input type and code width."""
+    print(f"exact encode full steps d={d} bits={bits} {dtype}", flush=True)
+    monkeypatch.setenv("PQKV_ENCODE_KERNEL", "exact")
+    n = 256 * (32768 // d) * 2 + 77
+    x = torch.from_numpy(_inputs(n, d, d + bits)).to(DEV).to(getattr(torch, dtype))
+    R32 = O.rotation_matrix(d, 42).astype(np.float32)
+    c = quantizer.allocate_cache(1, 1, n, d, bits, DEV)
+    quantizer.compress_pq(x.view(1, 1, n, d), torch.from_numpy(R32).to(DEV), cache=c)
+    want, *_ = _oracle_encode(x.float().cpu().numpy(), R32, bits)
+    assert np.array_equal(c.blocks.cpu().numpy().reshape(n, -1), want)
+
+
 @pytest.mark.parametrize("layout", ["contiguous", "paged", "misaligned", "qjl"])
 def test_encode_bf16_bit_exact(layout):
     """bf16 input (a bf16 model's states) goes to the exact encoders as is,
