@@ -35,6 +35,8 @@
 // reference's SoA codes (packed[p] = code(2p) | code(2p+1) << 4) with fp32
 // radii, staged in LDS and stored one step later, 16-byte pieces for one
 // aligned run of vectors, dwords otherwise.
+#include <type_traits>
+
 #include "pqkv_cells.h"
 #include "pqkv_device.h"
 #include "pqkv_launch.h"
@@ -73,7 +75,13 @@ typedef __attribute__((address_space(3))) uint32_t lds_u32;
 // OUT: 4 / 2 = block_pq4 / block_pq2 vectors through a's output addressing;
 // 0 = SoA codes at a.blocks (d / 2 bytes per vector) and fp32 radii at
 // soa_radius, one run of n_inner vectors. nl levels (<= 16).
-template <int D, int OUT, typename TIN, bool HALF>
+// QJL (keys, m = d projections, half-size steps): after a step's quantiser
+// each thread writes its residuals e = y - r c[code] (fp32 r) to LDS, and
+// the projections P_rot e run as a second tiled product over k ascending,
+// P_rot staged in 16-coordinate chunks (transposed, double-buffered); sign
+// bit m = (P_rot e)[m] >= 0, LSB first, stored one step later like the
+// blocks.
+template <int D, int OUT, typename TIN, bool HALF, bool QJL = false>
 __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a, const int nl, float *soa_radius) {
   using S = TiledShape<D, HALF>;
   constexpr int NG = S::NG, VT = S::VT, VS = S::VS, NC = S::NC;
@@ -85,6 +93,12 @@ __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a
   constexpr int NP = (NPC + kTT - 1) / kTT;                      // pieces per thread per chunk
   static_assert(NPC % kTT == 0 || NP == 1, "threads past the chunk's pieces take none");
   static_assert(NC % 2 == 0, "chunk c of every step in buffer c % 2");
+  constexpr int SB = D / 8;          // sign bytes per vector
+  constexpr int PK = 16;             // projection k per staged chunk of P_rot
+  constexpr int NPK = D / PK;        // chunks per projection
+  constexpr int ESP = D + 4;         // floats per residual row (padded like xs)
+  static_assert(!QJL || (HALF && OUT != 0), "QJL keys: blocks, half-size steps");
+  static_assert(PK * D / 4 <= kTT, "one P_rot piece per thread and chunk");
   __shared__ __attribute__((aligned(16))) float rt[D * D];           // rt[k * D + j] = R[j][k]
   __shared__ __attribute__((aligned(16))) float xs[2][VS * kTXP];    // xs[b][v * kTXP + kk]
   __shared__ __attribute__((aligned(16))) uint8_t stage[VS * VB];
@@ -92,6 +106,9 @@ __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a
   __shared__ float cb[16], thr[16];
   __shared__ int ucell[16];
   __shared__ int table_ok;
+  __shared__ __attribute__((aligned(16))) float es[QJL ? VS * ESP : 4];        // residuals e[v][k]
+  __shared__ __attribute__((aligned(16))) float pt[2][QJL ? PK * D : 4];       // pt[b][kk * D + m] = P_rot[m][PK pc + kk]
+  __shared__ __attribute__((aligned(16))) uint8_t sstage[QJL ? VS * SB : 16];  // the step's sign bytes
 
   const int tid = threadIdx.x;
   const int tj = tid & 15, tv = tid >> 4;
@@ -253,20 +270,94 @@ __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a
         const uint32_t v = s * VS + vl;
         if (tj == 0 && v < n) soa_radius[v] = r;
       }
+      if constexpr (QJL) {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          float4_t e;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) e[i] = __builtin_fmaf(-r, cb[code[g][i]], acc[u][g][i]);
+          *(float4_t *)&es[vl * ESP + 64 * g + 4 * tj] = e;
+        }
+      }
     }
   };
 
-  // ---- step s's output from stage to memory ----
-  const bool run16 = a.n_outer <= 1 && a.pages == nullptr && ((uintptr_t)a.blocks & 15) == 0;
-  auto flush = [&](uint32_t s) {
+  // ---- QJL: P_rot chunk pc (coordinates PK pc ..) through registers into
+  // pt[b]; thread t < PK D / 4 takes row m = t % D, 4 coordinates ----
+  float4_t ppre;
+  auto load_p = [&](int pc) {
+    if (tid < PK * D / 4) ppre = *(const float4_t *)(a.p_rot + (int64_t)(tid % D) * D + PK * pc + 4 * (tid / D));
+  };
+  auto store_p = [&](int b) {
+    if (tid < PK * D / 4) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pt[b][(4 * (tid / D) + e) * D + tid % D] = ppre[e];
+    }
+  };
+  // projections acc2[u][g][i] of vector VT tv + u, m = 64 g + 4 tj + i: the
+  // FMA chain over k ascending, k = PK pc .. PK pc + PK - 1 in this call
+  float acc2[VT][NG][4];
+  auto project = [&](int b, int pc) {
+    const float *eb = &es[(VT * tv) * ESP + PK * pc];
+    const float *pb = &pt[b][4 * tj];
+    float4_t ev[VT], pv[4][NG];
+    auto read = [&](int k4, float4_t (&eo)[VT], float4_t (&po)[4][NG]) {
+#pragma unroll
+      for (int u = 0; u < VT; ++u) eo[u] = *(const float4_t *)(eb + u * ESP + 4 * k4);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int g = 0; g < NG; ++g) po[kk][g] = *(const float4_t *)(pb + (4 * k4 + kk) * D + 64 * g);
+    };
+    read(0, ev, pv);
+#pragma nounroll
+    for (int k4 = 0; k4 < PK / 4; ++k4) {
+      float4_t en[VT], pn[4][NG];
+      if (k4 + 1 < PK / 4) read(k4 + 1, en, pn);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int u = 0; u < VT; ++u)
+#pragma unroll
+          for (int g = 0; g < NG; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc2[u][g][i] = __builtin_fmaf(ev[u][kk], pv[kk][g][i], acc2[u][g][i]);
+#pragma unroll
+      for (int u = 0; u < VT; ++u) ev[u] = en[u];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int g = 0; g < NG; ++g) pv[kk][g] = pn[kk][g];
+    }
+  };
+  // sign bytes of step s into sstage: lane tj holds bits 4 (tj & 1) .. + 3
+  // of byte 8 g + tj / 2; the even lane of each pair writes the byte
+  auto signs = [&] {
+#pragma unroll
+    for (int u = 0; u < VT; ++u)
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        uint32_t nib = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) nib |= (acc2[u][g][i] >= 0.0f ? 1u : 0u) << i;
+        const uint32_t other = (uint32_t)__builtin_amdgcn_mov_dpp((int)nib, 0xB1, 0xF, 0xF, true);  // quad_perm [1,0,3,2]
+        if ((tj & 1) == 0) sstage[(VT * tv + u) * SB + 8 * g + (tj >> 1)] = (uint8_t)(nib | (other << 4));
+      }
+  };
+
+  // ---- step s's output from a stage (W bytes per vector) to memory: one
+  // run of 16-byte pieces when the outputs are one aligned run, else dwords
+  // through the output addressing ----
+  auto flush_any = [&](auto wc, uint32_t s, const lds_u8 *stg, uint8_t *outb, uint8_t *const *pages, int64_t stride,
+                       bool r16) {
+    constexpr int W = decltype(wc)::value;
     const uint32_t v0 = s * VS;
     const int nv = (int)min(n - v0, (uint32_t)VS);
-    const lds_u8 *stg = (const lds_u8 *)stage;
-    if (run16) {
-      const int nbytes = nv * VB;
-      uint8_t *base = a.blocks + (int64_t)v0 * VB;
+    if (r16) {
+      const int nbytes = nv * W;
+      uint8_t *base = outb + (int64_t)v0 * W;
 #pragma unroll
-      for (int it = 0; it < (VS * VB / 16 + kTT - 1) / kTT; ++it) {
+      for (int it = 0; it < (VS * W / 16 + kTT - 1) / kTT; ++it) {
         const int p = tid + kTT * it;
         if (16 * p + 16 <= nbytes) {
           *(u32x4 *)(base + 16 * p) = *(const __attribute__((address_space(3))) u32x4 *)(stg + 16 * p);
@@ -277,7 +368,7 @@ __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a
       }
       return;
     }
-    constexpr int DW = VB / 4;
+    constexpr int DW = W / 4;
 #pragma unroll
     for (int it = 0; it < (VS * DW + kTT - 1) / kTT; ++it) {
       const int q = tid + kTT * it;
@@ -285,10 +376,20 @@ __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a
       if (q < VS * DW && vl < nv) {
         const uint32_t v = v0 + vl;
         const uint32_t vo = by_inner.div(v), vi = v - vo * (uint32_t)a.n_inner;
-        *(uint32_t *)(encode_out_addr(a, a.blocks, a.pages, a.blocks_outer_stride, vo, vi, VB) + 4 * c) =
-            *(const lds_u32 *)(stg + vl * VB + 4 * c);
+        *(uint32_t *)(encode_out_addr(a, outb, pages, stride, vo, vi, W) + 4 * c) = *(const lds_u32 *)(stg + vl * W + 4 * c);
       }
     }
+  };
+  const bool run16 = a.n_outer <= 1 && a.pages == nullptr && ((uintptr_t)a.blocks & 15) == 0;
+  const bool srun16 = QJL && a.n_outer <= 1 && a.qjl_pages == nullptr && ((uintptr_t)a.qjl & 15) == 0;
+  auto flush = [&](uint32_t s) {
+    flush_any(std::integral_constant<int, VB>{}, s, (const lds_u8 *)stage, a.blocks, a.pages, a.blocks_outer_stride,
+              run16);
+  };
+  auto flush_signs = [&](uint32_t s) {
+    if constexpr (QJL)
+      flush_any(std::integral_constant<int, SB>{}, s, (const lds_u8 *)sstage, a.qjl, a.qjl_pages, a.qjl_outer_stride,
+                srun16);
   };
 
   // ---- pipeline: chunk c of step s computes from xs[c % 2] while chunk
@@ -324,29 +425,54 @@ __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a
       const bool have_next = !last || s + gridDim.x < steps;
       if (last && have_next) set_rows(s + gridDim.x);
       if (have_next) load(last ? 0 : c + 1);
+      if (QJL && last) load_p(0);
       if (c == 0 && s != blockIdx.x) flush(s - gridDim.x);
+      if (QJL && c == 1 && s != blockIdx.x) flush_signs(s - gridDim.x);
       compute(c & 1, c);
       if (last) quantise(s);
       if (have_next) store_x((c + 1) & 1);
+      if (QJL && last) store_p(0);
       __syncthreads();
     }
+    if constexpr (QJL) {
+#pragma unroll
+      for (int u = 0; u < VT; ++u)
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc2[u][g][i] = 0.0f;
+#pragma unroll
+      for (int pc = 0; pc < NPK; ++pc) {
+        if (pc + 1 < NPK) load_p(pc + 1);
+        project(pc & 1, pc);
+        if (pc + 1 < NPK) store_p((pc + 1) & 1);
+        __syncthreads();
+      }
+      signs();
+    }
   }
+  if constexpr (QJL) __syncthreads();   // the last step's sign bytes
   flush(s - gridDim.x);
+  flush_signs(s - gridDim.x);
 }
 
 // The tiled encoder applies to inputs it can read in 16-byte pieces and
-// outputs it can write in dwords: 16-byte aligned x rows and R, 4-byte
-// aligned blocks and row strides (pages are 16-byte aligned by contract),
-// fewer than 2^32 vectors, no QJL signs.
+// outputs it can write in dwords: 16-byte aligned x rows, R and P_rot,
+// 4-byte aligned blocks, signs and row strides (pages are 16-byte aligned by
+// contract), fewer than 2^32 vectors.
 bool tiled_encode_ok(const EncodeArgs &a, int x_dtype) {
   const int64_t es = x_dtype == 0 ? 4 : 2;
   const int64_t n = a.n_outer * a.n_inner;
+  const bool qjl = a.qjl != nullptr || a.qjl_pages != nullptr;
   if (a.d != 64 && a.d != 128) return false;
-  if (a.qjl != nullptr || a.qjl_pages != nullptr) return false;
   if (n <= 0 || n > ((int64_t)1 << 32) - 1024) return false;
   if ((uintptr_t)a.x % 16 || (uintptr_t)a.R % 16) return false;
   if (a.n_outer > 1 && (a.x_outer_stride * es) % 16) return false;
   if (a.pages == nullptr && ((uintptr_t)a.blocks % 4 || (a.n_outer > 1 && a.blocks_outer_stride % 4))) return false;
+  if (qjl) {
+    if (a.m != a.d || a.p_rot == nullptr || (uintptr_t)a.p_rot % 16) return false;
+    if (a.qjl_pages == nullptr && ((uintptr_t)a.qjl % 4 || (a.n_outer > 1 && a.qjl_outer_stride % 4))) return false;
+  }
   return true;
 }
 
@@ -365,6 +491,23 @@ static int tiled_grid(int64_t n, int vs) {
 
 hipError_t launch_encode_tiled(const EncodeArgs &a, int x_dtype, hipStream_t s) {
   const int64_t n = a.n_outer * a.n_inner;
+  if (a.qjl != nullptr || a.qjl_pages != nullptr) {
+    // QJL keys: half-size steps (LDS room for the residuals and P_rot)
+    const int grid = tiled_grid(n, a.d == 128 ? TiledShape<128, true>::VS : TiledShape<64, true>::VS);
+    const int nl = 1 << a.bits;
+#define PQKV_ETQ(DD, BB)                                                                                    \
+  do {                                                                                                      \
+    if (x_dtype == 0) encode_tiled_kernel<DD, BB, float, true, true><<<grid, kTT, 0, s>>>(a, nl, nullptr);  \
+    else if (x_dtype == 1) encode_tiled_kernel<DD, BB, half_t, true, true><<<grid, kTT, 0, s>>>(a, nl, nullptr); \
+    else encode_tiled_kernel<DD, BB, bf16_t, true, true><<<grid, kTT, 0, s>>>(a, nl, nullptr);              \
+  } while (0)
+    if (a.d == 128 && a.bits == 4) PQKV_ETQ(128, 4);
+    else if (a.d == 128) PQKV_ETQ(128, 2);
+    else if (a.bits == 4) PQKV_ETQ(64, 4);
+    else PQKV_ETQ(64, 2);
+#undef PQKV_ETQ
+    return hipGetLastError();
+  }
   const int vs = tiled_step(n, a.d);
   const bool half = vs < (a.d == 128 ? TiledShape<128, false>::VS : TiledShape<64, false>::VS);
   const int grid = tiled_grid(n, vs);

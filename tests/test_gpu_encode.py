@@ -248,6 +248,57 @@ def test_encode_bf16_bit_exact(layout):
         assert (sg != want_s).mean() < 1e-3
 
 
+def _qjl_check(signs, y, r, idx, cb, P_rot, d):
+    """Sign m of a vector is (P_rot e)[m] >= 0 for e = y - r c[idx] of the
+    FMA-chain rotation, up to ties within fp32 summation error of zero."""
+    e = y.astype(np.float64) - r[:, None].astype(np.float64) * cb[idx].astype(np.float64)
+    proj = e @ P_rot.astype(np.float64).T
+    want = O.bit_unpack_lsb(O.bit_pack_lsb(proj >= 0), d)
+    got = O.bit_unpack_lsb(signs.reshape(-1, d // 8), d)
+    tol = 1e-5 * np.linalg.norm(e, axis=1, keepdims=True) * np.linalg.norm(P_rot, axis=1)[None]
+    assert not ((got != want) & (np.abs(proj) > tol)).any()
+    assert (got != want).mean() < 1e-3
+
+
+@pytest.mark.parametrize("layout", ["contiguous", "paged", "misaligned", "many_steps"])
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("d,bits", [(128, 4), (128, 2), (64, 4)])
+def test_encode_exact_qjl(d, bits, dtype, layout, monkeypatch):
+    """QJL keys on the exact encoders: the register-blocked kernel's
+    projection pass (contiguous, paged, many steps per workgroup) and the
+    four-chain kernel (rows 2 or 4 bytes off a 16-byte boundary). The blocks
+    equal the oracle's bit for bit, the signs up to ties."""
+    print(f"exact QJL d={d} bits={bits} {dtype} {layout}", flush=True)
+    monkeypatch.setenv("PQKV_ENCODE_KERNEL", "exact")
+    R = O.rotation_matrix(d, 42)
+    R32 = R.astype(np.float32)
+    Rt = torch.from_numpy(R32).to(DEV)
+    P_rot = (O.jl_matrix(d, d, 43) @ R.T).astype(np.float32)
+    Pt = torch.from_numpy(P_rot).to(DEV)
+    tdt = getattr(torch, dtype)
+    B, H, T = (1, 1, 2 * 256 * 64 + 33) if layout == "many_steps" else (2, 2, 150)
+    x = torch.from_numpy(_inputs(B * H * T, d, d + bits)).to(DEV).to(tdt).view(B, H, T, d)
+    if layout == "paged":
+        c = quantizer.allocate_paged_cache(B, H, d, bits, DEV, page_tokens=64, jl_dim=d)
+        quantizer.compress_pq(x[:, :, :90].contiguous(), Rt, cache=c, jl_rot=Pt)
+        quantizer.compress_pq(x[:, :, 90:].contiguous(), Rt, cache=c, jl_rot=Pt)
+        cc = c.to_contiguous()
+        blocks, signs = cc.blocks.cpu().numpy(), cc.qjl_signs.cpu().numpy()
+    else:
+        xin = x
+        if layout == "misaligned":
+            buf = torch.zeros(x.numel() + 1, dtype=tdt, device=DEV)
+            xin = buf[1:].view(B, H, T, d)
+            xin.copy_(x)
+            assert xin.data_ptr() % 16 != 0
+        c = quantizer.allocate_cache(B, H, T, d, bits, DEV, jl_dim=d)
+        quantizer.compress_pq(xin, Rt, cache=c, jl_rot=Pt)
+        blocks, signs = c.blocks.cpu().numpy(), c.qjl_signs.cpu().numpy()
+    want, y, r, idx, cb = _oracle_encode(x.float().cpu().numpy().reshape(-1, d), R32, bits)
+    assert np.array_equal(blocks.reshape(B * H * T, -1), want)
+    _qjl_check(signs, y, r, idx, cb, P_rot, d)
+
+
 def test_encode_qjl_signs(monkeypatch):
     """The exact encoder's QJL signs (fp32 FMA-chain rotation)."""
     monkeypatch.setenv("PQKV_ENCODE_KERNEL", "exact")
