@@ -34,7 +34,9 @@
 // Output: block_pq4 / block_pq2 vectors (fp16 radius per block) or the
 // reference's SoA codes (packed[p] = code(2p) | code(2p+1) << 4) with fp32
 // radii, staged in LDS and stored one step later, 16-byte pieces for one
-// aligned run of vectors, dwords otherwise.
+// aligned run of vectors, dwords otherwise. QJL keys add the sign sketch of
+// the residual (src/polarquant_kv_cuda/compress_kernel.py:166-175) as a
+// second tiled product (encode_tiled_kernel's QJL flag).
 #include <type_traits>
 
 #include "pqkv_cells.h"
