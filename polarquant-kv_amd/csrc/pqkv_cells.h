@@ -22,6 +22,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace pqkv {
 
 constexpr int kECells = 1024;           // direction cells over [-1, 1], 1/512 wide
@@ -65,6 +67,36 @@ __device__ __forceinline__ int scan_index_rolled(float d, const float *cb, int n
   return b;
 }
 
+// scan_index as a tree over register-held codebook values: the leftmost
+// strict minimum of |d - c_i| over i < nl, then against the scan's start
+// (1e30, index 0). The same index as the sequential scan for every d (the
+// "keep the left one unless the right one is strictly smaller" rule is
+// associative), with a 4-level instead of a 16-long dependency chain.
+__device__ __forceinline__ int scan_index_tree(float d, const float (&c)[16], int nl) {
+#pragma clang fp contract(off)
+  float v[16];
+  int ix[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    v[k] = k < nl ? fabsf(d - c[k]) : __builtin_inff();
+    ix[k] = k;
+  }
+  auto level = [&](auto wc) {
+    constexpr int W = decltype(wc)::value;
+#pragma unroll
+    for (int k = 0; k < 16; k += 2 * W) {
+      const bool r = v[k + W] < v[k];
+      v[k] = r ? v[k + W] : v[k];
+      ix[k] = r ? ix[k + W] : ix[k];
+    }
+  };
+  level(std::integral_constant<int, 1>{});
+  level(std::integral_constant<int, 2>{});
+  level(std::integral_constant<int, 4>{});
+  level(std::integral_constant<int, 8>{});
+  return v[0] < 1e30f ? ix[0] : 0;
+}
+
 // Direction cell, monotone in d: round(512 d) + 513, for |d| <= kEClamp in
 // 0 .. kECellSlots - 1.
 __device__ __forceinline__ uint32_t cell_bits(float d) {
@@ -100,34 +132,74 @@ __device__ __forceinline__ void build_cell_table(const float *cb, int nl, int ti
   if (tid == 0) *table_ok = 1;
   lds_barrier();
   static_assert(NT >= 256 && NT % 64 == 0, "16 lanes for each of up to 15 switch points");
-  // Switch points: 16 lanes per point i search (c_i, c_{i+1}] 16-ary; lane j
-  // tests the (j + 1)/16 point of the range, and the first that the scan maps
-  // to i + 1 or more closes it. Keys of fp32 values differ by < 2^33, so 9
-  // steps reach a range of one.
+  // the codebook in registers for the scans
+  float c[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) c[e] = cb[e];
+  // Switch points: 16 lanes per point i, each the smallest fp32 d in
+  // (c_i, c_{i+1}] that the scan maps to i + 1 or more. Once the scan maps
+  // c_i to i or less and c_{i+1} to i + 1 or more (one lane each), that
+  // holds for such d exactly when fl(c_{i+1} - d) < fl(d - c_i) (and below
+  // the scan's 1e30 start): rounding is monotone, so every earlier centroid
+  // is at least as far as c_i and every later one at least as far as
+  // c_{i+1}. First, one probe: lane j tests the fp32 value j - 8 steps from
+  // the midpoint of c_i and c_{i+1}, where the switch point lies up to the
+  // subtractions' rounding for all but a pair around zero; when lane 0's
+  // value fails and lane 15's passes, the first lane that passes holds it.
+  // Otherwise the lanes search 16-ary: lane j tests the (j + 1)/16 point of
+  // the range, and the first that passes closes it (keys of fp32 values
+  // differ by < 2^32, so 8 steps reach a range of one; a wave with no open
+  // range leaves the loop).
   {
     const int i = tid >> 4, j = tid & 15;
     const bool act = i < nl - 1;
-    bool ok = act;
-    int64_t lo = 0, hi = 0;
-    if (act) {
-      ok = cb[i] < cb[i + 1] && scan_index(cb[i], cb, nl) <= i && scan_index(cb[i + 1], cb, nl) >= i + 1;
-      lo = fkey(cb[i]);
-      hi = fkey(cb[i + 1]);
+    const float ci = act ? cb[i] : 0.0f, cn = act ? cb[i + 1] : 0.0f;
+    bool ok = false;
+    {
+      const bool bad = act && j < 2 && (j == 0 ? scan_index_tree(ci, c, nl) > i : scan_index_tree(cn, c, nl) < i + 1);
+      ok = act && ci < cn && ((uint32_t)(__builtin_amdgcn_ballot_w64(bad) >> (16 * (i & 3))) & 3u) == 0;
+    }
+    auto pass = [&](int32_t key) {
+#pragma clang fp contract(off)
+      const float d = kfloat(key);
+      const float en = cn - d, ei = d - ci;
+      return en < ei && en < 1e30f;
+    };
+    // keys as unsigned differences (hi > lo, so hi - lo < 2^32 is exact
+    // modulo 2^32) and lo + floor(span q / 16) without 64-bit products
+    auto span_of = [](int32_t l, int32_t h) { return (uint32_t)h - (uint32_t)l; };
+    auto part = [](uint32_t span, int q) { return (span >> 4) * (uint32_t)q + (((span & 15u) * (uint32_t)q) >> 4); };
+    auto add = [](int32_t l, uint32_t off) { return (int32_t)((uint32_t)l + off); };
+    int32_t lo = act ? (int32_t)fkey(ci) : 0, hi = act ? (int32_t)fkey(cn) : 0;
+    const int32_t mid = act ? (int32_t)fkey(0.5f * ci + 0.5f * cn) : 0;
+    auto probe_key = [&](int q) {
+      const int64_t k = (int64_t)mid - 8 + q;
+      return (int32_t)(k < lo ? lo : k > hi ? hi : k);
+    };
+    {
+      const bool pp = ok && pass(probe_key(j));
+      const uint32_t pm = (uint32_t)(__builtin_amdgcn_ballot_w64(pp) >> (16 * (i & 3))) & 0xFFFFu;
+      if (ok && (pm & 1u) == 0 && (pm >> 15) != 0) {
+        hi = probe_key(__builtin_ctz(pm));
+        lo = add(hi, 0xFFFFFFFFu);   // hi - 1
+      }
     }
     for (int step = 0; step < 10; ++step) {
-      const int64_t span = hi - lo;
-      const int64_t cand = j == 15 ? hi : lo + ((span * (j + 1)) >> 4);
-      const bool p = ok && span > 1 && scan_index(kfloat(cand), cb, nl) >= i + 1;
+      const bool open = ok && span_of(lo, hi) > 1u;
+      if (__builtin_amdgcn_ballot_w64(open) == 0) break;
+      const uint32_t span = span_of(lo, hi);
+      const int32_t cand = j == 15 ? hi : add(lo, part(span, j + 1));
+      const bool p = open && pass(cand);
       const uint32_t gm = (uint32_t)(__builtin_amdgcn_ballot_w64(p) >> (16 * (i & 3))) & 0xFFFFu;
       const int k = gm ? __builtin_ctz(gm) : 15;
-      if (ok && span > 1) {
-        const int64_t nhi = k == 15 ? hi : lo + ((span * (k + 1)) >> 4);
-        lo = k == 0 ? lo : lo + ((span * k) >> 4);
+      if (open) {
+        const int32_t nhi = k == 15 ? hi : add(lo, part(span, k + 1));
+        lo = k == 0 ? lo : add(lo, part(span, k));
         hi = nhi;
       }
     }
     if (act && j == 0) {
-      if (!ok || hi - lo != 1) {
+      if (!ok || span_of(lo, hi) != 1u) {
         *table_ok = 0;
       } else {
         const float t = kfloat(hi);
@@ -139,17 +211,28 @@ __device__ __forceinline__ void build_cell_table(const float *cb, int nl, int ti
   }
   lds_barrier();
   if (*table_ok != 0) {
+    // the switch points' cells in registers (read once: the table stores
+    // below could alias them); cells past the last switch point match no slot
+    int uc[15];
+#pragma unroll
+    for (int e = 0; e < 15; ++e) uc[e] = e < nl - 1 ? ucell[e] : 0x7FFFFFFF;
+    // index at each cell's start: the switch points in earlier cells
+    // (branch-free); the switch point inside a cell is written below
     for (int u = tid; u < kECellSlots; u += NT) {
-      int base = 0, inside = -1, count = 0;
-      for (int i = 0; i < nl - 1; ++i) {
-        if (ucell[i] < u) ++base;
-        else if (ucell[i] == u) {
-          inside = i;
-          ++count;
-        }
-      }
-      if (count > 1) *table_ok = 0;
-      cells[u] = make_uint2((uint32_t)base, inside >= 0 ? __builtin_bit_cast(uint32_t, thr[inside]) : 0x7F800000u);
+      int base = 0;
+#pragma unroll
+      for (int e = 0; e < 15; ++e) base += uc[e] < u ? 1 : 0;
+      cells[u] = make_uint2((uint32_t)base, 0x7F800000u);   // +inf: no switch point inside
+    }
+    // two switch points in one cell: no table (the cells are non-decreasing)
+    bool crowded = false;
+#pragma unroll
+    for (int e = 0; e + 1 < 15; ++e) crowded |= e + 1 < nl - 1 && uc[e] == uc[e + 1];
+    lds_barrier();
+    if (crowded) {
+      if (tid == 0) *table_ok = 0;
+    } else if (tid < nl - 1) {
+      cells[ucell[tid]].y = __builtin_bit_cast(uint32_t, thr[tid]);
     }
   }
   lds_barrier();

@@ -160,6 +160,9 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
   typedef __attribute__((address_space(3))) uint32_t lds_u32;
 
   const int tid = threadIdx.x, lane = tid & 63;
+  // the codebook's load first: its LDS copy below then waits for it alone,
+  // not for R's loads behind it
+  const float cbv = tid < NL ? a.codebook[tid] : 0.0f;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
   // chunk swizzle of a vector's 16-byte pieces in LDS: the B-operand reads of
@@ -216,7 +219,7 @@ __global__ void __launch_bounds__(kEW * 64, kEBlocksPerCU) encode_mfma_kernel(co
       }
   }
 
-  if (tid < 16) cb[tid] = tid < NL ? a.codebook[tid] : 0.0f;
+  if (tid < 16) cb[tid] = cbv;
 
   const half_t *x = (const half_t *)a.x;
   // vector v = n_inner * vo + vi; the host keeps n below 2^32 (a single row

@@ -398,9 +398,10 @@ __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a
   // c + 1 (or the next step's chunk 0) is in flight into registers; one
   // barrier per chunk. The host launches at most `steps` workgroups. ----
   uint32_t s = blockIdx.x;
+  const float cbv = tid < nl ? a.codebook[tid] : 0.0f;   // first, so its LDS copy waits for it alone
   set_rows(s);
   load(0);   // in flight during the set-up below
-  if (tid < 16) cb[tid] = tid < nl ? a.codebook[tid] : 0.0f;
+  if (tid < 16) cb[tid] = cbv;
   // R^T: consecutive lanes take consecutive rows j of one 4-column slice, so
   // the transposed LDS writes fall in distinct banks
   for (int q = tid; q < D * D / 4; q += kTT) {
