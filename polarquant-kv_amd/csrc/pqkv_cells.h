@@ -4,10 +4,11 @@
 // |dir - c_i| over the codebook and keeps the first minimum. For a strictly
 // increasing codebook that index is a step function of dir: it equals the
 // number of switch points theta_i <= dir, where theta_i is the smallest fp32
-// value the scan maps to i + 1. build_cell_table() finds the switch points by
-// bisection over fp32 values with the scan itself, then fills a table over
-// 1027 direction cells holding (index at the cell start, the switch point
-// inside the cell or +inf): one LDS read and one compare per coordinate. The
+// value the scan maps to i + 1. build_cell_table() finds the switch points
+// (a probe around each midpoint, then a 16-ary search over fp32 values, both
+// with a test equivalent to the scan there), then fills a table over 1027
+// direction cells holding (index at the cell start, the switch point inside
+// the cell or +inf): one LDS read and one compare per coordinate. The
 // cell of dir is round(512 dir) + 513, read from the low bits of
 // fma(dir, 512, 1.5 * 2^23), monotone in dir; the table is built with the same
 // function. A codebook that is not strictly increasing, with a switch point
