@@ -4,9 +4,9 @@
 // quantiser of csrc/flash_turboquant.cu:141-170 on the values in registers.
 //
 // Work split. A workgroup of 8 waves takes VS vectors per step (128 at
-// d = 128, 256 at d = 64; half that when full-size steps would leave compute
-// units without one). Lane row tv = tid / 16 owns VT consecutive vectors of
-// the step (4 / 8, or 2 / 4) and lane tj = tid % 16 of the row owns output
+// d = 128, 256 at d = 64; a half or a quarter of that when full-size steps
+// would leave compute units without one). Lane row tv = tid / 16 owns VT
+// consecutive vectors of the step (4 / 8, 2 / 4 or 1 / 2) and lane tj = tid % 16 of the row owns output
 // coordinates j = 64 g + 4 tj + i (g < d / 64, i < 4): 32 accumulators per
 // thread, each the chain of one (vector, coordinate) over k ascending, so
 // every rotated value is bit-identical to the one-chain form. Per k a thread
@@ -53,12 +53,12 @@ constexpr int kTK = 32;             // input coordinates per staged chunk
 constexpr int kTXP = kTK + 4;       // floats per staged vector chunk (padded: 16-byte aligned rows in
                                     // different banks)
 
-// HALF: half the vectors per thread and step, for launches with fewer
-// full-size steps than compute units.
-template <int D, bool HALF>
+// SH: the vectors per thread and step halved SH times (0..2), for launches
+// with fewer full-size steps than compute units.
+template <int D, int SH>
 struct TiledShape {
   static constexpr int NG = D / 64;               // 64-coordinate groups per thread
-  static constexpr int VT = (8 / NG) >> HALF;     // vectors per thread
+  static constexpr int VT = (8 / NG) >> SH;       // vectors per thread
   static constexpr int VS = 32 * VT;              // vectors per step (32 rows of 16 lanes)
   static constexpr int NC = D / kTK;              // chunks per step
 };
@@ -83,9 +83,9 @@ typedef __attribute__((address_space(3))) uint32_t lds_u32;
 // P_rot staged in 16-coordinate chunks (transposed, double-buffered); sign
 // bit m = (P_rot e)[m] >= 0, LSB first, stored one step later like the
 // blocks.
-template <int D, int OUT, typename TIN, bool HALF, bool QJL = false>
+template <int D, int OUT, typename TIN, int SH, bool QJL = false>
 __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a, const int nl, float *soa_radius) {
-  using S = TiledShape<D, HALF>;
+  using S = TiledShape<D, SH>;
   constexpr int NG = S::NG, VT = S::VT, VS = S::VS, NC = S::NC;
   constexpr int VB = OUT == 0 ? D / 2 : vector_bytes(D, OUT);   // output bytes per vector
   constexpr int BB = OUT == 0 ? 0 : block_bytes(OUT);
@@ -99,7 +99,8 @@ __global__ void __launch_bounds__(kTT, 1) encode_tiled_kernel(const EncodeArgs a
   constexpr int PK = 16;             // projection k per staged chunk of P_rot
   constexpr int NPK = D / PK;        // chunks per projection
   constexpr int ESP = D + 4;         // floats per residual row (padded like xs)
-  static_assert(!QJL || (HALF && OUT != 0), "QJL keys: blocks, half-size steps");
+  static_assert(VT >= 1, "at least one vector per thread");
+  static_assert(!QJL || (SH >= 1 && OUT != 0), "QJL keys: blocks, half-size or smaller steps");
   static_assert(PK * D / 4 <= kTT, "one P_rot piece per thread and chunk");
   __shared__ __attribute__((aligned(16))) float rt[D * D];           // rt[k * D + j] = R[j][k]
   __shared__ __attribute__((aligned(16))) float xs[2][VS * kTXP];    // xs[b][v * kTXP + kk]
@@ -479,14 +480,17 @@ bool tiled_encode_ok(const EncodeArgs &a, int x_dtype) {
   return true;
 }
 
-// Vectors per step: full-size steps, or half-size ones when full-size steps
-// would leave compute units without one.
-static int tiled_step(int64_t n, int d) {
-  const int full = d == 128 ? TiledShape<128, false>::VS : TiledShape<64, false>::VS;
-  return (n + full - 1) / full < device_compute_units() ? full / 2 : full;
+// Step size: the smallest halving (from min_sh, at most 2) whose steps give
+// every compute unit one, so small launches spread over more compute units.
+static int tiled_shift(int64_t n, int d, int min_sh) {
+  const int full = d == 128 ? TiledShape<128, 0>::VS : TiledShape<64, 0>::VS;
+  int sh = min_sh;
+  while (sh < 2 && (n + (full >> sh) - 1) / (full >> sh) < device_compute_units()) ++sh;
+  return sh;
 }
 
-static int tiled_grid(int64_t n, int vs) {
+static int tiled_grid(int64_t n, int d, int sh) {
+  const int vs = (d == 128 ? TiledShape<128, 0>::VS : TiledShape<64, 0>::VS) >> sh;
   const int64_t steps = (n + vs - 1) / vs;
   const int64_t cap = device_compute_units();
   return (int)(steps < cap ? steps : cap);
@@ -494,31 +498,37 @@ static int tiled_grid(int64_t n, int vs) {
 
 hipError_t launch_encode_tiled(const EncodeArgs &a, int x_dtype, hipStream_t s) {
   const int64_t n = a.n_outer * a.n_inner;
+  const int nl = 1 << a.bits;
   if (a.qjl != nullptr || a.qjl_pages != nullptr) {
-    // QJL keys: half-size steps (LDS room for the residuals and P_rot)
-    const int grid = tiled_grid(n, a.d == 128 ? TiledShape<128, true>::VS : TiledShape<64, true>::VS);
-    const int nl = 1 << a.bits;
-#define PQKV_ETQ(DD, BB)                                                                                    \
-  do {                                                                                                      \
-    if (x_dtype == 0) encode_tiled_kernel<DD, BB, float, true, true><<<grid, kTT, 0, s>>>(a, nl, nullptr);  \
-    else if (x_dtype == 1) encode_tiled_kernel<DD, BB, half_t, true, true><<<grid, kTT, 0, s>>>(a, nl, nullptr); \
-    else encode_tiled_kernel<DD, BB, bf16_t, true, true><<<grid, kTT, 0, s>>>(a, nl, nullptr);              \
+    // QJL keys: half-size steps or smaller (LDS room for the residuals and P_rot)
+    const int sh = tiled_shift(n, a.d, 1);
+    const int grid = tiled_grid(n, a.d, sh);
+#define PQKV_ETQ_T(DD, BB, TT)                                                                   \
+  do {                                                                                           \
+    if (sh == 1) encode_tiled_kernel<DD, BB, TT, 1, true><<<grid, kTT, 0, s>>>(a, nl, nullptr);  \
+    else encode_tiled_kernel<DD, BB, TT, 2, true><<<grid, kTT, 0, s>>>(a, nl, nullptr);          \
+  } while (0)
+#define PQKV_ETQ(DD, BB)                              \
+  do {                                                \
+    if (x_dtype == 0) PQKV_ETQ_T(DD, BB, float);      \
+    else if (x_dtype == 1) PQKV_ETQ_T(DD, BB, half_t); \
+    else PQKV_ETQ_T(DD, BB, bf16_t);                  \
   } while (0)
     if (a.d == 128 && a.bits == 4) PQKV_ETQ(128, 4);
     else if (a.d == 128) PQKV_ETQ(128, 2);
     else if (a.bits == 4) PQKV_ETQ(64, 4);
     else PQKV_ETQ(64, 2);
 #undef PQKV_ETQ
+#undef PQKV_ETQ_T
     return hipGetLastError();
   }
-  const int vs = tiled_step(n, a.d);
-  const bool half = vs < (a.d == 128 ? TiledShape<128, false>::VS : TiledShape<64, false>::VS);
-  const int grid = tiled_grid(n, vs);
-  const int nl = 1 << a.bits;
-#define PQKV_ET_T(DD, BB, TT)                                                                     \
-  do {                                                                                            \
-    if (!half) encode_tiled_kernel<DD, BB, TT, false><<<grid, kTT, 0, s>>>(a, nl, nullptr);       \
-    else encode_tiled_kernel<DD, BB, TT, true><<<grid, kTT, 0, s>>>(a, nl, nullptr);              \
+  const int sh = tiled_shift(n, a.d, 0);
+  const int grid = tiled_grid(n, a.d, sh);
+#define PQKV_ET_T(DD, BB, TT)                                                             \
+  do {                                                                                    \
+    if (sh == 0) encode_tiled_kernel<DD, BB, TT, 0><<<grid, kTT, 0, s>>>(a, nl, nullptr); \
+    else if (sh == 1) encode_tiled_kernel<DD, BB, TT, 1><<<grid, kTT, 0, s>>>(a, nl, nullptr); \
+    else encode_tiled_kernel<DD, BB, TT, 2><<<grid, kTT, 0, s>>>(a, nl, nullptr);         \
   } while (0)
 #define PQKV_ET(DD, BB)                          \
   do {                                           \
@@ -551,13 +561,17 @@ hipError_t launch_encode_soa_tiled(const float *x, const float *R, const float *
   a.n_outer = 1;
   a.n_inner = n;
   a.d = d;
-  const int vs = tiled_step(n, d);
-  const bool half = vs < (d == 128 ? TiledShape<128, false>::VS : TiledShape<64, false>::VS);
-  const int grid = tiled_grid(n, vs);
-  if (d == 128 && !half) encode_tiled_kernel<128, 0, float, false><<<grid, kTT, 0, s>>>(a, n_levels, radius);
-  else if (d == 128) encode_tiled_kernel<128, 0, float, true><<<grid, kTT, 0, s>>>(a, n_levels, radius);
-  else if (!half) encode_tiled_kernel<64, 0, float, false><<<grid, kTT, 0, s>>>(a, n_levels, radius);
-  else encode_tiled_kernel<64, 0, float, true><<<grid, kTT, 0, s>>>(a, n_levels, radius);
+  const int sh = tiled_shift(n, d, 0);
+  const int grid = tiled_grid(n, d, sh);
+#define PQKV_ES(DD)                                                                                  \
+  do {                                                                                               \
+    if (sh == 0) encode_tiled_kernel<DD, 0, float, 0><<<grid, kTT, 0, s>>>(a, n_levels, radius);     \
+    else if (sh == 1) encode_tiled_kernel<DD, 0, float, 1><<<grid, kTT, 0, s>>>(a, n_levels, radius); \
+    else encode_tiled_kernel<DD, 0, float, 2><<<grid, kTT, 0, s>>>(a, n_levels, radius);             \
+  } while (0)
+  if (d == 128) PQKV_ES(128);
+  else PQKV_ES(64);
+#undef PQKV_ES
   return hipGetLastError();
 }
 

@@ -183,6 +183,23 @@ def test_encode_exact_layouts(layout, monkeypatch):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("n", [40, 9000, 20000, 40000])
+def test_encode_exact_step_sizes(n, monkeypatch):
+    """The register-blocked exact encoder picks quarter-, half- or full-size
+    steps by how many full-size steps a launch has (40 and 9000 vectors:
+    quarter, 20000: half, 40000: full on 256 compute units); every size
+    equals the oracle bit for bit."""
+    print(f"exact encode step sizes n={n}", flush=True)
+    monkeypatch.setenv("PQKV_ENCODE_KERNEL", "exact")
+    d, bits = 128, 4
+    x = _inputs(n, d, 17)
+    R32 = O.rotation_matrix(d, 42).astype(np.float32)
+    c = quantizer.allocate_cache(1, 1, n, d, bits, DEV)
+    quantizer.compress_pq(torch.from_numpy(x).to(DEV).view(1, 1, n, d), torch.from_numpy(R32).to(DEV), cache=c)
+    want, *_ = _oracle_encode(x, R32, bits)
+    assert np.array_equal(c.blocks.cpu().numpy().reshape(n, -1), want)
+
+
 @pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
 @pytest.mark.parametrize("d,bits", [(128, 4), (128, 2), (64, 4), (64, 2)])
 def test_encode_exact_full_steps(d, bits, dtype, monkeypatch):
