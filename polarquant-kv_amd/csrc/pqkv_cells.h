@@ -5,8 +5,9 @@
 // increasing codebook that index is a step function of dir: it equals the
 // number of switch points theta_i <= dir, where theta_i is the smallest fp32
 // value the scan maps to i + 1. build_cell_table() finds the switch points
-// (a probe around each midpoint, then a 16-ary search over fp32 values, both
-// with a test equivalent to the scan there), then fills a table over 1027
+// (a probe around each midpoint, a second one half an ulp from zero for a
+// pair symmetric about it, then a 16-ary search over fp32 values, all with a
+// test equivalent to the scan there), then fills a table over 1027
 // direction cells holding (index at the cell start, the switch point inside
 // the cell or +inf): one LDS read and one compare per coordinate. The
 // cell of dir is round(512 dir) + 513, read from the low bits of
@@ -147,7 +148,8 @@ __device__ __forceinline__ void build_cell_table(const float *cb, int nl, int ti
   // the midpoint of c_i and c_{i+1}, where the switch point lies up to the
   // subtractions' rounding for all but a pair around zero; when lane 0's
   // value fails and lane 15's passes, the first lane that passes holds it.
-  // Otherwise the lanes search 16-ary: lane j tests the (j + 1)/16 point of
+  // A pair symmetric about zero gets a second probe around half an ulp of
+  // its centroids. Otherwise the lanes search 16-ary: lane j tests the (j + 1)/16 point of
   // the range, and the first that passes closes it (keys of fp32 values
   // differ by < 2^32, so 8 steps reach a range of one; a wave with no open
   // range leaves the loop).
@@ -173,17 +175,29 @@ __device__ __forceinline__ void build_cell_table(const float *cb, int nl, int ti
     auto add = [](int32_t l, uint32_t off) { return (int32_t)((uint32_t)l + off); };
     int32_t lo = act ? (int32_t)fkey(ci) : 0, hi = act ? (int32_t)fkey(cn) : 0;
     const int32_t mid = act ? (int32_t)fkey(0.5f * ci + 0.5f * cn) : 0;
-    auto probe_key = [&](int q) {
-      const int64_t k = (int64_t)mid - 8 + q;
-      return (int32_t)(k < lo ? lo : k > hi ? hi : k);
-    };
-    {
-      const bool pp = ok && pass(probe_key(j));
+    // one probe of 16 consecutive keys from around - 8; closes the range
+    // when the first key fails and the last passes
+    auto probe = [&](int32_t around) {
+      auto key_at = [&](int q) {
+        const int64_t k = (int64_t)around - 8 + q;
+        return (int32_t)(k < lo ? lo : k > hi ? hi : k);
+      };
+      const bool open = ok && span_of(lo, hi) > 1u;
+      const bool pp = open && pass(key_at(j));
       const uint32_t pm = (uint32_t)(__builtin_amdgcn_ballot_w64(pp) >> (16 * (i & 3))) & 0xFFFFu;
-      if (ok && (pm & 1u) == 0 && (pm >> 15) != 0) {
-        hi = probe_key(__builtin_ctz(pm));
+      if (open && (pm & 1u) == 0 && (pm >> 15) != 0) {
+        hi = key_at(__builtin_ctz(pm));
         lo = add(hi, 0xFFFFFFFFu);   // hi - 1
       }
+    };
+    probe(mid);
+    // A pair symmetric about zero (c_i = -c_{i+1}, midpoint 0): the switch
+    // point is where fl(c_{i+1} - d) or fl(-c_i + d) first rounds away from
+    // its centroid, half an ulp of it (the smaller of the ulp below c_{i+1}
+    // and the ulp above -c_i), up to the tie rule.
+    if (__builtin_amdgcn_ballot_w64(ok && span_of(lo, hi) > 1u) != 0) {
+      const float ub = cn - kfloat((int64_t)fkey(cn) - 1), ua = kfloat((int64_t)fkey(-ci) + 1) + ci;
+      probe(act && mid == 0 ? (int32_t)fkey(0.5f * (ub < ua ? ub : ua)) : mid);
     }
     for (int step = 0; step < 10; ++step) {
       const bool open = ok && span_of(lo, hi) > 1u;
