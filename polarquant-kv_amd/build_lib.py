@@ -40,6 +40,18 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", "--offload-arch=gfx950", "-Wall", "-Wno-
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
+# Per-unit device flags. The 4-bit-key split-decode units schedule for
+# instruction-level parallelism: their loop is latency-bound at two waves per
+# SIMD, and the ILP scheduler keeps them within 256 VGPRs without spills
+# (config-3 split kernel 0.4-0.9 us faster, config 2 0.2 us). The 2-bit-key
+# units ran 0.4 us slower under it, the ggml and SoA units spill, and the
+# encode and prefill kernels run slower, so they keep the default scheduler.
+ILP = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
+UNIT_FLAGS = {f: ILP for f in ("pqkv_decode_mfma_k4v4_shared.hip", "pqkv_decode_mfma_k4v4_own.hip",
+                               "pqkv_decode_mfma_k4v2.hip", "pqkv_decode_mfma_paged_k4v4_shared.hip",
+                               "pqkv_decode_mfma_paged_k4v4_own.hip")}
+
+
 def _headers_mtime() -> float:
     hs = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
     hs.append(os.path.join(HERE, "..", "include", "pqkv.h"))
@@ -53,7 +65,7 @@ def compile_one(src: str, changed_only: bool = False) -> str:
             os.path.getmtime(obj) > max(os.path.getmtime(path), _headers_mtime()):
         return obj
     if src.endswith(".hip"):
-        cmd = [hipcc(), *COMMON, "-x", "hip", "-c", path, "-o", obj]
+        cmd = [hipcc(), *COMMON, *UNIT_FLAGS.get(src, []), "-x", "hip", "-c", path, "-o", obj]
     else:
         # host-only units (validation, C ABI, the ggml type's CPU traits): plain
         # g++ against the HIP headers; no contraction, so host arithmetic
