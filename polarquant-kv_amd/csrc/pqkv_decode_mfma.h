@@ -337,8 +337,11 @@ struct DecodeSmem {
 // tokens (>= 64, so a 64-token chunk lies in one page) found through the
 // page tables a.k_pages / a.v_pages / a.s_pages; each chunk's loads go
 // through a buffer over its own page.
+// FREE: the steady-state iteration has no scheduling fences between its
+// table reads, softmax weights and products (the mixed-width pair kernel,
+// 3.5 % faster that way; the single-width kernels are faster with them).
 template <int D, int G, int KB, int VBITS, bool QJL, bool VSH, bool SOA = false, bool GG = false, bool HW = false,
-          bool PG = false>
+          bool PG = false, bool FREE = false>
 __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem<D, G, KB, VBITS, QJL, VSH> &sm,
                                                  const int split, const int bh) {
   static_assert(!SOA || (KB == 4 && VBITS == 4 && !QJL), "the SoA layout carries 4-bit codes and no QJL signs");
@@ -922,9 +925,9 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs &a, DecodeSmem
           if constexpr (kCompact) load_mask(k, tk);
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (!FREE) __builtin_amdgcn_sched_barrier(0);
       const half8_t pav = fweights(sv[j], rvl, j, f);
-      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (!FREE) __builtin_amdgcn_sched_barrier(0);
       kmma(kt, rkl, j, k.mw, sn[j]);
       vmma(pav, vt);
     }
@@ -1075,9 +1078,11 @@ __global__ void __launch_bounds__(256, kMfmaBlocksPerCU) decode_mfma_pair_kernel
   __shared__ __attribute__((aligned(16))) uint8_t raw[sizeof(S4) > sizeof(S2) ? sizeof(S4) : sizeof(S2)];
   const int n4 = a4.B * a4.n_heads;
   if ((int)blockIdx.y < n4)
-    decode_mfma_body<D, G, 4, 4, QJL, true>(a4, *reinterpret_cast<S4 *>(raw), blockIdx.x, blockIdx.y);
+    decode_mfma_body<D, G, 4, 4, QJL, true, false, false, false, false, true>(a4, *reinterpret_cast<S4 *>(raw),
+                                                                              blockIdx.x, blockIdx.y);
   else
-    decode_mfma_body<D, G, 2, 2, QJL, false>(a2, *reinterpret_cast<S2 *>(raw), blockIdx.x, blockIdx.y - n4);
+    decode_mfma_body<D, G, 2, 2, QJL, false, false, false, false, false, true>(a2, *reinterpret_cast<S2 *>(raw),
+                                                                               blockIdx.x, blockIdx.y - n4);
 }
 
 
